@@ -1,0 +1,257 @@
+#!/usr/bin/env python3
+"""bench.py - XeStrata's MoE-layer hot path on one MI355X.
+
+Metric: MoE-layer decode us/token and expert-weight HBM GB/s (% of peak); prefill TFLOP/s.
+Workload of `value`: config 2 (Qwen3-30B-A3B-shaped layer: hidden 2048, 128 experts, top-8, F 768, Q4_K gate/up,
+Q6_K down), decode batch 1; a step = one whole MoE layer (router -> plan -> q8_1 -> grouped experts -> combine ->
+residual) for one token, the layer's weights rotated over `--copies` distinct HBM copies (>= 1 GB, past the 256 MB
+Infinity Cache).  value = expert-weight GB/s = (distinct experts touched x blob bytes) / time per step.
+Each step sequence is captured once in a HIP graph and replayed; inputs are resident in HBM before timing.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+import argparse
+import json
+import math
+import os
+import pathlib
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "xestrata-win_amd"))
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, published
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, published
+METRIC = "MoE-layer decode µs/token + expert-weight HBM GB/s (% of peak); prefill TFLOP/s"
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def graph_time(torch, fn, replays):
+    """Capture fn() once in a HIP graph; replay `replays` times between two events; return ms per replay."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()                                  # eager warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    g.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(replays):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / replays, g
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--copies", type=int, default=8, help="distinct HBM copies of the layer's weights to rotate over")
+    ap.add_argument("--prefill-steps", type=int, default=10)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU only: this build's MoE path runs on a single MI355X (no multi-GPU path); "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+    import xsmoe as xm
+
+    dev = "cuda:0"
+    torch.cuda.set_device(0)
+    E, H, F, k = 128, 2048, 768, 8
+    copies = args.copies
+    log(f"building {copies} copies of the config-2 layer ({E} experts, Q4_K/Q6_K)")
+    arena, L = xm.build_arena(E, H, F, xm.Q4_K, xm.Q6_K, seed=0, copies=copies)
+    blob = L.bytes
+    layer_bytes = E * blob
+    log(f"arena {copies * layer_bytes / 1e9:.2f} GB, blob {blob} B")
+    gen = torch.Generator(device=dev).manual_seed(1)
+
+    def decode_run(T, steps, warmup):
+        """Time `steps` decode layer steps of T tokens (one graph = one step per copy); returns (ms/step, bytes/step)."""
+        n_logit_sets = copies
+        logits = torch.randn(n_logit_sets, T, E, device=dev, generator=gen)
+        x = torch.randn(T, H, device=dev, generator=gen).to(torch.bfloat16).float()
+        res = torch.randn(T, H, device=dev, generator=gen)
+        out = torch.empty(copies, T, H, device=dev)
+        layer = xm.MoeLayer(L, arena, E, k, T)
+        distinct = []
+        for c in range(copies):
+            ids = torch.topk(logits[c], k, dim=1).indices
+            distinct.append(len(torch.unique(ids)))
+
+        def one_round():
+            for c in range(copies):
+                layer(x, logits[c], res, out[c], arena=arena[c * E])
+
+        replays = max(1, math.ceil(steps / copies))
+        wrep = max(1, math.ceil(warmup / copies))
+        graph_time(torch, one_round, wrep)                   # warm-up replays
+        ms, _ = graph_time(torch, one_round, replays)
+        ms_step = ms / copies
+        bytes_step = float(np.mean(distinct)) * blob
+        return ms_step, bytes_step, replays * copies
+
+    # ---------------------------------------------------------------- decode, batch 1 (the value)
+    ms1, bytes1, steps1 = decode_run(1, args.steps, args.warmup)
+    gbs1 = bytes1 / (ms1 * 1e-3) / 1e9
+    log(f"decode T=1: {ms1 * 1e3:.2f} us/layer, {gbs1:.0f} GB/s expert weights")
+
+    # ---------------------------------------------------------------- the dominant kernel alone (gate/up rows)
+    T = 1
+    ids_l, plans = [], []
+    capx = T * k
+    logits = torch.randn(copies, T, E, device=dev, generator=gen)
+    x = torch.randn(T, H, device=dev, generator=gen).to(torch.bfloat16).float()
+    xq = xm.quantize_q8_1_rows(x)
+    o = xm.plan_offsets(capx)
+    for c in range(copies):
+        ids, w = xm.router_top10(logits[c], k)
+        plan = torch.zeros(xm.plan_words(capx) + 2, dtype=torch.int32, device=dev)
+        skip = torch.zeros(1, dtype=torch.int32, device=dev)
+        xm.resident_plan(ids.reshape(-1), k, None, E, arena[c * E].data_ptr(), None, blob, plan, capx, skip, 1)
+        plans.append(plan)
+    scratch = torch.zeros(xm.native_expert_scratch_bytes(capx, F), dtype=torch.uint8, device=dev)
+    parts = torch.zeros(capx, H, device=dev)
+    cap_groups = min(capx, E)
+
+    def gu_round():
+        for p in plans:
+            ptr = p[o["ptr"]:o["ptr"] + 2 * capx].view(torch.int64)
+            xm.native_expert_gate_up(L, ptr, p[4:], p[0:1], p[o["tok"]:], cap_groups, capx, xq, scratch)
+
+    def down_round():
+        for p in plans:
+            ptr = p[o["ptr"]:o["ptr"] + 2 * capx].view(torch.int64)
+            xm.native_expert_down(L, ptr, p[4:], p[0:1], p[o["dst"]:], cap_groups, capx, scratch, parts)
+
+    kreps = max(4, args.steps // copies)
+    ms_gu, _ = graph_time(torch, gu_round, kreps)
+    ms_dn, _ = graph_time(torch, down_round, kreps)
+    us_gu = ms_gu * 1e3 / copies
+    us_dn = ms_dn * 1e3 / copies
+    gu_bytes = k * 2 * F * L.gu_row          # algorithmic: 8 experts' gate + up rows per launch
+    dn_bytes = k * H * L.d_row               # 8 experts' down rows per launch
+    gu_gbs = gu_bytes / (us_gu * 1e-6) / 1e9
+    dn_gbs = dn_bytes / (us_dn * 1e-6) / 1e9
+    log(f"gate/up kernel {us_gu:.2f} us ({gu_gbs:.0f} GB/s), down kernel {us_dn:.2f} us ({dn_gbs:.0f} GB/s)")
+
+    # ---------------------------------------------------------------- decode batches 4 and 16, verify 4
+    extra = {}
+    for T in (4, 16):
+        ms, b, _ = decode_run(T, max(copies, args.steps // 4), copies)
+        extra[f"T{T}"] = dict(us_per_layer=round(ms * 1e3, 2), us_per_token=round(ms * 1e3 / T, 3),
+                              tokens_per_s=round(T / (ms * 1e-3), 1), expert_gbs=round(b / (ms * 1e-3) / 1e9, 1),
+                              frac_hbm_peak=round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                              distinct_experts=round(b / blob, 2))
+        log(f"decode T={T}: {ms * 1e3:.2f} us/layer, {extra[f'T{T}']['expert_gbs']} GB/s")
+
+    # ---------------------------------------------------------------- prefill 2048 tokens, Zipf(1.2) routing
+    Tp = 2048
+    rng = np.random.default_rng(3)
+    pop = -1.2 * np.log(np.arange(1, E + 1))[rng.permutation(E)]
+    zl = torch.from_numpy((pop[None, :] + rng.gumbel(size=(Tp, E))).astype(np.float32)).to(dev)
+    xp = torch.randn(Tp, H, device=dev, generator=gen).to(torch.bfloat16).float()
+    rp = torch.randn(Tp, H, device=dev, generator=gen)
+    op = torch.empty(2, Tp, H, device=dev)
+    player = xm.MoeLayer(L, arena, E, k, Tp, prefill=True)
+    pc = min(2, copies)
+
+    def prefill_round():
+        for c in range(pc):
+            player(xp, zl, rp, op[c], arena=arena[c * E])
+
+    ms_p, _ = graph_time(torch, prefill_round, max(1, args.prefill_steps // pc))
+    ms_p /= pc
+    flops = 6.0 * Tp * k * H * F
+    tf = flops / (ms_p * 1e-3) / 1e12
+    log(f"prefill T={Tp}: {ms_p * 1e3:.1f} us/layer, {tf:.1f} TFLOP/s")
+    prefill = dict(tokens=Tp, us_per_layer=round(ms_p * 1e3, 1), tflops=round(tf, 2),
+                   frac_bf16_peak=round(tf / BF16_PEAK_TFLOPS, 4), tokens_per_s=round(Tp / (ms_p * 1e-3), 0),
+                   flops_per_layer=flops, routing="Zipf alpha=1.2 (Gumbel-top-k)")
+
+    # ---------------------------------------------------------------- the CPU baseline (the oracle, host cores)
+    cpu = None
+    if not args.no_cpu:
+        sys.path.insert(0, str(ROOT / "oracle"))
+        import xs_oracle as xo
+        cores = min(16, os.cpu_count() or 1)
+        blobs = list(arena[:E].cpu().numpy())
+        ol = xo.layout(xm.Q4_K, xm.Q6_K, H, F)
+        lg = logits[0].cpu().numpy()
+        xx = x.cpu().numpy()
+        rr = np.zeros((1, H), np.float32)
+        xo.moe_layer_decode(ol, blobs, k, xx, lg, rr, n_threads=cores)     # warm-up
+        n = 0
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < args.cpu_seconds:
+            xo.moe_layer_decode(ol, blobs, k, xx, lg, rr, n_threads=cores)
+            n += 1
+        dt = (time.perf_counter() - t0) / n
+        model = "unknown"
+        try:
+            for line in open("/proc/cpuinfo"):
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+        except OSError:
+            pass
+        cpu = dict(value=round(1.0 / dt, 3), unit="tokens/s", cores=cores, kind="port",
+                   sample=f"{n} single-token config-2 decode layers (oracle/xs_oracle.c, {cores} OpenMP threads) in "
+                          f"{n * dt:.1f} s", us_per_token=round(dt * 1e6, 1),
+                   expert_gbs=round(k * blob / dt / 1e9, 3), cpu_model=model)
+        log(f"cpu baseline: {dt * 1e3:.1f} ms/token on {cores} threads")
+
+    line = {
+        "metric": METRIC,
+        "value": round(gbs1, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps1,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms1, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic: N(0,0.02) fp32 weights quantized by this library's quantizer, bf16 N(0,1) activations, "
+                "uniform routing (i.i.d. N(0,1) logits)",
+        "config": {"workload": "config 2 decode batch 1: Qwen3-30B-A3B-shaped MoE layer (hidden 2048, 128 experts, "
+                               "top-8, F 768, Q4_K gate/up, Q6_K down), weights rotated over "
+                               f"{copies} HBM copies ({copies * layer_bytes / 1e9:.2f} GB)",
+                   "global_batch": 1, "seq_len": 1, "parallelism": "none (1 GPU)"},
+        "us_per_token": round(ms1 * 1e3, 3),
+        "tokens_per_s": round(1.0 / (ms1 * 1e-3), 1),
+        "frac_hbm_peak": round(gbs1 / HBM_PEAK_GBS, 4),
+        "roofline": {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "grouped_kernel<Q4_K, 64, gate/up> (xs_native_expert_gate_up)",
+                     "algorithmic_bytes_per_launch": gu_bytes, "avg_launch_us": round(us_gu, 3),
+                     "down_kernel": {"avg_launch_us": round(us_dn, 3), "gbs": round(dn_gbs, 1),
+                                     "algorithmic_bytes_per_launch": dn_bytes}},
+        "decode_batches": extra,
+        "prefill": prefill,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,184 @@
+/*
+ * include/xs_moe.h - the C ABI of the MI355X MoE-layer library (libxsmoe.so).
+ *
+ * The drop-in boundary for XeStrata's mixture-of-experts hot path.  Each entry point names the reference interface it
+ * replaces (paths relative to the reference repository, 32x-k/XeStrata-win).  Conventions, as the reference's:
+ *   - every buffer is device memory owned by the caller; no entry point allocates device memory or synchronises,
+ *     except where a NULL stream is allowed and documented to synchronise (the reference's `sync_if_needed`);
+ *   - `stream` is a hipStream_t passed as void* (the reference's opaque `void* stream`);
+ *   - group and entry counts are read on the device, so one captured graph with capacity grids serves every routing;
+ *   - blob addresses (expert weights) are 16-byte aligned; float spans 4-byte aligned; outputs do not overlap inputs.
+ * Every function returns XS_OK (0) or an error code, with a message for the calling thread in xs_last_error().  The
+ * C++ wrappers in xs_strata_kernels.hpp turn a non-zero code back into the reference's exceptions.
+ *
+ * ggml type ids: Q8_0 = 8, Q4_K = 12, Q6_K = 14, IQ4_XS = 23.
+ */
+#ifndef XS_MOE_H
+#define XS_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define XS_OK 0
+#define XS_EINVAL 1 /* bad geometry, alignment, overlap or a missing stream: the reference's std::invalid_argument */
+#define XS_EDEVICE 2 /* a HIP error: the reference's core::DeviceError */
+
+/* The message of this thread's last failed call ("" if none). */
+const char* xs_last_error(void);
+/* ABI version (this header's). */
+int xs_abi_version(void);
+
+/* One native expert blob: [gate rows | up rows | down rows], raw GGUF blocks.
+ * Mirrors NativeExpertLayout (include/strata/kernels/iq_kernels.hpp:66-75). */
+typedef struct xs_expert_layout {
+    int gu_type, d_type, up_type;
+    int64_t n_embd, n_ff;
+    size_t gu_row, d_row, up_row;
+    size_t up_off, down_off, bytes;
+} xs_expert_layout_t;
+
+/* Bytes of one row of n values of `type` (0 when unsupported). Replaces iq_row_bytes (iq_kernels.hpp:22). */
+size_t xs_iq_row_bytes(int type, int64_t n);
+
+/* 1 when the grouped expert kernels take this gate/up and down type pair at these dimensions, else 0.
+ * Replaces native_expert_supported (include/strata/kernels/iq_kernels.hpp:79). up_type -1: the gate's. */
+int xs_native_expert_supported(int gu_type, int d_type, int64_t n_embd, int64_t n_ff, int up_type);
+
+/* Replaces native_expert_layout (iq_kernels.hpp:81). */
+int xs_native_expert_layout(int gu_type, int d_type, int64_t n_embd, int64_t n_ff, int up_type,
+                            xs_expert_layout_t* out);
+
+/* Scratch bytes xs_native_expert_grouped needs for cap_entries entries. Replaces native_expert_scratch_bytes
+ * (iq_kernels.hpp:83): the reference's gate | up | h | hq areas, plus one 256-byte status word area at the end. */
+size_t xs_native_expert_scratch_bytes(int64_t cap_entries, int64_t n_ff);
+
+/* q8_1 blocks of n_rows rows of n_cols floats (n_cols a multiple of 32), canonical scale: one a 256 values when
+ * n_cols % 256 == 0, else one a 32.  Replaces quantize_q8_1_rows (iq_kernels.hpp:26; iq_kernels.cpp:1850-1879).
+ * A NULL stream runs on the default stream and synchronises. */
+int xs_quantize_q8_1_rows(const float* x, int64_t n_rows, int64_t n_cols, void* y, void* stream);
+
+/* Grouped experts in the native format (decode and verify windows).  Group g's blob is at device address
+ * grp_ptr[g]; its entries [grp_start[g], grp_start[g+1]) read token ent_tok[e]'s q8_1 row (n_embd/32 blocks a token
+ * in x_q8_1) and write row ent_dst[e] of `out` (n_embd floats).  Counts are read on the device; grid_groups (0:
+ * cap_groups) rows of work-groups stride over the groups.  Replaces native_expert_grouped
+ * (include/strata/kernels/iq_kernels.hpp:90-93; src/kernels/xe/iq_kernels.cpp:2042-2178).  A NULL stream runs on
+ * the default stream and synchronises.  A blob address that is not 16-byte aligned is skipped and flagged in the
+ * scratch status word (xs_native_expert_status). */
+int xs_native_expert_grouped(const xs_expert_layout_t* L, const unsigned long long* grp_ptr,
+                             const int32_t* grp_start, const int32_t* n_groups, const int32_t* ent_dst,
+                             const int32_t* ent_tok, int64_t cap_groups, int64_t cap_entries, const void* x_q8_1,
+                             void* scratch, float* out, void* stream, int64_t grid_groups);
+/* The two halves of xs_native_expert_grouped, for callers that schedule them apart (and for timing each): the gate and
+ * up rows into scratch (the reference's launch_native_gu, src/kernels/xe/iq_kernels.cpp:997-1031), then SwiGLU +
+ * q8_1 of them and the down rows into `out` (its SwiGLU pass :2118-2133 and launch_native_down :1033-1063).  The same
+ * scratch and cap_entries must be passed to both. */
+int xs_native_expert_gate_up(const xs_expert_layout_t* L, const unsigned long long* grp_ptr, const int32_t* grp_start,
+                             const int32_t* n_groups, const int32_t* ent_tok, int64_t cap_groups, int64_t cap_entries,
+                             const void* x_q8_1, void* scratch, void* stream, int64_t grid_groups);
+int xs_native_expert_down(const xs_expert_layout_t* L, const unsigned long long* grp_ptr, const int32_t* grp_start,
+                          const int32_t* n_groups, const int32_t* ent_dst, int64_t cap_groups, int64_t cap_entries,
+                          void* scratch, float* out, void* stream, int64_t grid_groups);
+/* Device address of the status word inside a scratch of xs_native_expert_scratch_bytes(cap_entries, n_ff) bytes
+ * (int32; non-zero once a call met a misaligned blob; the caller clears it). No reference counterpart. */
+int32_t* xs_native_expert_status(void* scratch, int64_t cap_entries, int64_t n_ff);
+
+/* Dequantize n values (a whole number of blocks) to fp32: the reference host dequantizers' values bit for bit
+ * (include/strata/artifact/dequant.hpp).  Replaces iq_dequant_f32 (iq_kernels.hpp:30). */
+int xs_iq_dequant_f32(int type, const void* src, int64_t n, float* dst, void* stream);
+/* The same values rounded to bf16 (nearest even): the prompt path's dequantizer.  Replaces dequant_f16 /
+ * iq_dequant_f16 (include/strata/kernels/dequant_bf16.hpp:23-25, iq_kernels.hpp:29), which produce FP16. */
+int xs_iq_dequant_bf16(int type, const void* src, int64_t n, uint16_t* dst, void* stream);
+
+/* This library's quantizer: n floats (a whole number of blocks) to `type` blocks.  No reference counterpart (the
+ * reference's tests call ggml_quantize_chunk, src/kernels/native_expert_parity.cpp:483-487). */
+int xs_quantize_rows(int type, const float* x, int64_t n, void* y, void* stream);
+
+/* Router: logits (n_tokens, n_expert) -> ids (n_tokens, k) int32 and renormalised weights (n_tokens, k) f32, in
+ * descending probability rank.  Bit for bit the reference's router_top10 (include/strata/kernels/router_top10.hpp:
+ * 20-21; src/kernels/xe/router.cpp:59-308).  n_expert <= 1024, k <= 64 and k <= n_expert.  A NULL stream runs on the
+ * default stream and synchronises. */
+int xs_router_top10(const float* logits, int n_tokens, int n_expert, int k, int32_t* ids, float* weights,
+                    void* stream);
+
+/* DeepSeek-V3 routing: sigmoid scores, selection by score + bias (bias may be NULL), group-limited top-k (n_group
+ * groups, the topk_group best by their two best scores), weights normalised over the k and times routed_scale.  No
+ * reference counterpart (absent from XeStrata). n_expert <= 1024, n_group <= 64, k <= 64. */
+int xs_router_grouped_sigmoid(const float* logits, const float* bias, int n_tokens, int n_expert, int n_group,
+                              int topk_group, int k, float routed_scale, int32_t* ids, float* weights, void* stream);
+
+/* Router logits logits[t, e] = x[t] . w[e] in fp32 (w: n_expert rows of n_embd floats).  Replaces the F32 router
+ * GEMV f32_gemv_fp32_mmvf_multi / f32_gemm_rows (src/kernels/xe/bf16_gemv.cpp:464-517). */
+int xs_router_logits_f32(const float* x, const float* w, float* logits, int n_tokens, int64_t n_embd, int n_expert,
+                         void* stream);
+
+/* The decode / verify-window plan built on the device when every routed expert is resident, in the host pool's
+ * layout (counts | start | dst | tok | pad | ptr | ptr2 | start2, capx entries): distinct experts in routing order,
+ * their entries ascending; *skip = ring when built, 0 (plan untouched) when a routed expert is not resident.
+ * res_layer NULL: every expert resident at slot = its id.  n_entries <= 1024, n_expert <= 16384.
+ * Replaces resident_plan (include/strata/kernels/verify_kernels.hpp:81-83; verify_kernels.cpp:819-890). */
+int xs_resident_plan(const int32_t* ids, int n_entries, int k, const int32_t* res_layer, int n_expert,
+                     const uint8_t* cache_base, const unsigned long long* slot_off, long long blob, int32_t* plan,
+                     long long capx, uint32_t* skip, uint32_t ring, void* stream);
+/* Offsets (in int32 words) of the plan's parts for a capacity capx: start, dst, tok, ptr, start2. */
+void xs_plan_offsets(long long capx, long long* start, long long* dst, long long* tok, long long* ptr,
+                     long long* start2);
+
+/* The prompt path's permutation on the device: histogram of n_entries ids, experts ascending, exclusive prefix, a
+ * stable fill.  src[row] = entry / k, slot[entry] = row, entry_of[row] = entry; bounds[g] (g < *n_groups, then the
+ * total) and experts[g] list the experts with rows.  When grp_ptr is not NULL, grp_ptr[g] = cache_base + experts[g]
+ * * blob.  *n_groups = -1 when an id is out of range.  n_expert <= 1024.  Replaces the host grouping of
+ * src/prefill/plain_prompt.cpp:576-645 (every expert on the GPU). */
+int xs_prefill_route(const int32_t* ids, int64_t n_entries, int k, int n_expert, int32_t* src, int32_t* slot,
+                     int32_t* entry_of, int32_t* bounds, int32_t* experts, int32_t* n_groups,
+                     const uint8_t* cache_base, long long blob, unsigned long long* grp_ptr, void* stream);
+
+/* Grouped experts for prompt and verify batches: bf16 MFMA products on expert tiles dequantized in LDS.  Rows are
+ * the routed rows in expert order (xs_prefill_route): row r reads token src[r] of x (fp32, n_embd a token) and its
+ * down output lands in row entry_of[r] of `parts` (routing order, n_embd floats a row); h = SwiGLU(gate, up) is kept
+ * in bf16.  scratch: xs_moe_prefill_scratch_bytes.  Replaces the prompt path's mmq::Context::run + swiglu +
+ * quantize (include/strata/prefill/moe_mmq.hpp:50-94), iq_mmq_grouped (iq_mmq.hpp:49-58), xmx_gemm_grouped
+ * (xmx_gemm.hpp:39-43) and the rocBLAS fallback Gemm::f16_groups (src/prefill/gemm.cpp:371-388). */
+int xs_moe_prefill_experts(const xs_expert_layout_t* L, const float* x, int64_t n_tok, const int32_t* src,
+                           const int32_t* entry_of, const int32_t* bounds, const int32_t* n_groups,
+                           const unsigned long long* grp_ptr, int64_t cap_groups, int64_t rows, void* scratch,
+                           float* parts, void* stream);
+size_t xs_moe_prefill_scratch_bytes(int64_t n_tok, int64_t rows, int64_t n_embd, int64_t n_ff);
+
+/* The weighted combine: output = fl(p0 w0) + fl(p1 w1) + ... in rank order, + shared (the shared row once; times
+ * the sigmoid of shared_gate[t] when given).  k in 1..15, a non-NULL stream.  Replaces native_moe_combine and
+ * native_moe_combine_multi (include/strata/kernels/native_moe.hpp:22-25; src/kernels/xe/native_moe.cpp:36-58). */
+int xs_native_moe_combine(const float* parts, const float* weights, const float* shared, float* output,
+                          int64_t n_embd, int64_t k, void* stream);
+int xs_native_moe_combine_multi(const float* parts, const float* weights, const float* shared, float* output,
+                                int64_t n_embd, int64_t k, int n_tok, void* stream, const float* shared_gate);
+/* The combine with the residual add fused: output = residual + combine (output may equal residual).  The reference
+ * runs native_moe_combine_multi then add_inplace (src/core/plain_model.cpp:985-987). */
+int xs_moe_combine_residual(const float* parts, const float* weights, const float* shared, const float* shared_gate,
+                            const float* residual, float* output, int64_t n_embd, int64_t k, int n_tok, void* stream);
+/* x += y (n floats).  Replaces add_inplace (src/core/plain_model.cpp:987). */
+int xs_add_inplace(float* x, const float* y, int64_t n, void* stream);
+
+/* The whole decode MoE layer on the device, every expert resident in one arena (expert e's blob at
+ * arena + e * blob_bytes): router -> plan -> q8_1 -> grouped experts -> combine -> residual.
+ * out = residual + MoE(x); out may equal residual.  workspace: xs_moe_layer_decode_workspace_bytes.  The engine's
+ * moe_route + moe_finish surface (include/strata/core/layer.hpp:108-199) on one GPU, without the host ring. */
+int xs_moe_layer_decode(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_bytes, int n_expert, int k,
+                        const float* x, const float* logits, const float* residual, float* out, int n_tok,
+                        void* workspace, size_t workspace_bytes, void* stream);
+size_t xs_moe_layer_decode_workspace_bytes(const xs_expert_layout_t* L, int n_expert, int k, int n_tok);
+
+/* The whole prompt / verify MoE layer on the device (same arena): router -> permutation -> bf16 MFMA grouped
+ * experts -> combine -> residual.  The engine's prompt MoE section (src/prefill/plain_prompt.cpp:558-797). */
+int xs_moe_layer_prefill(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_bytes, int n_expert,
+                         int k, const float* x, const float* logits, const float* residual, float* out, int n_tok,
+                         void* workspace, size_t workspace_bytes, void* stream);
+size_t xs_moe_layer_prefill_workspace_bytes(const xs_expert_layout_t* L, int n_expert, int k, int n_tok);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

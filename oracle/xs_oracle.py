@@ -1,0 +1,273 @@
+"""ctypes loader of oracle/liboracle.so (the CPU restatement of the reference's MoE hot path) and of oracle/_ref's
+shim over the reference's own host headers.  TEST INFRASTRUCTURE: only tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg may load this module, and only as the checker."""
+import ctypes
+import pathlib
+import subprocess
+
+import numpy as np
+
+HERE = pathlib.Path(__file__).resolve().parent
+LIB = HERE / "liboracle.so"
+REF = HERE / "_ref" / "libxsref.so"
+
+Q8_0, Q4_K, Q6_K, IQ4_XS = 8, 12, 14, 23
+BLOCK_VALUES = {Q8_0: 32, Q4_K: 256, Q6_K: 256, IQ4_XS: 256}
+BLOCK_BYTES = {Q8_0: 34, Q4_K: 144, Q6_K: 210, IQ4_XS: 136}
+
+P = ctypes.c_void_p
+I, I64, F = ctypes.c_int, ctypes.c_int64, ctypes.c_float
+
+
+class Layout(ctypes.Structure):
+    _fields_ = [("gu_type", I), ("d_type", I), ("n_embd", I64), ("n_ff", I64), ("gu_row", I64), ("d_row", I64),
+                ("up_off", I64), ("down_off", I64), ("bytes", I64)]
+
+
+_lib = None
+_ref = None
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", str(HERE), "liboracle.so"], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not LIB.exists():
+            build()
+        L = ctypes.CDLL(str(LIB))
+        L.xso_fp16_to_fp32.restype = F
+        L.xso_fp16_to_fp32.argtypes = [ctypes.c_uint16]
+        L.xso_fp32_to_fp16.restype = ctypes.c_uint16
+        L.xso_fp32_to_fp16.argtypes = [F]
+        L.xso_row_bytes.restype = I64
+        L.xso_vec_dot.restype = F
+        L.xso_vec_dot.argtypes = [I, P, P, I64, I]
+        L.xso_canon_rcp.restype = F
+        L.xso_canon_rcp.argtypes = [F]
+        L.xso_canon_exp.restype = F
+        L.xso_canon_exp.argtypes = [F]
+        L.xso_decode_plan.restype = I
+        L.xso_prefill_route.restype = I
+        L.xso_prefill_route.argtypes = [P, I64, I, I, P, P, P, P, P, P]
+        L.xso_dequant_row.argtypes = [I, P, I64, P]
+        L.xso_quantize_q8_1_rows.argtypes = [P, I64, I64, P]
+        L.xso_quantize_q8_1_per32.argtypes = [P, I64, P]
+        L.xso_native_layout.argtypes = [I, I, I64, I64, ctypes.POINTER(Layout)]
+        L.xso_native_expert_grouped.argtypes = [ctypes.POINTER(Layout), P, P, I, P, P, P, P, P, P, P, I]
+        L.xso_router_top10.argtypes = [P, I, I, I, P, P]
+        L.xso_router_grouped_sigmoid.argtypes = [P, P, I, I, I, I, I, F, P, P]
+        L.xso_decode_plan.argtypes = [P, I, I, P, P, P, P, P]
+        L.xso_combine.argtypes = [P, P, P, P, P, I64, I, I]
+        L.xso_expert_float.argtypes = [ctypes.POINTER(Layout), P, P, P, I, P, I]
+        L.xso_moe_layer_decode.argtypes = [ctypes.POINTER(Layout), P, I, I, P, P, P, I, P, I]
+        L.xso_canon_silu_mul_n.argtypes = [P, P, I64, P]
+        L.xso_canon_exp_n.argtypes = [P, I64, P]
+        L.xso_canon_rcp_n.argtypes = [P, I64, P]
+        _lib = L
+    return _lib
+
+
+def ref():
+    """oracle/_ref's shim over the reference's dequant.hpp / canon_math.hpp, or None where it is not built."""
+    global _ref
+    if _ref is None and REF.exists():
+        R = ctypes.CDLL(str(REF))
+        R.xsref_fp16_to_fp32.restype = F
+        R.xsref_fp16_to_fp32.argtypes = [ctypes.c_uint16]
+        R.xsref_dequant.argtypes = [I, P, I64, P]
+        R.xsref_canon_exp.argtypes = [P, I64, P]
+        R.xsref_canon_rcp.argtypes = [P, I64, P]
+        R.xsref_canon_silu_mul.argtypes = [P, P, I64, P]
+        _ref = R
+    return _ref
+
+
+def _a(x):
+    return x.ctypes.data_as(P)
+
+
+def row_bytes(t, n):
+    return n // BLOCK_VALUES[t] * BLOCK_BYTES[t]
+
+
+def dequant(t, blocks, n):
+    out = np.zeros(n, np.float32)
+    b = np.ascontiguousarray(blocks, dtype=np.uint8)
+    lib().xso_dequant_row(t, _a(b), n, _a(out))
+    return out
+
+
+def canon_exp(x):
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    lib().xso_canon_exp_n(_a(x), x.size, _a(y))
+    return y
+
+
+def canon_rcp(x):
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    lib().xso_canon_rcp_n(_a(x), x.size, _a(y))
+    return y
+
+
+def canon_silu_mul(g, u):
+    g = np.ascontiguousarray(g, np.float32)
+    u = np.ascontiguousarray(u, np.float32)
+    h = np.empty_like(g)
+    lib().xso_canon_silu_mul_n(_a(g), _a(u), g.size, _a(h))
+    return h
+
+
+def quantize_q8_1_rows(x):
+    x = np.ascontiguousarray(x, np.float32)
+    rows, cols = x.shape
+    y = np.zeros(rows * cols // 32 * 36, np.uint8)
+    lib().xso_quantize_q8_1_rows(_a(x), rows, cols, _a(y))
+    return y
+
+
+def quantize_q8_1_per32(x):
+    x = np.ascontiguousarray(x, np.float32).ravel()
+    y = np.zeros(x.size // 32 * 36, np.uint8)
+    lib().xso_quantize_q8_1_per32(_a(x), x.size, _a(y))
+    return y
+
+
+def q8_1_values(y):
+    """q8_1 bytes -> (int8 values, fp32 d per block, fp32 s per block)."""
+    b = np.asarray(y, np.uint8).reshape(-1, 36)
+    d = b[:, 0:2].copy().view(np.float16).astype(np.float32).ravel()
+    s = b[:, 2:4].copy().view(np.float16).astype(np.float32).ravel()
+    q = b[:, 4:].copy().view(np.int8)
+    return q, d, s
+
+
+def vec_dot(t, row, xq, n, s256):
+    row = np.ascontiguousarray(row, np.uint8)
+    xq = np.ascontiguousarray(xq, np.uint8)
+    return lib().xso_vec_dot(t, _a(row), _a(xq), n, int(s256))
+
+
+def layout(gu, d, n_embd, n_ff):
+    L = Layout()
+    if not lib().xso_native_layout(gu, d, n_embd, n_ff, ctypes.byref(L)):
+        raise ValueError("unsupported layout")
+    return L
+
+
+def native_expert_grouped(L, blobs, start, ent_dst, ent_tok, x_q8_1, n_out_rows, n_threads=8, want_inner=False):
+    """blobs: list of uint8 arrays (one per group).  Returns out [n_out_rows, n_embd] (and gate, up, hq)."""
+    ng = len(blobs)
+    keep = [np.ascontiguousarray(b, np.uint8) for b in blobs]
+    arr = (ctypes.c_void_p * max(ng, 1))(*[b.ctypes.data for b in keep])
+    start = np.ascontiguousarray(start, np.int32)
+    ent_dst = np.ascontiguousarray(ent_dst, np.int32)
+    ent_tok = np.ascontiguousarray(ent_tok, np.int32)
+    x_q8_1 = np.ascontiguousarray(x_q8_1, np.uint8)
+    out = np.zeros((n_out_rows, L.n_embd), np.float32)
+    n_ent = int(start[ng] - start[0])
+    gate = np.zeros((max(n_ent, 1), L.n_ff), np.float32)
+    up = np.zeros_like(gate)
+    hq = np.zeros(max(n_ent, 1) * (L.n_ff // 32) * 36, np.uint8)
+    lib().xso_native_expert_grouped(ctypes.byref(L), ctypes.cast(arr, P), _a(start), ng, _a(ent_dst), _a(ent_tok),
+                                    _a(x_q8_1), _a(out), _a(gate), _a(up), _a(hq), n_threads)
+    if want_inner:
+        return out, gate[:n_ent], up[:n_ent], hq[: n_ent * (L.n_ff // 32) * 36]
+    return out
+
+
+def expert_float(L, blobs, x, tok, n_threads=8):
+    keep = [np.ascontiguousarray(b, np.uint8) for b in blobs]
+    arr = (ctypes.c_void_p * len(keep))(*[b.ctypes.data for b in keep])
+    x = np.ascontiguousarray(x, np.float32)
+    tok = np.ascontiguousarray(tok, np.int32)
+    out = np.zeros((len(keep), L.n_embd), np.float32)
+    lib().xso_expert_float(ctypes.byref(L), ctypes.cast(arr, P), _a(x), _a(tok), len(keep), _a(out), n_threads)
+    return out
+
+
+def router_top10(logits, k, ids=None, weights=None):
+    logits = np.ascontiguousarray(logits, np.float32)
+    T, E = logits.shape
+    ids = np.zeros((T, k), np.int32) if ids is None else ids.copy()
+    w = np.zeros((T, k), np.float32) if weights is None else weights.copy()
+    lib().xso_router_top10(_a(logits), T, E, k, _a(ids), _a(w))
+    return ids, w
+
+
+def router_grouped_sigmoid(logits, bias, n_group, topk_group, k, routed_scale):
+    logits = np.ascontiguousarray(logits, np.float32)
+    T, E = logits.shape
+    ids = np.zeros((T, k), np.int32)
+    w = np.zeros((T, k), np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    lib().xso_router_grouped_sigmoid(_a(logits), None if b is None else _a(b), T, E, n_group, topk_group, k,
+                                     routed_scale, _a(ids), _a(w))
+    return ids, w
+
+
+def decode_plan(ids, k):
+    ids = np.ascontiguousarray(ids, np.int32).ravel()
+    n = ids.size
+    counts = np.zeros(4, np.int32)
+    start = np.zeros(n + 1, np.int32)
+    dst = np.zeros(n, np.int32)
+    tok = np.zeros(n, np.int32)
+    gexp = np.zeros(n, np.int32)
+    g = lib().xso_decode_plan(_a(ids), n, k, _a(counts), _a(start), _a(dst), _a(tok), _a(gexp))
+    return dict(counts=counts, start=start[: g + 1], dst=dst, tok=tok, experts=gexp[:g], groups=g)
+
+
+def prefill_route(ids, k, n_expert):
+    ids = np.ascontiguousarray(ids, np.int32).ravel()
+    n = ids.size
+    src = np.zeros(n, np.int32)
+    slot = np.zeros(n, np.int32)
+    entry = np.zeros(n, np.int32)
+    bounds = np.zeros(n_expert + 1, np.int32)
+    experts = np.zeros(n_expert, np.int32)
+    counts = np.zeros(n_expert, np.int32)
+    g = lib().xso_prefill_route(_a(ids), n, k, n_expert, _a(src), _a(slot), _a(entry), _a(bounds), _a(experts),
+                                _a(counts))
+    return dict(src=src, slot=slot, entry=entry, bounds=bounds[: g + 1], experts=experts[:g], counts=counts, groups=g)
+
+
+def combine(parts, weights, shared=None, shared_gate=None, n_embd=None, k=None, n_tok=None):
+    parts = np.ascontiguousarray(parts, np.float32)
+    weights = np.ascontiguousarray(weights, np.float32)
+    out = np.zeros((n_tok, n_embd), np.float32)
+    sh = None if shared is None else np.ascontiguousarray(shared, np.float32)
+    sg = None if shared_gate is None else np.ascontiguousarray(shared_gate, np.float32)
+    lib().xso_combine(_a(parts), _a(weights), None if sh is None else _a(sh), None if sg is None else _a(sg), _a(out),
+                      n_embd, k, n_tok)
+    return out
+
+
+def moe_layer_decode(L, blobs_by_expert, k, x, logits, residual, n_threads=1):
+    keep = [np.ascontiguousarray(b, np.uint8) for b in blobs_by_expert]
+    arr = (ctypes.c_void_p * len(keep))(*[b.ctypes.data for b in keep])
+    x = np.ascontiguousarray(x, np.float32)
+    logits = np.ascontiguousarray(logits, np.float32)
+    residual = np.ascontiguousarray(residual, np.float32)
+    out = np.zeros_like(residual)
+    lib().xso_moe_layer_decode(ctypes.byref(L), ctypes.cast(arr, P), len(keep), k, _a(x), _a(logits), _a(residual),
+                               x.shape[0], _a(out), n_threads)
+    return out
+
+
+def rel_max(a, b):
+    """The reference's relative error: max |a - b| / max |b| (src/kernels/iq_mmq_parity.cpp:126-134)."""
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.max(np.abs(a - b)) / max(np.max(np.abs(b)), 1e-30))
+
+
+def rel_sum(a, b):
+    """Sum-relative error: sum |a - b| / sum |b| (src/kernels/native_expert_parity.cpp:46-50)."""
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.sum(np.abs(a - b)) / (np.sum(np.abs(b)) + 1e-30))

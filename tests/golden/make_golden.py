@@ -1,0 +1,84 @@
+"""Regenerate tests/golden/*.npz.  Run in the build container (it needs the reference tree for oracle/_ref):
+
+    python tests/golden/make_golden.py
+
+  reference_vectors.npz - outputs of the reference's OWN host code, compiled from include/strata/artifact/dequant.hpp
+      and include/strata/kernels/canon_math.hpp where they lie (oracle/_ref, built by oracle/Makefile): dequantized
+      Q8_0 / Q4_K / Q6_K / IQ4_XS blocks, fp16 -> fp32 for all 65536 halves, canon exp / rcp / silu_mul.
+  seeded_inputs.npz     - the reference parity tests' seeded inputs (tests/golden/seeded_inputs.cpp).
+Inputs are data and outputs are data: no reference source is copied into the repository.
+"""
+import pathlib
+import subprocess
+import sys
+import tempfile
+
+import numpy as np
+
+HERE = pathlib.Path(__file__).resolve().parent
+ROOT = HERE.parent.parent
+sys.path.insert(0, str(ROOT / "oracle"))
+import xs_oracle as xo  # noqa: E402
+
+
+def blocks(rng, t, nb):
+    """Random blocks of type t with finite, realistic fp16 scales (and a few edge values)."""
+    bs = xo.BLOCK_BYTES[t]
+    b = rng.integers(0, 256, size=(nb, bs), dtype=np.uint8)
+    d = (rng.standard_normal(nb) * 0.01).astype(np.float16)
+    d[:4] = np.array([0.0, -0.0, 6.0e-8, 65504.0], np.float16)       # zero, signed zero, subnormal, max
+    dm = np.abs(rng.standard_normal(nb) * 0.01).astype(np.float16)
+    if t == xo.Q6_K:
+        b[:, 208:210] = d.view(np.uint8).reshape(nb, 2)
+    else:
+        b[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+    if t == xo.Q4_K:
+        b[:, 2:4] = dm.view(np.uint8).reshape(nb, 2)
+    return b
+
+
+def main():
+    subprocess.run(["make", "-s", "-C", str(ROOT / "oracle")], check=True)
+    R = xo.ref()
+    if R is None:
+        sys.exit("oracle/_ref/libxsref.so is not built (the reference tree is absent)")
+    rng = np.random.default_rng(20261201)
+    out = {}
+    for t in (xo.Q8_0, xo.Q4_K, xo.Q6_K, xo.IQ4_XS):
+        nb = 96
+        b = blocks(rng, t, nb)
+        y = np.zeros(nb * xo.BLOCK_VALUES[t], np.float32)
+        assert R.xsref_dequant(t, xo._a(b), nb, xo._a(y)) == 0
+        out[f"blocks_{t}"] = b
+        out[f"dequant_{t}"] = y
+    out["fp16_to_fp32"] = np.array([R.xsref_fp16_to_fp32(h) for h in range(65536)], np.float32)
+    x = np.concatenate([rng.standard_normal(4096).astype(np.float32) * 20,
+                        np.array([-90, -80, -79.9, -0.0, 0.0, 1e-30, 80, 88.7, 100], np.float32)])
+    y = np.empty_like(x)
+    R.xsref_canon_exp(xo._a(x), x.size, xo._a(y))
+    out["canon_exp_x"], out["canon_exp_y"] = x, y
+    r = np.abs(rng.standard_normal(4096).astype(np.float32)) * np.exp(rng.uniform(-20, 20, 4096)).astype(np.float32)
+    r = r.astype(np.float32) + np.float32(1e-6)
+    y = np.empty_like(r)
+    R.xsref_canon_rcp(xo._a(r), r.size, xo._a(y))
+    out["canon_rcp_x"], out["canon_rcp_y"] = r, y
+    g = (rng.standard_normal(4096) * 6).astype(np.float32)
+    u = rng.standard_normal(4096).astype(np.float32)
+    h = np.empty_like(g)
+    R.xsref_canon_silu_mul(xo._a(g), xo._a(u), g.size, xo._a(h))
+    out["silu_g"], out["silu_u"], out["silu_h"] = g, u, h
+    np.savez_compressed(HERE / "reference_vectors.npz", **out)
+
+    with tempfile.TemporaryDirectory() as tmp:
+        exe = pathlib.Path(tmp) / "seeded"
+        subprocess.run(["g++", "-O2", "-std=c++17", "-o", str(exe), str(HERE / "seeded_inputs.cpp")], check=True)
+        subprocess.run([str(exe), tmp], check=True)
+        seeded = dict(router_cases=np.fromfile(pathlib.Path(tmp) / "router_cases.f32", np.float32).reshape(-1, 512),
+                      plan_ids=np.fromfile(pathlib.Path(tmp) / "plan_ids.i32", np.int32),
+                      router256=np.fromfile(pathlib.Path(tmp) / "router256.f32", np.float32).reshape(3, 256))
+    np.savez_compressed(HERE / "seeded_inputs.npz", **seeded)
+    print("wrote", HERE / "reference_vectors.npz", HERE / "seeded_inputs.npz")
+
+
+if __name__ == "__main__":
+    main()

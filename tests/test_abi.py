@@ -1,0 +1,86 @@
+"""The C ABI without a GPU: libxsmoe.so loads and exports every symbol include/xs_moe.h declares; geometry helpers
+agree with the reference's formulas; argument checks fail with the reference's messages before any launch."""
+import ctypes
+import pathlib
+import re
+
+import pytest
+
+ROOT = pathlib.Path(__file__).resolve().parent.parent
+
+
+@pytest.fixture(scope="module")
+def xm():
+    import xsmoe
+    return xsmoe
+
+
+def declared_symbols():
+    text = (ROOT / "include" / "xs_moe.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(xs_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_exports_every_declared_symbol(xm):
+    lib = xm.lib()
+    names = declared_symbols()
+    assert len(names) >= 25
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_binding_covers_header(xm):
+    assert set(declared_symbols()) == set(xm._SIGS)
+
+
+# the native blob sizes of the five BASELINE configs (gate | up | down, raw GGUF blocks)
+@pytest.mark.parametrize("gu,d,H,F,blob", [(8, 8, 1024, 512, 1_671_168), (12, 14, 2048, 768, 3_059_712),
+                                           (23, 23, 4096, 1536, 10_027_008), (12, 12, 7168, 2048, 24_772_608),
+                                           (8, 8, 7168, 2048, 46_792_704)])
+def test_layout(xm, gu, d, H, F, blob):
+    L = xm.native_expert_layout(gu, d, H, F)
+    assert L.bytes == blob
+    assert L.gu_row == H // xm.BLOCK_VALUES[gu] * xm.BLOCK_BYTES[gu]
+    assert L.up_off == F * L.gu_row and L.down_off == 2 * F * L.gu_row
+    assert L.bytes % 16 == 0
+
+
+def test_supported(xm):
+    assert xm.native_expert_supported(12, 14, 2048, 768)
+    assert not xm.native_expert_supported(12, 14, 2048 + 32, 768)       # n_embd not a whole number of 256s
+    assert not xm.native_expert_supported(12, 14, 2048, 700)             # down rows not whole Q6_K blocks
+    assert not xm.native_expert_supported(2, 14, 2048, 768)              # Q4_0: not one of the four formats
+    assert not xm.native_expert_supported(12, 14, 2048, 768, up=14)      # mixed gate/up types
+
+
+def test_scratch_bytes(xm):
+    # the reference's gate | up | h | hq areas (iq_kernels.cpp:2037-2040) plus the 256-byte status area
+    cap, F = 8, 768
+    f = cap * F * 4
+    up = lambda v: (v + 255) & ~255
+    assert xm.native_expert_scratch_bytes(cap, F) == 3 * up(f) + up(cap * (F // 32) * 36) + 256
+
+
+def test_plan_offsets(xm):
+    capx = 80
+    o = xm.plan_offsets(capx)
+    ptr_off = ((4 + (capx + 1) + 2 * capx) + 1) & ~1      # verify_kernels.cpp:860-866
+    assert o == dict(start=4, dst=4 + capx + 1, tok=4 + 2 * capx + 1, ptr=ptr_off, start2=ptr_off + 4 * capx)
+
+
+def test_argument_errors(xm):
+    lib = xm.lib()
+    # k past 64, checked before any launch (router.cpp:294)
+    assert lib.xs_router_top10(8, 1, 128, 65, 8, 8, None) == xm.XS_EINVAL
+    assert b"exceeds the kernel's 64" in lib.xs_last_error()
+    # the combine requires a stream (native_moe.cpp:116)
+    assert lib.xs_native_moe_combine_multi(8, 8, None, 8, 2048, 8, 1, None, None) == xm.XS_EINVAL
+    assert b"requires a stream" in lib.xs_last_error()
+    # the combine's k range is 1..15
+    assert lib.xs_native_moe_combine_multi(8, 8, None, 8, 2048, 16, 1, 8, None) == xm.XS_EINVAL
+    # an unsupported layout
+    L = xm.Layout()
+    L.gu_type, L.d_type, L.up_type, L.n_embd, L.n_ff = 2, 14, -1, 2048, 768
+    assert lib.xs_native_expert_grouped(ctypes.byref(L), 8, 8, 8, 8, 8, 1, 1, 8, 16, 8, None, 0) == xm.XS_EINVAL
+    # resident_plan: more entries than a work-group
+    assert lib.xs_resident_plan(8, 2000, 8, None, 128, None, None, 16, 8, 4000, 8, 1, 8) == xm.XS_EINVAL

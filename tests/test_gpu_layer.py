@@ -1,0 +1,169 @@
+"""Whole MoE layers on the GPU (xs_moe_layer_decode / xs_moe_layer_prefill and the shared-expert composition) at the
+BASELINE configs' shapes, against the CPU oracle on the same seeded inputs.
+
+Bars: expert ids and the plan bit for bit (the router's and plan's own tests); layer output (residual + MoE) within
+max|a - b| / max|ref| <= 1e-3 for the fp32-accumulate decode path, <= 2e-2 for the bf16 MFMA prefill path."""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def t2n(t):
+    return t.detach().cpu().numpy()
+
+
+def decode_case(xm, xo, arena, L, E, k, T, logits, seed):
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    x = torch.randn(T, L.n_embd, device=DEV, generator=g).to(torch.bfloat16).float()
+    res = torch.randn(T, L.n_embd, device=DEV, generator=g)
+    layer = xm.MoeLayer(L, arena, E, k, T)
+    out = torch.empty_like(res)
+    layer(x, logits, res, out)
+    torch.cuda.synchronize()
+    ids, _ = xo.router_top10(t2n(logits), k)
+    used = sorted(set(ids.ravel().tolist()))
+    blobs = t2n(arena[:E]) if E <= 32 else None
+    by_expert = [blobs[e] if blobs is not None else (t2n(arena[e]) if e in used else np.zeros(16, np.uint8))
+                 for e in range(E)]
+    ol = xo.layout(L.gu_type, L.d_type, L.n_embd, L.n_ff)
+    want = xo.moe_layer_decode(ol, by_expert, k, t2n(x), t2n(logits), t2n(res), n_threads=8)
+    moe_rel = xo.rel_max(t2n(out) - t2n(res), want - t2n(res))
+    return xo.rel_max(t2n(out), want), moe_rel
+
+
+def test_config1_host_path_layer(xm, xo):
+    """Config 1: hidden 1024, 8 experts, top-2, F 512, Q8_0, router weights N(0, 0.02), 4 tokens, seed 0."""
+    H, E, k, F, T = 1024, 8, 2, 512, 4
+    arena, L = xm.build_arena(E, H, F, 8, 8, seed=0, gen_device="cpu")
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(T, H, generator=g).to(DEV)
+    wr = (torch.randn(E, H, generator=g) * 0.02).to(DEV)
+    logits = xm.router_logits_f32(x, wr)
+    rel, moe_rel = decode_case(xm, xo, arena, L, E, k, T, logits, 0)
+    assert rel <= 1e-3 and moe_rel <= 1e-3, (rel, moe_rel)
+
+
+@pytest.fixture(scope="module")
+def c2_arena(xm):
+    return xm.build_arena(128, 2048, 768, 12, 14, seed=2)
+
+
+@pytest.mark.parametrize("T", [1, 4, 16])
+def test_config2_decode(xm, xo, c2_arena, T):
+    """Config 2: Qwen3-30B-A3B-shaped, Q4_K gate/up, Q6_K down, uniform routing, batch 1 / 4 / 16."""
+    arena, L = c2_arena
+    g = torch.Generator(device=DEV).manual_seed(100 + T)
+    logits = torch.randn(T, 128, device=DEV, generator=g)
+    rel, moe_rel = decode_case(xm, xo, arena, L, 128, 8, T, logits, T)
+    assert rel <= 1e-3 and moe_rel <= 1e-3, (rel, moe_rel)
+
+
+def zipf_logits(T, E, seed):
+    rng = np.random.default_rng(seed)
+    pop = -1.2 * np.log(np.arange(1, E + 1))[rng.permutation(E)]
+    return torch.from_numpy((pop[None, :] + rng.gumbel(size=(T, E))).astype(np.float32)).to(DEV)
+
+
+def test_config3_verify_decode_path(xm, xo, c2_arena):
+    """Config 3's 4-token spec-verify batch with Zipf-skewed logits, on the decode path."""
+    arena, L = c2_arena
+    rel, moe_rel = decode_case(xm, xo, arena, L, 128, 8, 4, zipf_logits(4, 128, 7), 4)
+    assert rel <= 1e-3 and moe_rel <= 1e-3, (rel, moe_rel)
+
+
+@pytest.mark.parametrize("T", [4, 2048])
+def test_config3_prefill(xm, c2_arena, T):
+    """Config 3: prefill 2048 tokens and the 4-token verify batch through the bf16 MFMA path, against a plain PyTorch
+    fp32 reference over the exactly dequantized weights (router ids shared: they are pinned bit for bit elsewhere)."""
+    from test_gpu_experts import torch_reference_prefill
+    arena, L = c2_arena
+    E, k = 128, 8
+    g = torch.Generator(device=DEV).manual_seed(T)
+    x = torch.randn(T, L.n_embd, device=DEV, generator=g).to(torch.bfloat16).float()
+    res = torch.randn(T, L.n_embd, device=DEV, generator=g)
+    logits = zipf_logits(T, E, 3 + T)
+    layer = xm.MoeLayer(L, arena, E, k, T, prefill=True)
+    out = torch.empty_like(res)
+    layer(x, logits, res, out)
+    ids, w = xm.router_top10(logits, k)
+    parts = torch_reference_prefill(xm, arena, L, x, ids, E)
+    moe = (parts.reshape(T, k, -1) * w[:, :, None]).sum(1)
+    rel = float(((out - res) - moe).abs().max() / moe.abs().max())
+    assert rel <= 2e-2, rel
+
+
+def test_prefill_matches_decode_path(xm, xo, c2_arena):
+    """The same 16 tokens through both paths: the bf16 MFMA layer within 2e-2 of the fp32-accumulate one."""
+    arena, L = c2_arena
+    T = 16
+    g = torch.Generator(device=DEV).manual_seed(77)
+    x = torch.randn(T, L.n_embd, device=DEV, generator=g).to(torch.bfloat16).float()
+    res = torch.zeros(T, L.n_embd, device=DEV)
+    logits = torch.randn(T, 128, device=DEV, generator=g)
+    a = torch.empty_like(res)
+    b = torch.empty_like(res)
+    xm.MoeLayer(L, arena, 128, 8, T)(x, logits, res, a)
+    xm.MoeLayer(L, arena, 128, 8, T, prefill=True)(x, logits, res, b)
+    assert xo.rel_max(t2n(b), t2n(a)) <= 2e-2
+
+
+@pytest.mark.parametrize("T", [1, 8])
+def test_config4_iq4_xs(xm, xo, T):
+    """Config 4's layer shape (hidden 4096, 128 experts, top-8, F 1536, IQ4_XS both sides), decode batch 1 and 8;
+    16 distinct experts resident here (the oracle reads only the routed ones)."""
+    E = 16
+    arena, L = xm.build_arena(E, 4096, 1536, 23, 23, seed=4)
+    g = torch.Generator(device=DEV).manual_seed(40 + T)
+    logits = torch.randn(T, E, device=DEV, generator=g)
+    rel, moe_rel = decode_case(xm, xo, arena, L, E, 8, T, logits, T)
+    assert rel <= 1e-3 and moe_rel <= 1e-3, (rel, moe_rel)
+
+
+def test_config5_deepseek_decode(xm, xo):
+    """Config 5: hidden 7168, 256 routed Q4_K experts + 1 shared Q8_0, sigmoid + bias, 8 groups / top-4 / top-8, F
+    2048, decode batch 1: the routed experts through the plan and the grouped kernels, the shared expert as one
+    more group, the combine adding it once."""
+    H, F, E, k, T = 7168, 2048, 256, 8, 1
+    arena, L = xm.build_arena(E, H, F, 12, 12, seed=5)
+    sh_arena, SL = xm.build_arena(1, H, F, 8, 8, seed=55)
+    g = torch.Generator(device=DEV).manual_seed(5)
+    x = torch.randn(T, H, device=DEV, generator=g).to(torch.bfloat16).float()
+    res = torch.randn(T, H, device=DEV, generator=g)
+    logits = torch.randn(T, E, device=DEV, generator=g)
+    bias = torch.randn(E, device=DEV, generator=g) * 0.1
+    ids, w = xm.router_grouped_sigmoid(logits, bias, 8, 4, k, 2.5)
+    n = T * k
+    plan = torch.zeros(xm.plan_words(n) + 2, dtype=torch.int32, device=DEV)
+    skip = torch.zeros(1, dtype=torch.int32, device=DEV)
+    xm.resident_plan(ids.reshape(-1), k, None, E, arena.data_ptr(), None, L.bytes, plan, n, skip, 1)
+    o = xm.plan_offsets(n)
+    xq = xm.quantize_q8_1_rows(x)
+    scratch = torch.zeros(xm.native_expert_scratch_bytes(n, F), dtype=torch.uint8, device=DEV)
+    parts = torch.zeros(n, H, device=DEV)
+    ptr = plan[o["ptr"]:o["ptr"] + 2 * n].view(torch.int64)
+    xm.native_expert_grouped(L, ptr, plan[4:], plan[0:1], plan[o["dst"]:], plan[o["tok"]:], min(n, E), n, xq, scratch,
+                             parts)
+    sh_ptr = torch.tensor([sh_arena.data_ptr()], dtype=torch.int64, device=DEV)
+    one = torch.tensor([0, 1], dtype=torch.int32, device=DEV)
+    zero = torch.zeros(1, dtype=torch.int32, device=DEV)
+    sh_scratch = torch.zeros(xm.native_expert_scratch_bytes(1, F), dtype=torch.uint8, device=DEV)
+    shared = torch.zeros(T, H, device=DEV)
+    xm.native_expert_grouped(SL, sh_ptr, one, one[1:], zero, zero, 1, 1, xq, sh_scratch, shared)
+    out = res.clone()
+    xm.moe_combine_residual(parts, w, out, out, H, k, T, shared=shared)
+    torch.cuda.synchronize()
+    # the oracle: the same composition
+    rids, rw = xo.router_grouped_sigmoid(t2n(logits), t2n(bias), 8, 4, k, 2.5)
+    assert np.array_equal(t2n(ids), rids) and np.array_equal(t2n(w).view(np.uint32), rw.view(np.uint32))
+    p = xo.decode_plan(rids, k)
+    oxq = xo.quantize_q8_1_rows(t2n(x))
+    ol = xo.layout(12, 12, H, F)
+    blobs = [t2n(arena[e]) for e in p["experts"]]
+    oparts = xo.native_expert_grouped(ol, blobs, p["start"], p["dst"], p["tok"], oxq, n)
+    osh = xo.native_expert_grouped(xo.layout(8, 8, H, F), [t2n(sh_arena[0])], np.array([0, 1], np.int32),
+                                   np.zeros(1, np.int32), np.zeros(1, np.int32), oxq, 1)
+    want = t2n(res) + xo.combine(oparts, rw, osh, None, H, k, T)
+    assert xo.rel_max(t2n(out), want) <= 1e-3

@@ -1,0 +1,506 @@
+// xestrata-win_amd/csrc/abi.cpp - the C ABI (include/xs_moe.h): argument checks with the reference's rules, the
+// thread's error message, and the launches.  Nothing here allocates device memory.
+#include "../../include/xs_moe.h"
+#include "xs_kernels.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+int ok() { return XS_OK; }
+int hip_status(hipError_t e, const char* what) {
+    if (e != hipSuccess) return fail(XS_EDEVICE, "%s: %s", what, hipGetErrorString(e));
+    return ok();
+}
+hipStream_t S(void* s) { return (hipStream_t)s; }
+// a NULL stream: the default stream, then a wait (the reference's sync_if_needed)
+int finish(void* stream, hipError_t launched, const char* what) {
+    if (launched != hipSuccess) return hip_status(launched, what);
+    if (!stream) return hip_status(hipStreamSynchronize(nullptr), what);
+    return ok();
+}
+bool aligned(const void* p, size_t a) { return p && ((uintptr_t)p % a) == 0; }
+bool overlap(const void* a, size_t an, const void* b, size_t bn) {
+    const auto ap = (uintptr_t)a, bp = (uintptr_t)b;
+    return a && b && ap < bp + bn && bp < ap + an;
+}
+size_t up256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+int type_qk(int t) { return t == 8 ? 32 : (t == 12 || t == 14 || t == 23) ? 256 : 0; }
+int type_bytes(int t) { return t == 8 ? 34 : t == 12 ? 144 : t == 14 ? 210 : t == 23 ? 136 : 0; }
+
+xs::ExpertLayout to_layout(const xs_expert_layout_t* L) {
+    xs::ExpertLayout x;
+    x.gu_type = L->gu_type;
+    x.d_type = L->d_type;
+    x.n_embd = L->n_embd;
+    x.n_ff = L->n_ff;
+    x.gu_row = (int64_t)L->gu_row;
+    x.d_row = (int64_t)L->d_row;
+    x.up_off = (int64_t)L->up_off;
+    x.down_off = (int64_t)L->down_off;
+    x.bytes = (int64_t)L->bytes;
+    return x;
+}
+
+int check_layout(const xs_expert_layout_t* L, const char* what) {
+    if (!L) return fail(XS_EINVAL, "%s: no layout", what);
+    if (!xs_native_expert_supported(L->gu_type, L->d_type, L->n_embd, L->n_ff, L->up_type))
+        return fail(XS_EINVAL, "%s: gate/up type %d, down type %d at %lld x %lld is not supported", what, L->gu_type,
+                    L->d_type, (long long)L->n_embd, (long long)L->n_ff);
+    xs_expert_layout_t want;
+    if (xs_native_expert_layout(L->gu_type, L->d_type, L->n_embd, L->n_ff, L->up_type, &want) != XS_OK) return XS_EINVAL;
+    if (want.bytes != L->bytes || want.up_off != L->up_off || want.down_off != L->down_off)
+        return fail(XS_EINVAL, "%s: the layout's offsets are not native_expert_layout's", what);
+    return ok();
+}
+
+// plan layout for capx entries (reference src/kernels/xe/verify_kernels.cpp:860-866)
+long long plan_ptr_off(long long capx) { return ((4 + (capx + 1) + 2 * capx) + 1) & ~1ll; }
+size_t plan_words(long long capx) { return (size_t)(plan_ptr_off(capx) + 4 * capx + capx + 1 + 1); }
+
+}  // namespace
+
+extern "C" {
+
+const char* xs_last_error(void) { return g_err.c_str(); }
+int xs_abi_version(void) { return 1; }
+
+size_t xs_iq_row_bytes(int type, int64_t n) {
+    const int qk = type_qk(type);
+    return qk && n > 0 && n % qk == 0 ? (size_t)(n / qk) * (size_t)type_bytes(type) : 0;
+}
+
+// the gate/up and down types of the four formats; every row a whole number of blocks; n_embd a whole number of 256s
+// (the q8_1 activation's 256-value scale; reference iq_kernels.cpp:2002-2019) and of 32s of units per lane set
+int xs_native_expert_supported(int gu_type, int d_type, int64_t n_embd, int64_t n_ff, int up_type) {
+    if (up_type >= 0 && up_type != gu_type) return 0;   // mixed gate/up types: not built (no config uses them)
+    if (!type_qk(gu_type) || !type_qk(d_type)) return 0;
+    if (n_embd <= 0 || n_ff <= 0 || n_embd % 256 || n_ff % 32) return 0;
+    if (n_embd % type_qk(gu_type) || n_ff % type_qk(d_type)) return 0;
+    if (n_embd > (1 << 20) || n_ff > (1 << 20)) return 0;
+    return 1;
+}
+
+int xs_native_expert_layout(int gu_type, int d_type, int64_t n_embd, int64_t n_ff, int up_type,
+                            xs_expert_layout_t* out) {
+    if (!out) return fail(XS_EINVAL, "native_expert_layout: no output");
+    if (!xs_native_expert_supported(gu_type, d_type, n_embd, n_ff, up_type))
+        return fail(XS_EINVAL, "native_expert_layout: gate/up type %d, down type %d at %lld x %lld not supported",
+                    gu_type, d_type, (long long)n_embd, (long long)n_ff);
+    out->gu_type = gu_type;
+    out->d_type = d_type;
+    out->up_type = gu_type;
+    out->n_embd = n_embd;
+    out->n_ff = n_ff;
+    out->gu_row = xs_iq_row_bytes(gu_type, n_embd);
+    out->up_row = out->gu_row;
+    out->d_row = xs_iq_row_bytes(d_type, n_ff);
+    out->up_off = (size_t)n_ff * out->gu_row;
+    out->down_off = out->up_off + (size_t)n_ff * out->up_row;
+    out->bytes = out->down_off + (size_t)n_embd * out->d_row;
+    return ok();
+}
+
+size_t xs_native_expert_scratch_bytes(int64_t cap, int64_t n_ff) {
+    if (cap <= 0 || n_ff <= 0) return 0;
+    const size_t f = (size_t)cap * (size_t)n_ff * sizeof(float);
+    return 3 * up256(f) + up256((size_t)cap * (size_t)(n_ff / 32) * 36) + 256;
+}
+
+int32_t* xs_native_expert_status(void* scratch, int64_t cap, int64_t n_ff) {
+    if (!scratch || cap <= 0 || n_ff <= 0) return nullptr;
+    return (int32_t*)((uint8_t*)scratch + xs_native_expert_scratch_bytes(cap, n_ff) - 256);
+}
+
+int xs_quantize_q8_1_rows(const float* x, int64_t n_rows, int64_t n_cols, void* y, void* stream) {
+    if (n_rows * n_cols <= 0) return ok();
+    if (n_cols % 32) return fail(XS_EINVAL, "quantize_q8_1_rows: n_cols %lld is not a multiple of 32", (long long)n_cols);
+    if (!aligned(x, 4) || !aligned(y, 4)) return fail(XS_EINVAL, "quantize_q8_1_rows: unaligned span");
+    return finish(stream, xs::launch_quantize_q8_1_rows(x, n_rows, n_cols, y, S(stream)), "quantize_q8_1_rows");
+}
+
+namespace {
+int grouped_args(const xs_expert_layout_t* L, const unsigned long long* grp_ptr, const int32_t* grp_start,
+                 const int32_t* n_groups, const int32_t* ent_dst, const int32_t* ent_tok, int64_t cap_groups,
+                 int64_t cap_entries, const void* x_q8_1, void* scratch, float* out, int64_t grid_groups,
+                 const char* what, xs::GroupedArgs* a) {
+    if (int r = check_layout(L, what)) return r;
+    if (cap_groups > 65535) return fail(XS_EINVAL, "%s: cap_groups %lld", what, (long long)cap_groups);
+    if (!aligned(grp_ptr, 8) || !aligned(grp_start, 4) || !aligned(n_groups, 4) || (ent_dst && !aligned(ent_dst, 4)) ||
+        (ent_tok && !aligned(ent_tok, 4)) || (x_q8_1 && !aligned(x_q8_1, 4)) || !aligned(scratch, 16) ||
+        (out && !aligned(out, 4)))
+        return fail(XS_EINVAL, "%s: a span is missing or misaligned", what);
+    const size_t f = (size_t)cap_entries * (size_t)L->n_ff * sizeof(float), fa = up256(f);
+    a->grp_ptr = grp_ptr;
+    a->grp_start = grp_start;
+    a->n_groups = n_groups;
+    a->ent_dst = ent_dst;
+    a->ent_tok = ent_tok;
+    a->x_q8_1 = x_q8_1;
+    a->gate = (float*)scratch;
+    a->up = (float*)((uint8_t*)scratch + fa);
+    a->hq = (uint8_t*)scratch + 3 * fa;
+    a->out = out;
+    a->err = xs_native_expert_status(scratch, cap_entries, L->n_ff);
+    a->cap_groups = cap_groups;
+    a->grid_groups = grid_groups;
+    return ok();
+}
+}  // namespace
+
+int xs_native_expert_grouped(const xs_expert_layout_t* L, const unsigned long long* grp_ptr,
+                             const int32_t* grp_start, const int32_t* n_groups, const int32_t* ent_dst,
+                             const int32_t* ent_tok, int64_t cap_groups, int64_t cap_entries, const void* x_q8_1,
+                             void* scratch, float* out, void* stream, int64_t grid_groups) {
+    if (cap_groups <= 0 || cap_entries <= 0) return ok();
+    if (!ent_dst || !ent_tok || !x_q8_1 || !out) return fail(XS_EINVAL, "native_expert_grouped: a span is missing");
+    xs::GroupedArgs a;
+    if (int r = grouped_args(L, grp_ptr, grp_start, n_groups, ent_dst, ent_tok, cap_groups, cap_entries, x_q8_1,
+                             scratch, out, grid_groups, "native_expert_grouped", &a))
+        return r;
+    const xs::ExpertLayout XL = to_layout(L);
+    hipError_t e = xs::launch_native_gu(XL, a, S(stream));
+    if (e == hipSuccess) e = xs::launch_native_down(XL, a, S(stream));
+    return finish(stream, e, "native_expert_grouped");
+}
+
+int xs_native_expert_gate_up(const xs_expert_layout_t* L, const unsigned long long* grp_ptr, const int32_t* grp_start,
+                             const int32_t* n_groups, const int32_t* ent_tok, int64_t cap_groups, int64_t cap_entries,
+                             const void* x_q8_1, void* scratch, void* stream, int64_t grid_groups) {
+    if (cap_groups <= 0 || cap_entries <= 0) return ok();
+    if (!ent_tok || !x_q8_1) return fail(XS_EINVAL, "native_expert_gate_up: a span is missing");
+    xs::GroupedArgs a;
+    if (int r = grouped_args(L, grp_ptr, grp_start, n_groups, nullptr, ent_tok, cap_groups, cap_entries, x_q8_1,
+                             scratch, nullptr, grid_groups, "native_expert_gate_up", &a))
+        return r;
+    return finish(stream, xs::launch_native_gu(to_layout(L), a, S(stream)), "native_expert_gate_up");
+}
+
+int xs_native_expert_down(const xs_expert_layout_t* L, const unsigned long long* grp_ptr, const int32_t* grp_start,
+                          const int32_t* n_groups, const int32_t* ent_dst, int64_t cap_groups, int64_t cap_entries,
+                          void* scratch, float* out, void* stream, int64_t grid_groups) {
+    if (cap_groups <= 0 || cap_entries <= 0) return ok();
+    if (!ent_dst || !out) return fail(XS_EINVAL, "native_expert_down: a span is missing");
+    xs::GroupedArgs a;
+    if (int r = grouped_args(L, grp_ptr, grp_start, n_groups, ent_dst, nullptr, cap_groups, cap_entries, nullptr,
+                             scratch, out, grid_groups, "native_expert_down", &a))
+        return r;
+    return finish(stream, xs::launch_native_down(to_layout(L), a, S(stream)), "native_expert_down");
+}
+
+int xs_iq_dequant_f32(int type, const void* src, int64_t n, float* dst, void* stream) {
+    if (n <= 0) return ok();
+    if (!type_qk(type) || n % type_qk(type)) return fail(XS_EINVAL, "iq_dequant_f32: type %d, %lld values", type, (long long)n);
+    if (!src || !aligned(dst, 4)) return fail(XS_EINVAL, "iq_dequant_f32: a span is missing or misaligned");
+    return finish(stream, xs::launch_dequant(type, src, n, dst, false, S(stream)), "iq_dequant_f32");
+}
+
+int xs_iq_dequant_bf16(int type, const void* src, int64_t n, uint16_t* dst, void* stream) {
+    if (n <= 0) return ok();
+    if (!type_qk(type) || n % type_qk(type)) return fail(XS_EINVAL, "iq_dequant_bf16: type %d, %lld values", type, (long long)n);
+    if (!src || !aligned(dst, 2)) return fail(XS_EINVAL, "iq_dequant_bf16: a span is missing or misaligned");
+    return finish(stream, xs::launch_dequant(type, src, n, dst, true, S(stream)), "iq_dequant_bf16");
+}
+
+int xs_quantize_rows(int type, const float* x, int64_t n, void* y, void* stream) {
+    if (n <= 0) return ok();
+    if (!type_qk(type) || n % type_qk(type)) return fail(XS_EINVAL, "quantize_rows: type %d, %lld values", type, (long long)n);
+    if (!aligned(x, 4) || !y) return fail(XS_EINVAL, "quantize_rows: a span is missing or misaligned");
+    return finish(stream, xs::launch_quantize_rows(type, x, n, y, S(stream)), "quantize_rows");
+}
+
+int xs_router_top10(const float* logits, int n_tokens, int n_expert, int k, int32_t* ids, float* weights,
+                    void* stream) {
+    if (n_tokens <= 0 || n_expert <= 0 || k <= 0) return ok();
+    if (k > 64) return fail(XS_EINVAL, "router_top10: k %d exceeds the kernel's 64", k);
+    if (n_expert > 1024) return fail(XS_EINVAL, "router_top10: n_expert %d is past the kernel's 1024", n_expert);
+    if (k > n_expert) return fail(XS_EINVAL, "router_top10: k %d > n_expert %d", k, n_expert);
+    if (!aligned(logits, 4) || !aligned(ids, 4) || !aligned(weights, 4))
+        return fail(XS_EINVAL, "router_top10: a span is missing or misaligned");
+    return finish(stream, xs::launch_router_topk(logits, n_tokens, n_expert, k, ids, weights, S(stream)), "router_top10");
+}
+
+int xs_router_grouped_sigmoid(const float* logits, const float* bias, int n_tokens, int n_expert, int n_group,
+                              int topk_group, int k, float routed_scale, int32_t* ids, float* weights, void* stream) {
+    if (n_tokens <= 0) return ok();
+    if (n_expert <= 0 || n_expert > 1024 || n_group <= 0 || n_group > 64 || n_expert % n_group || topk_group <= 0 ||
+        topk_group > n_group || k <= 0 || k > 64 || k > (n_expert / n_group) * topk_group)
+        return fail(XS_EINVAL, "router_grouped_sigmoid: geometry %d experts, %d groups, top %d groups, k %d", n_expert,
+                    n_group, topk_group, k);
+    if (!aligned(logits, 4) || !aligned(ids, 4) || !aligned(weights, 4) || (bias && !aligned(bias, 4)))
+        return fail(XS_EINVAL, "router_grouped_sigmoid: a span is missing or misaligned");
+    return finish(stream, xs::launch_router_grouped_sigmoid(logits, bias, n_tokens, n_expert, n_group, topk_group, k,
+                                                            routed_scale, ids, weights, S(stream)),
+                  "router_grouped_sigmoid");
+}
+
+int xs_router_logits_f32(const float* x, const float* w, float* logits, int n_tokens, int64_t n_embd, int n_expert,
+                         void* stream) {
+    if (n_tokens <= 0 || n_expert <= 0) return ok();
+    if (n_embd <= 0 || !aligned(x, 4) || !aligned(w, 4) || !aligned(logits, 4))
+        return fail(XS_EINVAL, "router_logits_f32: bad geometry or span");
+    return finish(stream, xs::launch_logits_f32(x, w, logits, n_tokens, n_embd, n_expert, S(stream)), "router_logits_f32");
+}
+
+void xs_plan_offsets(long long capx, long long* start, long long* dst, long long* tok, long long* ptr,
+                     long long* start2) {
+    if (start) *start = 4;
+    if (dst) *dst = 4 + capx + 1;
+    if (tok) *tok = 4 + capx + 1 + capx;
+    if (ptr) *ptr = plan_ptr_off(capx);
+    if (start2) *start2 = plan_ptr_off(capx) + 4 * capx;
+}
+
+int xs_resident_plan(const int32_t* ids, int n_entries, int k, const int32_t* res_layer, int n_expert,
+                     const uint8_t* cache_base, const unsigned long long* slot_off, long long blob, int32_t* plan,
+                     long long capx, uint32_t* skip, uint32_t ring, void* stream) {
+    if (n_entries <= 0) return ok();
+    if (n_entries > 1024) return fail(XS_EINVAL, "resident_plan: more entries (%d) than a work-group", n_entries);
+    if (n_entries > capx || k <= 0 || n_expert <= 0 || n_expert > 16384)
+        return fail(XS_EINVAL, "resident_plan: %d entries, capx %lld, k %d, %d experts", n_entries, capx, k, n_expert);
+    if (!aligned(ids, 4) || !aligned(plan, 8) || !aligned(skip, 4) || (res_layer && !aligned(res_layer, 4)) ||
+        (slot_off && !aligned(slot_off, 8)))
+        return fail(XS_EINVAL, "resident_plan: a span is missing or misaligned");
+    if (!stream) return fail(XS_EINVAL, "resident_plan requires an explicit stream");
+    return finish(stream, xs::launch_resident_plan(ids, n_entries, k, res_layer, n_expert, cache_base, slot_off, blob,
+                                                   plan, capx, skip, ring, S(stream)),
+                  "resident_plan");
+}
+
+int xs_prefill_route(const int32_t* ids, int64_t n_entries, int k, int n_expert, int32_t* src, int32_t* slot,
+                     int32_t* entry_of, int32_t* bounds, int32_t* experts, int32_t* n_groups,
+                     const uint8_t* cache_base, long long blob, unsigned long long* grp_ptr, void* stream) {
+    if (n_entries <= 0) return ok();
+    if (k <= 0 || n_expert <= 0 || n_expert > 1024 || n_entries > (1ll << 30))
+        return fail(XS_EINVAL, "prefill_route: %lld entries, k %d, %d experts", (long long)n_entries, k, n_expert);
+    if (!aligned(ids, 4) || !aligned(src, 4) || !aligned(slot, 4) || !aligned(entry_of, 4) || !aligned(bounds, 4) ||
+        !aligned(experts, 4) || !aligned(n_groups, 4) || (grp_ptr && !aligned(grp_ptr, 8)))
+        return fail(XS_EINVAL, "prefill_route: a span is missing or misaligned");
+    if (!stream) return fail(XS_EINVAL, "prefill_route requires an explicit stream");
+    return finish(stream, xs::launch_prefill_route(ids, n_entries, k, n_expert, src, slot, entry_of, bounds, experts,
+                                                   n_groups, cache_base, blob, grp_ptr, S(stream)),
+                  "prefill_route");
+}
+
+size_t xs_moe_prefill_scratch_bytes(int64_t n_tok, int64_t rows, int64_t n_embd, int64_t n_ff) {
+    if (n_tok <= 0 || rows <= 0) return 256;
+    return up256((size_t)n_tok * (size_t)n_embd * 2) + up256((size_t)rows * (size_t)n_ff * 2) +
+           up256((size_t)(rows + 1) * 4) + 256;
+}
+
+int xs_moe_prefill_experts(const xs_expert_layout_t* L, const float* x, int64_t n_tok, const int32_t* src,
+                           const int32_t* entry_of, const int32_t* bounds, const int32_t* n_groups,
+                           const unsigned long long* grp_ptr, int64_t cap_groups, int64_t rows, void* scratch,
+                           float* parts, void* stream) {
+    if (rows <= 0 || cap_groups <= 0) return ok();
+    if (int r = check_layout(L, "moe_prefill_experts")) return r;
+    if (cap_groups > rows) return fail(XS_EINVAL, "moe_prefill_experts: cap_groups %lld > rows %lld", (long long)cap_groups,
+                                       (long long)rows);
+    if (L->n_ff % 64 || L->n_embd % 128)
+        return fail(XS_EINVAL, "moe_prefill_experts: n_ff %% 64 and n_embd %% 128 must be 0 (%lld, %lld)",
+                    (long long)L->n_ff, (long long)L->n_embd);
+    if (cap_groups > 65535 || !aligned(x, 4) || !aligned(src, 4) || !aligned(entry_of, 4) || !aligned(bounds, 4) ||
+        !aligned(n_groups, 4) || !aligned(grp_ptr, 8) || !aligned(scratch, 256) || !aligned(parts, 4))
+        return fail(XS_EINVAL, "moe_prefill_experts: a span is missing or misaligned");
+    if (!stream) return fail(XS_EINVAL, "moe_prefill_experts requires an explicit stream");
+    xs::PrefillArgs a;
+    a.x = x;
+    a.src = src;
+    a.entry = entry_of;
+    a.bounds = bounds;
+    a.n_groups = n_groups;
+    a.wptr = grp_ptr;
+    a.xb = (uint16_t*)scratch;
+    a.h = (uint16_t*)((uint8_t*)scratch + up256((size_t)n_tok * (size_t)L->n_embd * 2));
+    a.mtile = (int32_t*)((uint8_t*)a.h + up256((size_t)rows * (size_t)L->n_ff * 2));
+    a.err = (int32_t*)((uint8_t*)scratch + xs_moe_prefill_scratch_bytes(n_tok, rows, L->n_embd, L->n_ff) - 256);
+    a.parts = parts;
+    a.n_tok = n_tok;
+    a.rows = rows;
+    a.cap_groups = cap_groups;
+    return finish(stream, xs::launch_prefill_experts(to_layout(L), a, S(stream)), "moe_prefill_experts");
+}
+
+int xs_native_moe_combine_multi(const float* parts, const float* weights, const float* shared, float* output,
+                                int64_t n_embd, int64_t k, int n_tok, void* stream, const float* shared_gate) {
+    if (!stream || n_embd <= 0 || k < 1 || k > 15 || n_tok < 1 || (shared_gate && !shared))
+        return fail(XS_EINVAL, "native MoE combine (multi) requires a stream, width, 1..15 experts, tokens");
+    if (!aligned(parts, 4) || !aligned(weights, 4) || !aligned(output, 4) || (shared && !aligned(shared, 4)))
+        return fail(XS_EINVAL, "native MoE combine requires aligned spans");
+    const size_t ob = (size_t)n_tok * n_embd * 4;
+    if (overlap(output, ob, parts, ob * k) || overlap(output, ob, weights, (size_t)n_tok * k * 4) ||
+        overlap(output, ob, shared, ob))
+        return fail(XS_EINVAL, "native MoE combine requires disjoint output");
+    return finish(stream, xs::launch_combine(parts, weights, shared, shared_gate, nullptr, output, n_embd, (int)k, n_tok,
+                                             S(stream)),
+                  "native_moe_combine_multi");
+}
+
+int xs_native_moe_combine(const float* parts, const float* weights, const float* shared, float* output,
+                          int64_t n_embd, int64_t k, void* stream) {
+    if (!stream || n_embd <= 0 || n_embd > 0x7fffffff || k < 1 || k > 15)
+        return fail(XS_EINVAL, "native MoE combine requires a stream, positive width and 1..15 experts");
+    return xs_native_moe_combine_multi(parts, weights, shared, output, n_embd, k, 1, stream, nullptr);
+}
+
+int xs_moe_combine_residual(const float* parts, const float* weights, const float* shared, const float* shared_gate,
+                            const float* residual, float* output, int64_t n_embd, int64_t k, int n_tok, void* stream) {
+    if (!stream || n_embd <= 0 || k < 1 || k > 64 || n_tok < 1 || (shared_gate && !shared))
+        return fail(XS_EINVAL, "moe_combine_residual requires a stream, width, 1..64 experts, tokens");
+    if (!aligned(parts, 4) || !aligned(weights, 4) || !aligned(output, 4) || !aligned(residual, 4))
+        return fail(XS_EINVAL, "moe_combine_residual requires aligned spans");
+    const size_t ob = (size_t)n_tok * n_embd * 4;
+    if (overlap(output, ob, parts, ob * k)) return fail(XS_EINVAL, "moe_combine_residual: output overlaps parts");
+    if (residual != output && overlap(output, ob, residual, ob))
+        return fail(XS_EINVAL, "moe_combine_residual: output partly overlaps the residual");
+    return finish(stream, xs::launch_combine(parts, weights, shared, shared_gate, residual, output, n_embd, (int)k, n_tok,
+                                             S(stream)),
+                  "moe_combine_residual");
+}
+
+int xs_add_inplace(float* x, const float* y, int64_t n, void* stream) {
+    if (n <= 0) return ok();
+    if (!aligned(x, 4) || !aligned(y, 4)) return fail(XS_EINVAL, "add_inplace: a span is missing or misaligned");
+    return finish(stream, xs::launch_add_inplace(x, y, n, S(stream)), "add_inplace");
+}
+
+// ---------------------------------------------------------------- whole layers
+
+namespace {
+struct DecodeWs {
+    int32_t* ids;
+    float* w;
+    int32_t* plan;
+    uint32_t* skip;
+    void* xq;
+    void* scratch;
+    float* parts;
+    size_t bytes;
+};
+DecodeWs decode_ws(const xs_expert_layout_t* L, int k, int n_tok, uint8_t* base) {
+    DecodeWs d;
+    const long long capx = (long long)n_tok * k;
+    size_t off = 0;
+    auto take = [&](size_t b) { uint8_t* p = base ? base + off : nullptr; off += up256(b); return p; };
+    d.ids = (int32_t*)take((size_t)capx * 4);
+    d.w = (float*)take((size_t)capx * 4);
+    d.plan = (int32_t*)take(plan_words(capx) * 4);
+    d.skip = (uint32_t*)take(4);
+    d.xq = take((size_t)n_tok * (size_t)(L->n_embd / 32) * 36);
+    d.scratch = take(xs_native_expert_scratch_bytes(capx, L->n_ff));
+    d.parts = (float*)take((size_t)capx * (size_t)L->n_embd * 4);
+    d.bytes = off;
+    return d;
+}
+struct PrefillWs {
+    int32_t* ids;
+    float* w;
+    int32_t *src, *slot, *entry, *bounds, *experts, *n_groups;
+    unsigned long long* grp_ptr;
+    void* scratch;
+    float* parts;
+    size_t bytes;
+};
+PrefillWs prefill_ws(const xs_expert_layout_t* L, int n_expert, int k, int n_tok, uint8_t* base) {
+    PrefillWs d;
+    const size_t n = (size_t)n_tok * k;
+    size_t off = 0;
+    auto take = [&](size_t b) { uint8_t* p = base ? base + off : nullptr; off += up256(b); return p; };
+    d.ids = (int32_t*)take(n * 4);
+    d.w = (float*)take(n * 4);
+    d.src = (int32_t*)take(n * 4);
+    d.slot = (int32_t*)take(n * 4);
+    d.entry = (int32_t*)take(n * 4);
+    d.bounds = (int32_t*)take((size_t)(n_expert + 1) * 4);
+    d.experts = (int32_t*)take((size_t)n_expert * 4);
+    d.n_groups = (int32_t*)take(4);
+    d.grp_ptr = (unsigned long long*)take((size_t)n_expert * 8);
+    d.scratch = take(xs_moe_prefill_scratch_bytes(n_tok, (int64_t)n, L->n_embd, L->n_ff));
+    d.parts = (float*)take(n * (size_t)L->n_embd * 4);
+    d.bytes = off;
+    return d;
+}
+}  // namespace
+
+size_t xs_moe_layer_decode_workspace_bytes(const xs_expert_layout_t* L, int n_expert, int k, int n_tok) {
+    (void)n_expert;
+    if (!L || k <= 0 || n_tok <= 0) return 0;
+    return decode_ws(L, k, n_tok, nullptr).bytes;
+}
+
+int xs_moe_layer_decode(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_bytes, int n_expert, int k,
+                        const float* x, const float* logits, const float* residual, float* out, int n_tok,
+                        void* workspace, size_t workspace_bytes, void* stream) {
+    if (n_tok <= 0) return ok();
+    if (int r = check_layout(L, "moe_layer_decode")) return r;
+    if (!stream) return fail(XS_EINVAL, "moe_layer_decode requires an explicit stream");
+    if (n_tok * k > 1024) return fail(XS_EINVAL, "moe_layer_decode: %d tokens x top-%d is past 1024 entries", n_tok, k);
+    if (blob_bytes < L->bytes || blob_bytes % 16 || !aligned(arena, 16))
+        return fail(XS_EINVAL, "moe_layer_decode: the arena must hold 16-byte aligned blobs of at least %zu bytes", L->bytes);
+    if (!aligned(workspace, 256) || workspace_bytes < xs_moe_layer_decode_workspace_bytes(L, n_expert, k, n_tok))
+        return fail(XS_EINVAL, "moe_layer_decode: workspace missing, misaligned or short");
+    const DecodeWs w = decode_ws(L, k, n_tok, (uint8_t*)workspace);
+    const long long capx = (long long)n_tok * k;
+    const hipStream_t s = S(stream);
+    if (int r = xs_router_top10(logits, n_tok, n_expert, k, w.ids, w.w, stream)) return r;
+    if (int r = xs_resident_plan(w.ids, (int)capx, k, nullptr, n_expert, arena, nullptr, (long long)blob_bytes, w.plan,
+                                 capx, w.skip, 1u, stream))
+        return r;
+    if (int r = xs_quantize_q8_1_rows(x, n_tok, L->n_embd, w.xq, stream)) return r;
+    const int64_t cap_groups = capx < n_expert ? capx : n_expert;
+    long long o_start, o_dst, o_tok, o_ptr;
+    xs_plan_offsets(capx, &o_start, &o_dst, &o_tok, &o_ptr, nullptr);
+    if (int r = xs_native_expert_grouped(L, (const unsigned long long*)(w.plan + o_ptr), w.plan + o_start, w.plan,
+                                         w.plan + o_dst, w.plan + o_tok, cap_groups, capx, w.xq, w.scratch, w.parts,
+                                         stream, 0))
+        return r;
+    (void)s;
+    return xs_moe_combine_residual(w.parts, w.w, nullptr, nullptr, residual, out, L->n_embd, k, n_tok, stream);
+}
+
+size_t xs_moe_layer_prefill_workspace_bytes(const xs_expert_layout_t* L, int n_expert, int k, int n_tok) {
+    if (!L || k <= 0 || n_tok <= 0 || n_expert <= 0) return 0;
+    return prefill_ws(L, n_expert, k, n_tok, nullptr).bytes;
+}
+
+int xs_moe_layer_prefill(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_bytes, int n_expert,
+                         int k, const float* x, const float* logits, const float* residual, float* out, int n_tok,
+                         void* workspace, size_t workspace_bytes, void* stream) {
+    if (n_tok <= 0) return ok();
+    if (int r = check_layout(L, "moe_layer_prefill")) return r;
+    if (!stream) return fail(XS_EINVAL, "moe_layer_prefill requires an explicit stream");
+    if (blob_bytes < L->bytes || blob_bytes % 16 || !aligned(arena, 16))
+        return fail(XS_EINVAL, "moe_layer_prefill: the arena must hold 16-byte aligned blobs of at least %zu bytes", L->bytes);
+    if (!aligned(workspace, 256) || workspace_bytes < xs_moe_layer_prefill_workspace_bytes(L, n_expert, k, n_tok))
+        return fail(XS_EINVAL, "moe_layer_prefill: workspace missing, misaligned or short");
+    const PrefillWs w = prefill_ws(L, n_expert, k, n_tok, (uint8_t*)workspace);
+    const int64_t n = (int64_t)n_tok * k;
+    if (int r = xs_router_top10(logits, n_tok, n_expert, k, w.ids, w.w, stream)) return r;
+    if (int r = xs_prefill_route(w.ids, n, k, n_expert, w.src, w.slot, w.entry, w.bounds, w.experts, w.n_groups, arena,
+                                 (long long)blob_bytes, w.grp_ptr, stream))
+        return r;
+    const int64_t cap_groups = n < n_expert ? n : n_expert;
+    if (int r = xs_moe_prefill_experts(L, x, n_tok, w.src, w.entry, w.bounds, w.n_groups, w.grp_ptr, cap_groups, n,
+                                       w.scratch, w.parts, stream))
+        return r;
+    return xs_moe_combine_residual(w.parts, w.w, nullptr, nullptr, residual, out, L->n_embd, k, n_tok, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,57 @@
+// xestrata-win_amd/csrc/combine.hip - the weighted combine of a token's expert outputs, back into the residual stream
+// (reference src/kernels/xe/native_moe.cpp:36-58, and add_inplace at src/core/plain_model.cpp:987).
+//
+// out[t, c] = fl(p0 w0), then + fl(pj wj) for j = 1..k-1 in rank order (each product rounded: no fused multiply-add),
+// then + shared[t, c] (scaled by 1 / (1 + exp(-gate[t])), that product rounded, when gated), then, when a residual is
+// given, residual[t, c] + that.  A gather over the routing-order parts: no atomics, one thread a column.
+#include "xs_device.h"
+#include "xs_kernels.h"
+
+namespace xs {
+
+__global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ parts, const float* __restrict__ weights,
+                                                      const float* __restrict__ shared,
+                                                      const float* __restrict__ shared_gate,
+                                                      const float* __restrict__ residual, float* __restrict__ out,
+                                                      int64_t n_embd, int k) {
+    const int64_t t = blockIdx.y;
+    const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= n_embd) return;
+    const float* p = parts + t * k * n_embd + c;
+    const float* w = weights + t * k;
+    float sum = p[0] * w[0];
+    for (int e = 1; e < k; ++e) {
+        const float prod = p[(int64_t)e * n_embd] * w[e];
+        sum = sum + prod;
+    }
+    if (shared) {
+        float sv = shared[t * n_embd + c];
+        if (shared_gate) {
+            const float gt = 1.0f / (1.0f + expf(-shared_gate[t]));
+            sv = sv * gt;
+        }
+        sum += sv;
+    }
+    if (residual) sum = residual[t * n_embd + c] + sum;
+    out[t * n_embd + c] = sum;
+}
+
+__global__ __launch_bounds__(256) void add_inplace_kernel(float* __restrict__ x, const float* __restrict__ y, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) x[i] = x[i] + y[i];
+}
+
+hipError_t launch_combine(const float* parts, const float* weights, const float* shared, const float* shared_gate,
+                          const float* residual, float* out, int64_t n_embd, int k, int n_tok, hipStream_t s) {
+    const dim3 grid((unsigned)((n_embd + 255) / 256), (unsigned)n_tok);
+    hipLaunchKernelGGL(combine_kernel, grid, dim3(256), 0, s, parts, weights, shared, shared_gate, residual, out, n_embd,
+                       k);
+    return hipGetLastError();
+}
+
+hipError_t launch_add_inplace(float* x, const float* y, int64_t n, hipStream_t s) {
+    hipLaunchKernelGGL(add_inplace_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, y, n);
+    return hipGetLastError();
+}
+
+}  // namespace xs

@@ -1,0 +1,128 @@
+// xestrata-win_amd/csrc/xs_device.h - device-side building blocks shared by the MoE kernels (gfx950, wave64).
+//
+// GGUF block layouts (ggml-common.h, the reference's third_party/main/ggml/ggml-common.h):
+//   Q8_0 34 B/32, Q8_1 36 B/32, Q4_K 144 B/256, Q6_K 210 B/256, IQ4_XS 136 B/256.
+// Every source file is compiled with -ffp-contract=off: products and sums round on their own unless a fused
+// multiply-add is written out (__builtin_fmaf), which is what the reference's canonical arithmetic requires
+// (include/strata/kernels/canon_math.hpp, CMakeLists.txt:396).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace xs {
+
+enum : int { kQ8_0 = 8, kQ4_K = 12, kQ6_K = 14, kIQ4_XS = 23 };
+constexpr int kWave = 64;
+
+__host__ __device__ constexpr int block_values(int t) { return t == kQ8_0 ? 32 : 256; }
+__host__ __device__ constexpr int block_bytes(int t) {
+    return t == kQ8_0 ? 34 : t == kQ4_K ? 144 : t == kQ6_K ? 210 : t == kIQ4_XS ? 136 : 0;
+}
+__host__ __device__ constexpr int64_t row_bytes(int t, int64_t n) { return n / block_values(t) * block_bytes(t); }
+
+// ---------------------------------------------------------------- scalar conversions
+
+__device__ __forceinline__ float u2f(uint32_t u) { return __uint_as_float(u); }
+__device__ __forceinline__ uint32_t f2u(float f) { return __float_as_uint(f); }
+
+// fp16 bits -> float (exact; the hardware conversion keeps subnormals)
+__device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+// float -> fp16 bits, round to nearest even
+__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+// float -> bf16 bits, round to nearest even (NaN kept quiet)
+__device__ __forceinline__ uint16_t f2bf(float f) {
+    const uint32_t u = f2u(f);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
+    return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+
+// ---------------------------------------------------------------- canonical arithmetic
+// canon_math.hpp's SwiGLU and int8 scale: the same IEEE operations in the same order on every device, so the GPU and
+// the CPU give the same bits (reference include/strata/kernels/canon_math.hpp:55-108).
+
+__device__ __forceinline__ float canon_rcp(float v) {
+    float r = u2f(0x7EF311C3u - f2u(v));
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        const float e = __builtin_fmaf(-v, r, 1.0f);
+        r = __builtin_fmaf(r, e, r);
+    }
+    return r;
+}
+__device__ __forceinline__ float canon_exp(float x) {
+    x = x < -80.0f ? -80.0f : x > 80.0f ? 80.0f : x;
+    const float t = x * 1.44269504f;
+    const float kf = (t + 12582912.0f) - 12582912.0f;
+    float r = __builtin_fmaf(-kf, 0.693145752f, x);
+    r = __builtin_fmaf(-kf, 1.42860677e-06f, r);
+    float p = 1.0f / 720.0f;
+    p = __builtin_fmaf(p, r, 1.0f / 120.0f);
+    p = __builtin_fmaf(p, r, 1.0f / 24.0f);
+    p = __builtin_fmaf(p, r, 1.0f / 6.0f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    return u2f(f2u(p) + (uint32_t)((int32_t)kf << 23));
+}
+__device__ __forceinline__ float canon_silu_mul(float g, float u) {
+    const float den = 1.0f + canon_exp(-g);
+    const float a = g * canon_rcp(den);
+    return a * u;
+}
+__device__ __forceinline__ float q8_scale(float amax) {
+    const float d = amax * (1.0f / 127.0f);
+    return d > 65504.0f ? 65504.0f : d;
+}
+__device__ __forceinline__ float q8_inv(float d) { return d >= 1e-30f ? canon_rcp(d) : 0.0f; }
+__device__ __forceinline__ int q8_value(float x, float id) {
+    const float t = x * id;
+    const float r = t + (t < 0.0f ? -0.5f : 0.5f);
+    const float c = r > 127.0f ? 127.0f : r < -127.0f ? -127.0f : r;
+    return (int)(int8_t)(int32_t)c;
+}
+__device__ __forceinline__ float q8_1_finite(float v) { return fabsf(v) > 65504.0f ? copysignf(65504.0f, v) : v; }
+
+// ---------------------------------------------------------------- integer dot and wave reductions
+
+__device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+
+// sum over groups of `W` neighbouring lanes (W a power of two up to 64); every lane of a group ends with the sum
+template <int W>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+template <int W>
+__device__ __forceinline__ int group_sum_i(int v) {
+#pragma unroll
+    for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+template <int W>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+    for (int o = W / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// bytes of a 16-entry signed table picked by the 4 nibbles of `idx` bytes (each byte < 16): v_perm over the table's
+// halves, then a select on bit 3 of each index
+__device__ __forceinline__ int table16_lookup(uint32_t idx, uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3) {
+    const uint32_t sel = idx & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(t1, t0, sel);
+    const uint32_t hi = __builtin_amdgcn_perm(t3, t2, sel);
+    const uint32_t m = ((idx & 0x08080808u) >> 3) * 0xFFu;   // 0xFF in every byte whose index is >= 8
+    return (int)((hi & m) | (lo & ~m));
+}
+
+// ---------------------------------------------------------------- 2-byte aligned reads
+// Q8_0 and Q6_K blocks are 34 / 210 bytes: inside a row they sit at even addresses only.  Words are assembled from
+// 16-bit reads, never from an unaligned 32-bit one.
+__device__ __forceinline__ uint32_t ld_u32_a2(const uint8_t* p) {
+    const uint16_t* q = (const uint16_t*)p;
+    return (uint32_t)q[0] | ((uint32_t)q[1] << 16);
+}
+
+}  // namespace xs

@@ -1,0 +1,80 @@
+// xestrata-win_amd/csrc/xs_kernels.h - launchers of the HIP kernels, called by the C ABI layer (abi.cpp).
+// Launchers check nothing the ABI layer has not already checked; they return the launch's hipError_t.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace xs {
+
+struct ExpertLayout {   // one native expert blob: [gate rows | up rows | down rows], raw GGUF blocks
+    int gu_type, d_type;
+    int64_t n_embd, n_ff;
+    int64_t gu_row, d_row, up_off, down_off, bytes;
+};
+
+// formats.hip
+hipError_t launch_quantize_rows(int type, const float* x, int64_t n, void* y, hipStream_t s);
+hipError_t launch_dequant(int type, const void* src, int64_t n, void* dst, bool bf16, hipStream_t s);
+
+// quant_act.hip
+hipError_t launch_quantize_q8_1_rows(const float* x, int64_t n_rows, int64_t n_cols, void* y, hipStream_t s);
+
+// experts_decode.hip
+struct GroupedArgs {
+    const unsigned long long* grp_ptr;
+    const int32_t* grp_start;
+    const int32_t* n_groups;
+    const int32_t* ent_dst;
+    const int32_t* ent_tok;
+    const void* x_q8_1;
+    float* gate;   // scratch: [cap_entries, n_ff]
+    float* up;     // scratch: [cap_entries, n_ff]
+    void* hq;      // scratch: [cap_entries, n_ff / 32] q8_1 blocks
+    float* out;
+    int32_t* err;  // device word: set non-zero when a blob address is not 16-byte aligned
+    int64_t cap_groups, grid_groups;
+};
+hipError_t launch_native_gu(const ExpertLayout& L, const GroupedArgs& a, hipStream_t s);
+hipError_t launch_native_down(const ExpertLayout& L, const GroupedArgs& a, hipStream_t s);
+
+// router.hip
+hipError_t launch_router_topk(const float* logits, int n_tokens, int n_expert, int k, int32_t* ids, float* weights,
+                              hipStream_t s);
+hipError_t launch_router_grouped_sigmoid(const float* logits, const float* bias, int n_tokens, int n_expert,
+                                         int n_group, int topk_group, int k, float routed_scale, int32_t* ids,
+                                         float* weights, hipStream_t s);
+hipError_t launch_logits_f32(const float* x, const float* w, float* logits, int n_tokens, int64_t n_embd,
+                             int n_expert, hipStream_t s);
+
+// dispatch.hip
+hipError_t launch_resident_plan(const int32_t* ids, int n, int k, const int32_t* res, int n_expert,
+                                const uint8_t* cache_base, const unsigned long long* slot_off, long long blob,
+                                int32_t* plan, long long capx, uint32_t* skip, uint32_t ring, hipStream_t s);
+hipError_t launch_prefill_route(const int32_t* ids, int64_t n, int k, int n_expert, int32_t* src, int32_t* slot,
+                                int32_t* entry, int32_t* bounds, int32_t* experts, int32_t* n_groups,
+                                const uint8_t* cache_base, long long blob, unsigned long long* grp_ptr, hipStream_t s);
+
+// combine.hip
+hipError_t launch_combine(const float* parts, const float* weights, const float* shared, const float* shared_gate,
+                          const float* residual, float* out, int64_t n_embd, int k, int n_tok, hipStream_t s);
+hipError_t launch_add_inplace(float* x, const float* y, int64_t n, hipStream_t s);
+
+// experts_prefill.hip
+struct PrefillArgs {
+    const float* x;                 // [n_tok, n_embd] activations (fp32)
+    const int32_t* src;             // [rows] token of each routed row (expert-sorted order)
+    const int32_t* entry;           // [rows] routing entry each row writes
+    const int32_t* bounds;          // [groups + 1] row bounds of each group
+    const int32_t* n_groups;        // device count of groups
+    const unsigned long long* wptr; // [groups] blob address of each group's expert
+    uint16_t* xb;                   // scratch: [n_tok, n_embd] bf16 copy of x
+    uint16_t* h;                    // scratch: [rows, n_ff] bf16 SwiGLU output
+    float* parts;                   // [n_tok * k, n_embd] routing-order outputs
+    int32_t* mtile;                 // scratch: [cap_groups + 1] m-tile prefix of the groups
+    int32_t* err;
+    int64_t n_tok, rows, cap_groups;
+};
+hipError_t launch_prefill_experts(const ExpertLayout& L, const PrefillArgs& a, hipStream_t s);
+
+}  // namespace xs

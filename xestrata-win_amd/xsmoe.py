@@ -1,0 +1,327 @@
+"""Host-side mirror of XeStrata's MoE kernel API over libxsmoe.so (include/xs_moe.h), for Python callers.
+
+Device memory and streams are torch tensors on a HIP device and torch's current stream: plumbing only; every
+computation runs in the library's HIP kernels.  Names and argument meanings follow the reference's
+strata::kernels functions (router_top10, quantize_q8_1_rows, native_expert_grouped, resident_plan,
+native_moe_combine_multi, ...); a failing call raises XsError with the library's message, as the reference's
+entry points throw (std::invalid_argument / core::DeviceError).
+
+There is no fallback: when libxsmoe.so is missing every call raises.
+"""
+import ctypes
+import pathlib
+
+import torch
+
+HERE = pathlib.Path(__file__).resolve().parent
+LIB_PATH = HERE / "libxsmoe.so"
+
+Q8_0, Q4_K, Q6_K, IQ4_XS = 8, 12, 14, 23
+BLOCK_VALUES = {Q8_0: 32, Q4_K: 256, Q6_K: 256, IQ4_XS: 256}
+BLOCK_BYTES = {Q8_0: 34, Q4_K: 144, Q6_K: 210, IQ4_XS: 136}
+XS_OK, XS_EINVAL, XS_EDEVICE = 0, 1, 2
+
+
+class XsError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(msg)
+        self.code = code
+
+
+class Layout(ctypes.Structure):
+    """xs_expert_layout_t: the reference's NativeExpertLayout (include/strata/kernels/iq_kernels.hpp:66-75)."""
+    _fields_ = [("gu_type", ctypes.c_int), ("d_type", ctypes.c_int), ("up_type", ctypes.c_int),
+                ("n_embd", ctypes.c_int64), ("n_ff", ctypes.c_int64),
+                ("gu_row", ctypes.c_size_t), ("d_row", ctypes.c_size_t), ("up_row", ctypes.c_size_t),
+                ("up_off", ctypes.c_size_t), ("down_off", ctypes.c_size_t), ("bytes", ctypes.c_size_t)]
+
+
+_lib = None
+P, I, I64, SZ, F = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t, ctypes.c_float
+LP = ctypes.POINTER(Layout)
+LL = ctypes.c_longlong
+U32 = ctypes.c_uint32
+
+_SIGS = {
+    "xs_last_error": (ctypes.c_char_p, []),
+    "xs_abi_version": (I, []),
+    "xs_iq_row_bytes": (SZ, [I, I64]),
+    "xs_native_expert_supported": (I, [I, I, I64, I64, I]),
+    "xs_native_expert_layout": (I, [I, I, I64, I64, I, LP]),
+    "xs_native_expert_scratch_bytes": (SZ, [I64, I64]),
+    "xs_native_expert_status": (P, [P, I64, I64]),
+    "xs_native_expert_gate_up": (I, [LP, P, P, P, P, I64, I64, P, P, P, I64]),
+    "xs_native_expert_down": (I, [LP, P, P, P, P, I64, I64, P, P, P, I64]),
+    "xs_quantize_q8_1_rows": (I, [P, I64, I64, P, P]),
+    "xs_native_expert_grouped": (I, [LP, P, P, P, P, P, I64, I64, P, P, P, P, I64]),
+    "xs_iq_dequant_f32": (I, [I, P, I64, P, P]),
+    "xs_iq_dequant_bf16": (I, [I, P, I64, P, P]),
+    "xs_quantize_rows": (I, [I, P, I64, P, P]),
+    "xs_router_top10": (I, [P, I, I, I, P, P, P]),
+    "xs_router_grouped_sigmoid": (I, [P, P, I, I, I, I, I, F, P, P, P]),
+    "xs_router_logits_f32": (I, [P, P, P, I, I64, I, P]),
+    "xs_resident_plan": (I, [P, I, I, P, I, P, P, LL, P, LL, P, U32, P]),
+    "xs_plan_offsets": (None, [LL, P, P, P, P, P]),
+    "xs_prefill_route": (I, [P, I64, I, I, P, P, P, P, P, P, P, LL, P, P]),
+    "xs_moe_prefill_experts": (I, [LP, P, I64, P, P, P, P, P, I64, I64, P, P, P]),
+    "xs_moe_prefill_scratch_bytes": (SZ, [I64, I64, I64, I64]),
+    "xs_native_moe_combine": (I, [P, P, P, P, I64, I64, P]),
+    "xs_native_moe_combine_multi": (I, [P, P, P, P, I64, I64, I, P, P]),
+    "xs_moe_combine_residual": (I, [P, P, P, P, P, P, I64, I64, I, P]),
+    "xs_add_inplace": (I, [P, P, I64, P]),
+    "xs_moe_layer_decode": (I, [LP, P, SZ, I, I, P, P, P, P, I, P, SZ, P]),
+    "xs_moe_layer_decode_workspace_bytes": (SZ, [LP, I, I, I]),
+    "xs_moe_layer_prefill": (I, [LP, P, SZ, I, I, P, P, P, P, I, P, SZ, P]),
+    "xs_moe_layer_prefill_workspace_bytes": (SZ, [LP, I, I, I]),
+}
+
+
+def lib():
+    """The loaded libxsmoe.so; raises when it is not built (no fallback exists)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} is not built: run `python xestrata-win_amd/build.py`")
+        L = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _check(code):
+    if code != XS_OK:
+        raise XsError(code, lib().xs_last_error().decode())
+
+
+def _p(t):
+    """Device address of a tensor (None -> NULL)."""
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    return t.data_ptr()
+
+
+def _stream(stream=None):
+    if stream is not None:
+        return stream
+    return torch.cuda.current_stream().cuda_stream
+
+
+# ------------------------------------------------------------------------------------------------ formats
+
+def row_bytes(t, n):
+    return lib().xs_iq_row_bytes(t, n)
+
+
+def native_expert_supported(gu, d, n_embd, n_ff, up=-1):
+    return bool(lib().xs_native_expert_supported(gu, d, n_embd, n_ff, up))
+
+
+def native_expert_layout(gu, d, n_embd, n_ff, up=-1):
+    L = Layout()
+    _check(lib().xs_native_expert_layout(gu, d, n_embd, n_ff, up, ctypes.byref(L)))
+    return L
+
+
+def native_expert_scratch_bytes(cap_entries, n_ff):
+    return lib().xs_native_expert_scratch_bytes(cap_entries, n_ff)
+
+
+def quantize_rows(t, x, out=None, stream=None):
+    """Float rows (device fp32, a whole number of blocks) -> `t` blocks (uint8 device tensor)."""
+    n = x.numel()
+    if out is None:
+        out = torch.empty(n // BLOCK_VALUES[t] * BLOCK_BYTES[t], dtype=torch.uint8, device=x.device)
+    _check(lib().xs_quantize_rows(t, _p(x), n, _p(out), _stream(stream)))
+    return out
+
+
+def iq_dequant_f32(t, src, n, out=None, stream=None):
+    if out is None:
+        out = torch.empty(n, dtype=torch.float32, device=src.device)
+    _check(lib().xs_iq_dequant_f32(t, _p(src), n, _p(out), _stream(stream)))
+    return out
+
+
+def iq_dequant_bf16(t, src, n, out=None, stream=None):
+    if out is None:
+        out = torch.empty(n, dtype=torch.int16, device=src.device)
+    _check(lib().xs_iq_dequant_bf16(t, _p(src), n, _p(out), _stream(stream)))
+    return out
+
+
+# ------------------------------------------------------------------------------------------------ activations
+
+def quantize_q8_1_rows(x, out=None, stream=None):
+    """x [rows, cols] fp32 -> q8_1 blocks, rows * cols / 32 * 36 bytes (reference quantize_q8_1_rows)."""
+    rows, cols = x.shape
+    if out is None:
+        out = torch.empty(rows * cols // 32 * 36, dtype=torch.uint8, device=x.device)
+    _check(lib().xs_quantize_q8_1_rows(_p(x), rows, cols, _p(out), _stream(stream)))
+    return out
+
+
+# ------------------------------------------------------------------------------------------------ routing
+
+def router_top10(logits, k, ids=None, weights=None, stream=None):
+    """logits [T, E] fp32 -> (ids [T, k] int32, weights [T, k] fp32) (reference router_top10)."""
+    T, E = logits.shape
+    if ids is None:
+        ids = torch.empty(T, k, dtype=torch.int32, device=logits.device)
+    if weights is None:
+        weights = torch.empty(T, k, dtype=torch.float32, device=logits.device)
+    _check(lib().xs_router_top10(_p(logits), T, E, k, _p(ids), _p(weights), _stream(stream)))
+    return ids, weights
+
+
+def router_grouped_sigmoid(logits, bias, n_group, topk_group, k, routed_scale, stream=None):
+    T, E = logits.shape
+    ids = torch.empty(T, k, dtype=torch.int32, device=logits.device)
+    weights = torch.empty(T, k, dtype=torch.float32, device=logits.device)
+    _check(lib().xs_router_grouped_sigmoid(_p(logits), _p(bias), T, E, n_group, topk_group, k, float(routed_scale),
+                                           _p(ids), _p(weights), _stream(stream)))
+    return ids, weights
+
+
+def router_logits_f32(x, w, stream=None):
+    T, H = x.shape
+    E = w.shape[0]
+    logits = torch.empty(T, E, dtype=torch.float32, device=x.device)
+    _check(lib().xs_router_logits_f32(_p(x), _p(w), _p(logits), T, H, E, _stream(stream)))
+    return logits
+
+
+def plan_offsets(capx):
+    v = [ctypes.c_longlong() for _ in range(5)]
+    lib().xs_plan_offsets(capx, *[ctypes.byref(x) for x in v])
+    return dict(zip(("start", "dst", "tok", "ptr", "start2"), (x.value for x in v)))
+
+
+def plan_words(capx):
+    o = plan_offsets(capx)
+    return o["start2"] + capx + 2
+
+
+def resident_plan(ids, k, res, n_expert, cache_base, slot_off, blob, plan, capx, skip, ring, stream=None):
+    n = ids.numel()
+    _check(lib().xs_resident_plan(_p(ids), n, k, _p(res), n_expert, cache_base, _p(slot_off), blob, _p(plan), capx,
+                                  _p(skip), ring, _stream(stream)))
+
+
+def prefill_route(ids, k, n_expert, cache_base=None, blob=0, with_ptr=False, stream=None):
+    """ids [T*k] -> dict(src, slot, entry, bounds, experts, n_groups, grp_ptr) (reference plain_prompt.cpp:576-637)."""
+    n = ids.numel()
+    dev = ids.device
+    o = dict(src=torch.empty(n, dtype=torch.int32, device=dev), slot=torch.empty(n, dtype=torch.int32, device=dev),
+             entry=torch.empty(n, dtype=torch.int32, device=dev),
+             bounds=torch.empty(n_expert + 1, dtype=torch.int32, device=dev),
+             experts=torch.empty(n_expert, dtype=torch.int32, device=dev),
+             n_groups=torch.empty(1, dtype=torch.int32, device=dev),
+             grp_ptr=torch.empty(n_expert, dtype=torch.int64, device=dev) if with_ptr else None)
+    _check(lib().xs_prefill_route(_p(ids), n, k, n_expert, _p(o["src"]), _p(o["slot"]), _p(o["entry"]),
+                                  _p(o["bounds"]), _p(o["experts"]), _p(o["n_groups"]), cache_base, blob,
+                                  _p(o["grp_ptr"]), _stream(stream)))
+    return o
+
+
+# ------------------------------------------------------------------------------------------------ experts
+
+def native_expert_grouped(L, grp_ptr, grp_start, n_groups, ent_dst, ent_tok, cap_groups, cap_entries, x_q8_1, scratch,
+                          out, grid_groups=0, stream=None):
+    _check(lib().xs_native_expert_grouped(ctypes.byref(L), _p(grp_ptr), _p(grp_start), _p(n_groups), _p(ent_dst),
+                                          _p(ent_tok), cap_groups, cap_entries, _p(x_q8_1), _p(scratch), _p(out),
+                                          _stream(stream), grid_groups))
+
+
+def native_expert_gate_up(L, grp_ptr, grp_start, n_groups, ent_tok, cap_groups, cap_entries, x_q8_1, scratch,
+                          grid_groups=0, stream=None):
+    _check(lib().xs_native_expert_gate_up(ctypes.byref(L), _p(grp_ptr), _p(grp_start), _p(n_groups), _p(ent_tok),
+                                          cap_groups, cap_entries, _p(x_q8_1), _p(scratch), _stream(stream),
+                                          grid_groups))
+
+
+def native_expert_down(L, grp_ptr, grp_start, n_groups, ent_dst, cap_groups, cap_entries, scratch, out, grid_groups=0,
+                       stream=None):
+    _check(lib().xs_native_expert_down(ctypes.byref(L), _p(grp_ptr), _p(grp_start), _p(n_groups), _p(ent_dst),
+                                       cap_groups, cap_entries, _p(scratch), _p(out), _stream(stream), grid_groups))
+
+
+def native_expert_status(scratch, cap_entries, n_ff):
+    return lib().xs_native_expert_status(_p(scratch), cap_entries, n_ff)
+
+
+def moe_prefill_scratch_bytes(n_tok, rows, n_embd, n_ff):
+    return lib().xs_moe_prefill_scratch_bytes(n_tok, rows, n_embd, n_ff)
+
+
+def moe_prefill_experts(L, x, src, entry, bounds, n_groups, grp_ptr, cap_groups, rows, scratch, parts, stream=None):
+    _check(lib().xs_moe_prefill_experts(ctypes.byref(L), _p(x), x.shape[0], _p(src), _p(entry), _p(bounds),
+                                        _p(n_groups), _p(grp_ptr), cap_groups, rows, _p(scratch), _p(parts),
+                                        _stream(stream)))
+
+
+# ------------------------------------------------------------------------------------------------ combine
+
+def native_moe_combine_multi(parts, weights, shared, output, n_embd, k, n_tok, shared_gate=None, stream=None):
+    _check(lib().xs_native_moe_combine_multi(_p(parts), _p(weights), _p(shared), _p(output), n_embd, k, n_tok,
+                                             _stream(stream), _p(shared_gate)))
+
+
+def moe_combine_residual(parts, weights, residual, output, n_embd, k, n_tok, shared=None, shared_gate=None,
+                         stream=None):
+    _check(lib().xs_moe_combine_residual(_p(parts), _p(weights), _p(shared), _p(shared_gate), _p(residual),
+                                         _p(output), n_embd, k, n_tok, _stream(stream)))
+
+
+# ------------------------------------------------------------------------------------------------ whole layers
+
+class MoeLayer:
+    """One MoE layer whose experts live in one HBM arena (expert e's native blob at arena + e * blob_bytes), with its
+    workspace allocated once, so calls allocate nothing (graph-capturable)."""
+
+    def __init__(self, L, arena, n_expert, k, max_tokens, prefill=False, device="cuda"):
+        self.L, self.arena, self.n_expert, self.k, self.max_tokens = L, arena, n_expert, k, max_tokens
+        self.blob = L.bytes
+        self.prefill = prefill
+        fn = lib().xs_moe_layer_prefill_workspace_bytes if prefill else lib().xs_moe_layer_decode_workspace_bytes
+        self.ws_bytes = fn(ctypes.byref(L), n_expert, k, max_tokens)
+        self.ws = torch.empty(self.ws_bytes + 256, dtype=torch.uint8, device=device)
+        self.ws_ptr = (self.ws.data_ptr() + 255) & ~255
+
+    def __call__(self, x, logits, residual, out, n_tok=None, arena=None, stream=None):
+        n_tok = x.shape[0] if n_tok is None else n_tok
+        fn = lib().xs_moe_layer_prefill if self.prefill else lib().xs_moe_layer_decode
+        _check(fn(ctypes.byref(self.L), _p(self.arena if arena is None else arena), self.blob, self.n_expert, self.k,
+                  _p(x), _p(logits), _p(residual), _p(out), n_tok, self.ws_ptr, self.ws_bytes, _stream(stream)))
+        return out
+
+
+# ------------------------------------------------------------------------------------------------ synthetic experts
+
+def build_arena(n_expert, n_embd, n_ff, gu_type, d_type, seed=0, std=0.02, device="cuda", gen_device="cuda",
+                copies=1):
+    """Random fp32 N(0, std) expert weights quantized with this library's quantizer into the native in-place pack
+    layout: `copies` x n_expert blobs of [gate rows | up rows | down rows] back to back in one HBM arena (uint8
+    [copies * n_expert, blob]).  Weights are drawn with a torch generator seeded by `seed` on `gen_device` ("cpu"
+    gives the same bits everywhere); copy c > 0 repeats copy 0's bytes at other addresses (for rotating past the
+    caches in timing loops).  Returns (arena, layout)."""
+    L = native_expert_layout(gu_type, d_type, n_embd, n_ff)
+    blob = L.bytes
+    arena = torch.empty(copies * n_expert, blob, dtype=torch.uint8, device=device)
+    g = torch.Generator(device=gen_device)
+    g.manual_seed(seed)
+    for e in range(n_expert):
+        for off, rows, cols, t in ((0, n_ff, n_embd, gu_type), (L.up_off, n_ff, n_embd, gu_type),
+                                   (L.down_off, n_embd, n_ff, d_type)):
+            w = torch.randn(rows, cols, generator=g, device=gen_device, dtype=torch.float32) * std
+            w = w.to(device)
+            nbytes = rows * row_bytes(t, cols)
+            quantize_rows(t, w.reshape(-1), out=arena[e, off:off + nbytes])
+    for c in range(1, copies):
+        arena[c * n_expert:(c + 1) * n_expert].copy_(arena[:n_expert])
+    torch.cuda.synchronize()
+    return arena, L
