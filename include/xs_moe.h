@@ -5,7 +5,10 @@
  * replaces (paths relative to the reference repository, 32x-k/XeStrata-win).  Conventions, as the reference's:
  *   - every buffer is device memory owned by the caller; no entry point allocates device memory or synchronises,
  *     except where a NULL stream is allowed and documented to synchronise (the reference's `sync_if_needed`);
- *   - `stream` is a hipStream_t passed as void* (the reference's opaque `void* stream`);
+ *   - `stream` is a hipStream_t passed as void* (the reference's opaque `void* stream`).  NULL is HIP's ordered default
+ *     stream everywhere; the entry points the reference lets run on a null queue then also synchronise.  (The
+ *     reference's native router, combine and plan reject a null SYCL queue; the C++ wrappers in
+ *     xs_strata_kernels.hpp keep that rule for drop-in callers);
  *   - group and entry counts are read on the device, so one captured graph with capacity grids serves every routing;
  *   - blob addresses (expert weights) are 16-byte aligned; float spans 4-byte aligned; outputs do not overlap inputs.
  * Every function returns XS_OK (0) or an error code, with a message for the calling thread in xs_last_error().  The
@@ -149,7 +152,7 @@ int xs_moe_prefill_experts(const xs_expert_layout_t* L, const float* x, int64_t 
 size_t xs_moe_prefill_scratch_bytes(int64_t n_tok, int64_t rows, int64_t n_embd, int64_t n_ff);
 
 /* The weighted combine: output = fl(p0 w0) + fl(p1 w1) + ... in rank order, + shared (the shared row once; times
- * the sigmoid of shared_gate[t] when given).  k in 1..15, a non-NULL stream.  Replaces native_moe_combine and
+ * the sigmoid of shared_gate[t] when given).  k in 1..15.  Replaces native_moe_combine and
  * native_moe_combine_multi (include/strata/kernels/native_moe.hpp:22-25; src/kernels/xe/native_moe.cpp:36-58). */
 int xs_native_moe_combine(const float* parts, const float* weights, const float* shared, float* output,
                           int64_t n_embd, int64_t k, void* stream);

@@ -1,0 +1,150 @@
+// include/xs_strata_kernels.hpp - the reference engine's C++ MoE kernel surface (namespace strata::kernels) over the
+// C ABI of xs_moe.h, header-only: the same names, argument meanings and exceptions as the reference's headers, so the
+// engine's callers (src/core/moe_window.cpp:191-245, src/core/plain_model.cpp:955-988, src/core/verify.cpp:1160-1360,
+// src/prefill/plain_prompt.cpp:558-797) build against it unchanged.  A failing call throws
+// strata::core::DeviceError (a HIP error) or std::invalid_argument (geometry, alignment, overlap, a missing stream),
+// as the reference's entry points do.
+#pragma once
+
+#include "xs_moe.h"
+
+#include <cstddef>
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+namespace strata::core {
+struct DeviceError : std::runtime_error {   // the reference's include/strata/core/runtime.hpp error type
+    using std::runtime_error::runtime_error;
+};
+}  // namespace strata::core
+
+namespace strata::kernels {
+
+namespace detail {
+inline void check(int code) {
+    if (code == XS_OK) return;
+    if (code == XS_EINVAL) throw std::invalid_argument(xs_last_error());
+    throw core::DeviceError(xs_last_error());
+}
+}  // namespace detail
+
+/// include/strata/kernels/iq_kernels.hpp:66-75
+struct NativeExpertLayout {
+    int gu_type = -1, d_type = -1;
+    int up_type = -1;
+    int64_t n_embd = 0, n_ff = 0;
+    size_t gu_row = 0, d_row = 0;
+    size_t up_row = 0;
+    size_t up_off = 0, down_off = 0;
+    size_t bytes = 0;
+};
+
+namespace detail {
+inline xs_expert_layout_t to_c(const NativeExpertLayout& L) {
+    xs_expert_layout_t c;
+    c.gu_type = L.gu_type;
+    c.d_type = L.d_type;
+    c.up_type = L.up_type;
+    c.n_embd = L.n_embd;
+    c.n_ff = L.n_ff;
+    c.gu_row = L.gu_row;
+    c.d_row = L.d_row;
+    c.up_row = L.up_row;
+    c.up_off = L.up_off;
+    c.down_off = L.down_off;
+    c.bytes = L.bytes;
+    return c;
+}
+}  // namespace detail
+
+/// include/strata/kernels/iq_kernels.hpp:22
+inline size_t iq_row_bytes(int ggml_type, int64_t n) noexcept { return xs_iq_row_bytes(ggml_type, n); }
+
+/// include/strata/kernels/iq_kernels.hpp:79
+inline bool native_expert_supported(int gu, int d, int64_t n_embd, int64_t n_ff, int up = -1) noexcept {
+    return xs_native_expert_supported(gu, d, n_embd, n_ff, up) != 0;
+}
+
+/// include/strata/kernels/iq_kernels.hpp:81
+inline NativeExpertLayout native_expert_layout(int gu, int d, int64_t n_embd, int64_t n_ff, int up = -1) {
+    xs_expert_layout_t c;
+    detail::check(xs_native_expert_layout(gu, d, n_embd, n_ff, up, &c));
+    NativeExpertLayout L;
+    L.gu_type = c.gu_type;
+    L.d_type = c.d_type;
+    L.up_type = c.up_type;
+    L.n_embd = c.n_embd;
+    L.n_ff = c.n_ff;
+    L.gu_row = c.gu_row;
+    L.d_row = c.d_row;
+    L.up_row = c.up_row;
+    L.up_off = c.up_off;
+    L.down_off = c.down_off;
+    L.bytes = c.bytes;
+    return L;
+}
+
+/// include/strata/kernels/iq_kernels.hpp:83
+inline size_t native_expert_scratch_bytes(int64_t cap_entries, int64_t n_ff) {
+    return xs_native_expert_scratch_bytes(cap_entries, n_ff);
+}
+
+/// include/strata/kernels/iq_kernels.hpp:26
+inline void quantize_q8_1_rows(const float* x, int64_t n_rows, int64_t n_cols, void* y, void* stream) {
+    detail::check(xs_quantize_q8_1_rows(x, n_rows, n_cols, y, stream));
+}
+
+/// include/strata/kernels/iq_kernels.hpp:30
+inline void iq_dequant_f32(int ggml_type, const void* src, int64_t n, float* dst, void* stream) {
+    detail::check(xs_iq_dequant_f32(ggml_type, src, n, dst, stream));
+}
+
+/// include/strata/kernels/iq_kernels.hpp:90-93
+inline void native_expert_grouped(const NativeExpertLayout& L, const unsigned long long* grp_ptr,
+                                  const int32_t* grp_start, const int32_t* n_groups, const int32_t* ent_dst,
+                                  const int32_t* ent_tok, int64_t cap_groups, int64_t cap_entries, const void* x_q8_1,
+                                  void* scratch, float* out, void* stream, int64_t grid_groups = 0) {
+    const xs_expert_layout_t c = detail::to_c(L);
+    detail::check(xs_native_expert_grouped(&c, grp_ptr, grp_start, n_groups, ent_dst, ent_tok, cap_groups, cap_entries,
+                                           x_q8_1, scratch, out, stream, grid_groups));
+}
+
+/// include/strata/kernels/router_top10.hpp:20-21 (a null stream synchronises)
+inline void router_top10(const float* logits, int n_tokens, int n_expert, int k, int* ids, float* weights,
+                         void* stream) {
+    detail::check(xs_router_top10(logits, n_tokens, n_expert, k, ids, weights, stream));
+}
+
+/// include/strata/kernels/verify_kernels.hpp:81-83 (the reference's native kernels require an explicit queue)
+inline void resident_plan(const int32_t* ids, int n_entries, int k, const int32_t* res_layer, int n_expert,
+                          const uint8_t* cache_base, const unsigned long long* slot_off, long long blob, int32_t* plan,
+                          long long capx, uint32_t* skip, uint32_t ring, void* stream) {
+    if (!stream) throw std::invalid_argument("resident_plan requires an explicit stream");
+    if (!res_layer) throw std::invalid_argument("resident_plan requires the layer's residency table");
+    detail::check(xs_resident_plan(ids, n_entries, k, res_layer, n_expert, cache_base, slot_off, blob, plan, capx, skip,
+                                   ring, stream));
+}
+
+/// include/strata/kernels/native_moe.hpp:22-23
+inline void native_moe_combine(const float* parts, const float* weights, const float* shared, float* output,
+                               int64_t n_embd, int64_t k, void* stream) {
+    if (!stream) throw std::invalid_argument("native MoE combine requires a stream, positive width and 1..15 experts");
+    detail::check(xs_native_moe_combine(parts, weights, shared, output, n_embd, k, stream));
+}
+
+/// include/strata/kernels/native_moe.hpp:24-25
+inline void native_moe_combine_multi(const float* parts, const float* weights, const float* shared, float* output,
+                                     int64_t n_embd, int64_t k, int n_tok, void* stream,
+                                     const float* shared_gate = nullptr) {
+    if (!stream)
+        throw std::invalid_argument("native MoE combine (multi) requires a stream, width, 1..15 experts, tokens");
+    detail::check(xs_native_moe_combine_multi(parts, weights, shared, output, n_embd, k, n_tok, stream, shared_gate));
+}
+
+/// src/core/plain_model.cpp:987 (add_inplace)
+inline void add_inplace(float* x, const float* y, int64_t n, void* stream) {
+    detail::check(xs_add_inplace(x, y, n, stream));
+}
+
+}  // namespace strata::kernels

@@ -73,9 +73,6 @@ def test_argument_errors(xm):
     # k past 64, checked before any launch (router.cpp:294)
     assert lib.xs_router_top10(8, 1, 128, 65, 8, 8, None) == xm.XS_EINVAL
     assert b"exceeds the kernel's 64" in lib.xs_last_error()
-    # the combine requires a stream (native_moe.cpp:116)
-    assert lib.xs_native_moe_combine_multi(8, 8, None, 8, 2048, 8, 1, None, None) == xm.XS_EINVAL
-    assert b"requires a stream" in lib.xs_last_error()
     # the combine's k range is 1..15
     assert lib.xs_native_moe_combine_multi(8, 8, None, 8, 2048, 16, 1, 8, None) == xm.XS_EINVAL
     # an unsupported layout

@@ -278,7 +278,6 @@ int xs_resident_plan(const int32_t* ids, int n_entries, int k, const int32_t* re
     if (!aligned(ids, 4) || !aligned(plan, 8) || !aligned(skip, 4) || (res_layer && !aligned(res_layer, 4)) ||
         (slot_off && !aligned(slot_off, 8)))
         return fail(XS_EINVAL, "resident_plan: a span is missing or misaligned");
-    if (!stream) return fail(XS_EINVAL, "resident_plan requires an explicit stream");
     return finish(stream, xs::launch_resident_plan(ids, n_entries, k, res_layer, n_expert, cache_base, slot_off, blob,
                                                    plan, capx, skip, ring, S(stream)),
                   "resident_plan");
@@ -293,7 +292,6 @@ int xs_prefill_route(const int32_t* ids, int64_t n_entries, int k, int n_expert,
     if (!aligned(ids, 4) || !aligned(src, 4) || !aligned(slot, 4) || !aligned(entry_of, 4) || !aligned(bounds, 4) ||
         !aligned(experts, 4) || !aligned(n_groups, 4) || (grp_ptr && !aligned(grp_ptr, 8)))
         return fail(XS_EINVAL, "prefill_route: a span is missing or misaligned");
-    if (!stream) return fail(XS_EINVAL, "prefill_route requires an explicit stream");
     return finish(stream, xs::launch_prefill_route(ids, n_entries, k, n_expert, src, slot, entry_of, bounds, experts,
                                                    n_groups, cache_base, blob, grp_ptr, S(stream)),
                   "prefill_route");
@@ -319,7 +317,6 @@ int xs_moe_prefill_experts(const xs_expert_layout_t* L, const float* x, int64_t 
     if (cap_groups > 65535 || !aligned(x, 4) || !aligned(src, 4) || !aligned(entry_of, 4) || !aligned(bounds, 4) ||
         !aligned(n_groups, 4) || !aligned(grp_ptr, 8) || !aligned(scratch, 256) || !aligned(parts, 4))
         return fail(XS_EINVAL, "moe_prefill_experts: a span is missing or misaligned");
-    if (!stream) return fail(XS_EINVAL, "moe_prefill_experts requires an explicit stream");
     xs::PrefillArgs a;
     a.x = x;
     a.src = src;
@@ -340,8 +337,8 @@ int xs_moe_prefill_experts(const xs_expert_layout_t* L, const float* x, int64_t 
 
 int xs_native_moe_combine_multi(const float* parts, const float* weights, const float* shared, float* output,
                                 int64_t n_embd, int64_t k, int n_tok, void* stream, const float* shared_gate) {
-    if (!stream || n_embd <= 0 || k < 1 || k > 15 || n_tok < 1 || (shared_gate && !shared))
-        return fail(XS_EINVAL, "native MoE combine (multi) requires a stream, width, 1..15 experts, tokens");
+    if (n_embd <= 0 || k < 1 || k > 15 || n_tok < 1 || (shared_gate && !shared))
+        return fail(XS_EINVAL, "native MoE combine (multi) requires a width, 1..15 experts, tokens");
     if (!aligned(parts, 4) || !aligned(weights, 4) || !aligned(output, 4) || (shared && !aligned(shared, 4)))
         return fail(XS_EINVAL, "native MoE combine requires aligned spans");
     const size_t ob = (size_t)n_tok * n_embd * 4;
@@ -355,15 +352,15 @@ int xs_native_moe_combine_multi(const float* parts, const float* weights, const 
 
 int xs_native_moe_combine(const float* parts, const float* weights, const float* shared, float* output,
                           int64_t n_embd, int64_t k, void* stream) {
-    if (!stream || n_embd <= 0 || n_embd > 0x7fffffff || k < 1 || k > 15)
-        return fail(XS_EINVAL, "native MoE combine requires a stream, positive width and 1..15 experts");
+    if (n_embd <= 0 || n_embd > 0x7fffffff || k < 1 || k > 15)
+        return fail(XS_EINVAL, "native MoE combine requires a positive width and 1..15 experts");
     return xs_native_moe_combine_multi(parts, weights, shared, output, n_embd, k, 1, stream, nullptr);
 }
 
 int xs_moe_combine_residual(const float* parts, const float* weights, const float* shared, const float* shared_gate,
                             const float* residual, float* output, int64_t n_embd, int64_t k, int n_tok, void* stream) {
-    if (!stream || n_embd <= 0 || k < 1 || k > 64 || n_tok < 1 || (shared_gate && !shared))
-        return fail(XS_EINVAL, "moe_combine_residual requires a stream, width, 1..64 experts, tokens");
+    if (n_embd <= 0 || k < 1 || k > 64 || n_tok < 1 || (shared_gate && !shared))
+        return fail(XS_EINVAL, "moe_combine_residual requires a width, 1..64 experts, tokens");
     if (!aligned(parts, 4) || !aligned(weights, 4) || !aligned(output, 4) || !aligned(residual, 4))
         return fail(XS_EINVAL, "moe_combine_residual requires aligned spans");
     const size_t ob = (size_t)n_tok * n_embd * 4;
@@ -450,7 +447,6 @@ int xs_moe_layer_decode(const xs_expert_layout_t* L, const uint8_t* arena, size_
                         void* workspace, size_t workspace_bytes, void* stream) {
     if (n_tok <= 0) return ok();
     if (int r = check_layout(L, "moe_layer_decode")) return r;
-    if (!stream) return fail(XS_EINVAL, "moe_layer_decode requires an explicit stream");
     if (n_tok * k > 1024) return fail(XS_EINVAL, "moe_layer_decode: %d tokens x top-%d is past 1024 entries", n_tok, k);
     if (blob_bytes < L->bytes || blob_bytes % 16 || !aligned(arena, 16))
         return fail(XS_EINVAL, "moe_layer_decode: the arena must hold 16-byte aligned blobs of at least %zu bytes", L->bytes);
@@ -485,7 +481,6 @@ int xs_moe_layer_prefill(const xs_expert_layout_t* L, const uint8_t* arena, size
                          void* workspace, size_t workspace_bytes, void* stream) {
     if (n_tok <= 0) return ok();
     if (int r = check_layout(L, "moe_layer_prefill")) return r;
-    if (!stream) return fail(XS_EINVAL, "moe_layer_prefill requires an explicit stream");
     if (blob_bytes < L->bytes || blob_bytes % 16 || !aligned(arena, 16))
         return fail(XS_EINVAL, "moe_layer_prefill: the arena must hold 16-byte aligned blobs of at least %zu bytes", L->bytes);
     if (!aligned(workspace, 256) || workspace_bytes < xs_moe_layer_prefill_workspace_bytes(L, n_expert, k, n_tok))
