@@ -368,9 +368,10 @@ static void iq4xs_parts(const uint8_t* blk, const uint8_t* xb, int sb, float* c,
     *c = h2f(blk) * q8d(b8);
 }
 
-/* one row: the calls in order; IQ4_XS against an activation with one scale a 256 (s256, the gate/up rows) adds its
- * block's 8 integer sums first and takes one fma (seg_dot_canon, iq_kernels.cpp:832-884); elsewhere the plain loop */
-float xso_vec_dot(int type, const uint8_t* row, const uint8_t* xq, int64_t n, int s256) {
+/* one row with the reference's per-call float expressions, calls in order (a cross-check of the canonical order below:
+ * the same exact products, summed in another order); IQ4_XS against a 256-scale activation adds its block's 8 integer
+ * sums first and takes one fma (seg_dot_canon, iq_kernels.cpp:832-884) */
+float xso_vec_dot_calls(int type, const uint8_t* row, const uint8_t* xq, int64_t n, int s256) {
     const int qk = xso_block_values(type), bs = block_bytes(type);
     float s = 0.0f;
     for (int64_t kb = 0; kb < n / qk; ++kb) {
@@ -410,6 +411,106 @@ float xso_vec_dot(int type, const uint8_t* row, const uint8_t* xq, int64_t n, in
         }
     }
     return s;
+}
+
+/* ---- the canonical row order (the order of the HIP kernels, so device and host agree bit for bit)
+ *
+ * The reference fixes one float order for the i-quant rows it keeps bitwise between its devices (seg_dot_canon,
+ * src/kernels/xe/iq_kernels.cpp:832-884; include/strata/kernels/canon_math.hpp): the exact integer sums of the calls
+ * that share one activation scale first, then one written-out fma a group, lane-strided, then a butterfly.  The
+ * canonical order here extends that to every format:
+ *   unit   = the values that share one weight scale set and one activation scale: a whole 256-value block when the
+ *            activation has one scale for each 256 (the gate/up rows: quantize_q8_1_rows), else 32 values (the down
+ *            rows, and Q8_0 blocks);
+ *   term   = its exact integer sums S (codes times int8 activations, scales applied in integers), then
+ *            acc = fma(d * d8, (float) S, acc)  [Q4_K also acc = fma(-(dmin * d8), (float) Smin, acc)];
+ *   row    = L = min(8, largest power of two dividing the unit count) lanes; lane c adds units c, c + L, ... in order;
+ *            then a butterfly: acc[c] += acc[c ^ o] for o = L/2 .. 1; the row is lane 0's value. */
+static int act(const uint8_t* xq, int64_t i) { return (int)(int8_t)xq[36 * (i / 32) + 4 + i % 32]; }
+static float actd(const uint8_t* xq, int64_t g) { return h2f(xq + 36 * g); }
+
+static int q4k_code(const uint8_t* blk, int v) { return (blk[16 + 32 * (v / 64) + v % 32] >> (4 * ((v / 32) % 2))) & 15; }
+static int q6k_code(const uint8_t* blk, int v) {
+    const int n = v / 128, s = (v % 128) / 32, l = v % 32;
+    return (((blk[64 * n + 32 * (s & 1) + l] >> (4 * (s >> 1))) & 15) | (((blk[128 + 32 * n + l] >> (2 * s)) & 3) << 4)) - 32;
+}
+static int iq4xs_ls(const uint8_t* blk, int sb) {
+    const unsigned scales_h = (unsigned)(blk[2] | (blk[3] << 8));
+    return (((blk[4 + sb / 2] >> (4 * (sb % 2))) & 0x0F) | (((scales_h >> (2 * sb)) & 3) << 4)) - 32;
+}
+static int iq4xs_code(const uint8_t* blk, int v) {
+    const uint8_t q = blk[8 + 16 * (v / 32) + v % 16];
+    return kIq4nl[(v % 32) < 16 ? (q & 0x0F) : (q >> 4)];
+}
+
+/* unit u of a row against xq (q8_1 of the row's n values); s256: one activation scale a 256 */
+static float canon_unit(int type, const uint8_t* row, int64_t u, const uint8_t* xq, int s256, float acc) {
+    if (type == XSO_Q8_0) {
+        const uint8_t* blk = row + 34 * u;
+        int s = 0;
+        for (int i = 0; i < 32; ++i) s += (int)(int8_t)blk[2 + i] * act(xq, 32 * u + i);
+        return fmaf(h2f(blk) * actd(xq, u), (float)s, acc);
+    }
+    const int bs = block_bytes(type);
+    const int64_t b = s256 ? u : u / 8;                    /* the block */
+    const int g0 = s256 ? 0 : (int)(u % 8), g1 = s256 ? 8 : g0 + 1;   /* its 32-value groups in this unit */
+    const uint8_t* blk = row + b * bs;
+    const int64_t v0 = 256 * b;
+    const float d8 = actd(xq, 8 * b + g0);
+    if (type == XSO_Q4_K) {
+        int s1 = 0, s2 = 0;
+        for (int g = g0; g < g1; ++g) {
+            int sc, m, is = 0, us = 0;
+            q4k_scale_min(g, blk + 4, &sc, &m);
+            for (int l = 0; l < 32; ++l) {
+                const int a = act(xq, v0 + 32 * g + l);
+                is += q4k_code(blk, 32 * g + l) * a;
+                us += a;
+            }
+            s1 += sc * is;
+            s2 += m * us;
+        }
+        acc = fmaf(h2f(blk) * d8, (float)s1, acc);
+        return fmaf(-(h2f(blk + 2) * d8), (float)s2, acc);
+    }
+    if (type == XSO_Q6_K) {
+        int s = 0;
+        for (int j = 2 * g0; j < 2 * g1; ++j) {             /* 16-value sub-blocks */
+            int is = 0;
+            for (int l = 0; l < 16; ++l) is += q6k_code(blk, 16 * j + l) * act(xq, v0 + 16 * j + l);
+            s += (int)(int8_t)blk[192 + j] * is;
+        }
+        return fmaf(h2f(blk + 208) * d8, (float)s, acc);
+    }
+    /* IQ4_XS */
+    int s = 0;
+    for (int g = g0; g < g1; ++g) {
+        int is = 0;
+        for (int l = 0; l < 32; ++l) is += iq4xs_code(blk, 32 * g + l) * act(xq, v0 + 32 * g + l);
+        s += iq4xs_ls(blk, g) * is;
+    }
+    return fmaf(h2f(blk) * d8, (float)s, acc);
+}
+
+int xso_canon_lanes(int64_t units) {
+    int l = 8;
+    while (l > 1 && units % l) l >>= 1;
+    return l;
+}
+
+float xso_vec_dot(int type, const uint8_t* row, const uint8_t* xq, int64_t n, int s256) {
+    const int su = (type != XSO_Q8_0) && s256;
+    const int64_t units = su ? n / 256 : n / 32;
+    const int L = xso_canon_lanes(units);
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int c = 0; c < L; ++c)
+        for (int64_t u = c; u < units; u += L) acc[c] = canon_unit(type, row, u, xq, su, acc[c]);
+    for (int o = L / 2; o > 0; o >>= 1) {
+        float b[8];
+        for (int c = 0; c < L; ++c) b[c] = acc[c] + acc[c ^ o];
+        memcpy(acc, b, sizeof b);
+    }
+    return acc[0];
 }
 
 /* ------------------------------------------------------------------------------------------------ experts */

@@ -44,8 +44,12 @@ void xso_canon_rcp_n(const float* x, int64_t n, float* y);
 void xso_quantize_q8_1_rows(const float* x, int64_t n_rows, int64_t n_cols, uint8_t* y);
 void xso_quantize_q8_1_per32(const float* x, int64_t n, uint8_t* y);
 
-/* ---- one row of quantized weights against one q8_1 activation row (iq_kernels.cpp:398-721) */
+/* ---- one row of quantized weights against one q8_1 activation row (iq_kernels.cpp:398-721): xso_vec_dot in the
+ * canonical order the HIP kernels take (integer-first units, lane-strided, butterfly; see xs_oracle.c), and
+ * xso_vec_dot_calls with the reference's per-call float expressions in call order (a cross-check). */
 float xso_vec_dot(int type, const uint8_t* row, const uint8_t* xq, int64_t n, int s256);
+float xso_vec_dot_calls(int type, const uint8_t* row, const uint8_t* xq, int64_t n, int s256);
+int xso_canon_lanes(int64_t units);
 
 /* ---- the native expert blob: [gate rows | up rows | down rows] (iq_kernels.cpp:2021-2036) */
 typedef struct {

@@ -45,6 +45,8 @@ def lib():
         L.xso_row_bytes.restype = I64
         L.xso_vec_dot.restype = F
         L.xso_vec_dot.argtypes = [I, P, P, I64, I]
+        L.xso_vec_dot_calls.restype = F
+        L.xso_vec_dot_calls.argtypes = [I, P, P, I64, I]
         L.xso_canon_rcp.restype = F
         L.xso_canon_rcp.argtypes = [F]
         L.xso_canon_exp.restype = F
@@ -146,10 +148,11 @@ def q8_1_values(y):
     return q, d, s
 
 
-def vec_dot(t, row, xq, n, s256):
+def vec_dot(t, row, xq, n, s256, calls=False):
     row = np.ascontiguousarray(row, np.uint8)
     xq = np.ascontiguousarray(xq, np.uint8)
-    return lib().xso_vec_dot(t, _a(row), _a(xq), n, int(s256))
+    fn = lib().xso_vec_dot_calls if calls else lib().xso_vec_dot
+    return fn(t, _a(row), _a(xq), n, int(s256))
 
 
 def layout(gu, d, n_embd, n_ff):

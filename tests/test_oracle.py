@@ -293,9 +293,10 @@ def test_vec_dot_exact_operands(xo, t, n, s256):
     a = q.astype(np.float64) * d[:, None].astype(np.float64)
     wv = xo.dequant(t, row, n).astype(np.float64)
     exact = float(np.dot(wv, a.ravel()))
-    got = xo.vec_dot(t, row, xq, n, s256)
     scale = float(np.sum(np.abs(wv * a.ravel())))
-    assert abs(got - exact) <= 1e-5 * scale
+    for calls in (False, True):    # the canonical order and the reference's per-call expressions
+        got = xo.vec_dot(t, row, xq, n, s256, calls=calls)
+        assert abs(got - exact) <= 1e-5 * scale
 
 
 # ------------------------------------------------------------------------------------------------ experts

@@ -161,7 +161,26 @@ int grouped_args(const xs_expert_layout_t* L, const unsigned long long* grp_ptr,
     a->err = xs_native_expert_status(scratch, cap_entries, L->n_ff);
     a->cap_groups = cap_groups;
     a->grid_groups = grid_groups;
+    a->max_entries = 0;
     return ok();
+}
+
+// max_entries: the most entries one group can hold (the call's token count), 0 when not known
+int grouped_impl(const xs_expert_layout_t* L, const unsigned long long* grp_ptr, const int32_t* grp_start,
+                 const int32_t* n_groups, const int32_t* ent_dst, const int32_t* ent_tok, int64_t cap_groups,
+                 int64_t cap_entries, const void* x_q8_1, void* scratch, float* out, void* stream, int64_t grid_groups,
+                 int max_entries) {
+    if (cap_groups <= 0 || cap_entries <= 0) return ok();
+    if (!ent_dst || !ent_tok || !x_q8_1 || !out) return fail(XS_EINVAL, "native_expert_grouped: a span is missing");
+    xs::GroupedArgs a;
+    if (int r = grouped_args(L, grp_ptr, grp_start, n_groups, ent_dst, ent_tok, cap_groups, cap_entries, x_q8_1,
+                             scratch, out, grid_groups, "native_expert_grouped", &a))
+        return r;
+    a.max_entries = max_entries;
+    const xs::ExpertLayout XL = to_layout(L);
+    hipError_t e = xs::launch_native_gu(XL, a, S(stream));
+    if (e == hipSuccess) e = xs::launch_native_down(XL, a, S(stream));
+    return finish(stream, e, "native_expert_grouped");
 }
 }  // namespace
 
@@ -169,16 +188,8 @@ int xs_native_expert_grouped(const xs_expert_layout_t* L, const unsigned long lo
                              const int32_t* grp_start, const int32_t* n_groups, const int32_t* ent_dst,
                              const int32_t* ent_tok, int64_t cap_groups, int64_t cap_entries, const void* x_q8_1,
                              void* scratch, float* out, void* stream, int64_t grid_groups) {
-    if (cap_groups <= 0 || cap_entries <= 0) return ok();
-    if (!ent_dst || !ent_tok || !x_q8_1 || !out) return fail(XS_EINVAL, "native_expert_grouped: a span is missing");
-    xs::GroupedArgs a;
-    if (int r = grouped_args(L, grp_ptr, grp_start, n_groups, ent_dst, ent_tok, cap_groups, cap_entries, x_q8_1,
-                             scratch, out, grid_groups, "native_expert_grouped", &a))
-        return r;
-    const xs::ExpertLayout XL = to_layout(L);
-    hipError_t e = xs::launch_native_gu(XL, a, S(stream));
-    if (e == hipSuccess) e = xs::launch_native_down(XL, a, S(stream));
-    return finish(stream, e, "native_expert_grouped");
+    return grouped_impl(L, grp_ptr, grp_start, n_groups, ent_dst, ent_tok, cap_groups, cap_entries, x_q8_1, scratch,
+                        out, stream, grid_groups, 0);
 }
 
 int xs_native_expert_gate_up(const xs_expert_layout_t* L, const unsigned long long* grp_ptr, const int32_t* grp_start,
@@ -454,20 +465,19 @@ int xs_moe_layer_decode(const xs_expert_layout_t* L, const uint8_t* arena, size_
         return fail(XS_EINVAL, "moe_layer_decode: workspace missing, misaligned or short");
     const DecodeWs w = decode_ws(L, k, n_tok, (uint8_t*)workspace);
     const long long capx = (long long)n_tok * k;
-    const hipStream_t s = S(stream);
-    if (int r = xs_router_top10(logits, n_tok, n_expert, k, w.ids, w.w, stream)) return r;
-    if (int r = xs_resident_plan(w.ids, (int)capx, k, nullptr, n_expert, arena, nullptr, (long long)blob_bytes, w.plan,
-                                 capx, w.skip, 1u, stream))
-        return r;
-    if (int r = xs_quantize_q8_1_rows(x, n_tok, L->n_embd, w.xq, stream)) return r;
+    if (n_expert > 1024 || k > 64 || k > n_expert)
+        return fail(XS_EINVAL, "moe_layer_decode: %d experts, top-%d (the router takes up to 1024 and 64)", n_expert, k);
+    if (!aligned(logits, 4) || !aligned(x, 4)) return fail(XS_EINVAL, "moe_layer_decode: a span is missing or misaligned");
+    // routing, plan and activations in one launch (the reference's router_top10 + resident_plan + quantize_q8_1_rows)
+    hipError_t e = xs::launch_decode_route(logits, x, n_tok, n_expert, k, L->n_embd, w.ids, w.w, w.plan, capx, w.skip,
+                                           arena, (long long)blob_bytes, w.xq, S(stream));
+    if (e != hipSuccess) return hip_status(e, "moe_layer_decode");
     const int64_t cap_groups = capx < n_expert ? capx : n_expert;
     long long o_start, o_dst, o_tok, o_ptr;
     xs_plan_offsets(capx, &o_start, &o_dst, &o_tok, &o_ptr, nullptr);
-    if (int r = xs_native_expert_grouped(L, (const unsigned long long*)(w.plan + o_ptr), w.plan + o_start, w.plan,
-                                         w.plan + o_dst, w.plan + o_tok, cap_groups, capx, w.xq, w.scratch, w.parts,
-                                         stream, 0))
+    if (int r = grouped_impl(L, (const unsigned long long*)(w.plan + o_ptr), w.plan + o_start, w.plan, w.plan + o_dst,
+                             w.plan + o_tok, cap_groups, capx, w.xq, w.scratch, w.parts, stream, 0, n_tok))
         return r;
-    (void)s;
     return xs_moe_combine_residual(w.parts, w.w, nullptr, nullptr, residual, out, L->n_embd, k, n_tok, stream);
 }
 

@@ -13,39 +13,11 @@
 //    exactly.
 #include "xs_device.h"
 #include "xs_kernels.h"
+#include "xs_route.h"
 
 namespace xs {
 
 constexpr int kPlanThreads = 1024;
-
-// exclusive scan of v over the work-group (blockDim.x threads, a multiple of 64); *total gets the sum
-__device__ int block_exclusive_scan(int v, int* s_wave, int* total) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    int inc = v;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int y = __shfl_up(inc, o, 64);
-        if (lane >= o) inc += y;
-    }
-    if (lane == 63) s_wave[wave] = inc;
-    __syncthreads();
-    if (wave == 0) {
-        const int w = lane < nw ? s_wave[lane] : 0;
-        int wi = w;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int y = __shfl_up(wi, o, 64);
-            if (lane >= o) wi += y;
-        }
-        if (lane < nw) s_wave[lane] = wi - w;   // exclusive over waves
-        if (lane == nw - 1) s_wave[63] = wi;    // total (nw <= 16 leaves slot 63 free)
-    }
-    __syncthreads();
-    const int r = s_wave[wave] + inc - v;
-    *total = s_wave[63];
-    __syncthreads();
-    return r;
-}
 
 __global__ __launch_bounds__(kPlanThreads) void resident_plan_kernel(const int32_t* __restrict__ ids, int n, int k,
                                                                      const int32_t* __restrict__ res, int n_expert,
@@ -59,61 +31,16 @@ __global__ __launch_bounds__(kPlanThreads) void resident_plan_kernel(const int32
     __shared__ int s_wave[64];
     const int t = threadIdx.x;
     bool bad = false;
-    int ex = -1;
     if (t < n) {
-        ex = ids[t];
+        const int ex = ids[t];
         s_ids[t] = ex;
         bad = ex < 0 || ex >= n_expert || (res && res[ex] < 0);
     }
-    for (int e = t; e < n_expert; e += blockDim.x) s_first[e] = n;
     if (__syncthreads_or(bad)) {   // a routed expert that is not resident: the plan is left alone
         if (t == 0) *skip = 0u;
         return;
     }
-    if (t < n) atomicMin(&s_first[ex], t);
-    __syncthreads();
-    int cnt = 0, pos = 0;
-    const bool leader = t < n && s_first[ex] == t;
-    if (t < n) {
-        for (int j = 0; j < n; ++j) {
-            if (s_ids[j] != ex) continue;
-            if (leader) ++cnt;
-            if (j < t) ++pos;
-        }
-    }
-    int total;
-    const int pack = leader ? ((cnt << 16) | 1) : 0;
-    const int excl = block_exclusive_scan(pack, s_wave, &total);
-    s_excl[t] = excl;
-    __syncthreads();
-    int32_t* counts = pl;
-    int32_t* start = pl + 4;
-    int32_t* dst = start + capx + 1;
-    int32_t* tok = dst + capx;
-    const long long ptr_off = ((4 + (capx + 1) + 2 * capx) + 1) & ~1ll;
-    unsigned long long* ptr = (unsigned long long*)(pl + ptr_off);
-    int32_t* start2 = pl + ptr_off + 4 * capx;
-    if (t < n) {
-        const int le = s_excl[s_first[ex]];
-        const int g = le & 0xffff, gstart = le >> 16;
-        dst[gstart + pos] = t;
-        tok[gstart + pos] = t / k;
-        if (leader) {
-            const int32_t slot = res ? res[ex] : ex;
-            ptr[g] = (unsigned long long)(uintptr_t)(cache_base + (slot_off ? (size_t)slot_off[slot] : (size_t)slot * (size_t)blob));
-            start[g] = gstart;
-        }
-    }
-    __syncthreads();
-    if (t != 0) return;
-    const int groups = total & 0xffff;
-    start[groups] = n;
-    start2[0] = n;
-    counts[0] = groups;
-    counts[1] = n;
-    counts[2] = 0;
-    __threadfence();
-    *skip = ring;
+    build_plan(s_ids, s_first, s_excl, s_wave, n, k, res, n_expert, cache_base, slot_off, blob, pl, capx, skip, ring);
 }
 
 constexpr int kRouteWaves = 16;

@@ -2,30 +2,40 @@
 // the MI355X form of the reference's native_expert_grouped (src/kernels/xe/iq_kernels.cpp:2042-2178; gate/up rows
 // :997-1031, the SwiGLU + q8_1 pass :2118-2133, down rows :1033-1063).
 //
-// Work split.  A work-group (4 waves) owns a slab of consecutive weight rows of one group's expert: gate and up rows
-// are one matrix of 2 n_ff rows (the blob stores them back to back), down rows another of n_embd rows.  The slab is
-// copied to LDS with 16-byte coalesced loads (the whole slab in flight at once), so the raw GGUF blocks are read from
-// HBM exactly once whatever their alignment (Q6_K and Q8_0 blocks sit at 2-byte boundaries).  The group's entries
-// (tokens routed to the expert) are applied to the staged rows kNE at a time, so each row is fetched once however
-// many entries the group has.
+// Work split.  A work-group (2 waves) owns a slab of consecutive weight rows of one group's expert: the gate and up
+// rows are one matrix of 2 n_ff rows (the blob stores them back to back), the down rows another of n_embd rows.  The
+// slab is fetched with 16-byte coalesced loads, all of a thread's loads in flight at once together with the group's
+// indices and activations, and parked in LDS, so the raw GGUF blocks are read from HBM once whatever their alignment
+// (Q6_K and Q8_0 blocks sit at 2-byte boundaries).  The group's entries (the tokens routed to the expert) are applied
+// to the staged rows kNE at a time.
 //
-// Inside a slab a row is a run of 32-value units; LPR lanes share a row (LPR divides the unit count), each taking
-// every LPR-th unit.  A unit's integer products are exact (v_dot4_i32_i8 against the q8_1 activation), its scales
-// are applied in fp32, and the LPR lanes reduce their partial sums with a xor butterfly.
+// Arithmetic: the canonical row order (shared bit for bit with the CPU oracle).  A row is a run of units: a whole
+// 256-value block when the activation has one scale for each 256 values (gate/up: quantize_q8_1_rows), else a
+// 32-value group (down, and Q8_0).  A unit's products are exact integers (v_dot4_i32_i8 of the codes against the q8_1
+// int8 values, the sub-block scales applied in integers); its scale enters once, acc = fma(d * d8, S, acc) (Q4_K's
+// min term a second fma) - the reference's integer-first canonical rows (seg_dot_canon, iq_kernels.cpp:832-884)
+// applied to every format.  L = min(8, the largest power of two dividing the unit count) lanes share a row, lane c
+// taking units c, c + L, ..., then a xor butterfly over the L lanes.
 //
-// Activations are q8_1 rows: for gate/up the caller's x_q8_1 (one scale per 256 values), for down the SwiGLU of the
-// gate/up results quantized per 32 values, both with the reference's canonical arithmetic.  The down kernel forms
-// that activation itself from the gate/up scratch (the reference's separate SwiGLU pass folded into its prologue);
-// the q8_1 rows it builds are also written to scratch (hq), as the reference's pass leaves them.
+// Activations: gate/up reads the caller's q8_1 rows; down forms its own from the gate/up scratch, h = SwiGLU(gate,
+// up) quantized per 32 values, both with the reference's canonical arithmetic (the reference's separate SwiGLU pass
+// folded into the down kernel's prologue); the q8_1 rows it builds are also written to scratch (hq).
 #include "xs_device.h"
 #include "xs_kernels.h"
 
 namespace xs {
 
-constexpr int kNE = 4;         // entries a pass over the staged rows (the reference's kEntriesPass)
-constexpr int kThreads = 256;
+constexpr int kNE = 4;          // the most entries a pass over the staged rows (the reference's kEntriesPass)
+constexpr int kThreads = 128;   // two waves a work-group
+constexpr int kSlabRegs = 10;   // 16-byte slab chunks a thread holds in flight
 
 __constant__ uint32_t kIq4Tab[4] = {0xBFAD9881u, 0xF6EADDCFu, 0x26190D01u, 0x71594535u};   // kvalues_iq4nl bytes
+
+struct Act {            // one entry's activation in LDS
+    const int8_t* q;    // n int8 values
+    const float* d8;    // n / 32 scales (the q8_1 blocks' fp16 d, as float)
+    const int* us16;    // n / 16 sums of 16 int8 values
+};
 
 __device__ __forceinline__ int byte_at(uint32_t s0, uint32_t s1, uint32_t s2, int k) {
     const uint32_t w = k < 4 ? s0 : k < 8 ? s1 : s2;
@@ -43,225 +53,289 @@ __device__ __forceinline__ void q4k_sm(uint32_t s0, uint32_t s1, uint32_t s2, in
     }
 }
 
-__device__ __forceinline__ float lds_h(const uint8_t* p) { return h2f(*(const uint16_t*)p); }
+// NW words at a 2-byte aligned byte offset `off` of a 16-byte aligned LDS buffer: aligned 32-bit reads, realigned
+// with v_alignbyte (the offset, not the address, gives the alignment: LDS pointers are not cast to integers)
+template <int NW>
+__device__ __forceinline__ void lds_words_a2(const uint8_t* base, int off, uint32_t (&w)[NW]) {
+    const uint32_t* q = (const uint32_t*)(base + (off & ~3));
+    const uint32_t sh = (uint32_t)(off & 3);
+    uint32_t d[NW + 1];
+#pragma unroll
+    for (int i = 0; i <= NW; ++i) d[i] = q[i];
+#pragma unroll
+    for (int i = 0; i < NW; ++i) w[i] = __builtin_amdgcn_alignbyte(d[i + 1], d[i], sh);
+}
 
-template <int T>
+__device__ __forceinline__ int us32(const Act& a, int g) { return a.us16[2 * g] + a.us16[2 * g + 1]; }
+
+template <int T, bool S256>
 struct Unit;
 
-// Q4_K unit u: 16 bytes of qs = 16 low nibbles of sub-block 2p and 16 high nibbles of sub-block 2p + 1
-template <>
-struct Unit<kQ4_K> {
-    struct W {
-        uint32_t q[4];
-        float d, dmin;
-        int sca, ma, scb, mb, pa;
-    };
-    __device__ static __forceinline__ W load(const uint8_t* row, int u) {
-        W w;
-        const int b = u >> 3, j = u & 7, p = j >> 1;
-        const uint8_t* blk = row + 144 * b;
+// ---- Q4_K
+template <bool S256>
+struct Unit<kQ4_K, S256> {
+    static constexpr int kUnit = S256 ? 256 : 32;
+    template <int NE>
+    __device__ static __forceinline__ void apply(const uint8_t* base, int roff, int u, const Act (&a)[NE], int n,
+                                                 float (&acc)[NE]) {
+        const int b = S256 ? u : u >> 3;
+        const uint8_t* blk = base + roff + 144 * b;
         const uint4 hdr = *(const uint4*)blk;
-        const uint4 qs = *(const uint4*)(blk + 16 + 16 * j);
-        w.q[0] = qs.x; w.q[1] = qs.y; w.q[2] = qs.z; w.q[3] = qs.w;
-        w.d = h2f((uint16_t)(hdr.x & 0xFFFFu));
-        w.dmin = h2f((uint16_t)(hdr.x >> 16));
-        q4k_sm(hdr.y, hdr.z, hdr.w, 2 * p, w.sca, w.ma);
-        q4k_sm(hdr.y, hdr.z, hdr.w, 2 * p + 1, w.scb, w.mb);
-        w.pa = 256 * b + 64 * p + 16 * (j & 1);
-        return w;
-    }
-    __device__ static __forceinline__ float apply(const W& w, const int8_t* act, const float* d8, const int* us16) {
-        const uint4 a = *(const uint4*)(act + w.pa);
-        const uint4 bq = *(const uint4*)(act + w.pa + 32);
-        int ia = 0, ib = 0;
-        ia = sdot4((int)(w.q[0] & 0x0F0F0F0Fu), (int)a.x, ia);
-        ia = sdot4((int)(w.q[1] & 0x0F0F0F0Fu), (int)a.y, ia);
-        ia = sdot4((int)(w.q[2] & 0x0F0F0F0Fu), (int)a.z, ia);
-        ia = sdot4((int)(w.q[3] & 0x0F0F0F0Fu), (int)a.w, ia);
-        ib = sdot4((int)((w.q[0] >> 4) & 0x0F0F0F0Fu), (int)bq.x, ib);
-        ib = sdot4((int)((w.q[1] >> 4) & 0x0F0F0F0Fu), (int)bq.y, ib);
-        ib = sdot4((int)((w.q[2] >> 4) & 0x0F0F0F0Fu), (int)bq.z, ib);
-        ib = sdot4((int)((w.q[3] >> 4) & 0x0F0F0F0Fu), (int)bq.w, ib);
-        const int ua = us16[w.pa >> 4], ub = us16[(w.pa >> 4) + 2];
-        const float fa = (float)(w.sca * ia) * w.d - (float)(w.ma * ua) * w.dmin;
-        const float fb = (float)(w.scb * ib) * w.d - (float)(w.mb * ub) * w.dmin;
-        return d8[w.pa >> 5] * fa + d8[(w.pa >> 5) + 1] * fb;
-    }
-};
-
-// Q6_K unit u = (block b, half n, c): ql bytes [64n + 16c, +16) hold values 128n + 16c + i (low nibbles) and
-// 128n + 64 + 16c + i (high); their 2 high bits are in qh[32n + 16(c & 1) + i] at shifts 2(c >> 1) and 4 + 2(c >> 1)
-template <>
-struct Unit<kQ6_K> {
-    struct W {
-        uint32_t lo[4], hi[4];
-        float d;
-        int scl, sch, pl;
-    };
-    __device__ static __forceinline__ W load(const uint8_t* row, int u) {
-        W w;
-        const int b = u >> 3, n = (u >> 2) & 1, c = u & 3;
-        const uint8_t* blk = row + 210 * b;
-        const uint8_t* ql = blk + 64 * n + 16 * c;
-        const uint8_t* qh = blk + 128 + 32 * n + 16 * (c & 1);
-        const int sh = 2 * (c >> 1);
+        const float d = h2f((uint16_t)(hdr.x & 0xFFFFu)), dmin = h2f((uint16_t)(hdr.x >> 16));
+        if (S256) {
+            int sc[8], m[8];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t l = ld_u32_a2(ql + 4 * i), h = ld_u32_a2(qh + 4 * i);
-            w.lo[i] = (l & 0x0F0F0F0Fu) | (((h >> sh) & 0x03030303u) << 4);
-            w.hi[i] = ((l >> 4) & 0x0F0F0F0Fu) | (((h >> (4 + sh)) & 0x03030303u) << 4);
+            for (int s = 0; s < 8; ++s) q4k_sm(hdr.y, hdr.z, hdr.w, s, sc[s], m[s]);
+            int s1[NE], s2[NE];
+#pragma unroll
+            for (int e = 0; e < NE; ++e) s1[e] = s2[e] = 0;
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const uint4 w0 = *(const uint4*)(blk + 16 + 32 * p), w1 = *(const uint4*)(blk + 32 + 32 * p);
+                const uint32_t w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+                for (int e = 0; e < NE; ++e) {
+                    if (e >= n) break;
+                    const int8_t* q = a[e].q + 256 * b + 64 * p;
+                    const uint4 l0 = *(const uint4*)q, l1 = *(const uint4*)(q + 16);
+                    const uint4 h0 = *(const uint4*)(q + 32), h1 = *(const uint4*)(q + 48);
+                    const uint32_t al[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
+                    const uint32_t ah[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+                    int il = 0, ih = 0;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        il = sdot4((int)(w[i] & 0x0F0F0F0Fu), (int)al[i], il);
+                        ih = sdot4((int)((w[i] >> 4) & 0x0F0F0F0Fu), (int)ah[i], ih);
+                    }
+                    s1[e] += sc[2 * p] * il + sc[2 * p + 1] * ih;
+                    s2[e] += m[2 * p] * us32(a[e], 8 * b + 2 * p) + m[2 * p + 1] * us32(a[e], 8 * b + 2 * p + 1);
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < NE; ++e) {
+                if (e >= n) break;
+                const float d8 = a[e].d8[8 * b];
+                acc[e] = __builtin_fmaf(d * d8, (float)s1[e], acc[e]);
+                acc[e] = __builtin_fmaf(-(dmin * d8), (float)s2[e], acc[e]);
+            }
+        } else {
+            const int g = u & 7;
+            int sc, m;
+            q4k_sm(hdr.y, hdr.z, hdr.w, g, sc, m);
+            const uint4 w0 = *(const uint4*)(blk + 16 + 32 * (g >> 1)), w1 = *(const uint4*)(blk + 32 + 32 * (g >> 1));
+            const uint32_t w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+            const int sh = 4 * (g & 1);
+#pragma unroll
+            for (int e = 0; e < NE; ++e) {
+                if (e >= n) break;
+                const int8_t* q = a[e].q + 32 * u;
+                const uint4 l0 = *(const uint4*)q, l1 = *(const uint4*)(q + 16);
+                const uint32_t al[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
+                int is = 0;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) is = sdot4((int)((w[i] >> sh) & 0x0F0F0F0Fu), (int)al[i], is);
+                const float d8 = a[e].d8[u];
+                acc[e] = __builtin_fmaf(d * d8, (float)(sc * is), acc[e]);
+                acc[e] = __builtin_fmaf(-(dmin * d8), (float)(m * us32(a[e], u)), acc[e]);
+            }
         }
-        w.scl = (int)(int8_t)blk[192 + 8 * n + c];
-        w.sch = (int)(int8_t)blk[192 + 8 * n + 4 + c];
-        w.d = lds_h(blk + 208);
-        w.pl = 256 * b + 128 * n + 16 * c;
-        return w;
-    }
-    __device__ static __forceinline__ float apply(const W& w, const int8_t* act, const float* d8, const int* us16) {
-        const uint4 a = *(const uint4*)(act + w.pl);
-        const uint4 h = *(const uint4*)(act + w.pl + 64);
-        int il = 0, ih = 0;
-        il = sdot4((int)w.lo[0], (int)a.x, il);
-        il = sdot4((int)w.lo[1], (int)a.y, il);
-        il = sdot4((int)w.lo[2], (int)a.z, il);
-        il = sdot4((int)w.lo[3], (int)a.w, il);
-        ih = sdot4((int)w.hi[0], (int)h.x, ih);
-        ih = sdot4((int)w.hi[1], (int)h.y, ih);
-        ih = sdot4((int)w.hi[2], (int)h.z, ih);
-        ih = sdot4((int)w.hi[3], (int)h.w, ih);
-        il -= 32 * us16[w.pl >> 4];              // the codes are q + 32
-        ih -= 32 * us16[(w.pl >> 4) + 4];
-        return w.d * (d8[w.pl >> 5] * (float)(w.scl * il) + d8[(w.pl >> 5) + 2] * (float)(w.sch * ih));
     }
 };
 
-// Q8_0 unit u = block u
-template <>
-struct Unit<kQ8_0> {
-    struct W {
+// ---- Q6_K: 32-value group gg of a block: half n = gg / 4, s = gg % 4; codes (ql >> 4(s >> 1)) & 15 | ((qh >> 2s) & 3) << 4
+// from ql[64n + 32(s & 1) + l] and qh[32n + l]; scales sc[2gg] (values 0..15), sc[2gg + 1] (16..31)
+template <bool S256>
+struct Unit<kQ6_K, S256> {
+    static constexpr int kUnit = S256 ? 256 : 32;
+    template <int NE>
+    __device__ static __forceinline__ void group(const uint8_t* base, int boff, int gg, int v0, const Act (&a)[NE],
+                                                 int n, int (&S)[NE]) {
+        const uint8_t* blk = base + boff;
+        const int hn = gg >> 2, s = gg & 3;
+        uint32_t ql[8], qh[8];
+        lds_words_a2<8>(base, boff + 64 * hn + 32 * (s & 1), ql);
+        lds_words_a2<8>(base, boff + 128 + 32 * hn, qh);
+        const int nsh = 4 * (s >> 1), hsh = 2 * s;
         uint32_t q[8];
-        float d;
-        int u;
-    };
-    __device__ static __forceinline__ W load(const uint8_t* row, int u) {
-        W w;
-        const uint8_t* blk = row + 34 * u;
-        w.d = lds_h(blk);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) w.q[i] = ld_u32_a2(blk + 2 + 4 * i);
-        w.u = u;
-        return w;
+        for (int i = 0; i < 8; ++i) q[i] = ((ql[i] >> nsh) & 0x0F0F0F0Fu) | (((qh[i] >> hsh) & 0x03030303u) << 4);
+        const int sc0 = (int)(int8_t)blk[192 + 2 * gg], sc1 = (int)(int8_t)blk[193 + 2 * gg];
+#pragma unroll
+        for (int e = 0; e < NE; ++e) {
+            if (e >= n) break;
+            const int8_t* x = a[e].q + v0;
+            const uint4 l0 = *(const uint4*)x, l1 = *(const uint4*)(x + 16);
+            int i0 = 0, i1 = 0;
+            i0 = sdot4((int)q[0], (int)l0.x, i0);
+            i0 = sdot4((int)q[1], (int)l0.y, i0);
+            i0 = sdot4((int)q[2], (int)l0.z, i0);
+            i0 = sdot4((int)q[3], (int)l0.w, i0);
+            i1 = sdot4((int)q[4], (int)l1.x, i1);
+            i1 = sdot4((int)q[5], (int)l1.y, i1);
+            i1 = sdot4((int)q[6], (int)l1.z, i1);
+            i1 = sdot4((int)q[7], (int)l1.w, i1);
+            i0 -= 32 * a[e].us16[v0 >> 4];          // codes are q + 32
+            i1 -= 32 * a[e].us16[(v0 >> 4) + 1];
+            S[e] += sc0 * i0 + sc1 * i1;
+        }
     }
-    __device__ static __forceinline__ float apply(const W& w, const int8_t* act, const float* d8, const int*) {
-        const uint4 a0 = *(const uint4*)(act + 32 * w.u);
-        const uint4 a1 = *(const uint4*)(act + 32 * w.u + 16);
-        int s = 0;
-        s = sdot4((int)w.q[0], (int)a0.x, s);
-        s = sdot4((int)w.q[1], (int)a0.y, s);
-        s = sdot4((int)w.q[2], (int)a0.z, s);
-        s = sdot4((int)w.q[3], (int)a0.w, s);
-        s = sdot4((int)w.q[4], (int)a1.x, s);
-        s = sdot4((int)w.q[5], (int)a1.y, s);
-        s = sdot4((int)w.q[6], (int)a1.z, s);
-        s = sdot4((int)w.q[7], (int)a1.w, s);
-        return (w.d * d8[w.u]) * (float)s;
+    template <int NE>
+    __device__ static __forceinline__ void apply(const uint8_t* base, int roff, int u, const Act (&a)[NE], int n,
+                                                 float (&acc)[NE]) {
+        const int b = S256 ? u : u >> 3;
+        const int boff = roff + 210 * b;
+        const float d = h2f(*(const uint16_t*)(base + boff + 208));
+        int S[NE];
+#pragma unroll
+        for (int e = 0; e < NE; ++e) S[e] = 0;
+        if (S256) {
+#pragma unroll 1
+            for (int gg = 0; gg < 8; ++gg) group<NE>(base, boff, gg, 256 * b + 32 * gg, a, n, S);
+        } else {
+            group<NE>(base, boff, u & 7, 32 * u, a, n, S);
+        }
+#pragma unroll
+        for (int e = 0; e < NE; ++e) {
+            if (e >= n) break;
+            acc[e] = __builtin_fmaf(d * a[e].d8[S256 ? 8 * b : u], (float)S[e], acc[e]);
+        }
     }
 };
 
-// IQ4_XS unit u = sub-block s of block b: 16 qs bytes, low nibbles values 0..15, high nibbles 16..31
-template <>
-struct Unit<kIQ4_XS> {
-    struct W {
-        int lo[4], hi[4];
-        float d;
-        int ls, p;
-    };
-    __device__ static __forceinline__ W load(const uint8_t* row, int u) {
-        W w;
-        const int b = u >> 3, s = u & 7;
-        const uint8_t* blk = row + 136 * b;
-        const uint2 hdr = *(const uint2*)blk;
+// ---- Q8_0: unit = block u (34 bytes)
+template <bool S256>
+struct Unit<kQ8_0, S256> {
+    static constexpr int kUnit = 32;
+    template <int NE>
+    __device__ static __forceinline__ void apply(const uint8_t* base, int roff, int u, const Act (&a)[NE], int n,
+                                                 float (&acc)[NE]) {
+        const int boff = roff + 34 * u;
+        const float d = h2f(*(const uint16_t*)(base + boff));
+        uint32_t w[8];
+        lds_words_a2<8>(base, boff + 2, w);
+#pragma unroll
+        for (int e = 0; e < NE; ++e) {
+            if (e >= n) break;
+            const int8_t* x = a[e].q + 32 * u;
+            const uint4 l0 = *(const uint4*)x, l1 = *(const uint4*)(x + 16);
+            const uint32_t al[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
+            int is = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) is = sdot4((int)w[i], (int)al[i], is);
+            acc[e] = __builtin_fmaf(d * a[e].d8[u], (float)is, acc[e]);
+        }
+    }
+};
+
+// ---- IQ4_XS: sub-block s: 16 qs bytes, low nibbles values 0..15, high 16..31, codebook kvalues_iq4nl, scale ls - 32
+template <bool S256>
+struct Unit<kIQ4_XS, S256> {
+    static constexpr int kUnit = S256 ? 256 : 32;
+    template <int NE>
+    __device__ static __forceinline__ void sub(const uint8_t* blk, uint2 hdr, int s, int v0, const Act (&a)[NE], int n,
+                                               int (&S)[NE]) {
         const uint2 q0 = *(const uint2*)(blk + 8 + 16 * s), q1 = *(const uint2*)(blk + 16 + 16 * s);
         const uint32_t qw[4] = {q0.x, q0.y, q1.x, q1.y};
         const uint32_t t0 = kIq4Tab[0], t1 = kIq4Tab[1], t2 = kIq4Tab[2], t3 = kIq4Tab[3];
+        int lo[4], hi[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            w.lo[i] = table16_lookup(qw[i] & 0x0F0F0F0Fu, t0, t1, t2, t3);
-            w.hi[i] = table16_lookup((qw[i] >> 4) & 0x0F0F0F0Fu, t0, t1, t2, t3);
+            lo[i] = table16_lookup(qw[i] & 0x0F0F0F0Fu, t0, t1, t2, t3);
+            hi[i] = table16_lookup((qw[i] >> 4) & 0x0F0F0F0Fu, t0, t1, t2, t3);
         }
-        w.d = h2f((uint16_t)(hdr.x & 0xFFFFu));
         const uint32_t scales_h = hdr.x >> 16;
         const uint32_t sl = (hdr.y >> (8 * (s >> 1))) & 0xFFu;
-        w.ls = (int)(((sl >> (4 * (s & 1))) & 0x0Fu) | (((scales_h >> (2 * s)) & 3u) << 4)) - 32;
-        w.p = 256 * b + 32 * s;
-        return w;
+        const int ls = (int)(((sl >> (4 * (s & 1))) & 0x0Fu) | (((scales_h >> (2 * s)) & 3u) << 4)) - 32;
+#pragma unroll
+        for (int e = 0; e < NE; ++e) {
+            if (e >= n) break;
+            const int8_t* x = a[e].q + v0;
+            const uint4 l0 = *(const uint4*)x, l1 = *(const uint4*)(x + 16);
+            int is = 0;
+            is = sdot4(lo[0], (int)l0.x, is);
+            is = sdot4(lo[1], (int)l0.y, is);
+            is = sdot4(lo[2], (int)l0.z, is);
+            is = sdot4(lo[3], (int)l0.w, is);
+            is = sdot4(hi[0], (int)l1.x, is);
+            is = sdot4(hi[1], (int)l1.y, is);
+            is = sdot4(hi[2], (int)l1.z, is);
+            is = sdot4(hi[3], (int)l1.w, is);
+            S[e] += ls * is;
+        }
     }
-    __device__ static __forceinline__ float apply(const W& w, const int8_t* act, const float* d8, const int*) {
-        const uint4 a0 = *(const uint4*)(act + w.p);
-        const uint4 a1 = *(const uint4*)(act + w.p + 16);
-        int s = 0;
-        s = sdot4(w.lo[0], (int)a0.x, s);
-        s = sdot4(w.lo[1], (int)a0.y, s);
-        s = sdot4(w.lo[2], (int)a0.z, s);
-        s = sdot4(w.lo[3], (int)a0.w, s);
-        s = sdot4(w.hi[0], (int)a1.x, s);
-        s = sdot4(w.hi[1], (int)a1.y, s);
-        s = sdot4(w.hi[2], (int)a1.z, s);
-        s = sdot4(w.hi[3], (int)a1.w, s);
-        return (w.d * d8[w.p >> 5]) * (float)(s * w.ls);
+    template <int NE>
+    __device__ static __forceinline__ void apply(const uint8_t* base, int roff, int u, const Act (&a)[NE], int n,
+                                                 float (&acc)[NE]) {
+        const int b = S256 ? u : u >> 3;
+        const uint8_t* blk = base + roff + 136 * b;
+        const uint2 hdr = *(const uint2*)blk;
+        const float d = h2f((uint16_t)(hdr.x & 0xFFFFu));
+        int S[NE];
+#pragma unroll
+        for (int e = 0; e < NE; ++e) S[e] = 0;
+        if (S256) {
+#pragma unroll 1
+            for (int s = 0; s < 8; ++s) sub<NE>(blk, hdr, s, 256 * b + 32 * s, a, n, S);
+        } else {
+            sub<NE>(blk, hdr, u & 7, 32 * u, a, n, S);
+        }
+#pragma unroll
+        for (int e = 0; e < NE; ++e) {
+            if (e >= n) break;
+            acc[e] = __builtin_fmaf(d * a[e].d8[S256 ? 8 * b : u], (float)S[e], acc[e]);
+        }
     }
 };
 
-// the slab: n16 16-byte chunks, all of a thread's loads issued before its stores
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ void stage_slab(const uint8_t* __restrict__ src, uint8_t* dst, int n16) {
-    const int tid = threadIdx.x;
-    for (int i0 = 0; i0 < n16; i0 += kThreads * 8) {
-        u32x4_t v[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int i = i0 + j * kThreads + tid;
-            if (i < n16) v[j] = __builtin_nontemporal_load((const u32x4_t*)src + i);
-        }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int i = i0 + j * kThreads + tid;
-            if (i < n16) ((u32x4_t*)dst)[i] = v[j];
-        }
-    }
-}
 
-template <int T, int LPR, bool DOWN>
+// The whole grouped pass of one matrix (gate/up: DOWN false, down: DOWN true).
+template <int T, int LPR, bool DOWN, int NE>
 __global__ __launch_bounds__(kThreads) void grouped_kernel(ExpertLayout L, GroupedArgs a, int rows_total, int slab_rows,
                                                            int64_t mat_off, int64_t rb) {
+    using U = Unit<T, !DOWN>;
     extern __shared__ __align__(16) uint8_t lds[];
     const int n_in = DOWN ? (int)L.n_ff : (int)L.n_embd;
-    const int U = n_in >> 5;
+    const int units = n_in / U::kUnit;
     const int64_t slab_bytes = (int64_t)slab_rows * rb;
     uint8_t* slab = lds;
-    int8_t* act = (int8_t*)(lds + slab_bytes);
-    float* d8 = (float*)(act + kNE * n_in);
-    int* us16 = (int*)(d8 + kNE * (n_in >> 5));
+    int8_t* actq = (int8_t*)(lds + slab_bytes);
+    float* actd = (float*)(actq + NE * n_in);
+    int* acts = (int*)(actd + NE * (n_in >> 5));
     const int tid = threadIdx.x, lane = tid & 63;
     const int r0 = blockIdx.x * slab_rows;
     const int nrows = min(slab_rows, rows_total - r0);
+    const int n16 = (int)(((int64_t)nrows * rb) >> 4);
     const int ngroups = *a.n_groups;
     const int F = (int)L.n_ff, H = (int)L.n_embd;
+    const int nb = n_in >> 5;
+    Act act[NE];
+#pragma unroll
+    for (int e = 0; e < NE; ++e) act[e] = Act{actq + e * n_in, actd + e * nb, acts + e * (n_in >> 4)};
+
     for (int g = blockIdx.y; g < ngroups; g += gridDim.y) {
         const uint8_t* blob = (const uint8_t*)a.grp_ptr[g];
+        const int e0 = a.grp_start[g], e1 = a.grp_start[g + 1];
         if (((uintptr_t)blob & 15u) != 0) {
             if (tid == 0) atomicOr(a.err, 1);
             continue;
         }
+        const u32x4_t* src = (const u32x4_t*)(blob + mat_off + (int64_t)r0 * rb);
         __syncthreads();   // the previous group's readers of the slab are done
-        stage_slab(blob + mat_off + (int64_t)r0 * rb, slab, (int)(((int64_t)nrows * rb) >> 4));
-        const int e0 = a.grp_start[g], e1 = a.grp_start[g + 1];
-        for (int p = e0; p < e1; p += kNE) {
-            const int n = min(kNE, e1 - p);
-            __syncthreads();   // the previous pass's readers of the activations are done
+        for (int p = e0; p < e1; p += NE) {
+            const int n = min(NE, e1 - p);
+            if (p > e0) __syncthreads();   // the previous pass's readers of the activations are done
+            // the slab (first pass only): every chunk of this thread in flight before any is stored
+            u32x4_t v[kSlabRegs];
+            if (p == e0) {
+#pragma unroll
+                for (int j = 0; j < kSlabRegs; ++j) {
+                    const int i = j * kThreads + tid;
+                    if (i < n16) v[j] = __builtin_nontemporal_load(src + i);
+                }
+            }
             if (!DOWN) {
                 // the entries' q8_1 rows: int8 values, fp32 scales, sums of 16
-                const int nb = n_in >> 5;
                 for (int i = tid; i < n * nb; i += kThreads) {
                     const int e = i / nb, bi = i - e * nb;
                     const uint32_t* blk =
@@ -269,17 +343,17 @@ __global__ __launch_bounds__(kThreads) void grouped_kernel(ExpertLayout L, Group
                     uint32_t w[9];
 #pragma unroll
                     for (int k = 0; k < 9; ++k) w[k] = blk[k];
-                    uint4* dst = (uint4*)(act + e * n_in + 32 * bi);
+                    uint4* dst = (uint4*)(actq + e * n_in + 32 * bi);
                     dst[0] = make_uint4(w[1], w[2], w[3], w[4]);
                     dst[1] = make_uint4(w[5], w[6], w[7], w[8]);
-                    d8[e * nb + bi] = h2f((uint16_t)(w[0] & 0xFFFFu));
+                    actd[e * nb + bi] = h2f((uint16_t)(w[0] & 0xFFFFu));
                     int s0 = 0, s1 = 0;
 #pragma unroll
                     for (int k = 1; k <= 4; ++k) s0 = sdot4((int)w[k], 0x01010101, s0);
 #pragma unroll
                     for (int k = 5; k <= 8; ++k) s1 = sdot4((int)w[k], 0x01010101, s1);
-                    us16[e * (n_in >> 4) + 2 * bi] = s0;
-                    us16[e * (n_in >> 4) + 2 * bi + 1] = s1;
+                    acts[e * (n_in >> 4) + 2 * bi] = s0;
+                    acts[e * (n_in >> 4) + 2 * bi + 1] = s1;
                 }
             } else {
                 // h = SwiGLU(gate, up) with the canonical arithmetic, then per-32 canonical q8_1 (reference
@@ -293,9 +367,9 @@ __global__ __launch_bounds__(kThreads) void grouped_kernel(ExpertLayout L, Group
                     const float sum = group_sum<32>(h);
                     const float d = q8_scale(amax);
                     const int q = q8_value(h, q8_inv(d));
-                    act[e * n_in + col] = (int8_t)q;
+                    actq[e * n_in + col] = (int8_t)q;
                     const uint16_t hd = f2h(d);
-                    if ((col & 31) == 0) d8[e * (n_in >> 5) + (col >> 5)] = h2f(hd);
+                    if ((col & 31) == 0) actd[e * nb + (col >> 5)] = h2f(hd);
                     if (write_hq) {
                         uint8_t* blk = (uint8_t*)a.hq + ((int64_t)(p + e) * (F >> 5) + (col >> 5)) * 36;
                         blk[4 + (col & 31)] = (uint8_t)q;
@@ -303,35 +377,38 @@ __global__ __launch_bounds__(kThreads) void grouped_kernel(ExpertLayout L, Group
                             *(uint32_t*)blk = (uint32_t)hd | ((uint32_t)f2h(q8_1_finite(sum)) << 16);
                     }
                 }
+            }
+            if (p == e0) {
+#pragma unroll
+                for (int j = 0; j < kSlabRegs; ++j) {
+                    const int i = j * kThreads + tid;
+                    if (i < n16) ((u32x4_t*)slab)[i] = v[j];
+                }
+                for (int i = kSlabRegs * kThreads + tid; i < n16; i += kThreads)   // a slab past the registers
+                    ((u32x4_t*)slab)[i] = __builtin_nontemporal_load(src + i);
+            }
+            if (DOWN) {
                 __syncthreads();
                 for (int i = tid; i < n * (n_in >> 4); i += kThreads) {
-                    const uint4 v = *(const uint4*)(act + 16 * i);
+                    const uint4 w = *(const uint4*)(actq + 16 * i);
                     int s = 0;
-                    s = sdot4((int)v.x, 0x01010101, s);
-                    s = sdot4((int)v.y, 0x01010101, s);
-                    s = sdot4((int)v.z, 0x01010101, s);
-                    s = sdot4((int)v.w, 0x01010101, s);
-                    const int e = i / (n_in >> 4);
-                    us16[i] = s;
-                    (void)e;
+                    s = sdot4((int)w.x, 0x01010101, s);
+                    s = sdot4((int)w.y, 0x01010101, s);
+                    s = sdot4((int)w.z, 0x01010101, s);
+                    s = sdot4((int)w.w, 0x01010101, s);
+                    acts[i] = s;
                 }
             }
             __syncthreads();
             const int c = lane & (LPR - 1);
             for (int rr = tid / LPR; rr < nrows; rr += kThreads / LPR) {
-                const uint8_t* row = slab + (int64_t)rr * rb;
-                float acc[kNE];
+                const int roff = rr * (int)rb;
+                float acc[NE];
 #pragma unroll
-                for (int e = 0; e < kNE; ++e) acc[e] = 0.0f;
-                for (int u = c; u < U; u += LPR) {
-                    const typename Unit<T>::W w = Unit<T>::load(row, u);
+                for (int e = 0; e < NE; ++e) acc[e] = 0.0f;
+                for (int u = c; u < units; u += LPR) U::template apply<NE>(slab, roff, u, act, n, acc);
 #pragma unroll
-                    for (int e = 0; e < kNE; ++e)
-                        if (e < n)
-                            acc[e] += Unit<T>::apply(w, act + e * n_in, d8 + e * (n_in >> 5), us16 + e * (n_in >> 4));
-                }
-#pragma unroll
-                for (int e = 0; e < kNE; ++e) acc[e] = group_sum<LPR>(acc[e]);
+                for (int e = 0; e < NE; ++e) acc[e] = group_sum<LPR>(acc[e]);
                 if (c == 0) {
                     const int r = r0 + rr;
                     for (int e = 0; e < n; ++e) {
@@ -345,8 +422,9 @@ __global__ __launch_bounds__(kThreads) void grouped_kernel(ExpertLayout L, Group
     }
 }
 
-static int lanes_per_row(int units) {
-    int l = 64;
+// L = min(8, the largest power of two dividing the unit count): the canonical lane count
+static int canon_lanes(int units) {
+    int l = 8;
     while (l > 1 && units % l) l >>= 1;
     return l;
 }
@@ -357,25 +435,33 @@ static hipError_t launch_t(const ExpertLayout& L, const GroupedArgs& a, hipStrea
     const int rows_total = DOWN ? (int)L.n_embd : (int)(2 * L.n_ff);
     const int64_t rb = DOWN ? L.d_row : L.gu_row;
     const int64_t mat_off = DOWN ? L.down_off : 0;
-    const int lpr = lanes_per_row(n_in / 32);
+    const int unit = Unit<T, !DOWN>::kUnit;
+    const int lpr = canon_lanes(n_in / unit);
     const int per_pass = kThreads / lpr;
-    const int base = per_pass > 8 ? per_pass : 8;
-    int64_t mult = 24576 / ((int64_t)base * rb);
-    if (mult < 1) mult = 1;
-    int slab_rows = (int)(base * mult);
+    int64_t rows = (20480 / rb) & ~(int64_t)7;               // about 20 KB of weights a work-group
+    if (rows < 8) rows = 8;
+    if (rows > 2 * per_pass) rows = 2 * per_pass;
+    int slab_rows = (int)rows;
     if (slab_rows > rows_total) slab_rows = rows_total;
-    const size_t lds = (size_t)slab_rows * rb + (size_t)kNE * (n_in + (n_in / 32) * 4 + (n_in / 16) * 4);
+    // entries a pass: the most a group can hold (one per token), up to kNE
+    const int ne = a.max_entries > 0 && a.max_entries < 4 ? (a.max_entries == 1 ? 1 : 2) : kNE;
+    const size_t lds = (size_t)slab_rows * rb + (size_t)ne * (n_in + (n_in / 32) * 4 + (n_in / 16) * 4);
     const int64_t gy = a.grid_groups > 0 && a.grid_groups < a.cap_groups ? a.grid_groups : a.cap_groups;
     const dim3 grid((unsigned)((rows_total + slab_rows - 1) / slab_rows), (unsigned)gy);
     void (*kern)(ExpertLayout, GroupedArgs, int, int, int64_t, int64_t) = nullptr;
-    switch (lpr) {
-        case 64: kern = grouped_kernel<T, 64, DOWN>; break;
-        case 32: kern = grouped_kernel<T, 32, DOWN>; break;
-        case 16: kern = grouped_kernel<T, 16, DOWN>; break;
-        case 8: kern = grouped_kernel<T, 8, DOWN>; break;
-        case 4: kern = grouped_kernel<T, 4, DOWN>; break;
-        case 2: kern = grouped_kernel<T, 2, DOWN>; break;
-        default: kern = grouped_kernel<T, 1, DOWN>; break;
+    switch (lpr * 8 + ne) {
+        case 8 * 8 + 1: kern = grouped_kernel<T, 8, DOWN, 1>; break;
+        case 8 * 8 + 2: kern = grouped_kernel<T, 8, DOWN, 2>; break;
+        case 8 * 8 + 4: kern = grouped_kernel<T, 8, DOWN, 4>; break;
+        case 4 * 8 + 1: kern = grouped_kernel<T, 4, DOWN, 1>; break;
+        case 4 * 8 + 2: kern = grouped_kernel<T, 4, DOWN, 2>; break;
+        case 4 * 8 + 4: kern = grouped_kernel<T, 4, DOWN, 4>; break;
+        case 2 * 8 + 1: kern = grouped_kernel<T, 2, DOWN, 1>; break;
+        case 2 * 8 + 2: kern = grouped_kernel<T, 2, DOWN, 2>; break;
+        case 2 * 8 + 4: kern = grouped_kernel<T, 2, DOWN, 4>; break;
+        case 1 * 8 + 1: kern = grouped_kernel<T, 1, DOWN, 1>; break;
+        case 1 * 8 + 2: kern = grouped_kernel<T, 1, DOWN, 2>; break;
+        default: kern = grouped_kernel<T, 1, DOWN, 4>; break;
     }
     if (lds > 65536) {
         const hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);

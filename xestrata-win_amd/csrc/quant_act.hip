@@ -6,39 +6,14 @@
 // xor-16..1 butterfly sum for each 32.  Both are the reference's bits.
 #include "xs_device.h"
 #include "xs_kernels.h"
+#include "xs_route.h"
 
 namespace xs {
 
 // 8 values a lane, 32 lanes = 256 values; a wave64 holds two 256-value groups
 __global__ void quantize_q8_1_256_kernel(const float* __restrict__ x, int64_t n8, uint8_t* __restrict__ y) {
     const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const bool in = j < n8;
-    float v[8], a = 0.0f, sum = 0.0f;
-#pragma unroll
-    for (int q = 0; q < 8; ++q) v[q] = in ? x[8 * j + q] : 0.0f;
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-        a = fmaxf(a, fabsf(v[q]));
-        sum += v[q];
-    }
-    const float amax = group_max<32>(a);
-    sum += __shfl_xor(sum, 1, 64);
-    sum += __shfl_xor(sum, 2, 64);
-    if (!in) return;
-    const float d = q8_scale(amax), id = q8_inv(d);
-    const int64_t ib = j / 4, o = 8 * (j % 4);
-    uint8_t* blk = y + 36 * ib;
-    uint32_t w0 = 0, w1 = 0;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) w0 |= (uint32_t)(uint8_t)q8_value(v[q], id) << (8 * q);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) w1 |= (uint32_t)(uint8_t)q8_value(v[4 + q], id) << (8 * q);
-    ((uint32_t*)(blk + 4 + o))[0] = w0;
-    ((uint32_t*)(blk + 4 + o))[1] = w1;
-    if (o == 0) {
-        const uint32_t ds = (uint32_t)f2h(d) | ((uint32_t)f2h(q8_1_finite(sum)) << 16);
-        *(uint32_t*)blk = ds;
-    }
+    q8_1_256_lane(x, j, j < n8, y);
 }
 
 // one lane a value, 32 lanes a block

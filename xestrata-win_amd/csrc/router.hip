@@ -2,103 +2,17 @@
 // style grouped sigmoid router (absent from the reference), and the f32 router-logit GEMV feeding them.
 #include "xs_device.h"
 #include "xs_kernels.h"
+#include "xs_route.h"
 
 namespace xs {
 
-constexpr int kRouterMaxPer = 16;   // experts a lane: one wave covers up to 1024 experts
 
-// the argmax order: the larger value wins, a tie keeps the lower index; NaN never wins (reference
-// src/kernels/xe/router.cpp:32-36)
-__device__ __forceinline__ void better(float& bv, int& bi, float ov, int oi) {
-    if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-}
-
-// Softmax top-k, bit for bit the reference's router_top10 (src/kernels/xe/router.cpp:59-145 and its fast form
-// :146-276): mx = max l; ex = exp((double) l - (double) mx); inv = (float) (1 / sum ex) with the sum serial and
-// ascending in double; p = (float) (ex * inv); k passes of argmax; renormalised in double by max(sum of the k,
-// 2^-14).  One wave a token.  The serial sum is only run when a tree sum cannot decide inv: the serial and tree sums
-// both lie within 2^-43 of the exact sum (every term is positive, the largest is exactly 1), so when the bracket
-// tree * (1 -+ 2^-40) maps to one float inv, that float is the serial sum's.
+// Softmax top-k (the reference's router_top10, src/kernels/xe/router.cpp:59-308): one wave a token, route_topk_wave
+template <int PER>
 __global__ __launch_bounds__(64) void router_topk_kernel(const float* __restrict__ logits, int n_expert, int k,
                                                          int32_t* __restrict__ ids, float* __restrict__ weights) {
-    const int t = blockIdx.x, lane = threadIdx.x;
-    const float* l = logits + (int64_t)t * n_expert;
-    float lv[kRouterMaxPer];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < kRouterMaxPer; ++j) {
-        const int x = lane + 64 * j;
-        lv[j] = x < n_expert ? l[x] : -INFINITY;
-        if (x < n_expert) mx = fmaxf(mx, lv[j]);
-    }
-    mx = group_max<64>(mx);
-    double ex[kRouterMaxPer];
-    double part = 0.0;
-#pragma unroll
-    for (int j = 0; j < kRouterMaxPer; ++j) {
-        const int x = lane + 64 * j;
-        ex[j] = x < n_expert ? exp((double)lv[j] - (double)mx) : 0.0;
-        part += ex[j];
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) part += __shfl_xor(part, o, 64);
-    const double lo = part * (1.0 - 0x1p-40), hi = part * (1.0 + 0x1p-40);
-    const float f_lo = (float)(1.0 / hi), f_hi = (float)(1.0 / lo);
-    float inv;
-    if (part >= 1.0 && hi < 1e300 && f_lo == f_hi) {
-        inv = f_lo;
-    } else {   // uniform over the wave: the serial ascending sum
-        double sum = 0.0;
-        for (int j = 0; j < kRouterMaxPer; ++j) {
-            if (64 * j >= n_expert) break;
-            for (int s = 0; s < 64 && 64 * j + s < n_expert; ++s) sum += __shfl(ex[j], s, 64);
-        }
-        inv = (float)(1.0 / sum);
-    }
-    float pv[kRouterMaxPer];
-    uint32_t live = 0;
-#pragma unroll
-    for (int j = 0; j < kRouterMaxPer; ++j) {
-        const int x = lane + 64 * j;
-        pv[j] = -INFINITY;
-        if (x < n_expert) { pv[j] = (float)(ex[j] * (double)inv); live |= 1u << j; }
-    }
-    float my_w = 0.0f;
-    int my_id = 0, nsel = 0;
-    for (int i = 0; i < k; ++i) {
-        float bv = -INFINITY;
-        int bi = n_expert;
-#pragma unroll
-        for (int j = 0; j < kRouterMaxPer; ++j)
-            if (((live >> j) & 1u) && pv[j] > bv) { bv = pv[j]; bi = lane + 64 * j; }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) better(bv, bi, __shfl_xor(bv, o, 64), __shfl_xor(bi, o, 64));
-        if (bi >= n_expert) break;   // every p left is NaN: ranks i.. keep the buffer's contents
-        if ((bi & 63) == lane) live &= ~(1u << (bi >> 6));
-        if (lane == i) { my_w = bv; my_id = bi; }
-        nsel = i + 1;
-    }
-    int32_t* id_row = ids + (int64_t)t * k;
-    float* w_row = weights + (int64_t)t * k;
-    if (nsel == k) {
-        double s = 0.0;
-        for (int i = 0; i < k; ++i) s += (double)__shfl(my_w, i, 64);
-        const double sc = fmax(s, 6.103515625e-05);
-        if (lane < k) {
-            id_row[lane] = my_id;
-            w_row[lane] = (float)((double)my_w / sc);
-        }
-    } else {
-        if (lane < nsel) { id_row[lane] = my_id; w_row[lane] = my_w; }
-        __threadfence_block();
-        __builtin_amdgcn_wave_barrier();
-        if (lane == 0) {
-            double s = 0.0;
-            for (int i = 0; i < k; ++i) s += (double)w_row[i];
-            const double sc = fmax(s, 6.103515625e-05);
-            for (int i = 0; i < k; ++i) w_row[i] = (float)((double)w_row[i] / sc);
-        }
-    }
+    const int t = blockIdx.x;
+    route_topk_wave<PER>(logits + (int64_t)t * n_expert, n_expert, k, ids + (int64_t)t * k, weights + (int64_t)t * k);
 }
 
 // DeepSeek-V3 routing (its technical report: sigmoid affinities, a selection bias, group-limited top-k): s =
@@ -183,7 +97,12 @@ __global__ __launch_bounds__(256) void logits_f32_kernel(const float* __restrict
 
 hipError_t launch_router_topk(const float* logits, int n_tokens, int n_expert, int k, int32_t* ids, float* weights,
                               hipStream_t s) {
-    hipLaunchKernelGGL(router_topk_kernel, dim3((unsigned)n_tokens), dim3(64), 0, s, logits, n_expert, k, ids, weights);
+    const dim3 g((unsigned)n_tokens), b(64);
+    if (n_expert <= 64) hipLaunchKernelGGL(router_topk_kernel<1>, g, b, 0, s, logits, n_expert, k, ids, weights);
+    else if (n_expert <= 128) hipLaunchKernelGGL(router_topk_kernel<2>, g, b, 0, s, logits, n_expert, k, ids, weights);
+    else if (n_expert <= 256) hipLaunchKernelGGL(router_topk_kernel<4>, g, b, 0, s, logits, n_expert, k, ids, weights);
+    else if (n_expert <= 512) hipLaunchKernelGGL(router_topk_kernel<8>, g, b, 0, s, logits, n_expert, k, ids, weights);
+    else hipLaunchKernelGGL(router_topk_kernel<16>, g, b, 0, s, logits, n_expert, k, ids, weights);
     return hipGetLastError();
 }
 

@@ -34,6 +34,7 @@ struct GroupedArgs {
     float* out;
     int32_t* err;  // device word: set non-zero when a blob address is not 16-byte aligned
     int64_t cap_groups, grid_groups;
+    int max_entries;   // the most entries a group can have (the call's token count), 0 when not known
 };
 hipError_t launch_native_gu(const ExpertLayout& L, const GroupedArgs& a, hipStream_t s);
 hipError_t launch_native_down(const ExpertLayout& L, const GroupedArgs& a, hipStream_t s);
@@ -54,6 +55,11 @@ hipError_t launch_resident_plan(const int32_t* ids, int n, int k, const int32_t*
 hipError_t launch_prefill_route(const int32_t* ids, int64_t n, int k, int n_expert, int32_t* src, int32_t* slot,
                                 int32_t* entry, int32_t* bounds, int32_t* experts, int32_t* n_groups,
                                 const uint8_t* cache_base, long long blob, unsigned long long* grp_ptr, hipStream_t s);
+
+// decode_layer.hip
+hipError_t launch_decode_route(const float* logits, const float* x, int n_tok, int n_expert, int k, int64_t n_embd,
+                               int32_t* ids, float* weights, int32_t* plan, long long capx, uint32_t* skip,
+                               const uint8_t* arena, long long blob, void* xq, hipStream_t s);
 
 // combine.hip
 hipError_t launch_combine(const float* parts, const float* weights, const float* shared, const float* shared_gate,

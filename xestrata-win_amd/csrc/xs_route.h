@@ -1,0 +1,221 @@
+// xestrata-win_amd/csrc/xs_route.h - device building blocks of routing, shared by the standalone kernels (router.hip,
+// dispatch.hip, quant_act.hip) and the fused decode route kernel (decode_layer.hip).
+#pragma once
+
+#include "xs_device.h"
+
+namespace xs {
+
+// the argmax order: the larger value wins, a tie keeps the lower index; NaN never wins (reference
+// src/kernels/xe/router.cpp:32-36)
+__device__ __forceinline__ void better(float& bv, int& bi, float ov, int oi) {
+    if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+}
+
+// Softmax top-k of one token on one wave, bit for bit the reference's router_top10 (src/kernels/xe/router.cpp:59-145
+// and its fast form :146-276): mx = max l; ex = exp((double) l - (double) mx); inv = (float) (1 / sum ex) with the
+// sum serial and ascending in double; p = (float) (ex * inv); k passes of argmax; renormalised in double by max(sum
+// of the k, 2^-14).  The serial sum runs only when a tree sum cannot decide inv: the serial and tree sums both lie
+// within 2^-43 of the exact sum (every term is positive, the largest exactly 1), so when the bracket tree * (1 -+
+// 2^-40) maps to one float inv, that float is the serial sum's.  PER experts a lane (n_expert <= 64 PER).  A row whose
+// ranks run out (NaN) leaves them as they were and renormalises the buffer (router.cpp:113-133).
+template <int PER>
+__device__ void route_topk_wave(const float* __restrict__ l, int n_expert, int k, int32_t* id_row, float* w_row) {
+    const int lane = threadIdx.x & 63;
+    float lv[PER];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        const int x = lane + 64 * j;
+        lv[j] = x < n_expert ? l[x] : -INFINITY;
+        if (x < n_expert) mx = fmaxf(mx, lv[j]);
+    }
+    mx = group_max<64>(mx);
+    double ex[PER];
+    double part = 0.0;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        const int x = lane + 64 * j;
+        ex[j] = x < n_expert ? exp((double)lv[j] - (double)mx) : 0.0;
+        part += ex[j];
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) part += __shfl_xor(part, o, 64);
+    const double lo = part * (1.0 - 0x1p-40), hi = part * (1.0 + 0x1p-40);
+    const float f_lo = (float)(1.0 / hi), f_hi = (float)(1.0 / lo);
+    float inv;
+    if (part >= 1.0 && hi < 1e300 && f_lo == f_hi) {
+        inv = f_lo;
+    } else {   // uniform over the wave: the serial ascending sum
+        double sum = 0.0;
+        for (int j = 0; j < PER; ++j) {
+            if (64 * j >= n_expert) break;
+            for (int s = 0; s < 64 && 64 * j + s < n_expert; ++s) sum += __shfl(ex[j], s, 64);
+        }
+        inv = (float)(1.0 / sum);
+    }
+    float pv[PER];
+    uint32_t live = 0;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        const int x = lane + 64 * j;
+        pv[j] = -INFINITY;
+        if (x < n_expert) { pv[j] = (float)(ex[j] * (double)inv); live |= 1u << j; }
+    }
+    float my_w = 0.0f;
+    int my_id = 0, nsel = 0;
+    for (int i = 0; i < k; ++i) {
+        float bv = -INFINITY;
+        int bi = n_expert;
+#pragma unroll
+        for (int j = 0; j < PER; ++j)
+            if (((live >> j) & 1u) && pv[j] > bv) { bv = pv[j]; bi = lane + 64 * j; }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) better(bv, bi, __shfl_xor(bv, o, 64), __shfl_xor(bi, o, 64));
+        if (bi >= n_expert) break;   // every p left is NaN: ranks i.. keep the buffer's contents
+        if ((bi & 63) == lane) live &= ~(1u << (bi >> 6));
+        if (lane == i) { my_w = bv; my_id = bi; }
+        nsel = i + 1;
+    }
+    if (nsel == k) {
+        double s = 0.0;
+        for (int i = 0; i < k; ++i) s += (double)__shfl(my_w, i, 64);
+        const double sc = fmax(s, 6.103515625e-05);
+        if (lane < k) {
+            id_row[lane] = my_id;
+            w_row[lane] = (float)((double)my_w / sc);
+        }
+    } else {
+        if (lane < nsel) { id_row[lane] = my_id; w_row[lane] = my_w; }
+        __threadfence_block();
+        __builtin_amdgcn_wave_barrier();
+        if (lane == 0) {
+            double s = 0.0;
+            for (int i = 0; i < k; ++i) s += (double)w_row[i];
+            const double sc = fmax(s, 6.103515625e-05);
+            for (int i = 0; i < k; ++i) w_row[i] = (float)((double)w_row[i] / sc);
+        }
+    }
+}
+
+// exclusive scan of v over the work-group (blockDim.x threads, a multiple of 64, at most 1024); *total gets the sum
+__device__ __forceinline__ int block_exclusive_scan(int v, int* s_wave, int* total) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    int inc = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(inc, o, 64);
+        if (lane >= o) inc += y;
+    }
+    if (lane == 63) s_wave[wave] = inc;
+    __syncthreads();
+    if (wave == 0) {
+        const int w = lane < nw ? s_wave[lane] : 0;
+        int wi = w;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(wi, o, 64);
+            if (lane >= o) wi += y;
+        }
+        if (lane < nw) s_wave[lane] = wi - w;   // exclusive over waves
+        if (lane == nw - 1) s_wave[63] = wi;    // total (nw <= 16 leaves slot 63 free)
+    }
+    __syncthreads();
+    const int r = s_wave[wave] + inc - v;
+    *total = s_wave[63];
+    __syncthreads();
+    return r;
+}
+
+// The decode plan in the reference's host-pool layout (src/kernels/xe/verify_kernels.cpp:819-890; layout
+// include/strata/core/expert_source.hpp:219-243): groups are the distinct experts in order of first occurrence, a
+// group's entries ascending.  A leader (an expert's first entry) is found with an LDS atomicMin, groups are numbered
+// by one work-group exclusive scan of (entries << 16 | 1) over the leaders, and an entry's place in its group is the
+// count of earlier entries with its expert.  s_ids[0..n) hold the ids (validated by the caller); s_first has n_expert
+// ints; every thread of the work-group calls this (n <= blockDim.x).  Returns nothing; *skip = ring at the end.
+__device__ __forceinline__ void build_plan(const int* s_ids, int* s_first, int* s_excl, int* s_wave, int n, int k,
+                                           const int32_t* __restrict__ res, int n_expert, const uint8_t* cache_base,
+                                           const unsigned long long* __restrict__ slot_off, long long blob,
+                                           int32_t* __restrict__ pl, long long capx, uint32_t* skip, uint32_t ring) {
+    const int t = threadIdx.x;
+    for (int e = t; e < n_expert; e += blockDim.x) s_first[e] = n;
+    __syncthreads();
+    const int ex = t < n ? s_ids[t] : -1;
+    if (t < n) atomicMin(&s_first[ex], t);
+    __syncthreads();
+    int cnt = 0, pos = 0;
+    const bool leader = t < n && s_first[ex] == t;
+    if (t < n) {
+        for (int j = 0; j < n; ++j) {
+            if (s_ids[j] != ex) continue;
+            if (leader) ++cnt;
+            if (j < t) ++pos;
+        }
+    }
+    int total;
+    const int pack = leader ? ((cnt << 16) | 1) : 0;
+    const int excl = block_exclusive_scan(pack, s_wave, &total);
+    s_excl[t] = excl;
+    __syncthreads();
+    int32_t* counts = pl;
+    int32_t* start = pl + 4;
+    int32_t* dst = start + capx + 1;
+    int32_t* tok = dst + capx;
+    const long long ptr_off = ((4 + (capx + 1) + 2 * capx) + 1) & ~1ll;
+    unsigned long long* ptr = (unsigned long long*)(pl + ptr_off);
+    int32_t* start2 = pl + ptr_off + 4 * capx;
+    if (t < n) {
+        const int le = s_excl[s_first[ex]];
+        const int g = le & 0xffff, gstart = le >> 16;
+        dst[gstart + pos] = t;
+        tok[gstart + pos] = t / k;
+        if (leader) {
+            const int32_t slot = res ? res[ex] : ex;
+            ptr[g] = (unsigned long long)(uintptr_t)(cache_base +
+                                                     (slot_off ? (size_t)slot_off[slot] : (size_t)slot * (size_t)blob));
+            start[g] = gstart;
+        }
+    }
+    __syncthreads();
+    if (t != 0) return;
+    const int groups = total & 0xffff;
+    start[groups] = n;
+    start2[0] = n;
+    counts[0] = groups;
+    counts[1] = n;
+    counts[2] = 0;
+    __threadfence();
+    *skip = ring;
+}
+
+// q8_1 of values 8j .. 8j + 7 of rows whose width is a whole number of 256s (reference iq_kernels.cpp:1850-1879):
+// one scale for each 256 values (32 neighbouring lanes), stored in each of their eight blocks; a block's fp16 sum is
+// its four 8-value serial sums combined by the xor-1 then xor-2 exchange.  Every lane of the wave calls it (lanes
+// with j >= n8 pass in == false).
+__device__ __forceinline__ void q8_1_256_lane(const float* __restrict__ x, int64_t j, bool in, uint8_t* __restrict__ y) {
+    float v[8], a = 0.0f, sum = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) v[q] = in ? x[8 * j + q] : 0.0f;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        a = fmaxf(a, fabsf(v[q]));
+        sum += v[q];
+    }
+    const float amax = group_max<32>(a);
+    sum += __shfl_xor(sum, 1, 64);
+    sum += __shfl_xor(sum, 2, 64);
+    if (!in) return;
+    const float d = q8_scale(amax), id = q8_inv(d);
+    const int64_t ib = j / 4, o = 8 * (j % 4);
+    uint8_t* blk = y + 36 * ib;
+    uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) w0 |= (uint32_t)(uint8_t)q8_value(v[q], id) << (8 * q);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) w1 |= (uint32_t)(uint8_t)q8_value(v[4 + q], id) << (8 * q);
+    ((uint32_t*)(blk + 4 + o))[0] = w0;
+    ((uint32_t*)(blk + 4 + o))[1] = w1;
+    if (o == 0) *(uint32_t*)blk = (uint32_t)f2h(d) | ((uint32_t)f2h(q8_1_finite(sum)) << 16);
+}
+
+}  // namespace xs
