@@ -167,12 +167,20 @@ int xs_add_inplace(float* x, const float* y, int64_t n, void* stream);
 
 /* The whole decode MoE layer on the device, every expert resident in one arena (expert e's blob at
  * arena + e * blob_bytes): router -> plan -> q8_1 -> grouped experts -> combine -> residual.
- * out = residual + MoE(x); out may equal residual.  workspace: xs_moe_layer_decode_workspace_bytes.  The engine's
- * moe_route + moe_finish surface (include/strata/core/layer.hpp:108-199) on one GPU, without the host ring. */
+ * out = residual + MoE(x); out may equal residual.  workspace: xs_moe_layer_decode_workspace_bytes for the largest
+ * n_tok it will serve, 256-byte aligned, zeroed once before its first call (every call leaves it ready for the next).
+ * The layer runs as one persistent launch when n_tok * k <= 256, n_tok <= 64 and the formats are one of Q4_K/Q6_K,
+ * Q4_K/Q4_K, Q8_0/Q8_0, IQ4_XS/IQ4_XS; else as the chain of kernels below.  The engine's moe_route + moe_finish
+ * surface (include/strata/core/layer.hpp:108-199) on one GPU, without the host ring. */
 int xs_moe_layer_decode(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_bytes, int n_expert, int k,
                         const float* x, const float* logits, const float* residual, float* out, int n_tok,
                         void* workspace, size_t workspace_bytes, void* stream);
 size_t xs_moe_layer_decode_workspace_bytes(const xs_expert_layout_t* L, int n_expert, int k, int n_tok);
+/* Device address of the decode workspace's status word: 0 after good calls; bit 1 a wait of the persistent layer
+ * passed its bound (50 ms), bit 2 a token's router produced fewer than k experts (NaN logits) - that call wrote no
+ * output.  Bits stay set until the caller clears the word; the workspace itself needs no reset after an error.  No
+ * counterpart in the reference (its layer reports through host-side checks of each launch). */
+int32_t* xs_moe_layer_decode_status(void* workspace);
 
 /* The whole prompt / verify MoE layer on the device (same arena): router -> permutation -> bf16 MFMA grouped
  * experts -> combine -> residual.  The engine's prompt MoE section (src/prefill/plain_prompt.cpp:558-797). */

@@ -169,3 +169,57 @@ def test_config5_deepseek_decode(xm, xo):
                                    np.zeros(1, np.int32), np.zeros(1, np.int32), oxq, 1)
     want = (t2n(res) + xo.combine(oparts, rw, osh, None, H, k, T)).astype(np.float32)
     assert np.array_equal(t2n(out).view(np.uint32), want.view(np.uint32)), xo.rel_max(t2n(out), want)
+
+
+def test_decode_workspace_reuse(xm, xo, c2_arena):
+    """One workspace, sized for 16 tokens and zeroed once, serves calls of 16, 1, 4 and 16 tokens in a row (the
+    persistent layer's counters return to zero after every call): each call bit for bit the oracle, status word 0."""
+    arena, L = c2_arena
+    layer = xm.MoeLayer(L, arena, 128, 8, 16)
+    ol = xo.layout(L.gu_type, L.d_type, L.n_embd, L.n_ff)
+    for i, T in enumerate([16, 1, 4, 16]):
+        g = torch.Generator(device=DEV).manual_seed(300 + i)
+        logits = torch.randn(T, 128, device=DEV, generator=g)
+        x = torch.randn(T, L.n_embd, device=DEV, generator=g)
+        res = torch.randn(T, L.n_embd, device=DEV, generator=g)
+        out = torch.empty_like(res)
+        layer(x, logits, res, out)
+        torch.cuda.synchronize()
+        assert layer.status() == 0
+        ids, _ = xo.router_top10(t2n(logits), k=8)
+        used = set(ids.ravel().tolist())
+        by_expert = [t2n(arena[e]) if e in used else np.zeros(16, np.uint8) for e in range(128)]
+        want = xo.moe_layer_decode(ol, by_expert, 8, t2n(x), t2n(logits), t2n(res), n_threads=8)
+        assert np.array_equal(t2n(out).view(np.uint32), want.view(np.uint32)), (T, xo.rel_max(t2n(out), want))
+
+
+def test_decode_graph_replays(xm, c2_arena):
+    """The decode layer captured in a HIP graph: every replay (with eager work and waits between them) gives the
+    eager call's bits."""
+    arena, L = c2_arena
+    T = 4
+    g = torch.Generator(device=DEV).manual_seed(77)
+    logits = torch.randn(T, 128, device=DEV, generator=g)
+    x = torch.randn(T, L.n_embd, device=DEV, generator=g)
+    res = torch.randn(T, L.n_embd, device=DEV, generator=g)
+    layer = xm.MoeLayer(L, arena, 128, 8, T)
+    eager = torch.empty_like(res)
+    layer(x, logits, res, eager)
+    torch.cuda.synchronize()
+    out = torch.zeros_like(res)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        layer(x, logits, res, out, stream=s)   # warm-up on the capture stream
+        s.synchronize()
+        with torch.cuda.graph(graph, stream=s):
+            layer(x, logits, res, out, stream=s)
+    torch.cuda.synchronize()
+    for r in range(4):
+        out.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int32), eager.view(torch.int32)), r
+    assert layer.status() == 0

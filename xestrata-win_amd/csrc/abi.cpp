@@ -42,6 +42,15 @@ bool overlap(const void* a, size_t an, const void* b, size_t bn) {
 }
 size_t up256(size_t v) { return (v + 255) & ~(size_t)255; }
 
+// 50 ms of the device's wall clock: the bound of the fused decode layer's waits (each normally a few microseconds)
+long long spin_ticks() {
+    int dev = 0, khz = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess ||
+        khz <= 0)
+        khz = 100000;
+    return (long long)khz * 50;
+}
+
 int type_qk(int t) { return t == 8 ? 32 : (t == 12 || t == 14 || t == 23) ? 256 : 0; }
 int type_bytes(int t) { return t == 8 ? 34 : t == 12 ? 144 : t == 14 ? 210 : t == 23 ? 136 : 0; }
 
@@ -393,6 +402,9 @@ int xs_add_inplace(float* x, const float* y, int64_t n, void* stream) {
 
 namespace {
 struct DecodeWs {
+    int32_t* status;   // the error word, first in the workspace
+    int32_t* sync;     // the persistent layer's epoch and done count (same 256 bytes)
+    unsigned long long *hx, *px;   // the persistent layer's tagged hand-over words (256 entries)
     int32_t* ids;
     float* w;
     int32_t* plan;
@@ -402,11 +414,23 @@ struct DecodeWs {
     float* parts;
     size_t bytes;
 };
-DecodeWs decode_ws(const xs_expert_layout_t* L, int k, int n_tok, uint8_t* base) {
+// The persistent layer's part of the workspace (head, tagged words) sits at fixed offsets whatever the call's token
+// count, ahead of everything else, so one workspace zeroed once serves calls of any size up to the one it was sized
+// for and the chained path never writes over tagged words.
+bool fused_possible(const xs_expert_layout_t* L, int n_expert, int k) {
+    xs::FusedPlan P;
+    return xs::fused_decode_plan(to_layout(L), n_expert, k, 1, &P);
+}
+DecodeWs decode_ws(const xs_expert_layout_t* L, int n_expert, int k, int n_tok, uint8_t* base) {
     DecodeWs d;
     const long long capx = (long long)n_tok * k;
     size_t off = 0;
     auto take = [&](size_t b) { uint8_t* p = base ? base + off : nullptr; off += up256(b); return p; };
+    d.status = (int32_t*)take(256);
+    d.sync = d.status ? d.status + 16 : nullptr;
+    const bool fused = fused_possible(L, n_expert, k);
+    d.hx = (unsigned long long*)take(fused ? (size_t)256 * (size_t)L->n_ff * 8 : 0);
+    d.px = (unsigned long long*)take(fused ? (size_t)256 * (size_t)L->n_embd * 8 : 0);
     d.ids = (int32_t*)take((size_t)capx * 4);
     d.w = (float*)take((size_t)capx * 4);
     d.plan = (int32_t*)take(plan_words(capx) * 4);
@@ -447,10 +471,13 @@ PrefillWs prefill_ws(const xs_expert_layout_t* L, int n_expert, int k, int n_tok
 }
 }  // namespace
 
+int32_t* xs_moe_layer_decode_status(void* workspace) {
+    return workspace ? (int32_t*)workspace : nullptr;
+}
+
 size_t xs_moe_layer_decode_workspace_bytes(const xs_expert_layout_t* L, int n_expert, int k, int n_tok) {
-    (void)n_expert;
-    if (!L || k <= 0 || n_tok <= 0) return 0;
-    return decode_ws(L, k, n_tok, nullptr).bytes;
+    if (!L || k <= 0 || n_tok <= 0 || n_expert <= 0) return 0;
+    return decode_ws(L, n_expert, k, n_tok, nullptr).bytes;
 }
 
 int xs_moe_layer_decode(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_bytes, int n_expert, int k,
@@ -463,11 +490,42 @@ int xs_moe_layer_decode(const xs_expert_layout_t* L, const uint8_t* arena, size_
         return fail(XS_EINVAL, "moe_layer_decode: the arena must hold 16-byte aligned blobs of at least %zu bytes", L->bytes);
     if (!aligned(workspace, 256) || workspace_bytes < xs_moe_layer_decode_workspace_bytes(L, n_expert, k, n_tok))
         return fail(XS_EINVAL, "moe_layer_decode: workspace missing, misaligned or short");
-    const DecodeWs w = decode_ws(L, k, n_tok, (uint8_t*)workspace);
+    const DecodeWs w = decode_ws(L, n_expert, k, n_tok, (uint8_t*)workspace);
     const long long capx = (long long)n_tok * k;
     if (n_expert > 1024 || k > 64 || k > n_expert)
         return fail(XS_EINVAL, "moe_layer_decode: %d experts, top-%d (the router takes up to 1024 and 64)", n_expert, k);
-    if (!aligned(logits, 4) || !aligned(x, 4)) return fail(XS_EINVAL, "moe_layer_decode: a span is missing or misaligned");
+    if (!aligned(logits, 4) || !aligned(x, 4) || !aligned(residual, 4) || !aligned(out, 4))
+        return fail(XS_EINVAL, "moe_layer_decode: a span is missing or misaligned");
+    const xs::ExpertLayout XL = to_layout(L);
+    xs::FusedPlan P;
+    if (xs::fused_decode_plan(XL, n_expert, k, n_tok, &P)) {
+        // the whole layer in one persistent launch
+        xs::FusedArgs a;
+        a.L = XL;
+        a.arena = arena;
+        a.blob = (long long)blob_bytes;
+        a.n_expert = n_expert;
+        a.k = k;
+        a.n_tok = n_tok;
+        a.logits = logits;
+        a.x = x;
+        a.residual = residual;
+        a.out = out;
+        a.ids = w.ids;
+        a.weights = w.w;
+        a.hx = w.hx;
+        a.px = w.px;
+        a.sync = w.sync;
+        a.err = w.status;
+        a.rh = P.rh;
+        a.rd = P.rd;
+        a.nu = P.nu;
+        a.nj = P.nj;
+        a.slab_gu_bytes = P.slab_gu;
+        a.slab_dn_bytes = P.slab_dn;
+        a.spin_ticks = spin_ticks();
+        return finish(stream, xs::launch_decode_fused(a, P, S(stream)), "moe_layer_decode");
+    }
     // routing, plan and activations in one launch (the reference's router_top10 + resident_plan + quantize_q8_1_rows)
     hipError_t e = xs::launch_decode_route(logits, x, n_tok, n_expert, k, L->n_embd, w.ids, w.w, w.plan, capx, w.skip,
                                            arena, (long long)blob_bytes, w.xq, S(stream));

@@ -1,0 +1,574 @@
+// xestrata-win_amd/csrc/decode_fused.hip - the whole decode MoE layer in one persistent launch.
+//
+// The reference runs a decode layer's MoE as a chain of launches with a host round trip (router_top10, the host or
+// resident plan, quantize_q8_1_rows, native_expert_grouped's gate/up, SwiGLU and down launches, and
+// native_moe_combine_multi + add_inplace: src/core/plain_model.cpp:951-988, src/core/moe_window.cpp:183-250).  At
+// decode sizes every launch costs more than its work (a token's 8 experts are 24.5 MB of config-2 weights, 3 us of
+// HBM time), so here one kernel does all of it, on the same arithmetic, bit for bit (xs_route.h, xs_units.h):
+//
+//   1. every work-group routes the tokens itself (softmax top-k, the plan, in LDS): no grid-wide wait before the
+//      weights can be fetched;
+//   2. gate/up units (a group, an h-slab of rh SwiGLU outputs = rh gate rows + rh up rows): the work-group fetches the
+//      unit's rows and, with them, the rows of its first down unit, all in flight at once; quantizes its entries'
+//      tokens to q8_1 in LDS; computes the rows; writes h = SwiGLU(gate, up) as tagged words;
+//   3. down units (a group, a slab of rd down rows): gather the entries' h, polling each word until it carries this
+//      call's tag, quantize it per 32 values in LDS, compute the rows into tagged `parts` words (routing order);
+//   4. combines (a token, a down slab), after the work-group's down units: poll the slab's columns of the token's k
+//      parts, add them in rank order, add the residual (native_moe_combine_multi + add_inplace).
+// Waits only point backwards (down units on gate/up units, combines on down units, and a work-group finishes its
+// gate/up units before its down units and those before its combines), every work-group of the grid is resident at
+// once, and every wait is bounded: a wait past the bound sets the error word and moves on.
+#include "xs_device.h"
+#include "xs_kernels.h"
+#include "xs_route.h"
+#include "xs_units.h"
+
+#include <mutex>
+#include <vector>
+
+namespace xs {
+
+constexpr int kFT = 256;          // threads a work-group
+constexpr int kFMaxN = 256;       // routed entries (tokens x k) a call
+constexpr int kFRegs = 12;        // 16-byte chunks of gate/up rows a thread holds in flight
+constexpr int kFRegsD = 8;        // and of the prefetched down rows
+
+struct FusedLds {                 // byte offsets in the dynamic LDS
+    int ids, w, excl, wave, first, gexp, start, dst, tok, misc, gu, slab_gu, slab_dn, act_g, act_d, total;
+};
+
+__host__ __device__ inline int up16(int v) { return (v + 15) & ~15; }
+// one entry's LDS activation of n values: int8 values | n / 32 fp32 scales | n / 16 int sums of 16
+__host__ __device__ inline int act_stride(int n) { return up16(n + n / 8 + n / 4); }
+
+template <int NE>
+__host__ __device__ inline FusedLds fused_lds(int n_expert, int H, int F, int rh, int slab_gu, int slab_dn) {
+    FusedLds o;
+    int at = 0;
+    o.ids = at; at += up16(kFMaxN * 4);
+    o.w = at; at += up16(kFMaxN * 4);
+    o.excl = at; at += up16(kFMaxN * 4);
+    o.wave = at; at += up16(64 * 4);
+    o.first = at; at += up16(n_expert * 4);
+    o.gexp = at; at += up16(kFMaxN * 4);
+    o.start = at; at += up16((kFMaxN + 1) * 4);
+    o.dst = at; at += up16(kFMaxN * 4);
+    o.tok = at; at += up16(kFMaxN * 4);
+    o.misc = at; at += up16(96 * 4);
+    o.gu = at; at += up16(NE * 2 * rh * 4);
+    o.slab_gu = at; at += up16(slab_gu);
+    o.slab_dn = at; at += up16(slab_dn);
+    o.act_g = at; at += NE * act_stride(H);
+    o.act_d = at; at += NE * act_stride(F);
+    o.total = at;
+    return o;
+}
+
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+// q8_1 of values 8j .. 8j + 7 of one row (one scale a 256: 32 neighbouring lanes) straight into an LDS activation
+// (int8 values, fp32 scale, sums of 16): the values quantize_q8_1_rows writes (q8_1_256_lane), as the grouped
+// kernels read them back
+__device__ __forceinline__ void q8_1_256_to_act(const float* __restrict__ x, int j, int8_t* q, float* d8, int* us16) {
+    float v[8], a = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        v[i] = x[8 * j + i];
+        a = fmaxf(a, fabsf(v[i]));
+    }
+    const float amax = group_max32(a);
+    const float d = q8_scale(amax), id = q8_inv(d);
+    uint32_t w0 = 0, w1 = 0;
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int q0 = q8_value(v[i], id), q1 = q8_value(v[4 + i], id);
+        w0 |= (uint32_t)(uint8_t)q0 << (8 * i);
+        w1 |= (uint32_t)(uint8_t)q1 << (8 * i);
+        s += q0 + q1;
+    }
+    *(uint2*)(q + 8 * j) = make_uint2(w0, w1);
+    const int s16 = s + dpp_i<kDppXor1>(s);
+    if ((j & 1) == 0) us16[j >> 1] = s16;
+    if ((j & 3) == 0) d8[j >> 2] = h2f(f2h(d));
+}
+
+// Hand-over between work-groups without cache maintenance.  A release or acquire fence at device scope writes back or
+// invalidates the whole L2 of the XCD (eight L2s are not coherent with each other for ordinary accesses), and with
+// hundreds of work-groups those serialise into tens of microseconds; a producer that waits for its stores to be
+// acknowledged before raising a flag waits behind the HBM write queue, which the weight stream starves.  So a value
+// handed over travels in a 64-bit word with the call's tag in its upper half, written and read with device-scope
+// relaxed atomics (coherent across XCDs by themselves: write-through stores, loads that refetch), and the reader
+// polls the words it needs until every one carries the tag.  Tags come from an epoch in the workspace that the last
+// work-group to finish advances, so no word needs resetting and a stale word never matches.
+__device__ __forceinline__ void st_tag(unsigned long long* p, float v, unsigned int tag) {
+    __hip_atomic_store(p, ((unsigned long long)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned long long ld_tag(const unsigned long long* p) {
+    return __hip_atomic_load((unsigned long long*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool tag_ok(unsigned long long w, unsigned int tag) { return (unsigned int)(w >> 32) == tag; }
+__device__ __forceinline__ float tag_val(unsigned long long w) { return __uint_as_float((unsigned int)w); }
+__device__ __forceinline__ int add_dev(int32_t* p, int v) {
+    return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// N tagged words from p into v, polled until all carry the tag or the bound passes (then false, values undefined)
+template <int N>
+__device__ __forceinline__ bool gather_tagged(const unsigned long long* p, int n, unsigned int tag, long long ticks,
+                                              float (&v)[N]) {
+    long long t0 = 0;
+    for (int it = 0;; ++it) {
+        unsigned long long w[N];
+#pragma unroll
+        for (int q = 0; q < N; ++q)
+            if (q < n) w[q] = ld_tag(p + q);
+        bool ok = true;
+#pragma unroll
+        for (int q = 0; q < N; ++q)
+            if (q < n) {
+                ok = ok && tag_ok(w[q], tag);
+                v[q] = tag_val(w[q]);
+            }
+        if (ok) return true;
+        if (it == 0) t0 = wall_clock64();
+        else if (wall_clock64() - t0 > ticks) return false;
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+// the row-dot lane sum for a run-time lane count (lane 0 of each group gets it)
+__device__ __forceinline__ float lanes_sum(float v, int l) {
+    return l == 8 ? lane0_sum<8>(v) : l == 4 ? lane0_sum<4>(v) : l == 2 ? lane0_sum<2>(v) : v;
+}
+
+// The work-group is done with the call; the last one advances the epoch (every work-group read it before it counted
+// itself done) and clears the count.
+__device__ __forceinline__ void done_call(const FusedArgs& a, unsigned int tag) {
+    if (threadIdx.x == 0 && add_dev(a.sync + 16, 1) == (int)gridDim.x - 1) {
+        __hip_atomic_store(a.sync + 16, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(a.sync, (int)tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+template <int TG, int TD, int NE>
+__global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    using UG = Unit<TG, true>;
+    using UD = Unit<TD, false>;
+    const ExpertLayout& L = a.L;
+    const int H = (int)L.n_embd, F = (int)L.n_ff, k = a.k, T = a.n_tok, n = T * k, E = a.n_expert;
+    const int rh = a.rh, rd = a.rd, nu = a.nu, nj = a.nj;
+    const FusedLds o = fused_lds<NE>(E, H, F, rh, a.slab_gu_bytes, a.slab_dn_bytes);
+    int* s_ids = (int*)(lds + o.ids);
+    float* s_w = (float*)(lds + o.w);
+    int* s_excl = (int*)(lds + o.excl);
+    int* s_wave = (int*)(lds + o.wave);
+    int* s_first = (int*)(lds + o.first);
+    int* s_gexp = (int*)(lds + o.gexp);
+    int* s_start = (int*)(lds + o.start);
+    int* s_dst = (int*)(lds + o.dst);
+    int* s_tok = (int*)(lds + o.tok);
+    int* s_misc = (int*)(lds + o.misc);   // [0] groups (-1: bad routing), [3] the epoch
+    float* s_gu = (float*)(lds + o.gu);
+    uint8_t* slab_gu = lds + o.slab_gu;
+    uint8_t* slab_dn = lds + o.slab_dn;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+    Act actg[NE], actd[NE];
+#pragma unroll
+    for (int e = 0; e < NE; ++e) {
+        int8_t* qg = (int8_t*)(lds + o.act_g) + e * act_stride(H);
+        actg[e] = Act{qg, (const float*)(qg + H), (const int*)(qg + H + H / 8)};
+        int8_t* qd = (int8_t*)(lds + o.act_d) + e * act_stride(F);
+        actd[e] = Act{qd, (const float*)(qd + F), (const int*)(qd + F + F / 8)};
+    }
+
+    if (tid == 0) s_misc[3] = __hip_atomic_load(a.sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // ---- 1. routing, in every work-group (router.cpp:59-308 and verify_kernels.cpp:819-890's order, in LDS)
+    for (int t = wave; t < T; t += kFT / 64) {
+        if (lane < k) {   // ranks a NaN row leaves unwritten stay invalid
+            s_ids[t * k + lane] = -1;
+            s_w[t * k + lane] = 0.0f;
+        }
+        const float* lr = a.logits + (int64_t)t * E;
+        if (E <= 64) route_topk_wave<1>(lr, E, k, s_ids + t * k, s_w + t * k);
+        else if (E <= 128) route_topk_wave<2>(lr, E, k, s_ids + t * k, s_w + t * k);
+        else if (E <= 256) route_topk_wave<4>(lr, E, k, s_ids + t * k, s_w + t * k);
+        else if (E <= 512) route_topk_wave<8>(lr, E, k, s_ids + t * k, s_w + t * k);
+        else route_topk_wave<16>(lr, E, k, s_ids + t * k, s_w + t * k);
+    }
+    __syncthreads();
+    // the plan: groups = distinct experts in order of first occurrence, a group's entries ascending
+    if (n <= 64) {   // one wave: uniform v_readlane loops, no work-group scan
+        if (wave == 0) {
+            const int ex = lane < n ? s_ids[lane] : -1;
+            if (__ballot(lane < n && (ex < 0 || ex >= E)) == 0) {
+                // first = the lane of the expert's first entry, pos = earlier entries with the expert
+                int first = lane, pos = 0;
+                for (int j = 0; j < n; ++j) {
+                    const bool same = __builtin_amdgcn_readlane(ex, j) == ex;
+                    first = same && j < first ? j : first;
+                    pos += same && j < lane ? 1 : 0;
+                }
+                const bool leader = lane < n && pos == 0;
+                // group = leaders before mine; start = entries whose expert's first entry is before mine
+                const unsigned long long lead = __ballot(leader);
+                const int g = __popcll(lead & ((1ull << first) - 1ull));
+                int gs = 0;
+                for (int j = 0; j < n; ++j) gs += __builtin_amdgcn_readlane(first, j) < first ? 1 : 0;
+                const int ngr = __popcll(lead);
+                if (lane < n) {
+                    s_dst[gs + pos] = lane;
+                    s_tok[gs + pos] = lane / k;
+                    if (leader) {
+                        s_gexp[g] = ex;
+                        s_start[g] = gs;
+                    }
+                }
+                if (lane == 0) {
+                    s_start[ngr] = n;
+                    s_misc[0] = ngr;
+                }
+            } else if (lane == 0) {
+                s_misc[0] = -1;
+            }
+        }
+    } else {   // the work-group: leaders by LDS atomicMin, group numbers and starts by one exclusive scan
+        for (int e = tid; e < E; e += kFT) s_first[e] = n;
+        __syncthreads();
+        const int ex = tid < n ? s_ids[tid] : -1;
+        if (__syncthreads_or(tid < n && (ex < 0 || ex >= E))) {
+            if (tid == 0) s_misc[0] = -1;
+        } else {
+            if (tid < n) atomicMin(&s_first[ex], tid);
+            __syncthreads();
+            int cnt = 0, pos = 0;
+            const bool leader = tid < n && s_first[ex] == tid;
+            if (tid < n)
+                for (int j = 0; j < n; ++j) {
+                    if (s_ids[j] != ex) continue;
+                    if (leader) ++cnt;
+                    if (j < tid) ++pos;
+                }
+            int total;
+            const int excl = block_exclusive_scan(leader ? ((cnt << 16) | 1) : 0, s_wave, &total);
+            s_excl[tid] = excl;
+            __syncthreads();
+            if (tid < n) {
+                const int le = s_excl[s_first[ex]];
+                const int g = le & 0xffff, gs = le >> 16;
+                s_dst[gs + pos] = tid;
+                s_tok[gs + pos] = tid / k;
+                if (leader) {
+                    s_gexp[g] = ex;
+                    s_start[g] = gs;
+                }
+            }
+            if (tid == 0) {
+                s_start[total & 0xffff] = n;
+                s_misc[0] = total & 0xffff;
+            }
+        }
+    }
+    __syncthreads();
+    const unsigned int tag = (unsigned int)s_misc[3] + 1u;
+    if (s_misc[0] < 0) {   // a rank left unwritten (NaN logits): no output this call
+        if (tid == 0) atomicOr(a.err, 4);
+        done_call(a, tag);
+        return;
+    }
+    if (blockIdx.x == 0 && tid < n) {
+        a.ids[tid] = s_ids[tid];
+        a.weights[tid] = s_w[tid];
+    }
+    const int ng = s_misc[0];
+    const int n_gu = ng * nu, n_dn = ng * nj;
+    const int lpr_g = canon_lanes(H / UG::kUnit), lpr_d = canon_lanes(F / UD::kUnit);
+
+    // ---- 2. gate/up units; the work-group's first down unit is fetched with its first one
+    bool dn_ready = false;
+    for (int u1 = blockIdx.x; u1 < n_gu; u1 += gridDim.x) {
+        const int g = u1 / nu, j = u1 - g * nu;
+        const uint8_t* blob = a.arena + (size_t)s_gexp[g] * (size_t)a.blob;
+        const int n16a = rh * (int)L.gu_row / 16;
+        const u32x4_t* srcg = (const u32x4_t*)(blob + (size_t)j * rh * L.gu_row);
+        const u32x4_t* srcu = (const u32x4_t*)(blob + L.up_off + (size_t)j * rh * L.gu_row);
+        __syncthreads();   // the previous unit's readers of the slab are done
+        u32x4_t v[kFRegs];
+#pragma unroll
+        for (int r = 0; r < kFRegs; ++r) {
+            const int i = r * kFT + tid;
+            if (i < 2 * n16a) v[r] = __builtin_nontemporal_load(i < n16a ? srcg + i : srcu + (i - n16a));
+        }
+        const bool pre = !dn_ready && blockIdx.x < n_dn;
+        u32x4_t vd[kFRegsD];
+        const int n16d = rd * (int)L.d_row / 16;
+        if (pre) {
+            const int gd = blockIdx.x / nj, jd = blockIdx.x - gd * nj;
+            const u32x4_t* srcd = (const u32x4_t*)(a.arena + (size_t)s_gexp[gd] * (size_t)a.blob + L.down_off +
+                                                   (size_t)jd * rd * L.d_row);
+#pragma unroll
+            for (int r = 0; r < kFRegsD; ++r) {
+                const int i = r * kFT + tid;
+                if (i < n16d) vd[r] = __builtin_nontemporal_load(srcd + i);
+            }
+            for (int i = kFRegsD * kFT + tid; i < n16d; i += kFT) ((u32x4_t*)slab_dn)[i] = srcd[i];
+        }
+        const int e0 = s_start[g], e1 = s_start[g + 1];
+        for (int p = e0; p < e1; p += NE) {
+            const int m = min(NE, e1 - p);
+            if (p > e0) __syncthreads();   // the previous pass's readers of the activations are done
+            for (int e = 0; e < m; ++e) {    // the entries' tokens to q8_1, one scale a 256
+                const float* xr = a.x + (int64_t)s_tok[p + e] * H;
+                int8_t* q = (int8_t*)(lds + o.act_g) + e * act_stride(H);
+                for (int j8 = tid; j8 < H / 8; j8 += kFT)
+                    q8_1_256_to_act(xr, j8, q, (float*)(q + H), (int*)(q + H + H / 8));
+            }
+            if (p == e0) {
+#pragma unroll
+                for (int r = 0; r < kFRegs; ++r) {
+                    const int i = r * kFT + tid;
+                    if (i < 2 * n16a) ((u32x4_t*)slab_gu)[i] = v[r];
+                }
+                for (int i = kFRegs * kFT + tid; i < 2 * n16a; i += kFT)
+                    ((u32x4_t*)slab_gu)[i] = i < n16a ? srcg[i] : srcu[i - n16a];
+                if (pre) {
+#pragma unroll
+                    for (int r = 0; r < kFRegsD; ++r) {
+                        const int i = r * kFT + tid;
+                        if (i < n16d) ((u32x4_t*)slab_dn)[i] = vd[r];
+                    }
+                    dn_ready = true;
+                }
+            }
+            __syncthreads();
+            const int c = lane & (lpr_g - 1);
+            for (int rr = tid / lpr_g; rr < 2 * rh; rr += kFT / lpr_g) {
+                float acc[NE];
+#pragma unroll
+                for (int e = 0; e < NE; ++e) acc[e] = 0.0f;
+                for (int u = c; u < H / UG::kUnit; u += lpr_g)
+                    UG::template apply<NE>(slab_gu, rr * (int)L.gu_row, u, actg, m, acc);
+#pragma unroll
+                for (int e = 0; e < NE; ++e) acc[e] = lanes_sum(acc[e], lpr_g);
+                if (c == 0) {
+#pragma unroll
+                    for (int e = 0; e < NE; ++e)
+                        if (e < m) s_gu[e * 2 * rh + rr] = acc[e];
+                }
+            }
+            __syncthreads();
+            for (int i = tid; i < m * rh; i += kFT) {
+                const int e = i / rh, r = i - e * rh;
+                st_tag(a.hx + (int64_t)(p + e) * F + j * rh + r,
+                       canon_silu_mul(s_gu[e * 2 * rh + r], s_gu[e * 2 * rh + rh + r]), tag);
+            }
+        }
+    }
+
+    // ---- 3. down units
+    for (int u2 = blockIdx.x; u2 < n_dn; u2 += gridDim.x) {
+        const int g = u2 / nj, j = u2 - g * nj;
+        const uint8_t* blob = a.arena + (size_t)s_gexp[g] * (size_t)a.blob;
+        const u32x4_t* srcd = (const u32x4_t*)(blob + L.down_off + (size_t)j * rd * L.d_row);
+        const int n16d = rd * (int)L.d_row / 16;
+        __syncthreads();   // the previous unit's readers of the slab are done
+        if (!dn_ready)
+            for (int i = tid; i < n16d; i += kFT) ((u32x4_t*)slab_dn)[i] = __builtin_nontemporal_load(srcd + i);
+        dn_ready = false;
+        const int e0 = s_start[g], e1 = s_start[g + 1];
+        for (int p = e0; p < e1; p += NE) {
+            const int m = min(NE, e1 - p);
+            if (p > e0) __syncthreads();
+            // h of the entries (polled until the gate/up units have written it) per 32 values to canonical q8_1
+            // (iq_kernels.cpp:2118-2133): 8 values a lane, a block on 4 neighbouring lanes
+            const int c8n = F / 8;
+            for (int i0 = 0; i0 < m * c8n; i0 += kFT) {
+                const int i = i0 + tid;
+                const bool in = i < m * c8n;
+                const int e = in ? i / c8n : 0, c8 = in ? i - e * c8n : 0;
+                float v[8];
+                if (!in || !gather_tagged<8>(a.hx + (int64_t)(p + e) * F + 8 * c8, 8, tag, a.spin_ticks, v)) {
+                    if (in) atomicOr(a.err, 2);
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) v[q] = 0.0f;
+                }
+                float amax = 0.0f;
+#pragma unroll
+                for (int q = 0; q < 8; ++q) amax = fmaxf(amax, fabsf(v[q]));
+                amax = fmaxf(amax, dpp_f<kDppXor1>(amax));
+                amax = fmaxf(amax, dpp_f<kDppXor2>(amax));
+                const float d = q8_scale(amax), id = q8_inv(d);
+                uint32_t w0 = 0, w1 = 0;
+                int sq = 0;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int q0 = q8_value(v[q], id), q1 = q8_value(v[4 + q], id);
+                    w0 |= (uint32_t)(uint8_t)q0 << (8 * q);
+                    w1 |= (uint32_t)(uint8_t)q1 << (8 * q);
+                    sq += q0 + q1;
+                }
+                const int s16 = sq + dpp_i<kDppXor1>(sq);
+                if (in) {
+                    int8_t* qd = (int8_t*)(lds + o.act_d) + e * act_stride(F);
+                    *(uint2*)(qd + 8 * c8) = make_uint2(w0, w1);
+                    if ((c8 & 1) == 0) ((int*)(qd + F + F / 8))[c8 >> 1] = s16;
+                    if ((c8 & 3) == 0) ((float*)(qd + F))[c8 >> 2] = h2f(f2h(d));
+                }
+            }
+            __syncthreads();
+            const int c = lane & (lpr_d - 1);
+            for (int rr = tid / lpr_d; rr < rd; rr += kFT / lpr_d) {
+                float acc[NE];
+#pragma unroll
+                for (int e = 0; e < NE; ++e) acc[e] = 0.0f;
+                for (int u = c; u < F / UD::kUnit; u += lpr_d)
+                    UD::template apply<NE>(slab_dn, rr * (int)L.d_row, u, actd, m, acc);
+#pragma unroll
+                for (int e = 0; e < NE; ++e) acc[e] = lanes_sum(acc[e], lpr_d);
+                if (c == 0) {
+#pragma unroll
+                    for (int e = 0; e < NE; ++e)
+                        if (e < m) st_tag(a.px + (int64_t)s_dst[p + e] * H + j * rd + rr, acc[e], tag);
+                }
+            }
+        }
+    }
+
+    // ---- 4. combines: (token t, down slab j), the slab's columns of the token's k parts in rank order + residual
+    for (int c = blockIdx.x; c < T * nj; c += gridDim.x) {
+        const int t = c / nj, j = c - t * nj;
+        for (int r = tid; r < rd; r += kFT) {
+            const int64_t col = (int64_t)j * rd + r;
+            const unsigned long long* pp = a.px + (int64_t)t * k * H + col;
+            const float* ww = s_w + t * k;
+            float sum = 0.0f;
+            bool good = true;
+            for (int e0 = 0; e0 < k; e0 += 16) {   // 16 parts in flight at once
+                float pv[16];
+                unsigned long long w[16];
+                const int ne = min(16, k - e0);
+                long long t0 = 0;
+                for (int it = 0;; ++it) {
+                    bool ok = true;
+#pragma unroll
+                    for (int q = 0; q < 16; ++q)
+                        if (q < ne) w[q] = ld_tag(pp + (int64_t)(e0 + q) * H);
+#pragma unroll
+                    for (int q = 0; q < 16; ++q)
+                        if (q < ne) {
+                            ok = ok && tag_ok(w[q], tag);
+                            pv[q] = tag_val(w[q]);
+                        }
+                    if (ok) break;
+                    if (it == 0) t0 = wall_clock64();
+                    else if (wall_clock64() - t0 > a.spin_ticks) {
+                        good = false;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+                }
+#pragma unroll
+                for (int q = 0; q < 16; ++q)
+                    if (q < ne) {
+                        const float prod = pv[q] * ww[e0 + q];
+                        sum = e0 + q == 0 ? prod : sum + prod;
+                    }
+            }
+            if (!good) atomicOr(a.err, 2);
+            a.out[(int64_t)t * H + col] = a.residual[(int64_t)t * H + col] + sum;
+        }
+    }
+    done_call(a, tag);
+}
+
+// ---------------------------------------------------------------- host side
+
+bool fused_decode_plan(const ExpertLayout& L, int n_expert, int k, int n_tok, FusedPlan* P) {
+    const int H = (int)L.n_embd, F = (int)L.n_ff, n = n_tok * k;
+    if (n > kFMaxN || n_expert > 1024 || k > 64 || n_tok > 64) return false;
+    const bool pair = (L.gu_type == kQ4_K && L.d_type == kQ6_K) || (L.gu_type == kQ8_0 && L.d_type == kQ8_0) ||
+                      (L.gu_type == kIQ4_XS && L.d_type == kIQ4_XS) || (L.gu_type == kQ4_K && L.d_type == kQ4_K);
+    if (!pair || H % 256 || F % 32) return false;
+    // h-slab rows: about 36 KB of gate + up rows, a multiple of 8 dividing n_ff
+    int rh = (int)((36864 / (2 * L.gu_row)) & ~7ll);
+    if (rh < 8) rh = 8;
+    while (rh > 8 && F % rh) rh -= 8;
+    if (F % rh) return false;
+    int rd = (int)((20480 / L.d_row) & ~7ll);
+    if (rd < 8) rd = 8;
+    if (rd > 64) rd = 64;
+    while (rd > 8 && H % rd) rd -= 8;
+    if (H % rd) return false;
+    P->rh = rh;
+    P->rd = rd;
+    P->nu = F / rh;
+    P->nj = H / rd;
+    P->slab_gu = 2 * rh * (int)L.gu_row;
+    P->slab_dn = rd * (int)L.d_row;
+    P->ne = n_tok >= 4 ? 4 : n_tok >= 2 ? 2 : 1;
+    const FusedLds lo = P->ne == 1 ? fused_lds<1>(n_expert, H, F, rh, P->slab_gu, P->slab_dn)
+                        : P->ne == 2 ? fused_lds<2>(n_expert, H, F, rh, P->slab_gu, P->slab_dn)
+                                     : fused_lds<4>(n_expert, H, F, rh, P->slab_gu, P->slab_dn);
+    P->lds = lo.total;
+    return P->lds <= 160 * 1024;
+}
+
+template <int TG, int TD>
+static void* pick(int ne) {
+    return ne == 1 ? (void*)moe_decode_fused_kernel<TG, TD, 1>
+         : ne == 2 ? (void*)moe_decode_fused_kernel<TG, TD, 2>
+                   : (void*)moe_decode_fused_kernel<TG, TD, 4>;
+}
+
+namespace {
+struct LaunchShape {   // per device and kernel: the attribute set and the resident work-groups
+    int dev;
+    const void* kern;
+    int lds, grid_max;
+};
+std::mutex g_shape_mu;
+std::vector<LaunchShape> g_shapes;
+}  // namespace
+
+static hipError_t resident_grid(const void* kern, int lds, int* grid_max) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    std::lock_guard<std::mutex> lock(g_shape_mu);
+    for (const LaunchShape& s : g_shapes)
+        if (s.dev == dev && s.kern == kern && s.lds == lds) {
+            *grid_max = s.grid_max;
+            return hipSuccess;
+        }
+    if (lds > 65536 && (e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds)) != hipSuccess)
+        return e;
+    int cus = 0, occ = 0;
+    if ((e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return e;
+    if ((e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, kFT, lds)) != hipSuccess) return e;
+    if (occ < 1) return hipErrorInvalidConfiguration;
+    *grid_max = cus * (occ > 2 ? 2 : occ);
+    g_shapes.push_back(LaunchShape{dev, kern, lds, *grid_max});
+    return hipSuccess;
+}
+
+hipError_t launch_decode_fused(const FusedArgs& a, const FusedPlan& P, hipStream_t s) {
+    void* kern = nullptr;
+    if (a.L.gu_type == kQ4_K && a.L.d_type == kQ6_K) kern = pick<kQ4_K, kQ6_K>(P.ne);
+    else if (a.L.gu_type == kQ8_0) kern = pick<kQ8_0, kQ8_0>(P.ne);
+    else if (a.L.gu_type == kIQ4_XS) kern = pick<kIQ4_XS, kIQ4_XS>(P.ne);
+    else kern = pick<kQ4_K, kQ4_K>(P.ne);
+    // every work-group resident at once: the down units wait on the gate/up units of others
+    int grid = 0;
+    hipError_t e = resident_grid(kern, P.lds, &grid);
+    if (e != hipSuccess) return e;
+    const int cap = a.n_tok * a.k < a.n_expert ? a.n_tok * a.k : a.n_expert;
+    const int need = cap * (P.nu > P.nj ? P.nu : P.nj);
+    if (grid > need) grid = need;
+    void* args[] = {(void*)&a};
+    return hipLaunchKernel(kern, dim3(grid), dim3(kFT), args, P.lds, s);
+}
+
+}  // namespace xs

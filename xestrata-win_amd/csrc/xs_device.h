@@ -107,6 +107,96 @@ __device__ __forceinline__ float group_max(float v) {
     return v;
 }
 
+// ---------------------------------------------------------------- DPP lane moves
+// A __shfl_xor is an LDS-unit round trip (ds_bpermute, ~100 cycles, serialised along a reduction); a DPP operand moves
+// lanes inside the VALU.  quad_perm [1,0,3,2] / [2,3,0,1] are the xor-1 / xor-2 exchanges; row_shl:4 gives lane i of a
+// 16-lane row the value of lane i + 4 (lanes 12..15 keep their own); row_ror:4 / :8 rotate a row.  The 16-lane rows
+// are joined with v_readlane (uniform results) or one ds_swizzle (xor 16 inside 32 lanes).
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppShl4 = 0x104, kDppRor4 = 0x124, kDppRor8 = 0x128;
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(v, v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(dpp_i<CTRL>(__float_as_int(v)));
+}
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double v) {
+    const long long b = __double_as_longlong(v);
+    const int lo = dpp_i<CTRL>((int)b), hi = dpp_i<CTRL>((int)(b >> 32));
+    return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+__device__ __forceinline__ float swz_xor16_f(float v) {   // lane i ^ 16 within each 32 lanes
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
+}
+__device__ __forceinline__ float readlane_f(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+__device__ __forceinline__ double readlane_d(double v, int l) {
+    const long long b = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_readlane((int)b, l), hi = __builtin_amdgcn_readlane((int)(b >> 32), l);
+    return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+
+constexpr int kDppBcast15 = 0x142, kDppBcast31 = 0x143;   // lane 15 of each row to the next row; lane 31 to rows 2, 3
+
+template <int CTRL, int ROWS>
+__device__ __forceinline__ unsigned long long dpp_u64(unsigned long long v) {
+    const int lo = __builtin_amdgcn_update_dpp((int)v, (int)v, CTRL, ROWS, 0xF, false);
+    const int hi = __builtin_amdgcn_update_dpp((int)(v >> 32), (int)(v >> 32), CTRL, ROWS, 0xF, false);
+    return ((unsigned long long)(unsigned int)hi << 32) | (unsigned int)lo;
+}
+__device__ __forceinline__ unsigned long long max_u64(unsigned long long a, unsigned long long b) { return a > b ? a : b; }
+// the largest 64-bit key of the wave, uniform: rows by xor and rotation, then rows 0+1 into row 1, 2+3 into row 3 and
+// row 1 into row 3 (row_bcast), read from lane 63.  Branch-free: no exec-mask or scalar round trips on the way.
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
+    v = max_u64(v, dpp_u64<kDppXor1, 0xF>(v));
+    v = max_u64(v, dpp_u64<kDppXor2, 0xF>(v));
+    v = max_u64(v, dpp_u64<kDppRor4, 0xF>(v));
+    v = max_u64(v, dpp_u64<kDppRor8, 0xF>(v));
+    v = max_u64(v, dpp_u64<kDppBcast15, 0xA>(v));
+    v = max_u64(v, dpp_u64<kDppBcast31, 0xC>(v));
+    const unsigned int lo = __builtin_amdgcn_readlane((int)v, 63), hi = __builtin_amdgcn_readlane((int)(v >> 32), 63);
+    return ((unsigned long long)hi << 32) | lo;
+}
+
+// max over each 16-lane row (every lane ends with its row's), over 32 lanes, over the wave (uniform); every lane of
+// the wave active
+__device__ __forceinline__ float row_max16(float v) {
+    v = fmaxf(v, dpp_f<kDppXor1>(v));
+    v = fmaxf(v, dpp_f<kDppXor2>(v));
+    v = fmaxf(v, dpp_f<kDppRor4>(v));
+    return fmaxf(v, dpp_f<kDppRor8>(v));
+}
+__device__ __forceinline__ float group_max32(float v) {
+    v = row_max16(v);
+    return fmaxf(v, swz_xor16_f(v));
+}
+__device__ __forceinline__ float wave_max(float v) {
+    v = row_max16(v);
+    return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
+}
+// a sum over the wave in an unspecified order (uniform result)
+__device__ __forceinline__ double wave_sum_d(double v) {
+    v += dpp_d<kDppXor1>(v);
+    v += dpp_d<kDppXor2>(v);
+    v += dpp_d<kDppRor4>(v);
+    v += dpp_d<kDppRor8>(v);
+    return (readlane_d(v, 0) + readlane_d(v, 16)) + (readlane_d(v, 32) + readlane_d(v, 48));
+}
+// The butterfly sum of a row dot over groups of L neighbouring lanes (L = 1, 2, 4, 8; o = L/2 .. 1): lane 0 of each
+// group ends with group_sum<L>'s value bit for bit (same operands in the same order); other lanes' values are
+// unspecified.
+template <int L>
+__device__ __forceinline__ float lane0_sum(float v) {
+    if (L >= 8) v += dpp_f<kDppShl4>(v);
+    if (L >= 4) v += dpp_f<kDppXor2>(v);
+    if (L >= 2) v += dpp_f<kDppXor1>(v);
+    return v;
+}
+
 // bytes of a 16-entry signed table picked by the 4 nibbles of `idx` bytes (each byte < 16): v_perm over the table's
 // halves, then a select on bit 3 of each index
 __device__ __forceinline__ int table16_lookup(uint32_t idx, uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3) {

@@ -61,6 +61,35 @@ hipError_t launch_decode_route(const float* logits, const float* x, int n_tok, i
                                int32_t* ids, float* weights, int32_t* plan, long long capx, uint32_t* skip,
                                const uint8_t* arena, long long blob, void* xq, hipStream_t s);
 
+// decode_fused.hip
+struct FusedPlan {     // the fused decode layer's unit sizes (a function of the layout alone, save ne and lds)
+    int rh, rd;        // SwiGLU outputs a gate/up unit, down rows a down unit
+    int nu, nj;        // gate/up units, down units a group
+    int slab_gu, slab_dn;
+    int ne, lds;       // entries a pass, dynamic LDS bytes
+};
+struct FusedArgs {
+    ExpertLayout L;
+    const uint8_t* arena;
+    long long blob;
+    int n_expert, k, n_tok;
+    const float* logits;    // [n_tok, n_expert]
+    const float* x;         // [n_tok, n_embd]
+    const float* residual;  // [n_tok, n_embd]
+    float* out;             // [n_tok, n_embd], may equal residual
+    int32_t* ids;           // [n_tok * k]
+    float* weights;         // [n_tok * k]
+    // hand-over words: a float's bits | the call's tag << 32 (tags never repeat, so no reset is needed)
+    unsigned long long* hx; // [256, n_ff] SwiGLU outputs, plan order
+    unsigned long long* px; // [256, n_embd] expert outputs, routing order
+    int32_t* sync;          // [0] the epoch (this call's tag - 1), [16] work-groups done; zero before the first call
+    int32_t* err;
+    int rh, rd, nu, nj, slab_gu_bytes, slab_dn_bytes;
+    long long spin_ticks;   // bound of a wait, in wall-clock ticks
+};
+bool fused_decode_plan(const ExpertLayout& L, int n_expert, int k, int n_tok, FusedPlan* P);
+hipError_t launch_decode_fused(const FusedArgs& a, const FusedPlan& P, hipStream_t s);
+
 // combine.hip
 hipError_t launch_combine(const float* parts, const float* weights, const float* shared, const float* shared_gate,
                           const float* residual, float* out, int64_t n_embd, int k, int n_tok, hipStream_t s);

@@ -18,7 +18,9 @@ __device__ __forceinline__ void better(float& bv, int& bi, float ov, int oi) {
 // of the k, 2^-14).  The serial sum runs only when a tree sum cannot decide inv: the serial and tree sums both lie
 // within 2^-43 of the exact sum (every term is positive, the largest exactly 1), so when the bracket tree * (1 -+
 // 2^-40) maps to one float inv, that float is the serial sum's.  PER experts a lane (n_expert <= 64 PER).  A row whose
-// ranks run out (NaN) leaves them as they were and renormalises the buffer (router.cpp:113-133).
+// ranks run out (NaN) leaves them as they were and renormalises the buffer (router.cpp:113-133).  Reductions move
+// lanes with DPP and v_readlane (xs_device.h): the argmax is order-free (a strict total order), the tree sum only
+// brackets inv, and the serial sums read lanes in order.  Every lane of the wave calls it.
 template <int PER>
 __device__ void route_topk_wave(const float* __restrict__ l, int n_expert, int k, int32_t* id_row, float* w_row) {
     const int lane = threadIdx.x & 63;
@@ -30,7 +32,7 @@ __device__ void route_topk_wave(const float* __restrict__ l, int n_expert, int k
         lv[j] = x < n_expert ? l[x] : -INFINITY;
         if (x < n_expert) mx = fmaxf(mx, lv[j]);
     }
-    mx = group_max<64>(mx);
+    mx = wave_max(mx);
     double ex[PER];
     double part = 0.0;
 #pragma unroll
@@ -39,8 +41,7 @@ __device__ void route_topk_wave(const float* __restrict__ l, int n_expert, int k
         ex[j] = x < n_expert ? exp((double)lv[j] - (double)mx) : 0.0;
         part += ex[j];
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) part += __shfl_xor(part, o, 64);
+    part = wave_sum_d(part);
     const double lo = part * (1.0 - 0x1p-40), hi = part * (1.0 + 0x1p-40);
     const float f_lo = (float)(1.0 / hi), f_hi = (float)(1.0 / lo);
     float inv;
@@ -48,38 +49,41 @@ __device__ void route_topk_wave(const float* __restrict__ l, int n_expert, int k
         inv = f_lo;
     } else {   // uniform over the wave: the serial ascending sum
         double sum = 0.0;
+#pragma unroll
         for (int j = 0; j < PER; ++j) {
             if (64 * j >= n_expert) break;
-            for (int s = 0; s < 64 && 64 * j + s < n_expert; ++s) sum += __shfl(ex[j], s, 64);
+            for (int s = 0; s < 64 && 64 * j + s < n_expert; ++s) sum += readlane_d(ex[j], s);
         }
         inv = (float)(1.0 / sum);
     }
-    float pv[PER];
-    uint32_t live = 0;
+    // candidates as 64-bit keys: the bits of p (non-negative, so ordered as unsigned) over the inverted index (a
+    // tie goes to the lower index); 0 = no candidate (NaN p never wins, taken experts drop out)
+    unsigned long long key[PER];
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
         const int x = lane + 64 * j;
-        pv[j] = -INFINITY;
-        if (x < n_expert) { pv[j] = (float)(ex[j] * (double)inv); live |= 1u << j; }
+        const float p = x < n_expert ? (float)(ex[j] * (double)inv) : __int_as_float(0x7FC00000);
+        key[j] = p == p ? ((unsigned long long)__float_as_uint(p) << 32) | (unsigned int)~x : 0ull;
     }
     float my_w = 0.0f;
     int my_id = 0, nsel = 0;
     for (int i = 0; i < k; ++i) {
-        float bv = -INFINITY;
-        int bi = n_expert;
+        unsigned long long best = key[0];
 #pragma unroll
-        for (int j = 0; j < PER; ++j)
-            if (((live >> j) & 1u) && pv[j] > bv) { bv = pv[j]; bi = lane + 64 * j; }
+        for (int j = 1; j < PER; ++j) best = max_u64(best, key[j]);
+        best = wave_max_u64(best);
+        if (best == 0ull) break;   // every p left is NaN: ranks i.. keep the buffer's contents
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) better(bv, bi, __shfl_xor(bv, o, 64), __shfl_xor(bi, o, 64));
-        if (bi >= n_expert) break;   // every p left is NaN: ranks i.. keep the buffer's contents
-        if ((bi & 63) == lane) live &= ~(1u << (bi >> 6));
-        if (lane == i) { my_w = bv; my_id = bi; }
+        for (int j = 0; j < PER; ++j) key[j] = key[j] == best ? 0ull : key[j];
+        if (lane == i) {
+            my_w = __uint_as_float((unsigned int)(best >> 32));
+            my_id = (int)~(unsigned int)best;
+        }
         nsel = i + 1;
     }
     if (nsel == k) {
         double s = 0.0;
-        for (int i = 0; i < k; ++i) s += (double)__shfl(my_w, i, 64);
+        for (int i = 0; i < k; ++i) s += (double)readlane_f(my_w, i);
         const double sc = fmax(s, 6.103515625e-05);
         if (lane < k) {
             id_row[lane] = my_id;
@@ -191,7 +195,7 @@ __device__ __forceinline__ void build_plan(const int* s_ids, int* s_first, int* 
 // q8_1 of values 8j .. 8j + 7 of rows whose width is a whole number of 256s (reference iq_kernels.cpp:1850-1879):
 // one scale for each 256 values (32 neighbouring lanes), stored in each of their eight blocks; a block's fp16 sum is
 // its four 8-value serial sums combined by the xor-1 then xor-2 exchange.  Every lane of the wave calls it (lanes
-// with j >= n8 pass in == false).
+// with j >= n8 pass in == false): the exchanges are DPP lane moves.
 __device__ __forceinline__ void q8_1_256_lane(const float* __restrict__ x, int64_t j, bool in, uint8_t* __restrict__ y) {
     float v[8], a = 0.0f, sum = 0.0f;
 #pragma unroll
@@ -201,9 +205,9 @@ __device__ __forceinline__ void q8_1_256_lane(const float* __restrict__ x, int64
         a = fmaxf(a, fabsf(v[q]));
         sum += v[q];
     }
-    const float amax = group_max<32>(a);
-    sum += __shfl_xor(sum, 1, 64);
-    sum += __shfl_xor(sum, 2, 64);
+    const float amax = group_max32(a);
+    sum += dpp_f<kDppXor1>(sum);
+    sum += dpp_f<kDppXor2>(sum);
     if (!in) return;
     const float d = q8_scale(amax), id = q8_inv(d);
     const int64_t ib = j / 4, o = 8 * (j % 4);

@@ -71,6 +71,7 @@ _SIGS = {
     "xs_add_inplace": (I, [P, P, I64, P]),
     "xs_moe_layer_decode": (I, [LP, P, SZ, I, I, P, P, P, P, I, P, SZ, P]),
     "xs_moe_layer_decode_workspace_bytes": (SZ, [LP, I, I, I]),
+    "xs_moe_layer_decode_status": (P, [P]),
     "xs_moe_layer_prefill": (I, [LP, P, SZ, I, I, P, P, P, P, I, P, SZ, P]),
     "xs_moe_layer_prefill_workspace_bytes": (SZ, [LP, I, I, I]),
 }
@@ -107,7 +108,7 @@ def _p(t):
 
 def _stream(stream=None):
     if stream is not None:
-        return stream
+        return getattr(stream, "cuda_stream", stream)   # a torch stream or a raw handle
     return torch.cuda.current_stream().cuda_stream
 
 
@@ -289,8 +290,17 @@ class MoeLayer:
         self.prefill = prefill
         fn = lib().xs_moe_layer_prefill_workspace_bytes if prefill else lib().xs_moe_layer_decode_workspace_bytes
         self.ws_bytes = fn(ctypes.byref(L), n_expert, k, max_tokens)
-        self.ws = torch.empty(self.ws_bytes + 256, dtype=torch.uint8, device=device)
+        # zeroed once: the decode layer's counters start at zero and every call leaves them there
+        self.ws = torch.zeros(self.ws_bytes + 256, dtype=torch.uint8, device=device)
         self.ws_ptr = (self.ws.data_ptr() + 255) & ~255
+
+    def status(self):
+        """The decode workspace's status word (0: every call so far was good).  Synchronizes the device."""
+        if self.prefill:
+            return 0
+        off = self.ws_ptr - self.ws.data_ptr()
+        torch.cuda.synchronize(self.ws.device)
+        return int(self.ws[off:off + 4].view(torch.int32).item())
 
     def __call__(self, x, logits, residual, out, n_tok=None, arena=None, stream=None):
         n_tok = x.shape[0] if n_tok is None else n_tok
