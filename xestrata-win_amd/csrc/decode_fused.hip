@@ -30,11 +30,12 @@ namespace xs {
 
 constexpr int kFT = 256;          // threads a work-group
 constexpr int kFMaxN = 256;       // routed entries (tokens x k) a call
-constexpr int kFRegs = 12;        // 16-byte chunks of gate/up rows a thread holds in flight
-constexpr int kFRegsD = 8;        // and of the prefetched down rows
+constexpr int kLoadWaves = 3;     // waves 0..2 issue every global load; wave 3 every tagged store
+constexpr int kLT = 64 * kLoadWaves;
 
 struct FusedLds {                 // byte offsets in the dynamic LDS
-    int ids, w, excl, wave, first, gexp, start, dst, tok, misc, gu, slab_gu, slab_dn, act_g, act_d, total;
+    int ids, w, excl, wave, first, gexp, start, dst, tok, misc, key, red, sel, gu, po, slab_gu, slab_dn, act_g, act_d,
+        total;
 };
 
 __host__ __device__ inline int up16(int v) { return (v + 15) & ~15; }
@@ -55,7 +56,11 @@ __host__ __device__ inline FusedLds fused_lds(int n_expert, int H, int F, int rh
     o.dst = at; at += up16(kFMaxN * 4);
     o.tok = at; at += up16(kFMaxN * 4);
     o.misc = at; at += up16(96 * 4);
+    o.key = at; at += 256 * 8;
+    o.red = at; at += 16 * 8;
+    o.sel = at; at += 128 * 4;
     o.gu = at; at += up16(NE * 2 * rh * 4);
+    o.po = at; at += up16(NE * 64 * 4);
     o.slab_gu = at; at += up16(slab_gu);
     o.slab_dn = at; at += up16(slab_dn);
     o.act_g = at; at += NE * act_stride(H);
@@ -114,6 +119,25 @@ __device__ __forceinline__ int add_dev(int32_t* p, int v) {
     return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Every vector memory access of a wave counts on one in-order counter (vmcnt): a wave that waits for a load also waits
+// for the acknowledgement of every store it issued before, and stores are acknowledged late while the weight stream
+// fills the memory queues.  So the waves that load never store a hand-over word: waves 0..2 fetch (weights by DMA,
+// activations, polls), wave 3 writes h and parts from LDS.
+__device__ __forceinline__ void vm_drain() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// n16 16-byte chunks to LDS dst[0 .. n16) by DMA (global_load_lds_dwordx4: a wave's instruction fills 64 consecutive
+// chunks at a wave-uniform LDS address), chunk i from src(i); issued by the load waves, complete at their vm_drain()
+template <typename Src>
+__device__ __forceinline__ void dma_to_lds(uint8_t* dst, int n16, Src src) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int base = 64 * wave; base < n16; base += kLT) {
+        const int i = base + lane;
+        if (i < n16)
+            __builtin_amdgcn_global_load_lds(src(i), (__attribute__((address_space(3))) void*)(dst + 16 * base), 16, 0,
+                                             2 /* nt */);
+    }
+}
+
 // N tagged words from p into v, polled until all carry the tag or the bound passes (then false, values undefined)
 template <int N>
 __device__ __forceinline__ bool gather_tagged(const unsigned long long* p, int n, unsigned int tag, long long ticks,
@@ -143,12 +167,36 @@ __device__ __forceinline__ float lanes_sum(float v, int l) {
     return l == 8 ? lane0_sum<8>(v) : l == 4 ? lane0_sum<4>(v) : l == 2 ? lane0_sum<2>(v) : v;
 }
 
-// The work-group is done with the call; the last one advances the epoch (every work-group read it before it counted
-// itself done) and clears the count.
+// The work-group is done with the call.  Work-groups count themselves done in eight sub-counters (blockIdx % 8, 64
+// atomics an address instead of 512 on one), the last of a sub-count in a top counter, and the last of the top count
+// advances the epoch and clears the counters: every work-group read the epoch before it counted itself done.
 __device__ __forceinline__ void done_call(const FusedArgs& a, unsigned int tag) {
-    if (threadIdx.x == 0 && add_dev(a.sync + 16, 1) == (int)gridDim.x - 1) {
-        __hip_atomic_store(a.sync + 16, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(a.sync, (int)tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x != 0) return;
+    const int G = (int)gridDim.x, sub = (int)blockIdx.x & 7;
+    const int in_sub = G / 8 + (sub < G % 8 ? 1 : 0);
+    const int subs = G < 8 ? G : 8;
+    if (add_dev(a.sync + 32 + 16 * sub, 1) != in_sub - 1) return;
+    __hip_atomic_store(a.sync + 32 + 16 * sub, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (add_dev(a.sync + 16, 1) != subs - 1) return;
+    __hip_atomic_store(a.sync + 16, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(a.sync, (int)tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int PER>
+__device__ __forceinline__ void route_tokens_wave(const FusedArgs& a, int* s_ids, float* s_w, int& epoch) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, E = a.n_expert, k = a.k;
+    float lv[PER];
+    if (wave < a.n_tok) load_logits_wave<PER>(a.logits + (int64_t)wave * E, E, lv);
+    if (tid == 0) {
+        epoch = __hip_atomic_load(a.sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    for (int t = wave; t < a.n_tok; t += kFT / 64) {
+        if (lane < k) {   // ranks a NaN row leaves unwritten stay invalid
+            s_ids[t * k + lane] = -1;
+            s_w[t * k + lane] = 0.0f;
+        }
+        if (t != wave) load_logits_wave<PER>(a.logits + (int64_t)t * E, E, lv);
+        route_topk_wave_lv<PER>(lv, E, k, s_ids + t * k, s_w + t * k);
     }
 }
 
@@ -185,23 +233,57 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
         actd[e] = Act{qd, (const float*)(qd + F), (const int*)(qd + F + F / 8)};
     }
 
-    if (tid == 0) s_misc[3] = __hip_atomic_load(a.sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // ---- 1. routing, in every work-group (router.cpp:59-308 and verify_kernels.cpp:819-890's order, in LDS)
-    for (int t = wave; t < T; t += kFT / 64) {
-        if (lane < k) {   // ranks a NaN row leaves unwritten stay invalid
-            s_ids[t * k + lane] = -1;
-            s_w[t * k + lane] = 0.0f;
+    // ---- 1. routing, in every work-group (router.cpp:59-308 and verify_kernels.cpp:819-890's order, in LDS): up to
+    // three tokens on the whole work-group each, more on a wave each.  The logits loads go out first; thread 0 then
+    // reads the epoch, used only after the routing, so its latency hides behind it.
+    int epoch = 0;
+    if (T <= 3 && E <= 256) {
+        float lvp[3];
+#pragma unroll
+        for (int t = 0; t < 3; ++t) lvp[t] = t < T && tid < E ? a.logits[(int64_t)t * E + tid] : 0.0f;
+        if (tid == 0) {
+            epoch = __hip_atomic_load(a.sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        const float* lr = a.logits + (int64_t)t * E;
-        if (E <= 64) route_topk_wave<1>(lr, E, k, s_ids + t * k, s_w + t * k);
-        else if (E <= 128) route_topk_wave<2>(lr, E, k, s_ids + t * k, s_w + t * k);
-        else if (E <= 256) route_topk_wave<4>(lr, E, k, s_ids + t * k, s_w + t * k);
-        else if (E <= 512) route_topk_wave<8>(lr, E, k, s_ids + t * k, s_w + t * k);
-        else route_topk_wave<16>(lr, E, k, s_ids + t * k, s_w + t * k);
+        if (tid < n) {   // ranks a NaN row leaves unwritten stay invalid
+            s_ids[tid] = -1;
+            s_w[tid] = 0.0f;
+        }
+#pragma unroll
+        for (int t = 0; t < 3; ++t)
+            if (t < T)
+                route_topk_block(lvp[t], E, k, (unsigned long long*)(lds + o.key), s_excl, (double*)(lds + o.red),
+                                 (int*)(lds + o.sel), s_ids + t * k, s_w + t * k);
+    } else if (E <= 64) {
+        route_tokens_wave<1>(a, s_ids, s_w, epoch);
+    } else if (E <= 128) {
+        route_tokens_wave<2>(a, s_ids, s_w, epoch);
+    } else if (E <= 256) {
+        route_tokens_wave<4>(a, s_ids, s_w, epoch);
+    } else if (E <= 512) {
+        route_tokens_wave<8>(a, s_ids, s_w, epoch);
+    } else {
+        route_tokens_wave<16>(a, s_ids, s_w, epoch);
     }
+    if (tid == 0) s_misc[3] = epoch;
     __syncthreads();
     // the plan: groups = distinct experts in order of first occurrence, a group's entries ascending
-    if (n <= 64) {   // one wave: uniform v_readlane loops, no work-group scan
+    if (T == 1) {   // one token: its k experts are distinct, each a group of one entry, in rank order
+        const int ex = tid < n ? s_ids[tid] : 0;
+        if (__syncthreads_or(tid < n && (ex < 0 || ex >= E))) {
+            if (tid == 0) s_misc[0] = -1;
+        } else {
+            if (tid < n) {
+                s_gexp[tid] = ex;
+                s_start[tid] = tid;
+                s_dst[tid] = tid;
+                s_tok[tid] = 0;
+            }
+            if (tid == 0) {
+                s_start[n] = n;
+                s_misc[0] = n;
+            }
+        }
+    } else if (n <= 64) {   // one wave: uniform v_readlane loops, no work-group scan
         if (wave == 0) {
             const int ex = lane < n ? s_ids[lane] : -1;
             if (__ballot(lane < n && (ex < 0 || ex >= E)) == 0) {
@@ -284,64 +366,36 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
         a.weights[tid] = s_w[tid];
     }
     const int ng = s_misc[0];
+    const int wg = blockIdx.x;
     const int n_gu = ng * nu, n_dn = ng * nj;
     const int lpr_g = canon_lanes(H / UG::kUnit), lpr_d = canon_lanes(F / UD::kUnit);
 
-    // ---- 2. gate/up units; the work-group's first down unit is fetched with its first one
-    bool dn_ready = false;
-    for (int u1 = blockIdx.x; u1 < n_gu; u1 += gridDim.x) {
+    // ---- 2. gate/up units
+    const int n16a = rh * (int)L.gu_row / 16, n16d = rd * (int)L.d_row / 16;
+    float* s_po = (float*)(lds + o.po);
+    const bool loader = wave < kLoadWaves;
+    for (int u1 = wg; u1 < n_gu; u1 += gridDim.x) {
         const int g = u1 / nu, j = u1 - g * nu;
         const uint8_t* blob = a.arena + (size_t)s_gexp[g] * (size_t)a.blob;
-        const int n16a = rh * (int)L.gu_row / 16;
-        const u32x4_t* srcg = (const u32x4_t*)(blob + (size_t)j * rh * L.gu_row);
-        const u32x4_t* srcu = (const u32x4_t*)(blob + L.up_off + (size_t)j * rh * L.gu_row);
+        const uint8_t* srcg = blob + (size_t)j * rh * L.gu_row;
+        const uint8_t* srcu = blob + L.up_off + (size_t)j * rh * L.gu_row;
         __syncthreads();   // the previous unit's readers of the slab are done
-        u32x4_t v[kFRegs];
-#pragma unroll
-        for (int r = 0; r < kFRegs; ++r) {
-            const int i = r * kFT + tid;
-            if (i < 2 * n16a) v[r] = __builtin_nontemporal_load(i < n16a ? srcg + i : srcu + (i - n16a));
-        }
-        const bool pre = !dn_ready && blockIdx.x < n_dn;
-        u32x4_t vd[kFRegsD];
-        const int n16d = rd * (int)L.d_row / 16;
-        if (pre) {
-            const int gd = blockIdx.x / nj, jd = blockIdx.x - gd * nj;
-            const u32x4_t* srcd = (const u32x4_t*)(a.arena + (size_t)s_gexp[gd] * (size_t)a.blob + L.down_off +
-                                                   (size_t)jd * rd * L.d_row);
-#pragma unroll
-            for (int r = 0; r < kFRegsD; ++r) {
-                const int i = r * kFT + tid;
-                if (i < n16d) vd[r] = __builtin_nontemporal_load(srcd + i);
-            }
-            for (int i = kFRegsD * kFT + tid; i < n16d; i += kFT) ((u32x4_t*)slab_dn)[i] = srcd[i];
-        }
+        if (loader)
+            dma_to_lds(slab_gu, 2 * n16a, [&](int i) {
+                return (const void*)(i < n16a ? srcg + 16 * (size_t)i : srcu + 16 * (size_t)(i - n16a));
+            });
         const int e0 = s_start[g], e1 = s_start[g + 1];
         for (int p = e0; p < e1; p += NE) {
             const int m = min(NE, e1 - p);
             if (p > e0) __syncthreads();   // the previous pass's readers of the activations are done
-            for (int e = 0; e < m; ++e) {    // the entries' tokens to q8_1, one scale a 256
-                const float* xr = a.x + (int64_t)s_tok[p + e] * H;
-                int8_t* q = (int8_t*)(lds + o.act_g) + e * act_stride(H);
-                for (int j8 = tid; j8 < H / 8; j8 += kFT)
-                    q8_1_256_to_act(xr, j8, q, (float*)(q + H), (int*)(q + H + H / 8));
-            }
-            if (p == e0) {
-#pragma unroll
-                for (int r = 0; r < kFRegs; ++r) {
-                    const int i = r * kFT + tid;
-                    if (i < 2 * n16a) ((u32x4_t*)slab_gu)[i] = v[r];
+            if (loader) {
+                for (int e = 0; e < m; ++e) {    // the entries' tokens to q8_1, one scale a 256
+                    const float* xr = a.x + (int64_t)s_tok[p + e] * H;
+                    int8_t* q = (int8_t*)(lds + o.act_g) + e * act_stride(H);
+                    for (int j8 = tid; j8 < H / 8; j8 += kLT)
+                        q8_1_256_to_act(xr, j8, q, (float*)(q + H), (int*)(q + H + H / 8));
                 }
-                for (int i = kFRegs * kFT + tid; i < 2 * n16a; i += kFT)
-                    ((u32x4_t*)slab_gu)[i] = i < n16a ? srcg[i] : srcu[i - n16a];
-                if (pre) {
-#pragma unroll
-                    for (int r = 0; r < kFRegsD; ++r) {
-                        const int i = r * kFT + tid;
-                        if (i < n16d) ((u32x4_t*)slab_dn)[i] = vd[r];
-                    }
-                    dn_ready = true;
-                }
+                vm_drain();   // the slab and the activations have landed
             }
             __syncthreads();
             const int c = lane & (lpr_g - 1);
@@ -360,63 +414,63 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
                 }
             }
             __syncthreads();
-            for (int i = tid; i < m * rh; i += kFT) {
-                const int e = i / rh, r = i - e * rh;
-                st_tag(a.hx + (int64_t)(p + e) * F + j * rh + r,
-                       canon_silu_mul(s_gu[e * 2 * rh + r], s_gu[e * 2 * rh + rh + r]), tag);
-            }
+            if (!loader)
+                for (int i = lane; i < m * rh; i += 64) {
+                    const int e = i / rh, r = i - e * rh;
+                    st_tag(a.hx + (int64_t)(p + e) * F + j * rh + r,
+                           canon_silu_mul(s_gu[e * 2 * rh + r], s_gu[e * 2 * rh + rh + r]), tag);
+                }
         }
     }
 
-    // ---- 3. down units
-    for (int u2 = blockIdx.x; u2 < n_dn; u2 += gridDim.x) {
+    // ---- 3. down units; the first one's rows are fetched once the gate/up rows are in (they go first)
+    for (int u2 = wg; u2 < n_dn; u2 += gridDim.x) {
         const int g = u2 / nj, j = u2 - g * nj;
-        const uint8_t* blob = a.arena + (size_t)s_gexp[g] * (size_t)a.blob;
-        const u32x4_t* srcd = (const u32x4_t*)(blob + L.down_off + (size_t)j * rd * L.d_row);
-        const int n16d = rd * (int)L.d_row / 16;
+        const uint8_t* srcd = a.arena + (size_t)s_gexp[g] * (size_t)a.blob + L.down_off + (size_t)j * rd * L.d_row;
         __syncthreads();   // the previous unit's readers of the slab are done
-        if (!dn_ready)
-            for (int i = tid; i < n16d; i += kFT) ((u32x4_t*)slab_dn)[i] = __builtin_nontemporal_load(srcd + i);
-        dn_ready = false;
+        if (loader) dma_to_lds(slab_dn, n16d, [&](int i) { return (const void*)(srcd + 16 * (size_t)i); });
         const int e0 = s_start[g], e1 = s_start[g + 1];
         for (int p = e0; p < e1; p += NE) {
             const int m = min(NE, e1 - p);
             if (p > e0) __syncthreads();
             // h of the entries (polled until the gate/up units have written it) per 32 values to canonical q8_1
             // (iq_kernels.cpp:2118-2133): 8 values a lane, a block on 4 neighbouring lanes
-            const int c8n = F / 8;
-            for (int i0 = 0; i0 < m * c8n; i0 += kFT) {
-                const int i = i0 + tid;
-                const bool in = i < m * c8n;
-                const int e = in ? i / c8n : 0, c8 = in ? i - e * c8n : 0;
-                float v[8];
-                if (!in || !gather_tagged<8>(a.hx + (int64_t)(p + e) * F + 8 * c8, 8, tag, a.spin_ticks, v)) {
-                    if (in) atomicOr(a.err, 2);
+            if (loader) {
+                const int c8n = F / 8;
+                for (int i0 = 0; i0 < m * c8n; i0 += kLT) {
+                    const int i = i0 + tid;
+                    const bool in = i < m * c8n;
+                    const int e = in ? i / c8n : 0, c8 = in ? i - e * c8n : 0;
+                    float v[8];
+                    if (!in || !gather_tagged<8>(a.hx + (int64_t)(p + e) * F + 8 * c8, 8, tag, a.spin_ticks, v)) {
+                        if (in) atomicOr(a.err, 2);
 #pragma unroll
-                    for (int q = 0; q < 8; ++q) v[q] = 0.0f;
-                }
-                float amax = 0.0f;
+                        for (int q = 0; q < 8; ++q) v[q] = 0.0f;
+                    }
+                    float amax = 0.0f;
 #pragma unroll
-                for (int q = 0; q < 8; ++q) amax = fmaxf(amax, fabsf(v[q]));
-                amax = fmaxf(amax, dpp_f<kDppXor1>(amax));
-                amax = fmaxf(amax, dpp_f<kDppXor2>(amax));
-                const float d = q8_scale(amax), id = q8_inv(d);
-                uint32_t w0 = 0, w1 = 0;
-                int sq = 0;
+                    for (int q = 0; q < 8; ++q) amax = fmaxf(amax, fabsf(v[q]));
+                    amax = fmaxf(amax, dpp_f<kDppXor1>(amax));
+                    amax = fmaxf(amax, dpp_f<kDppXor2>(amax));
+                    const float d = q8_scale(amax), id = q8_inv(d);
+                    uint32_t w0 = 0, w1 = 0;
+                    int sq = 0;
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int q0 = q8_value(v[q], id), q1 = q8_value(v[4 + q], id);
-                    w0 |= (uint32_t)(uint8_t)q0 << (8 * q);
-                    w1 |= (uint32_t)(uint8_t)q1 << (8 * q);
-                    sq += q0 + q1;
+                    for (int q = 0; q < 4; ++q) {
+                        const int q0 = q8_value(v[q], id), q1 = q8_value(v[4 + q], id);
+                        w0 |= (uint32_t)(uint8_t)q0 << (8 * q);
+                        w1 |= (uint32_t)(uint8_t)q1 << (8 * q);
+                        sq += q0 + q1;
+                    }
+                    const int s16 = sq + dpp_i<kDppXor1>(sq);
+                    if (in) {
+                        int8_t* qd = (int8_t*)(lds + o.act_d) + e * act_stride(F);
+                        *(uint2*)(qd + 8 * c8) = make_uint2(w0, w1);
+                        if ((c8 & 1) == 0) ((int*)(qd + F + F / 8))[c8 >> 1] = s16;
+                        if ((c8 & 3) == 0) ((float*)(qd + F))[c8 >> 2] = h2f(f2h(d));
+                    }
                 }
-                const int s16 = sq + dpp_i<kDppXor1>(sq);
-                if (in) {
-                    int8_t* qd = (int8_t*)(lds + o.act_d) + e * act_stride(F);
-                    *(uint2*)(qd + 8 * c8) = make_uint2(w0, w1);
-                    if ((c8 & 1) == 0) ((int*)(qd + F + F / 8))[c8 >> 1] = s16;
-                    if ((c8 & 3) == 0) ((float*)(qd + F))[c8 >> 2] = h2f(f2h(d));
-                }
+                vm_drain();   // the slab has landed
             }
             __syncthreads();
             const int c = lane & (lpr_d - 1);
@@ -431,14 +485,20 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
                 if (c == 0) {
 #pragma unroll
                     for (int e = 0; e < NE; ++e)
-                        if (e < m) st_tag(a.px + (int64_t)s_dst[p + e] * H + j * rd + rr, acc[e], tag);
+                        if (e < m) s_po[e * rd + rr] = acc[e];
                 }
             }
+            __syncthreads();
+            if (!loader)
+                for (int i = lane; i < m * rd; i += 64) {
+                    const int e = i / rd, r = i - e * rd;
+                    st_tag(a.px + (int64_t)s_dst[p + e] * H + j * rd + r, s_po[e * rd + r], tag);
+                }
         }
     }
 
     // ---- 4. combines: (token t, down slab j), the slab's columns of the token's k parts in rank order + residual
-    for (int c = blockIdx.x; c < T * nj; c += gridDim.x) {
+    for (int c = wg; c < T * nj; c += gridDim.x) {
         const int t = c / nj, j = c - t * nj;
         for (int r = tid; r < rd; r += kFT) {
             const int64_t col = (int64_t)j * rd + r;

@@ -82,7 +82,8 @@ struct FusedArgs {
     // hand-over words: a float's bits | the call's tag << 32 (tags never repeat, so no reset is needed)
     unsigned long long* hx; // [256, n_ff] SwiGLU outputs, plan order
     unsigned long long* px; // [256, n_embd] expert outputs, routing order
-    int32_t* sync;          // [0] the epoch (this call's tag - 1), [16] work-groups done; zero before the first call
+    int32_t* sync;          // [0] the epoch (this call's tag - 1), [16] sub-counts done, [32 + 16 s] work-groups
+                            // done in sub-count s (8); zero before the first call
     int32_t* err;
     int rh, rd, nu, nj, slab_gu_bytes, slab_dn_bytes;
     long long spin_ticks;   // bound of a wait, in wall-clock ticks

@@ -22,16 +22,19 @@ __device__ __forceinline__ void better(float& bv, int& bi, float ov, int oi) {
 // lanes with DPP and v_readlane (xs_device.h): the argmax is order-free (a strict total order), the tree sum only
 // brackets inv, and the serial sums read lanes in order.  Every lane of the wave calls it.
 template <int PER>
-__device__ void route_topk_wave(const float* __restrict__ l, int n_expert, int k, int32_t* id_row, float* w_row) {
+__device__ __forceinline__ void load_logits_wave(const float* __restrict__ l, int n_expert, float (&lv)[PER]) {
     const int lane = threadIdx.x & 63;
-    float lv[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) lv[j] = lane + 64 * j < n_expert ? l[lane + 64 * j] : -INFINITY;
+}
+// the same on logits already loaded (load_logits_wave)
+template <int PER>
+__device__ void route_topk_wave_lv(const float (&lv)[PER], int n_expert, int k, int32_t* id_row, float* w_row) {
+    const int lane = threadIdx.x & 63;
     float mx = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < PER; ++j) {
-        const int x = lane + 64 * j;
-        lv[j] = x < n_expert ? l[x] : -INFINITY;
-        if (x < n_expert) mx = fmaxf(mx, lv[j]);
-    }
+    for (int j = 0; j < PER; ++j)
+        if (lane + 64 * j < n_expert) mx = fmaxf(mx, lv[j]);
     mx = wave_max(mx);
     double ex[PER];
     double part = 0.0;
@@ -98,6 +101,94 @@ __device__ void route_topk_wave(const float* __restrict__ l, int n_expert, int k
             for (int i = 0; i < k; ++i) s += (double)w_row[i];
             const double sc = fmax(s, 6.103515625e-05);
             for (int i = 0; i < k; ++i) w_row[i] = (float)((double)w_row[i] / sc);
+        }
+    }
+}
+
+template <int PER>
+__device__ void route_topk_wave(const float* __restrict__ l, int n_expert, int k, int32_t* id_row, float* w_row) {
+    float lv[PER];
+    load_logits_wave<PER>(l, n_expert, lv);
+    route_topk_wave_lv<PER>(lv, n_expert, k, id_row, w_row);
+}
+
+// Softmax top-k of one token on a work-group of 256 threads (n_expert <= 256, expert tid on thread tid), bit for bit
+// route_topk_wave: the same max, exp, bracketed (else serial ascending) sum and p, the same renormalisation; the k
+// largest keys are found by counting, for every key, the keys above it - the four waves compare in parallel instead
+// of k dependent argmax passes on one wave.  lv: this thread's logit (ignored for tid >= n_expert).  Scratch in LDS:
+// s_key [256] u64, s_rank [256] int, s_red [16] double, s_sel [128] int.  Every thread calls it.  Ranks a NaN row
+// leaves unfilled are not written (id_row keeps what the caller put there).
+__device__ void route_topk_block(float lv, int n_expert, int k, unsigned long long* s_key, int* s_rank, double* s_red,
+                                 int* s_sel, int32_t* id_row, float* w_row) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const bool in = tid < n_expert;
+    const float m = wave_max(in ? lv : -INFINITY);
+    if (lane == 0) s_red[wave] = (double)m;
+    if (tid < k) s_sel[tid] = -1;
+    __syncthreads();
+    const float mx = fmaxf(fmaxf((float)s_red[0], (float)s_red[1]), fmaxf((float)s_red[2], (float)s_red[3]));
+    const double exv = in ? exp((double)lv - (double)mx) : 0.0;
+    const double ps = wave_sum_d(exv);
+    if (lane == 0) s_red[4 + wave] = ps;
+    __syncthreads();
+    const double part = (s_red[4] + s_red[5]) + (s_red[6] + s_red[7]);
+    const double lo = part * (1.0 - 0x1p-40), hi = part * (1.0 + 0x1p-40);
+    const float f_lo = (float)(1.0 / hi), f_hi = (float)(1.0 / lo);
+    float inv;
+    if (part >= 1.0 && hi < 1e300 && f_lo == f_hi) {
+        inv = f_lo;
+    } else {   // uniform over the work-group: the serial ascending sum
+        double* s_ex = (double*)s_key;
+        s_ex[tid] = exv;
+        __syncthreads();
+        if (tid == 0) {
+            double sum = 0.0;
+            for (int i = 0; i < n_expert; ++i) sum += s_ex[i];
+            s_red[8] = sum;
+        }
+        __syncthreads();
+        inv = (float)(1.0 / s_red[8]);
+        __syncthreads();
+    }
+    const float p = in ? (float)(exv * (double)inv) : 0.0f;
+    const unsigned long long key = in && p == p ? ((unsigned long long)__float_as_uint(p) << 32) | (unsigned int)~tid : 0ull;
+    s_key[tid] = key;   // 0 past n_expert: never above a key
+    __syncthreads();
+    int above = 0;
+    if (n_expert <= 128) {   // two threads a key, half the keys each
+        const int i = tid & 127, h = tid >> 7;
+        const unsigned long long mine = s_key[i];
+#pragma unroll 8
+        for (int j = 64 * h; j < 64 * h + 64; j += 2) {
+            const ulonglong2 kk = *(const ulonglong2*)(s_key + j);
+            above += (kk.x > mine ? 1 : 0) + (kk.y > mine ? 1 : 0);
+        }
+        s_rank[tid] = above;
+        __syncthreads();
+        if (tid < 128) above += s_rank[tid + 128];
+    } else {
+#pragma unroll 8
+        for (int j = 0; j < 256; j += 2) {
+            const ulonglong2 kk = *(const ulonglong2*)(s_key + j);
+            above += (kk.x > key ? 1 : 0) + (kk.y > key ? 1 : 0);
+        }
+    }
+    if (in && key != 0ull && above < k) {
+        s_sel[above] = tid;
+        s_sel[64 + above] = __float_as_int(p);
+    }
+    __syncthreads();
+    if (tid < k) {
+        double sum = 0.0;
+        bool full = true;
+        for (int q = 0; q < k; ++q) {
+            full = full && s_sel[q] >= 0;
+            sum += (double)__int_as_float(s_sel[64 + q]);
+        }
+        if (full) {
+            const double sc = fmax(sum, 6.103515625e-05);
+            id_row[tid] = s_sel[tid];
+            w_row[tid] = (float)((double)__int_as_float(s_sel[64 + tid]) / sc);
         }
     }
 }
