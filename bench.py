@@ -53,6 +53,45 @@ def graph_time(torch, fn, replays):
     return e0.elapsed_time(e1) / replays, g
 
 
+TRAFFIC_FILE = ROOT / "profiles" / "moe_decode_fused_config2_traffic.md"
+
+
+def read_traffic():
+    """HBM bytes per launch of the fused decode kernel, from the committed rocprofv3 --pmc summary (FETCH_SIZE +
+    WRITE_SIZE scaled by a copy kernel of known size), or None when that summary is absent."""
+    try:
+        for line in open(TRAFFIC_FILE):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1].strip())
+    except (OSError, ValueError):
+        pass
+    return None
+
+
+def pmc_run(torch, xm, copies):
+    """The workload of a rocprofv3 --pmc pass: 32 config-2 decode layers at T=1 (one launch each, rotating over the
+    HBM copies) and, for calibration, 4 device-to-device copies of 256 MiB."""
+    E, H, F, k = 128, 2048, 768, 8
+    arena, L = xm.build_arena(E, H, F, xm.Q4_K, xm.Q6_K, seed=0, copies=copies)
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    logits = torch.randn(copies, 1, E, device="cuda", generator=gen)
+    x = torch.randn(1, H, device="cuda", generator=gen).to(torch.bfloat16).float()
+    res = torch.randn(1, H, device="cuda", generator=gen)
+    out = torch.empty(1, H, device="cuda")
+    layer = xm.MoeLayer(L, arena, E, k, 1)
+    for i in range(32):
+        c = i % copies
+        layer(x, logits[c], res, out, arena=arena[c * E])
+    src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    distinct = [len(torch.unique(torch.topk(logits[c, 0], k).indices)) for c in range(copies)]
+    log(f"pmc run: 32 decode layers ({sum(distinct) / copies * L.bytes / 1e6:.2f} MB of expert weights each), "
+        f"4 copies of {256 << 20} bytes; status {layer.status()}")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -62,6 +101,7 @@ def main():
     ap.add_argument("--prefill-steps", type=int, default=10)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--pmc-run", action="store_true", help="only the short workload of a rocprofv3 --pmc pass")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -75,6 +115,9 @@ def main():
 
     dev = "cuda:0"
     torch.cuda.set_device(0)
+    if args.pmc_run:
+        pmc_run(torch, xm, args.copies)
+        return
     E, H, F, k = 128, 2048, 768, 8
     copies = args.copies
     log(f"building {copies} copies of the config-2 layer ({E} experts, Q4_K/Q6_K)")
@@ -114,44 +157,16 @@ def main():
     gbs1 = bytes1 / (ms1 * 1e-3) / 1e9
     log(f"decode T=1: {ms1 * 1e3:.2f} us/layer, {gbs1:.0f} GB/s expert weights")
 
-    # ---------------------------------------------------------------- the dominant kernel alone (gate/up rows)
-    T = 1
-    ids_l, plans = [], []
-    capx = T * k
-    logits = torch.randn(copies, T, E, device=dev, generator=gen)
-    x = torch.randn(T, H, device=dev, generator=gen).to(torch.bfloat16).float()
-    xq = xm.quantize_q8_1_rows(x)
-    o = xm.plan_offsets(capx)
-    for c in range(copies):
-        ids, w = xm.router_top10(logits[c], k)
-        plan = torch.zeros(xm.plan_words(capx) + 2, dtype=torch.int32, device=dev)
-        skip = torch.zeros(1, dtype=torch.int32, device=dev)
-        xm.resident_plan(ids.reshape(-1), k, None, E, arena[c * E].data_ptr(), None, blob, plan, capx, skip, 1)
-        plans.append(plan)
-    scratch = torch.zeros(xm.native_expert_scratch_bytes(capx, F), dtype=torch.uint8, device=dev)
-    parts = torch.zeros(capx, H, device=dev)
-    cap_groups = min(capx, E)
-
-    def gu_round():
-        for p in plans:
-            ptr = p[o["ptr"]:o["ptr"] + 2 * capx].view(torch.int64)
-            xm.native_expert_gate_up(L, ptr, p[4:], p[0:1], p[o["tok"]:], cap_groups, capx, xq, scratch)
-
-    def down_round():
-        for p in plans:
-            ptr = p[o["ptr"]:o["ptr"] + 2 * capx].view(torch.int64)
-            xm.native_expert_down(L, ptr, p[4:], p[0:1], p[o["dst"]:], cap_groups, capx, scratch, parts)
-
-    kreps = max(4, args.steps // copies)
-    ms_gu, _ = graph_time(torch, gu_round, kreps)
-    ms_dn, _ = graph_time(torch, down_round, kreps)
-    us_gu = ms_gu * 1e3 / copies
-    us_dn = ms_dn * 1e3 / copies
-    gu_bytes = k * 2 * F * L.gu_row          # algorithmic: 8 experts' gate + up rows per launch
-    dn_bytes = k * H * L.d_row               # 8 experts' down rows per launch
-    gu_gbs = gu_bytes / (us_gu * 1e-6) / 1e9
-    dn_gbs = dn_bytes / (us_dn * 1e-6) / 1e9
-    log(f"gate/up kernel {us_gu:.2f} us ({gu_gbs:.0f} GB/s), down kernel {us_dn:.2f} us ({dn_gbs:.0f} GB/s)")
+    # ---------------------------------------------------------------- the dominant kernel: the fused decode layer
+    # At T <= 64 the layer is one launch (moe_decode_fused_kernel), so the per-step time above is that kernel's average
+    # launch duration: events on the stream the graph replays on bracket the replays.  Algorithmic bytes per launch =
+    # the distinct experts' blob bytes.
+    roof_bytes = bytes1
+    roof_us = ms1 * 1e3
+    roof_gbs = roof_bytes / (roof_us * 1e-6) / 1e9
+    traffic = read_traffic()
+    log(f"fused decode kernel: {roof_us:.2f} us/launch, {roof_gbs:.0f} GB/s of {roof_bytes / 1e6:.2f} MB"
+        + (f", HBM traffic {traffic / 1e6:.2f} MB/launch (rocprofv3 --pmc)" if traffic else ""))
 
     # ---------------------------------------------------------------- decode batches 4 and 16, verify 4
     extra = {}
@@ -240,12 +255,10 @@ def main():
         "us_per_token": round(ms1 * 1e3, 3),
         "tokens_per_s": round(1.0 / (ms1 * 1e-3), 1),
         "frac_hbm_peak": round(gbs1 / HBM_PEAK_GBS, 4),
-        "roofline": {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "grouped_kernel<Q4_K, 64, gate/up> (xs_native_expert_gate_up)",
-                     "algorithmic_bytes_per_launch": gu_bytes, "avg_launch_us": round(us_gu, 3),
-                     "down_kernel": {"avg_launch_us": round(us_dn, 3), "gbs": round(dn_gbs, 1),
-                                     "algorithmic_bytes_per_launch": dn_bytes}},
+        "roofline": {"bound": "hbm", "achieved": round(roof_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(roof_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": "moe_decode_fused_kernel<Q4_K, Q6_K, 1> (xs_moe_layer_decode, one launch a layer)",
+                     "algorithmic_bytes_per_launch": round(roof_bytes), "avg_launch_us": round(roof_us, 3)},
         "decode_batches": extra,
         "prefill": prefill,
         "cpu_baseline": cpu,
