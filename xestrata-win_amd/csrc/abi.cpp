@@ -331,8 +331,8 @@ int xs_moe_prefill_experts(const xs_expert_layout_t* L, const float* x, int64_t 
     if (int r = check_layout(L, "moe_prefill_experts")) return r;
     if (cap_groups > rows) return fail(XS_EINVAL, "moe_prefill_experts: cap_groups %lld > rows %lld", (long long)cap_groups,
                                        (long long)rows);
-    if (L->n_ff % 64 || L->n_embd % 128)
-        return fail(XS_EINVAL, "moe_prefill_experts: n_ff %% 64 and n_embd %% 128 must be 0 (%lld, %lld)",
+    if (L->n_ff % 128 || L->n_embd % 256)
+        return fail(XS_EINVAL, "moe_prefill_experts: n_ff %% 128 and n_embd %% 256 must be 0 (%lld, %lld)",
                     (long long)L->n_ff, (long long)L->n_embd);
     if (cap_groups > 65535 || !aligned(x, 4) || !aligned(src, 4) || !aligned(entry_of, 4) || !aligned(bounds, 4) ||
         !aligned(n_groups, 4) || !aligned(grp_ptr, 8) || !aligned(scratch, 256) || !aligned(parts, 4))
