@@ -389,7 +389,9 @@ __global__ __launch_bounds__(512, 1) void grouped_mfma_kernel(ExpertLayout L, Pr
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
                     const float gv = acc[i][j][q], uv = acc[i][j + 2][q];
-                    const float hv = gv / (1.0f + expf(-gv)) * uv;
+                    // SwiGLU on the hardware exp2 and reciprocal (the bf16 path's tolerance, not canon's bits)
+                    const float e = __builtin_amdgcn_exp2f(-gv * 1.4426950408889634f);
+                    const float hv = gv * __builtin_amdgcn_rcpf(1.0f + e) * uv;
                     dst[cb[j] + (lane & 31)] = f2bf(hv);
                 }
             }
