@@ -139,10 +139,10 @@ int xs_prefill_route(const int32_t* ids, int64_t n_entries, int k, int n_expert,
                      int32_t* entry_of, int32_t* bounds, int32_t* experts, int32_t* n_groups,
                      const uint8_t* cache_base, long long blob, unsigned long long* grp_ptr, void* stream);
 
-/* Grouped experts for prompt and verify batches: bf16 MFMA products on expert tiles dequantized in LDS.  Rows are
- * the routed rows in expert order (xs_prefill_route): row r reads token src[r] of x (fp32, n_embd a token) and its
- * down output lands in row entry_of[r] of `parts` (routing order, n_embd floats a row); h = SwiGLU(gate, up) is kept
- * in bf16.  scratch: xs_moe_prefill_scratch_bytes.  Replaces the prompt path's mmq::Context::run + swiglu +
+/* Grouped experts for prompt and verify batches: f16 MFMA products (fp32 accumulate) on expert weights dequantized
+ * from the raw GGUF blocks.  Rows are the routed rows in expert order (xs_prefill_route): row r reads token src[r] of
+ * x (fp32, n_embd a token; taken in f16, saturated) and its down output lands in row entry_of[r] of `parts` (routing
+ * order, n_embd floats a row); h = SwiGLU(gate, up) is kept in f16.  scratch: xs_moe_prefill_scratch_bytes.  Replaces the prompt path's mmq::Context::run + swiglu +
  * quantize (include/strata/prefill/moe_mmq.hpp:50-94), iq_mmq_grouped (iq_mmq.hpp:49-58), xmx_gemm_grouped
  * (xmx_gemm.hpp:39-43) and the rocBLAS fallback Gemm::f16_groups (src/prefill/gemm.cpp:371-388). */
 int xs_moe_prefill_experts(const xs_expert_layout_t* L, const float* x, int64_t n_tok, const int32_t* src,
@@ -182,7 +182,7 @@ size_t xs_moe_layer_decode_workspace_bytes(const xs_expert_layout_t* L, int n_ex
  * counterpart in the reference (its layer reports through host-side checks of each launch). */
 int32_t* xs_moe_layer_decode_status(void* workspace);
 
-/* The whole prompt / verify MoE layer on the device (same arena): router -> permutation -> bf16 MFMA grouped
+/* The whole prompt / verify MoE layer on the device (same arena): router -> permutation -> f16 MFMA grouped
  * experts -> combine -> residual.  The engine's prompt MoE section (src/prefill/plain_prompt.cpp:558-797). */
 int xs_moe_layer_prefill(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_bytes, int n_expert,
                          int k, const float* x, const float* logits, const float* residual, float* out, int n_tok,

@@ -3,7 +3,7 @@
 Decode / verify (xs_native_expert_grouped, the reference's native_expert_grouped contract: q8_1 activations, exact
 integer block sums): gate / up within 1e-5 of each row's magnitude, the q8_1 of SwiGLU(gate, up) bit for bit for the
 same gate / up, outputs within max|a - b| / max|ref| <= 1e-3 (fp32 accumulate).
-Prefill (xs_moe_prefill_experts, bf16 MFMA): against a plain PyTorch fp32 reference over the dequantized weights
+Prefill (xs_moe_prefill_experts, f16 MFMA): against a plain PyTorch fp32 reference over the dequantized weights
 (xs_iq_dequant_f32 is bit-exact with the reference's dequantizer), max-relative <= 2e-2."""
 import numpy as np
 import pytest

@@ -2,7 +2,7 @@
 BASELINE configs' shapes, against the CPU oracle on the same seeded inputs.
 
 Bars: expert ids and the plan bit for bit (the router's and plan's own tests); layer output (residual + MoE) within
-max|a - b| / max|ref| <= 1e-3 for the fp32-accumulate decode path, <= 2e-2 for the bf16 MFMA prefill path."""
+max|a - b| / max|ref| <= 1e-3 for the fp32-accumulate decode path, <= 2e-2 for the f16 MFMA prefill path."""
 import numpy as np
 import pytest
 import torch
@@ -78,7 +78,7 @@ def test_config3_verify_decode_path(xm, xo, c2_arena):
 
 @pytest.mark.parametrize("T", [4, 2048])
 def test_config3_prefill(xm, c2_arena, T):
-    """Config 3: prefill 2048 tokens and the 4-token verify batch through the bf16 MFMA path, against a plain PyTorch
+    """Config 3: prefill 2048 tokens and the 4-token verify batch through the f16 MFMA path, against a plain PyTorch
     fp32 reference over the exactly dequantized weights (router ids shared: they are pinned bit for bit elsewhere)."""
     from test_gpu_experts import torch_reference_prefill
     arena, L = c2_arena
@@ -98,7 +98,7 @@ def test_config3_prefill(xm, c2_arena, T):
 
 
 def test_prefill_matches_decode_path(xm, xo, c2_arena):
-    """The same 16 tokens through both paths: the bf16 MFMA layer within 2e-2 of the fp32-accumulate one."""
+    """The same 16 tokens through both paths: the f16 MFMA layer within 2e-2 of the fp32-accumulate one."""
     arena, L = c2_arena
     T = 16
     g = torch.Generator(device=DEV).manual_seed(77)

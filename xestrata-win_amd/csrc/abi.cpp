@@ -320,7 +320,7 @@ int xs_prefill_route(const int32_t* ids, int64_t n_entries, int k, int n_expert,
 size_t xs_moe_prefill_scratch_bytes(int64_t n_tok, int64_t rows, int64_t n_embd, int64_t n_ff) {
     if (n_tok <= 0 || rows <= 0) return 256;
     return up256((size_t)n_tok * (size_t)n_embd * 2) + up256((size_t)rows * (size_t)n_ff * 2) +
-           up256((size_t)(rows + 1) * 4) + 256;
+           up256((size_t)(rows + 1) * 8) + 256;
 }
 
 int xs_moe_prefill_experts(const xs_expert_layout_t* L, const float* x, int64_t n_tok, const int32_t* src,

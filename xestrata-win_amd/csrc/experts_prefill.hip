@@ -1,23 +1,33 @@
-// xestrata-win_amd/csrc/experts_prefill.hip - grouped expert products for prompt and verify batches: a bf16 MFMA
-// grouped GEMM whose expert weight tiles are dequantized from the raw GGUF blocks into LDS (the MI355X replacement
-// of the reference's int8 iq_mmq_grouped, src/kernels/xe/iq_mmq.cpp:483-943, and of its FP16 fallbacks
-// xmx_gemm_grouped / Gemm::f16_groups, src/prefill/gemm.cpp:371-388).
+// xestrata-win_amd/csrc/experts_prefill.hip - grouped expert products for prompt and verify batches: an f16 MFMA
+// grouped GEMM over expert weights dequantized from the raw GGUF blocks (the MI355X replacement of the reference's
+// int8 iq_mmq_grouped, src/kernels/xe/iq_mmq.cpp:483-943, and of its FP16 path dequant_f16 + xmx_gemm_grouped /
+// Gemm::f16_groups, src/prefill/gemm.cpp:371-388, whose FP16 x FP16 -> FP32 arithmetic this follows).
 //
 // Rows are the routed rows in expert order (the permutation of src/prefill/plain_prompt.cpp:576-637).  Two launches:
-//   gate/up: h[row, j] = SwiGLU(x[src[row]] . gate_j, x[src[row]] . up_j) in bf16, a tile = 128 rows x 64 h columns
-//            (their 64 gate and 64 up weight rows, so the SwiGLU is formed in registers);
-//   down:    parts[entry[row], c] = h[row] . down_c in fp32, a tile = 128 rows x 128 output columns, written straight
+//   gate/up: h[row, j] = SwiGLU(x[src[row]] . gate_j, x[src[row]] . up_j) in f16, a tile = 128 rows x 128 h columns
+//            (their 128 gate and 128 up weight rows, so the SwiGLU is formed in registers);
+//   down:    parts[entry[row], c] = h[row] . down_c in fp32, a tile = 128 rows x 256 output columns, written straight
 //            into routing order for the combine.
-// Tiles: 128 rows x 256 weight rows, 256 threads, 4 waves of 64 x 128 (2 x 4 v_mfma_f32_32x32x16_bf16 tiles: the
-// 32 x 32 MFMA sustains ~80% of the bf16 peak where 16 x 16 x 32 needs twice the independent accumulators), K steps of
-// 64 with both operands in LDS as rows of 8 chunks of 16 bytes, chunk c of row r at slot c ^ (r & 7) (the fragment
-// reads of 8 neighbouring rows hit 8 different bank groups).  Each step's activation rows (gathered through src for
-// gate/up) and raw weight bytes are loaded into registers two steps ahead, so their latency runs under two steps of
-// MFMAs; at its turn a step's activations are stored to LDS and its weights dequantized to bf16 there (Q4_K and Q6_K
-// unpacked 16 bytes at a time, other formats 32 values at a time).  A work-group's m-tile comes from a flat index over every group's ceil(rows / 128) tiles (a
-// prefix computed on the device).  Work-group b runs on XCD b % 8; an XCD takes every eighth m-tile and runs its
-// n-tiles one after the other, so the m-tile's activations and its expert's weights are fetched into that XCD's L2
-// once and reused across the n-tiles.
+//
+// Why f16 and not bf16: the dequantization is the kernel's ALU cost, and gfx950 has packed f16 arithmetic
+// (v_pk_fma_f16, two values an instruction) but none for bf16.  A 4-bit code q becomes an f16 with one v_and_or_b32
+// that drops it into the mantissa of a constant (0x6400 | q = 1024 + q; 0x4C00 | q << 4 = 16 + q / 4), and one packed
+// FMA with the sub-block scale and the exactly representable -1024 d (or -64 d) turns two of them into d q, rounded
+// once; the Q4_K minimum is one packed add more.  The MFMA is v_mfma_f32_32x32x16_f16 (the bf16 rate).
+//
+// K order: in each step of 64 values, MFMA fragment slot p of both operands holds value 8 P[p / 8] + P[p % 8] with
+// P = (0 2 1 3 4 6 5 7) - the order in which the bytes of a little-endian quant word come out in pairs (bytes 0 and 2,
+// then 1 and 3).  The activations x and h are stored in that order (f16, saturated), so an activation fragment is one
+// 16-byte LDS read and a weight fragment is built from two quant words with no shuffles.
+//
+// Work-group: 4 waves over a 128-row x 256-weight-row tile; wave w owns 64 weight rows (two 32-column MFMA tiles)
+// and each lane dequantizes the fragments of its two weight rows in registers, one step ahead of their MFMAs.  The
+// tile's activation rows reach LDS by DMA (global_load_lds_dwordx4, gathered through src for gate/up) into a double
+// buffer, chunk c of row r at slot c ^ (r & 7) (fragment reads of 8 neighbouring rows hit 8 bank groups).  Row tiles
+// of 32 past the group's rows are skipped.  A work-group's m-tile comes from a flat index over every group's
+// ceil(rows / 128) tiles (a prefix computed on the device).  Work-group b runs on XCD b % 8; an XCD takes every
+// eighth m-tile and runs its n-tiles one after the other, so the m-tile's activations and its expert's weights are
+// fetched into that XCD's L2 once and reused across the n-tiles.
 #include "xs_device.h"
 #include "xs_dequant.h"
 #include "xs_kernels.h"
@@ -25,256 +35,272 @@
 
 namespace xs {
 
-typedef short bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
-constexpr int kBM = 128, kBN = 256, kBK = 64;
+constexpr int kBN = 256, kBK = 64;
+// row tiles of 32 a work-group: 4 for Q4_K weights, 2 where the weight words take more registers (Q6_K, others)
+__host__ __device__ constexpr int row_tiles(int t) { return t == kQ4_K ? 4 : 2; }
 
-__global__ __launch_bounds__(256) void to_bf16_kernel(const float* __restrict__ x, uint16_t* __restrict__ y, int64_t n) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) y[i] = f2bf(x[i]);
+// slot order inside an octet and octet order inside a step (an involution)
+__host__ __device__ constexpr int perm8(int i) { return (i == 1 || i == 5) ? i + 1 : (i == 2 || i == 6) ? i - 1 : i; }
+__host__ __device__ constexpr int perm64(int p) { return 8 * perm8(p >> 3) + perm8(p & 7); }
+
+__device__ __forceinline__ uint32_t sat_f16x2(float a, float b) {   // RNE, saturated to the f16 range (NaN kept)
+    a = __builtin_fminf(__builtin_fmaxf(a, -65504.0f), 65504.0f);
+    b = __builtin_fminf(__builtin_fmaxf(b, -65504.0f), 65504.0f);
+    return __builtin_bit_cast(uint32_t, (h2_t){(_Float16)a, (_Float16)b});
 }
 
-// mtile[g] = sum over groups before g of ceil(rows / kBM); mtile[n_groups] = the total
+// x [n, H] fp32 -> f16 in the step order: thread i writes chunk i (8 values)
+__global__ __launch_bounds__(256) void to_f16_kernel(const float* __restrict__ x, uint16_t* __restrict__ y,
+                                                     int64_t n_chunks) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n_chunks) return;
+    const int c = (int)(i & 7);
+    const float* s = x + (i & ~(int64_t)7) * 8 + 8 * perm8(c);
+    const float4 v0 = *(const float4*)s, v1 = *(const float4*)(s + 4);
+    *(uint4*)(y + 8 * i) = make_uint4(sat_f16x2(v0.x, v0.z), sat_f16x2(v0.y, v0.w), sat_f16x2(v1.x, v1.z),
+                                      sat_f16x2(v1.y, v1.w));
+}
+
+// m-tile prefixes for 128- and 64-row tiles: mt[g] = sum over groups before g of ceil(rows / 128), mt[n_groups] =
+// the total; the same for 64 at mt + cap_groups + 1
 __global__ __launch_bounds__(1024) void tile_map_kernel(const int32_t* __restrict__ bounds,
-                                                        const int32_t* __restrict__ n_groups, int32_t* __restrict__ mtile,
+                                                        const int32_t* __restrict__ n_groups, int32_t* __restrict__ mt,
                                                         int cap_groups) {
     __shared__ int s_wave[16];
     __shared__ int s_carry;
     const int ng = min(*n_groups, cap_groups);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if (tid == 0) s_carry = 0;
-    __syncthreads();
-    for (int g0 = 0; g0 <= ng; g0 += 1024) {
-        const int g = g0 + tid;
-        const int t = g < ng ? (bounds[g + 1] - bounds[g] + kBM - 1) / kBM : 0;
-        int inc = t;
-        for (int o = 1; o < 64; o <<= 1) {
-            const int y = __shfl_up(inc, o, 64);
-            if (lane >= o) inc += y;
+    for (int pass = 0; pass < 2; ++pass) {
+        const int bm = pass ? 64 : 128;
+        int32_t* mtile = mt + pass * (cap_groups + 1);
+        if (tid == 0) s_carry = 0;
+        __syncthreads();
+        for (int g0 = 0; g0 <= ng; g0 += 1024) {
+            const int g = g0 + tid;
+            const int t = g < ng ? (bounds[g + 1] - bounds[g] + bm - 1) / bm : 0;
+            int inc = t;
+            for (int o = 1; o < 64; o <<= 1) {
+                const int y = __shfl_up(inc, o, 64);
+                if (lane >= o) inc += y;
+            }
+            if (lane == 63) s_wave[wave] = inc;
+            __syncthreads();
+            int before = s_carry;
+            for (int w = 0; w < wave; ++w) before += s_wave[w];
+            if (g <= ng) mtile[g] = before + inc - t;
+            __syncthreads();
+            if (tid == 1023) s_carry = before + inc;
+            __syncthreads();
         }
-        if (lane == 63) s_wave[wave] = inc;
-        __syncthreads();
-        int before = s_carry;
-        for (int w = 0; w < wave; ++w) before += s_wave[w];
-        if (g <= ng) mtile[g] = before + inc - t;
-        __syncthreads();
-        if (tid == 1023) s_carry = before + inc;
-        __syncthreads();
     }
 }
 
-// A load through a global-address-space pointer.  Blob addresses come from memory (the group table), so the compiler
-// cannot prove them global and would emit FLAT loads, which also count on lgkmcnt: every wait for an LDS operand of
-// the MFMAs would then wait for the weight prefetch in flight.
-template <typename V>
-__device__ __forceinline__ V ldg(const void* p) {
-    return *(const __attribute__((address_space(1))) V*)p;
-}
-typedef unsigned int gu32x4_t __attribute__((ext_vector_type(4)));
+// Loads through a global-address-space pointer.  Blob addresses come from memory (the group table), so the compiler
+// cannot prove them global and would emit FLAT loads, which also count on lgkmcnt (every wait for an LDS operand
+// would then wait for the weight prefetch in flight).  Q6_K blocks are 210 bytes, so their words are only 2-byte
+// aligned: global loads take unaligned addresses on gfx9 (the HSA memory model's unaligned mode).
+typedef unsigned int g32x4_t __attribute__((ext_vector_type(4), aligned(2)));
+typedef unsigned int g32x2_t __attribute__((ext_vector_type(2), aligned(2)));
 __device__ __forceinline__ uint4 ldg16(const void* p) {
-    const gu32x4_t v = *(const __attribute__((address_space(1))) gu32x4_t*)p;
+    const g32x4_t v = *(const __attribute__((address_space(1))) g32x4_t*)p;
     return make_uint4(v.x, v.y, v.z, v.w);
 }
+__device__ __forceinline__ uint2 ldg8(const void* p) {
+    const g32x2_t v = *(const __attribute__((address_space(1))) g32x2_t*)p;
+    return make_uint2(v.x, v.y);
+}
+__device__ __forceinline__ uint32_t ldg_u16(const void* p) {
+    return *(const __attribute__((address_space(1))) uint16_t*)p;
+}
+
+__device__ __forceinline__ void vm_drain() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+template <int N>
+struct IntC {
+    static constexpr int value = N;
+};
 
 __device__ __forceinline__ int swz(int r, int c) { return r * 8 + (c ^ (r & 7)); }   // in 16-byte units
 
+__device__ __forceinline__ h2_t h2(uint32_t w) { return __builtin_bit_cast(h2_t, w); }
+__device__ __forceinline__ uint32_t u32(h2_t h) { return __builtin_bit_cast(uint32_t, h); }
+__device__ __forceinline__ h2_t h2b(float v) {   // v rounded to f16, in both halves
+    const _Float16 h = (_Float16)v;
+    return (h2_t){h, h};
+}
+// (a & m) | o as one v_and_or_b32 (left to itself the compiler regroups nested ones into v_and, v_and, v_or3_b32)
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t o) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(m), "v"(o));
+    return r;
+}
 
-// the raw bytes of one thread's share of a weight step (row br = the thread, the step's 64 values); see stage_b.
-// Q6_K blocks (210 bytes) sit at 2-byte alignment: their words are loaded aligned and realigned when staged, so the
-// loads stay in flight until then.
-struct BRegs {
-    uint4 a, b, c;     // Q4_K: a = block header, b, c = the 32 qs bytes
-    uint32_t q6[26];   // Q6_K: 17 aligned words over the step's 64 ql bytes, 9 over its 32 qh bytes
-    uint32_t s, t;     // Q6_K: the 4 int8 scales; d | the byte misalignment << 16
+// a constant held in a VGPR: gfx9's three-operand forms (v_and_or_b32) take no literal, and with the mask and the
+// magic as literals the compiler splits every v_and_or_b32 into an AND and an OR
+template <uint32_t C>
+__device__ __forceinline__ uint32_t vreg() {
+    uint32_t r;
+    asm("v_mov_b32 %0, %1" : "=v"(r) : "n"(C));
+    return r;
+}
+// the masks and magic words of the code unpacking: index 0 places a code at bits [5:0] of each half (f16 1024 + q),
+// index 1 at bits [9:4] (f16 16 + q / 4)
+struct QConst {
+    uint32_t nib[2];   // 4-bit code: 0x000F000F, 0x00F000F0
+    uint32_t two[2];   // Q6_K 2-bit high part: 0x00300030, 0x03000300
+    uint32_t mag[2];   // 0x64006400 (f16 1024), 0x4C004C00 (f16 16)
 };
-
-template <int T>
-__device__ __forceinline__ void load_b(const uint8_t* brow, int k0, BRegs& r) {
-    if (T == kQ4_K) {
-        const uint8_t* blk = brow + 144 * (k0 >> 8);
-        const int p = (k0 & 255) >> 6;
-        r.a = ldg16(blk);
-        r.b = ldg16(blk + 16 + 32 * p);
-        r.c = ldg16(blk + 32 + 32 * p);
-    } else if (T == kQ6_K) {
-        const uint8_t* blk = brow + 210 * (k0 >> 8);
-        const int t = (k0 & 255) >> 6, n = t >> 1, sel = t & 1;
-        const uintptr_t u = (uintptr_t)blk;
-        const __attribute__((address_space(1))) uint32_t* q =
-            (const __attribute__((address_space(1))) uint32_t*)(u & ~(uintptr_t)3);
-        // dword-aligned 16-byte loads (fewer address passes than one load a word)
-        typedef unsigned int u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
-        const __attribute__((address_space(1))) u32x4_a4* q4 = (const __attribute__((address_space(1))) u32x4_a4*)q;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const u32x4_a4 v = *(const __attribute__((address_space(1))) u32x4_a4*)(q + 16 * n + 4 * i);
-            r.q6[4 * i] = v.x; r.q6[4 * i + 1] = v.y; r.q6[4 * i + 2] = v.z; r.q6[4 * i + 3] = v.w;
-        }
-        r.q6[16] = q[16 * n + 16];
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const u32x4_a4 v = *(const __attribute__((address_space(1))) u32x4_a4*)(q + 32 + 8 * n + 4 * i);
-            r.q6[17 + 4 * i] = v.x; r.q6[18 + 4 * i] = v.y; r.q6[19 + 4 * i] = v.z; r.q6[20 + 4 * i] = v.w;
-        }
-        r.q6[25] = q[32 + 8 * n + 8];
-        (void)q4;
-        const uint8_t* sc = blk + 192 + 8 * n + 4 * sel;
-        r.s = (uint32_t)ldg<uint16_t>(sc) | ((uint32_t)ldg<uint16_t>(sc + 2) << 16);
-        r.t = (uint32_t)ldg<uint16_t>(blk + 208) | ((uint32_t)(u & 3) << 16);
-    }
+__device__ __forceinline__ QConst make_qconst() {
+    QConst c;
+    c.nib[0] = vreg<0x000F000Fu>();
+    c.nib[1] = vreg<0x00F000F0u>();
+    c.two[0] = vreg<0x00300030u>();
+    c.two[1] = vreg<0x03000300u>();
+    c.mag[0] = vreg<0x64006400u>();
+    c.mag[1] = vreg<0x4C004C00u>();
+    return c;
 }
 
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
-// two floats to packed bf16, round to nearest even (v_cvt_pk_bf16_f32)
-__device__ __forceinline__ uint32_t pk2(float a, float b) {
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, bf16x2_t));
+// ---------------------------------------------------------------- Q4_K
+// Lane l (half hf = l / 32) of weight row r, step p of a block (values 64 p .. 64 p + 63): the qs word run
+// D = qs[32 p + 16 hf, +16).  Fragment kk: kk 0, 1 the low nibbles of words (0, 1) / (2, 3) - sub-block 2 p; kk 2, 3
+// their high nibbles - sub-block 2 p + 1.
+struct Q4Step {
+    h2_t dlo, clo, mlo;   // d1, -1024 d1, -m1 of sub-block 2 p
+    h2_t dhi, chi, mhi;   // 4 d1, -64 d1, -m1 of sub-block 2 p + 1
+};
+__device__ __forceinline__ Q4Step q4k_step(const uint4& hdr, int p) {
+    const float d = h2f((uint16_t)(hdr.x & 0xFFFFu)), dmin = h2f((uint16_t)(hdr.x >> 16));
+    int s0, m0, s1, m1;
+    q4k_sm(hdr.y, hdr.z, hdr.w, 2 * p, s0, m0);
+    q4k_sm(hdr.y, hdr.z, hdr.w, 2 * p + 1, s1, m1);
+    Q4Step s;
+    s.dlo = h2b(d * (float)s0);
+    s.clo = s.dlo * (h2_t){-1024.0f16, -1024.0f16};
+    s.mlo = -h2b(dmin * (float)m0);
+    const h2_t d1 = h2b(d * (float)s1);
+    s.dhi = d1 * (h2_t){4.0f16, 4.0f16};
+    s.chi = d1 * (h2_t){-64.0f16, -64.0f16};
+    s.mhi = -h2b(dmin * (float)m1);
+    return s;
 }
-__device__ __forceinline__ float byte_f(uint32_t w, int i) { return (float)((w >> (8 * i)) & 0xFFu); }   // v_cvt_f32_ubyteN
-// scale * byte + offset for the 4 bytes of w, packed as two bf16 pairs
-__device__ __forceinline__ uint2 deq4(uint32_t w, float sc, float off) {
-    return make_uint2(pk2(__builtin_fmaf(sc, byte_f(w, 0), off), __builtin_fmaf(sc, byte_f(w, 1), off)),
-                      pk2(__builtin_fmaf(sc, byte_f(w, 2), off), __builtin_fmaf(sc, byte_f(w, 3), off)));
-}
-// 16 codes (4 registers of 4 bytes) -> 2 chunks of 8 bf16 at chunk c of row br
-__device__ __forceinline__ void put16(uint4* sb, int br, int c, const uint32_t (&q)[4], float sc, float off) {
-    const uint2 v0 = deq4(q[0], sc, off), v1 = deq4(q[1], sc, off), v2 = deq4(q[2], sc, off), v3 = deq4(q[3], sc, off);
-    sb[swz(br, c)] = make_uint4(v0.x, v0.y, v1.x, v1.y);
-    sb[swz(br, c + 1)] = make_uint4(v2.x, v2.y, v3.x, v3.y);
+__device__ __forceinline__ f16x8_t q4k_frag(const uint4& D, int kk, const Q4Step& s, const QConst& qc) {
+    const uint32_t w0 = (kk & 1) ? D.z : D.x, w1 = (kk & 1) ? D.w : D.y;
+    const bool hi = kk >= 2;
+    const uint32_t m = qc.nib[hi], o = qc.mag[hi];
+    const h2_t sc = hi ? s.dhi : s.dlo, c = hi ? s.chi : s.clo, mn = hi ? s.mhi : s.mlo;
+    const uint32_t v[4] = {and_or(w0, m, o), and_or(w0 >> 8, m, o), and_or(w1, m, o), and_or(w1 >> 8, m, o)};
+    uint32_t r[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = u32(__builtin_elementwise_fma(h2(v[i]), sc, c) + mn);
+    return __builtin_bit_cast(f16x8_t, make_uint4(r[0], r[1], r[2], r[3]));
 }
 
-// dequantize the thread's 64 values of the step (its weight row, chunks 0..7) to bf16 in the B stage.  Q4_K is
-// d·sc·q − dmin·m and Q6_K d·sc·(q − 32), each one fma of the code (4 codes a register: nibble masks, byte converts),
-// then packed bf16 converts; other formats go through dequant32.
-template <int T>
-__device__ __forceinline__ void stage_b(const BRegs& r, const uint8_t* brow, int type, int k0, int br, uint4* sb) {
-    if (T == kQ4_K) {
-        const int p = (k0 & 255) >> 6;
-        const float d = h2f((uint16_t)(r.a.x & 0xFFFFu)), dmin = h2f((uint16_t)(r.a.x >> 16));
-        int sc0, m0, sc1, m1;
-        q4k_sm(r.a.y, r.a.z, r.a.w, 2 * p, sc0, m0);
-        q4k_sm(r.a.y, r.a.z, r.a.w, 2 * p + 1, sc1, m1);
-        const float d0 = d * (float)sc0, n0 = -(dmin * (float)m0), d1 = d * (float)sc1, n1 = -(dmin * (float)m1);
-        const uint32_t w[8] = {r.b.x, r.b.y, r.b.z, r.b.w, r.c.x, r.c.y, r.c.z, r.c.w};
+// ---------------------------------------------------------------- Q6_K
+// Half n of a block (values 128 n .. 128 n + 127) is two steps t.  Lane hf of weight row r loads, once a half,
+// L0 = ql[64 n + 16 hf, +16), L1 = ql[64 n + 32 + 16 hf, +16), Hq = qh[32 n + 16 hf, +16) and the half's 8 scales.
+// Fragment kk of step t: ql words (0, 1) / (2, 3) of L0 (kk < 2) or L1 (kk >= 2) - low nibbles at t = 0, high at
+// t = 1 - and qh words (0, 1) / (2, 3) of Hq, bits 2 f .. 2 f + 1 of each byte with f = 2 t + kk / 2; its 16 values
+// share scale 4 t + 2 (kk / 2) + hf of the half.
+struct Q6Raw {
+    uint4 l0, l1, hq;
+    uint2 sc;
+    uint32_t d;
+};
+__device__ __forceinline__ void q6k_load(const uint8_t* blk, int n, int hf, Q6Raw& r) {
+    r.l0 = ldg16(blk + 64 * n + 16 * hf);
+    r.l1 = ldg16(blk + 64 * n + 32 + 16 * hf);
+    r.hq = ldg16(blk + 128 + 32 * n + 16 * hf);
+    r.sc = ldg8(blk + 192 + 8 * n);
+    r.d = ldg_u16(blk + 208);
+}
+__device__ __forceinline__ h2_t q6k_scale(const Q6Raw& r, int t, int kk, int hf) {
+    const int i = 4 * t + 2 * (kk >> 1) + hf;
+    const uint32_t w = i < 4 ? r.sc.x : r.sc.y;
+    const float s = h2f((uint16_t)r.d) * (float)(int8_t)((w >> (8 * (i & 3))) & 0xFFu);
+    const h2_t v = h2b(s);
+    return t ? v * (h2_t){4.0f16, 4.0f16} : v;
+}
+__device__ __forceinline__ f16x8_t q6k_frag(const Q6Raw& r, int t, int kk, h2_t sc, const QConst& qc) {
+    const uint4& L = kk < 2 ? r.l0 : r.l1;
+    const uint32_t l0 = (kk & 1) ? L.z : L.x, l1 = (kk & 1) ? L.w : L.y;
+    const uint32_t q0 = (kk & 1) ? r.hq.z : r.hq.x, q1 = (kk & 1) ? r.hq.w : r.hq.y;
+    const int sl = (kk >> 1) ? 2 : 4, sr = (kk >> 1) ? 6 : 4;   // the qh field to bits [5:4] (t 0) or [9:8] (t 1)
+    const uint32_t ml = qc.nib[t], mh = qc.two[t], o = qc.mag[t];
+    const uint32_t v[4] = {and_or(l0, ml, and_or(q0 << sl, mh, o)), and_or(l0 >> 8, ml, and_or(q0 >> sr, mh, o)),
+                           and_or(l1, ml, and_or(q1 << sl, mh, o)), and_or(l1 >> 8, ml, and_or(q1 >> sr, mh, o))};
+    const h2_t off = t ? (h2_t){-24.0f16, -24.0f16} : (h2_t){-1056.0f16, -1056.0f16};   // (q - 32) / 4, q - 32
+    uint32_t w[4];
 #pragma unroll
-        for (int g = 0; g < 2; ++g) {   // values 16 g .. (low nibbles) and 32 + 16 g .. (high nibbles)
-            const uint32_t lo[4] = {w[4 * g] & 0x0F0F0F0Fu, w[4 * g + 1] & 0x0F0F0F0Fu, w[4 * g + 2] & 0x0F0F0F0Fu,
-                                    w[4 * g + 3] & 0x0F0F0F0Fu};
-            const uint32_t hi[4] = {(w[4 * g] >> 4) & 0x0F0F0F0Fu, (w[4 * g + 1] >> 4) & 0x0F0F0F0Fu,
-                                    (w[4 * g + 2] >> 4) & 0x0F0F0F0Fu, (w[4 * g + 3] >> 4) & 0x0F0F0F0Fu};
-            put16(sb, br, 2 * g, lo, d0, n0);
-            put16(sb, br, 4 + 2 * g, hi, d1, n1);
-        }
-    } else if (T == kQ6_K) {
-        const int sel = ((k0 & 255) >> 6) & 1, ns = 4 * sel;
-        const float d = h2f((uint16_t)(r.t & 0xFFFFu));
-        const uint32_t sh = r.t >> 16;
-        uint32_t ql[16], qh[8];
+    for (int i = 0; i < 4; ++i) w[i] = u32((h2(v[i]) + off) * sc);
+    return __builtin_bit_cast(f16x8_t, make_uint4(w[0], w[1], w[2], w[3]));
+}
+
+// ---------------------------------------------------------------- other formats (Q8_0, IQ4_XS)
+// values [o, o + 8) of the 32-value group g of the block at b, as the reference's host dequantizers give them
+// (dequant.hpp:84-89 Q8_0, 283-299 IQ4_XS)
+__device__ __forceinline__ void dequant8(int type, const uint8_t* b, int g, int o, float (&y)[8]) {
+    if (type == kQ8_0) {
+        const float d = rd_h(b);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) ql[i] = __builtin_amdgcn_alignbyte(r.q6[i + 1], r.q6[i], sh);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) qh[i] = __builtin_amdgcn_alignbyte(r.q6[18 + i], r.q6[17 + i], sh);
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {   // values 16 g ..: ql bytes 32 (g / 2) + 16 (g % 2) .., qh bits ns + 2 (g / 2)
-            const float sc = d * (float)(int8_t)((r.s >> (8 * g)) & 0xFFu);
-            const int hs = ns + 2 * (g >> 1);
-            uint32_t q[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                q[i] = ((ql[4 * g + i] >> ns) & 0x0F0F0F0Fu) | (((qh[4 * (g & 1) + i] >> hs) & 0x03030303u) << 4);
-            put16(sb, br, 2 * g, q, sc, -32.0f * sc);
-        }
+        for (int j = 0; j < 8; ++j) y[j] = (float)(int8_t)b[2 + o + j] * d;
     } else {
-        const int qk = block_values(type), bs = block_bytes(type);
+        const float d = rd_h(b);
+        const unsigned scales_h = (unsigned)(b[2] | (b[3] << 8));
+        const int ls = ((b[4 + g / 2] >> (4 * (g % 2))) & 0x0F) | (((scales_h >> (2 * g)) & 3) << 4);
+        const float dl = d * (float)(ls - 32);
+        const uint8_t* qs = b + 8 + 16 * g + (o & 15);
+        const int sh = o >= 16 ? 4 : 0;
 #pragma unroll
-        for (int half = 0; half < 2; ++half) {
-            float v[32];
-            const int kv = k0 + 32 * half;
-            dequant32(type, brow + (int64_t)(kv / qk) * bs, (kv % qk) / 32, v);
+        for (int j = 0; j < 8; ++j) y[j] = dl * (float)iq4nl_value((qs[j] >> sh) & 0x0F);
+    }
+}
+__device__ __forceinline__ f16x8_t generic_frag(const uint8_t* brow, int type, int k0, int kk, int hf) {
+    const int qk = block_values(type), bs = block_bytes(type);
+    const int kv = k0 + 32 * (kk >> 1);
+    float v[8];
+    dequant8(type, brow + (int64_t)(kv / qk) * bs, (kv % qk) / 32, 16 * hf + 8 * (kk & 1), v);
+    uint32_t w[4];
 #pragma unroll
-            for (int c = 0; c < 4; ++c)
-                sb[swz(br, 4 * half + c)] = make_uint4(pk2(v[8 * c], v[8 * c + 1]), pk2(v[8 * c + 2], v[8 * c + 3]),
-                                                       pk2(v[8 * c + 4], v[8 * c + 5]), pk2(v[8 * c + 6], v[8 * c + 7]));
-        }
-    }
+    for (int i = 0; i < 4; ++i) w[i] = sat_f16x2(v[perm8(2 * i)], v[perm8(2 * i + 1)]);
+    return __builtin_bit_cast(f16x8_t, make_uint4(w[0], w[1], w[2], w[3]));
 }
 
-constexpr int kRing = 3;   // activation stages in LDS: a step's rows go out two steps before its MFMAs
-
-// one K step of a consumer wave: 4 k-chunks of 16 over its 2 x 4 tiles of 32 x 32 (lane l holds A[row l % 32][k 8 (l / 32)
-// ..] and B[k 8 (l / 32) ..][col l % 32]); the next chunk's fragments are read while this chunk's MFMAs run (one
-// consumer wave a SIMD: nothing else hides the LDS latency)
-struct Frags {
-    bf16x8_t a0, a1, b0, b1, b2, b3;
-};
-__device__ __forceinline__ Frags read_frags(const uint4* sA, const uint4* sB, int rw, const int (&cb)[4], int lane,
-                                            int kk) {
-    const int ch = 2 * kk + (lane >> 5), r = lane & 31;
-    Frags f;
-    f.a0 = __builtin_bit_cast(bf16x8_t, sA[swz(rw + r, ch)]);
-    f.a1 = __builtin_bit_cast(bf16x8_t, sA[swz(rw + 32 + r, ch)]);
-    f.b0 = __builtin_bit_cast(bf16x8_t, sB[swz(cb[0] + r, ch)]);
-    f.b1 = __builtin_bit_cast(bf16x8_t, sB[swz(cb[1] + r, ch)]);
-    f.b2 = __builtin_bit_cast(bf16x8_t, sB[swz(cb[2] + r, ch)]);
-    f.b3 = __builtin_bit_cast(bf16x8_t, sB[swz(cb[3] + r, ch)]);
-    return f;
-}
-__device__ __forceinline__ void mfma8(const Frags& f, f32x16_t (&acc)[2][4]) {
-    acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a0, f.b0, acc[0][0], 0, 0, 0);
-    acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a1, f.b0, acc[1][0], 0, 0, 0);
-    acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a0, f.b1, acc[0][1], 0, 0, 0);
-    acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a1, f.b1, acc[1][1], 0, 0, 0);
-    acc[0][2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a0, f.b2, acc[0][2], 0, 0, 0);
-    acc[1][2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a1, f.b2, acc[1][2], 0, 0, 0);
-    acc[0][3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a0, f.b3, acc[0][3], 0, 0, 0);
-    acc[1][3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a1, f.b3, acc[1][3], 0, 0, 0);
-}
-__device__ __forceinline__ void mfma_step(const uint4* sA, const uint4* sB, int rw, const int (&cb)[4], int lane,
-                                          f32x16_t (&acc)[2][4]) {
-    Frags f0 = read_frags(sA, sB, rw, cb, lane, 0);
-    Frags f1 = read_frags(sA, sB, rw, cb, lane, 1);
-    mfma8(f0, acc);
-    f0 = read_frags(sA, sB, rw, cb, lane, 2);
-    mfma8(f1, acc);
-    f1 = read_frags(sA, sB, rw, cb, lane, 3);
-    mfma8(f0, acc);
-    mfma8(f1, acc);
+// RT DMA instructions of a wave: instruction i copies 16 bytes at src[i] + off of each lane to LDS dst + 1024 i
+// (global_load_lds_dwordx4; a function of its own: in a lambda the LDS address-space cast breaks the host pass)
+template <int RT>
+__device__ __forceinline__ void dma_rows(const uint8_t* const* src, size_t off, uint8_t* dst) {
+#pragma unroll
+    for (int i = 0; i < RT; ++i)
+        __builtin_amdgcn_global_load_lds(src[i] + off, (__attribute__((address_space(3))) void*)(dst + i * 1024), 16, 0,
+                                         0);
 }
 
-// a producer's step: its weight row's raw bytes prefetched three steps ahead (register sets r0, r1, r2 in turn)
-template <int T>
-struct Producer {
-    const uint8_t* brow;
-    int wtype, row, nk;
-    BRegs r0, r1, r2;
-    __device__ __forceinline__ void load(int ks, BRegs& r) {
-        if (ks < nk) load_b<T>(brow, ks * kBK, r);
-    }
-    // dequantize step ks from r into the B stage, then reuse r for step ks + 3
-    __device__ __forceinline__ void turn(int ks, BRegs& r, uint4* sb) {
-        if (ks < nk) {
-            stage_b<T>(r, brow, wtype, ks * kBK, row, sb);
-            load(ks + 3, r);
-        }
-    }
-};
-
-// Work-group = 8 waves.  Waves 0-3 (consumers) hold the accumulators: they bring the activation rows into a ring of LDS
-// stages by DMA, two steps ahead, and run the MFMAs.  Waves 4-7 (producers) hold no accumulators, so each keeps three
-// steps of its weight row's raw bytes in flight in registers and dequantizes two steps ahead into a ring of three bf16
-// stages (a producer's slow step is absorbed).  One barrier a step hands the stages over.
-template <bool DOWN, int T>
-__global__ __launch_bounds__(512, 1) void grouped_mfma_kernel(ExpertLayout L, PrefillArgs a,
+template <bool DOWN, int T, int RT>
+__global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, PrefillArgs a,
                                                               const int32_t* __restrict__ mtile, int mt_bound,
                                                               int n_tiles) {
+    constexpr int kBM = 32 * RT;
     extern __shared__ __align__(16) uint8_t lds[];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    // the tile of this work-group: XCD x = blockIdx % 8 takes m-tiles x, x + 8, ..., each with its n-tiles one after
-    // the other (the m-tile's activation rows and its expert's weight slabs stay in that XCD's L2 across them)
-    const int c8 = (int)(blockIdx.x >> 3);
-    const int mt = (c8 / n_tiles) * 8 + (int)(blockIdx.x & 7), nt = c8 % n_tiles;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, hf = lane >> 5;
+    // work-group b runs on XCD x = b % 8.  With n-tiles a multiple of 8, XCD x takes n-tiles [x n8, x n8 + n8) of
+    // every m-tile, m-tile by m-tile: the weight slice of its n-tiles is fetched into its L2 once an expert and reused
+    // by the expert's m-tiles.  Otherwise XCD x takes m-tiles x, x + 8, ..., each with its n-tiles one after the
+    // other, so the m-tile's activations are fetched into its L2 once.
+    const int c8 = (int)(blockIdx.x >> 3), xcd = (int)(blockIdx.x & 7);
+    int mt, nt;
+    if (n_tiles % 8 == 0) {
+        const int n8 = n_tiles >> 3;
+        mt = c8 / n8;
+        nt = xcd * n8 + c8 % n8;
+    } else {
+        mt = (c8 / n_tiles) * 8 + xcd;
+        nt = c8 % n_tiles;
+    }
     if (mt >= mt_bound) return;
     const int ng = *a.n_groups;
     if (ng <= 0 || mt >= mtile[ng]) return;
@@ -287,140 +313,203 @@ __global__ __launch_bounds__(512, 1) void grouped_mfma_kernel(ExpertLayout L, Pr
     const int g = lo;
     const int r0 = a.bounds[g] + (mt - mtile[g]) * kBM;
     const int nrows = min(kBM, a.bounds[g + 1] - r0);
+    const int nrt = (nrows + 31) >> 5;   // live 32-row tiles
     const int H = (int)L.n_embd, F = (int)L.n_ff;
     const int K = DOWN ? F : H;
     const int nk = K / kBK;
     const int n0 = nt * (DOWN ? kBN : kBN / 2);
-    uint4* ring = (uint4*)lds;                          // kRing x 128 rows x 8 chunks
-    uint4* sB = (uint4*)(lds + kRing * kBM * 128);      // 3 x 256 rows x 8 chunks
-    auto stage_a = [&](int ks) { return ring + (ks % kRing) * (kBM * 8); };
-    auto stage_b_buf = [&](int ks) { return sB + (ks % 3) * (kBN * 8); };
+    const int wtype = DOWN ? L.d_type : L.gu_type;
+    const int64_t wrb = DOWN ? L.d_row : L.gu_row;
 
-    if (wave >= 4) {   // ---- producers: thread p = weight row p of the tile
-        const int p = tid - 256;
-        const int wrow = DOWN ? n0 + p : (p < kBN / 2 ? n0 + p : F + n0 + (p - kBN / 2));
-        Producer<T> pr;
-        pr.brow = (const uint8_t*)a.wptr[g] + (DOWN ? L.down_off : 0) + (int64_t)wrow * (DOWN ? L.d_row : L.gu_row);
-        pr.wtype = DOWN ? L.d_type : L.gu_type;
-        pr.row = p;
-        pr.nk = nk;
-        pr.load(0, pr.r0);
-        pr.load(1, pr.r1);
-        pr.load(2, pr.r2);
-        pr.turn(0, pr.r0, stage_b_buf(0));
-        pr.turn(1, pr.r1, stage_b_buf(1));
-        __syncthreads();   // barrier 0: steps 0 and 1 staged
-        // between barriers j and j + 1 (j = 0 .. nk - 2) the producers stage step j + 2 while the consumers run step
-        // j; step s uses register set s % 3
-        for (int st = 2; st <= nk; st += 3) {
-            pr.turn(st, pr.r2, stage_b_buf(st));
-            __syncthreads();
-            if (st + 1 > nk) break;
-            pr.turn(st + 1, pr.r0, stage_b_buf(st + 1));
-            __syncthreads();
-            if (st + 2 > nk) break;
-            pr.turn(st + 2, pr.r1, stage_b_buf(st + 2));
-            __syncthreads();
-        }
-        return;
-    }
-
-    // ---- consumers: A rows by DMA (instruction i of wave w fills slots [64 (4w + i), +64): row 8 (4w + i) + lane / 8,
-    // slot lane % 8 = chunk (lane % 8) ^ (row & 7); rows past the tile's end read its first row, unused)
-    const uint16_t* arow[4];
+    // A by DMA: wave w fills rows [8 RT w, 8 RT (w + 1)) of the tile, 8 rows an instruction; lane l of instruction i
+    // holds LDS slot swz(R, l & 7) of row R = 8 RT w + 8 i + l / 8, i.e. chunk (l & 7) ^ (R & 7) of that row (rows
+    // past the group's end read its first row)
+    const uint8_t* asrc[RT];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int r = 8 * (4 * wave + i) + (lane >> 3);
-        const int rr = r < nrows ? r : 0;
-        const int chunk = (lane & 7) ^ (r & 7);
-        arow[i] = (DOWN ? a.h + (int64_t)(r0 + rr) * F : a.xb + (int64_t)a.src[r0 + rr] * H) + 8 * chunk;
+    for (int i = 0; i < RT; ++i) {
+        const int R = 8 * RT * wave + 8 * i + (lane >> 3);
+        const int rr = R < nrows ? R : 0;
+        const int c = (lane & 7) ^ (R & 7);
+        asrc[i] = (const uint8_t*)(DOWN ? a.h + (int64_t)(r0 + rr) * F : a.xb + (int64_t)a.src[r0 + rr] * H) + 16 * c;
     }
-    auto dma_a = [&](int ks) {
-        uint4* dst = stage_a(ks);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            __builtin_amdgcn_global_load_lds(arow[i] + ks * kBK,
-                                             (__attribute__((address_space(3))) void*)(dst + 64 * (4 * wave + i)), 16,
-                                             0, 0);
+    // down: the routing entry of each row, staged in LDS for the epilogue (visible after the first step's barrier)
+    int32_t* const s_entry = (int32_t*)(lds + 2 * kBM * 128);
+    if (DOWN && tid < nrows) s_entry[tid] = a.entry[r0 + tid];
+    // the A rows of step ks into buffer `buf`
+    auto dma_a = [&](int ks, int buf) {
+        dma_rows<RT>(asrc, (size_t)ks * 128, lds + buf * (kBM * 128) + wave * 8 * RT * 128);
     };
-    const int rw = 64 * (wave >> 1), wn = wave & 1;
-    int cb[4];
+    // B: the lane's two weight rows (tile columns cb[j] + lane % 32); gate/up pairs a gate column with its up column
+    int cb[2];
+    cb[0] = DOWN ? 64 * wave : 32 * wave;
+    cb[1] = DOWN ? 64 * wave + 32 : 128 + 32 * wave;
+    const uint8_t* brow[2];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) cb[j] = DOWN ? 128 * wn + 32 * j : (j < 2 ? 64 * wn + 32 * j : 128 + 64 * wn + 32 * (j - 2));
-    f32x16_t acc[2][4];
+    for (int j = 0; j < 2; ++j) {
+        const int col = cb[j] + (lane & 31);
+        const int wrow = DOWN ? n0 + col : (col < kBN / 2 ? n0 + col : F + n0 + (col - kBN / 2));
+        brow[j] = (const uint8_t*)a.wptr[g] + (DOWN ? L.down_off : 0) + (int64_t)wrow * wrb;
+    }
+
+    f32x16_t acc[RT][2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < RT; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.0f;
 
-    dma_a(0);
-    if (nk > 1) {
-        dma_a(1);
-        asm volatile("s_waitcnt vmcnt(4)" ::: "memory");   // step 0's rows are in; step 1's fly
-    } else {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    }
-    __syncthreads();   // barrier 0
-    for (int ks = 0; ks < nk; ++ks) {   // barrier ks + 1 follows the MFMAs of step ks (none after the last)
-        const bool more = ks + 2 < nk;
-        if (more) dma_a(ks + 2);
-        mfma_step(stage_a(ks), stage_b_buf(ks), rw, cb, lane, acc);
-        if (ks + 1 < nk) {   // step ks + 1's rows have landed before the barrier hands them over
-            if (more) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-            else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            __syncthreads();
-        }
-    }
-    // lane holds C[rw + 32 i + 8 (q / 4) + 4 (lane / 32) + q % 4][cb[j] + lane % 32]
+    // a step's start: its A rows and raw weights (issued a step before) have landed in every wave
+    auto step_sync = [&]() {
+        vm_drain();
+        __syncthreads();
+    };
+    const QConst qc = make_qconst();
+
+    // The K loop for NRT live row tiles, a compile-time count: a fragment's operand reads and MFMAs are then
+    // straight-line code that the scheduler interleaves with the next fragment's dequantization.
+    auto kloop = [&](auto nrt_c) {
+        constexpr int NRT = decltype(nrt_c)::value;
+        // fragment kk of step ks: B fragments fb0, fb1 against the live row tiles of the step's A buffer
+        auto mfma_step = [&](int ks, int kk, const f16x8_t& fb0, const f16x8_t& fb1) {
+            const uint4* sA = (const uint4*)(lds + (ks & 1) * (kBM * 128));
+            const int ch = 2 * kk + hf;
+            f16x8_t fa[NRT];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < NRT; ++i) fa[i] = __builtin_bit_cast(f16x8_t, sA[swz(32 * i + (lane & 31), ch)]);
 #pragma unroll
-        for (int q = 0; q < 16; ++q) {
-            const int row = rw + 32 * i + 8 * (q >> 2) + 4 * (lane >> 5) + (q & 3);
-            if (row >= nrows) continue;
-            if (DOWN) {
-                float* dst = a.parts + (int64_t)a.entry[r0 + row] * H + n0;
+            for (int i = 0; i < NRT; ++i) {
+                acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i], fb0, acc[i][0], 0, 0, 0);
+                acc[i][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i], fb1, acc[i][1], 0, 0, 0);
+            }
+        };
+        dma_a(0, 0);
+        if (T == kQ4_K) {
+            const int nb = K / 256;
+            uint4 hdr[2], q[2][2];   // header of the block; the qs run of steps (even, odd)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) dst[cb[j] + (lane & 31)] = acc[i][j][q];
-            } else {
-                uint16_t* dst = a.h + (int64_t)(r0 + row) * F + n0;
+            for (int j = 0; j < 2; ++j) {
+                hdr[j] = ldg16(brow[j]);
+                q[0][j] = ldg16(brow[j] + 16 + 16 * hf);
+            }
+            for (int b = 0; b < nb; ++b) {
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const float gv = acc[i][j][q], uv = acc[i][j + 2][q];
-                    // SwiGLU on the hardware exp2 and reciprocal (the bf16 path's tolerance, not canon's bits)
-                    const float e = __builtin_amdgcn_exp2f(-gv * 1.4426950408889634f);
-                    const float hv = gv * __builtin_amdgcn_rcpf(1.0f + e) * uv;
-                    dst[cb[j] + (lane & 31)] = f2bf(hv);
+                for (int p = 0; p < 4; ++p) {
+                    const int ks = 4 * b + p;
+                    step_sync();
+                    // the step's scales first: at p = 3 the header registers then take the next block's header
+                    const Q4Step s0 = q4k_step(hdr[0], p), s1 = q4k_step(hdr[1], p);
+                    if (ks + 1 < nk) {
+                        dma_a(ks + 1, (ks + 1) & 1);
+                        const int bn = p == 3 ? b + 1 : b;   // the next step's block
+#pragma unroll
+                        for (int j = 0; j < 2; ++j) {
+                            const uint8_t* blk = brow[j] + 144 * bn;
+                            if (p == 3) hdr[j] = ldg16(blk);
+                            q[(p + 1) & 1][j] = ldg16(blk + 16 + 32 * ((p + 1) & 3) + 16 * hf);
+                        }
+                    }
+#pragma unroll
+                    for (int kk = 0; kk < 4; ++kk)
+                        mfma_step(ks, kk, q4k_frag(q[p & 1][0], kk, s0, qc), q4k_frag(q[p & 1][1], kk, s1, qc));
                 }
             }
+        } else if (T == kQ6_K) {
+            const int nb = K / 256;
+            Q6Raw r[2][2];   // the raw words of halves (even, odd), per row
+#pragma unroll
+            for (int j = 0; j < 2; ++j) q6k_load(brow[j], 0, hf, r[0][j]);
+            for (int b = 0; b < nb; ++b) {
+#pragma unroll
+                for (int n = 0; n < 2; ++n) {
+#pragma unroll
+                    for (int t = 0; t < 2; ++t) {
+                        const int ks = 4 * b + 2 * n + t;
+                        step_sync();
+                        if (ks + 1 < nk) {
+                            dma_a(ks + 1, (ks + 1) & 1);
+                            if (t == 1) {   // the next half's words
+                                const int bn = n == 0 ? b : b + 1;
+#pragma unroll
+                                for (int j = 0; j < 2; ++j) q6k_load(brow[j] + 210 * bn, n ^ 1, hf, r[n ^ 1][j]);
+                            }
+                        }
+#pragma unroll
+                        for (int kk = 0; kk < 4; ++kk) {
+                            const Q6Raw& ra = r[n][0];
+                            const Q6Raw& rb = r[n][1];
+                            mfma_step(ks, kk, q6k_frag(ra, t, kk, q6k_scale(ra, t, kk, hf), qc),
+                                      q6k_frag(rb, t, kk, q6k_scale(rb, t, kk, hf), qc));
+                        }
+                    }
+                }
+            }
+        } else {
+            for (int ks = 0; ks < nk; ++ks) {
+                step_sync();
+                if (ks + 1 < nk) dma_a(ks + 1, (ks + 1) & 1);
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk)
+                    mfma_step(ks, kk, generic_frag(brow[0], wtype, ks * kBK, kk, hf),
+                              generic_frag(brow[1], wtype, ks * kBK, kk, hf));
+            }
         }
+    };
+    if (nrt >= RT) kloop(IntC<RT>{});
+    else if (RT > 3 && nrt == 3) kloop(IntC<(RT > 3 ? 3 : 1)>{});
+    else if (RT > 2 && nrt == 2) kloop(IntC<(RT > 2 ? 2 : 1)>{});
+    else kloop(IntC<1>{});
+
+    // lane holds C[32 i + 8 (q / 4) + 4 (lane / 32) + q % 4][cb[j] + lane % 32]
+#pragma unroll
+    for (int i = 0; i < RT; ++i) {
+        if (i >= nrt) break;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            const int row = 32 * i + 8 * (q >> 2) + 4 * hf + (q & 3);
+            if (row >= nrows) continue;
+            if (DOWN) {
+                float* dst = a.parts + (int64_t)s_entry[row] * H + n0;
+#pragma unroll
+                for (int j = 0; j < 2; ++j) dst[cb[j] + (lane & 31)] = acc[i][j][q];
+            } else {
+                // SwiGLU on the hardware exp2 and reciprocal (the f16 path's tolerance, not canon's bits), stored in
+                // the step order the down product reads
+                const float gv = acc[i][0][q], uv = acc[i][1][q];
+                const float e = __builtin_amdgcn_exp2f(-gv * 1.4426950408889634f);
+                float hv = gv * __builtin_amdgcn_rcpf(1.0f + e) * uv;
+                hv = __builtin_fminf(__builtin_fmaxf(hv, -65504.0f), 65504.0f);
+                const int col = n0 + cb[0] + (lane & 31);
+                a.h[(int64_t)(r0 + row) * F + (col & ~63) + perm64(col & 63)] = f2h(hv);
+            }
+        }
+    }
 }
 
 template <bool DOWN>
-static hipError_t launch_gemm(const ExpertLayout& L, const PrefillArgs& a, int mt_bound, hipStream_t s) {
+static hipError_t launch_gemm(const ExpertLayout& L, const PrefillArgs& a, hipStream_t s) {
     const int n_tiles = DOWN ? (int)(L.n_embd / kBN) : (int)(L.n_ff / (kBN / 2));
-    const unsigned grid = (unsigned)(8 * ((mt_bound + 7) / 8) * n_tiles);
     const int t = DOWN ? L.d_type : L.gu_type;
-    const size_t lds = (size_t)(kRing * kBM + 3 * kBN) * 128;
+    const int bm = 32 * row_tiles(t);
+    const int mt_bound = (int)((a.rows + bm - 1) / bm + a.cap_groups);
+    const unsigned grid = (unsigned)(n_tiles % 8 == 0 ? mt_bound * n_tiles : 8 * ((mt_bound + 7) / 8) * n_tiles);
+    const size_t lds = (size_t)2 * bm * 128 + (DOWN ? (size_t)bm * 4 : 0);
+    const int32_t* mtile = a.mtile + (bm == 128 ? 0 : a.cap_groups + 1);
     void (*k)(ExpertLayout, PrefillArgs, const int32_t*, int, int) =
-        t == kQ4_K ? grouped_mfma_kernel<DOWN, kQ4_K> : t == kQ6_K ? grouped_mfma_kernel<DOWN, kQ6_K>
-                                                                    : grouped_mfma_kernel<DOWN, 0>;
-    hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k, dim3(grid), dim3(512), lds, s, L, a, (const int32_t*)a.mtile, mt_bound, n_tiles);
+        t == kQ4_K   ? grouped_mfma_kernel<DOWN, kQ4_K, row_tiles(kQ4_K)>
+        : t == kQ6_K ? grouped_mfma_kernel<DOWN, kQ6_K, row_tiles(kQ6_K)>
+                     : grouped_mfma_kernel<DOWN, 0, row_tiles(0)>;
+    hipLaunchKernelGGL(k, dim3(grid), dim3(256), lds, s, L, a, mtile, mt_bound, n_tiles);
     return hipGetLastError();
 }
 
 hipError_t launch_prefill_experts(const ExpertLayout& L, const PrefillArgs& a, hipStream_t s) {
-    const int64_t nx = a.n_tok * L.n_embd;
-    hipLaunchKernelGGL(to_bf16_kernel, dim3((unsigned)((nx + 255) / 256)), dim3(256), 0, s, a.x, a.xb, nx);
+    const int64_t nc = a.n_tok * L.n_embd / 8;
+    hipLaunchKernelGGL(to_f16_kernel, dim3((unsigned)((nc + 255) / 256)), dim3(256), 0, s, a.x, a.xb, nc);
     hipLaunchKernelGGL(tile_map_kernel, dim3(1), dim3(1024), 0, s, a.bounds, a.n_groups, a.mtile, (int)a.cap_groups);
-    const int mt_bound = (int)((a.rows + kBM - 1) / kBM + a.cap_groups);
-    hipError_t e = launch_gemm<false>(L, a, mt_bound, s);
+    hipError_t e = launch_gemm<false>(L, a, s);
     if (e != hipSuccess) return e;
-    return launch_gemm<true>(L, a, mt_bound, s);
+    return launch_gemm<true>(L, a, s);
 }
 
 }  // namespace xs

@@ -104,10 +104,10 @@ struct PrefillArgs {
     const int32_t* bounds;          // [groups + 1] row bounds of each group
     const int32_t* n_groups;        // device count of groups
     const unsigned long long* wptr; // [groups] blob address of each group's expert
-    uint16_t* xb;                   // scratch: [n_tok, n_embd] bf16 copy of x
-    uint16_t* h;                    // scratch: [rows, n_ff] bf16 SwiGLU output
+    uint16_t* xb;                   // scratch: [n_tok, n_embd] f16 copy of x, in the GEMM's K order
+    uint16_t* h;                    // scratch: [rows, n_ff] f16 SwiGLU output, in the GEMM's K order
     float* parts;                   // [n_tok * k, n_embd] routing-order outputs
-    int32_t* mtile;                 // scratch: [cap_groups + 1] m-tile prefix of the groups
+    int32_t* mtile;                 // scratch: [2, cap_groups + 1] m-tile prefixes of the groups (128-, 64-row tiles)
     int32_t* err;
     int64_t n_tok, rows, cap_groups;
 };
