@@ -323,10 +323,17 @@ size_t xs_moe_prefill_scratch_bytes(int64_t n_tok, int64_t rows, int64_t n_embd,
            up256((size_t)(rows + 1) * 8) + 256;
 }
 
-int xs_moe_prefill_experts(const xs_expert_layout_t* L, const float* x, int64_t n_tok, const int32_t* src,
-                           const int32_t* entry_of, const int32_t* bounds, const int32_t* n_groups,
-                           const unsigned long long* grp_ptr, int64_t cap_groups, int64_t rows, void* scratch,
-                           float* parts, void* stream) {
+namespace {
+// the m-tile prefixes inside the experts' scratch: after the f16 copy of x and h
+int32_t* prefill_mtile(void* scratch, int64_t n_tok, int64_t rows, const xs_expert_layout_t* L) {
+    return (int32_t*)((uint8_t*)scratch + up256((size_t)n_tok * (size_t)L->n_embd * 2) +
+                      up256((size_t)rows * (size_t)L->n_ff * 2));
+}
+// the grouped experts writing fp32 parts, or f16 parts when parts_h is set (the whole-layer path)
+int prefill_experts(const xs_expert_layout_t* L, const float* x, int64_t n_tok, const int32_t* src,
+                    const int32_t* entry_of, const int32_t* bounds, const int32_t* n_groups,
+                    const unsigned long long* grp_ptr, int64_t cap_groups, int64_t rows, void* scratch, float* parts,
+                    uint16_t* parts_h, bool mtile_ready, void* stream) {
     if (rows <= 0 || cap_groups <= 0) return ok();
     if (int r = check_layout(L, "moe_prefill_experts")) return r;
     if (cap_groups > rows) return fail(XS_EINVAL, "moe_prefill_experts: cap_groups %lld > rows %lld", (long long)cap_groups,
@@ -335,7 +342,8 @@ int xs_moe_prefill_experts(const xs_expert_layout_t* L, const float* x, int64_t 
         return fail(XS_EINVAL, "moe_prefill_experts: n_ff %% 128 and n_embd %% 256 must be 0 (%lld, %lld)",
                     (long long)L->n_ff, (long long)L->n_embd);
     if (cap_groups > 65535 || !aligned(x, 4) || !aligned(src, 4) || !aligned(entry_of, 4) || !aligned(bounds, 4) ||
-        !aligned(n_groups, 4) || !aligned(grp_ptr, 8) || !aligned(scratch, 256) || !aligned(parts, 4))
+        !aligned(n_groups, 4) || !aligned(grp_ptr, 8) || !aligned(scratch, 256) ||
+        !(parts_h ? aligned(parts_h, 2) : aligned(parts, 4)))
         return fail(XS_EINVAL, "moe_prefill_experts: a span is missing or misaligned");
     xs::PrefillArgs a;
     a.x = x;
@@ -346,13 +354,24 @@ int xs_moe_prefill_experts(const xs_expert_layout_t* L, const float* x, int64_t 
     a.wptr = grp_ptr;
     a.xb = (uint16_t*)scratch;
     a.h = (uint16_t*)((uint8_t*)scratch + up256((size_t)n_tok * (size_t)L->n_embd * 2));
-    a.mtile = (int32_t*)((uint8_t*)a.h + up256((size_t)rows * (size_t)L->n_ff * 2));
+    a.mtile = prefill_mtile(scratch, n_tok, rows, L);
+    a.mtile_ready = mtile_ready;
     a.err = (int32_t*)((uint8_t*)scratch + xs_moe_prefill_scratch_bytes(n_tok, rows, L->n_embd, L->n_ff) - 256);
     a.parts = parts;
+    a.parts_h = parts_h;
     a.n_tok = n_tok;
     a.rows = rows;
     a.cap_groups = cap_groups;
     return finish(stream, xs::launch_prefill_experts(to_layout(L), a, S(stream)), "moe_prefill_experts");
+}
+}  // namespace
+
+int xs_moe_prefill_experts(const xs_expert_layout_t* L, const float* x, int64_t n_tok, const int32_t* src,
+                           const int32_t* entry_of, const int32_t* bounds, const int32_t* n_groups,
+                           const unsigned long long* grp_ptr, int64_t cap_groups, int64_t rows, void* scratch,
+                           float* parts, void* stream) {
+    return prefill_experts(L, x, n_tok, src, entry_of, bounds, n_groups, grp_ptr, cap_groups, rows, scratch, parts,
+                           nullptr, false, stream);
 }
 
 int xs_native_moe_combine_multi(const float* parts, const float* weights, const float* shared, float* output,
@@ -447,7 +466,8 @@ struct PrefillWs {
     int32_t *src, *slot, *entry, *bounds, *experts, *n_groups;
     unsigned long long* grp_ptr;
     void* scratch;
-    float* parts;
+    uint16_t* parts;   // f16
+    int32_t* ghist;    // the split permutation's block histograms
     size_t bytes;
 };
 PrefillWs prefill_ws(const xs_expert_layout_t* L, int n_expert, int k, int n_tok, uint8_t* base) {
@@ -465,7 +485,8 @@ PrefillWs prefill_ws(const xs_expert_layout_t* L, int n_expert, int k, int n_tok
     d.n_groups = (int32_t*)take(4);
     d.grp_ptr = (unsigned long long*)take((size_t)n_expert * 8);
     d.scratch = take(xs_moe_prefill_scratch_bytes(n_tok, (int64_t)n, L->n_embd, L->n_ff));
-    d.parts = (float*)take(n * (size_t)L->n_embd * 4);
+    d.parts = (uint16_t*)take(n * (size_t)L->n_embd * 2);
+    d.ghist = (int32_t*)take(xs::prefill_route_split_scratch((int64_t)n, n_expert));
     d.bytes = off;
     return d;
 }
@@ -556,14 +577,19 @@ int xs_moe_layer_prefill(const xs_expert_layout_t* L, const uint8_t* arena, size
     const PrefillWs w = prefill_ws(L, n_expert, k, n_tok, (uint8_t*)workspace);
     const int64_t n = (int64_t)n_tok * k;
     if (int r = xs_router_top10(logits, n_tok, n_expert, k, w.ids, w.w, stream)) return r;
-    if (int r = xs_prefill_route(w.ids, n, k, n_expert, w.src, w.slot, w.entry, w.bounds, w.experts, w.n_groups, arena,
-                                 (long long)blob_bytes, w.grp_ptr, stream))
-        return r;
     const int64_t cap_groups = n < n_expert ? n : n_expert;
-    if (int r = xs_moe_prefill_experts(L, x, n_tok, w.src, w.entry, w.bounds, w.n_groups, w.grp_ptr, cap_groups, n,
-                                       w.scratch, w.parts, stream))
+    if (int r = finish(stream,
+                       xs::launch_prefill_route_split(w.ids, n, k, n_expert, w.src, w.slot, w.entry, w.bounds,
+                                                      w.experts, w.n_groups, arena, (long long)blob_bytes, w.grp_ptr,
+                                                      w.ghist, prefill_mtile(w.scratch, n_tok, n, L), (int)cap_groups,
+                                                      S(stream)),
+                       "moe_layer_prefill"))
         return r;
-    return xs_moe_combine_residual(w.parts, w.w, nullptr, nullptr, residual, out, L->n_embd, k, n_tok, stream);
+    if (int r = prefill_experts(L, x, n_tok, w.src, w.entry, w.bounds, w.n_groups, w.grp_ptr, cap_groups, n, w.scratch,
+                                nullptr, w.parts, true, stream))
+        return r;
+    return finish(stream, xs::launch_combine_h(w.parts, w.w, residual, out, L->n_embd, k, n_tok, S(stream)),
+                  "moe_layer_prefill");
 }
 
 }  // extern "C"

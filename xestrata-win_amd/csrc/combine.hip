@@ -41,6 +41,37 @@ __global__ __launch_bounds__(256) void add_inplace_kernel(float* __restrict__ x,
     if (i < n) x[i] = x[i] + y[i];
 }
 
+// The same sum over f16 parts (the prompt layer's, whose products are f16 MFMA results anyway), plus the residual:
+// 4 columns a thread (8-byte part reads, 16-byte residual and output accesses).
+__global__ __launch_bounds__(256) void combine_h_kernel(const uint16_t* __restrict__ parts,
+                                                        const float* __restrict__ weights,
+                                                        const float* __restrict__ residual, float* __restrict__ out,
+                                                        int64_t n_embd, int k) {
+    const int64_t t = blockIdx.y;
+    const int64_t c = 4 * ((int64_t)blockIdx.x * blockDim.x + threadIdx.x);
+    if (c >= n_embd) return;
+    const uint16_t* p = parts + t * k * n_embd + c;
+    const float* w = weights + t * k;
+    float4 sum = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int e = 0; e < k; ++e) {
+        const uint2 v = *(const uint2*)(p + (int64_t)e * n_embd);
+        const float we = w[e];
+        const float4 prod = make_float4(h2f((uint16_t)(v.x & 0xFFFFu)) * we, h2f((uint16_t)(v.x >> 16)) * we,
+                                        h2f((uint16_t)(v.y & 0xFFFFu)) * we, h2f((uint16_t)(v.y >> 16)) * we);
+        if (e == 0) sum = prod;
+        else sum = make_float4(sum.x + prod.x, sum.y + prod.y, sum.z + prod.z, sum.w + prod.w);
+    }
+    const float4 r = *(const float4*)(residual + t * n_embd + c);
+    *(float4*)(out + t * n_embd + c) = make_float4(r.x + sum.x, r.y + sum.y, r.z + sum.z, r.w + sum.w);
+}
+
+hipError_t launch_combine_h(const uint16_t* parts, const float* weights, const float* residual, float* out,
+                            int64_t n_embd, int k, int n_tok, hipStream_t s) {
+    const dim3 grid((unsigned)((n_embd / 4 + 255) / 256), (unsigned)n_tok);
+    hipLaunchKernelGGL(combine_h_kernel, grid, dim3(256), 0, s, parts, weights, residual, out, n_embd, k);
+    return hipGetLastError();
+}
+
 hipError_t launch_combine(const float* parts, const float* weights, const float* shared, const float* shared_gate,
                           const float* residual, float* out, int64_t n_embd, int k, int n_tok, hipStream_t s) {
     const dim3 grid((unsigned)((n_embd + 255) / 256), (unsigned)n_tok);

@@ -44,6 +44,7 @@ __global__ __launch_bounds__(kPlanThreads) void resident_plan_kernel(const int32
 }
 
 constexpr int kRouteWaves = 16;
+constexpr int kBatch = 16;   // 64-entry steps of ids loaded together
 
 __global__ __launch_bounds__(kRouteWaves * 64) void prefill_route_kernel(
     const int32_t* __restrict__ ids, int n, int k, int n_expert, int nbits, int32_t* __restrict__ src,
@@ -60,10 +61,21 @@ __global__ __launch_bounds__(kRouteWaves * 64) void prefill_route_kernel(
     if (tid == 0) s_bad = 0;
     __syncthreads();
     int* hist = s_hist + wave * n_expert;
-    for (int i = i0 + lane; i < i1; i += 64) {
-        const int e = ids[i];
-        if (e < 0 || e >= n_expert) s_bad = 1;
-        else atomicAdd(&hist[e], 1);
+    // the ids are read kBatch steps of 64 at a time, all loads in flight together (a step's latency once a batch)
+    for (int base = i0; base < i1; base += 64 * kBatch) {
+        int ev[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            const int i = base + 64 * u + lane;
+            ev[u] = i < i1 ? ids[i] : 0;
+        }
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            if (base + 64 * u + lane >= i1) continue;
+            const int e = ev[u];
+            if (e < 0 || e >= n_expert) s_bad = 1;
+            else atomicAdd(&hist[e], 1);
+        }
     }
     __syncthreads();
     if (s_bad) {
@@ -103,27 +115,181 @@ __global__ __launch_bounds__(kRouteWaves * 64) void prefill_route_kernel(
     __syncthreads();
     // the stable fill: wave by wave over its own segment, 64 entries a step, in entry order
     const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    for (int base = i0; base < i1; base += 64) {
-        const int i = base + lane;
-        const bool in = i < i1;
-        const int e = in ? ids[i] : 0;
-        uint64_t peers = __ballot(in);
-        for (int b = 0; b < nbits; ++b) {
-            const bool bit = (e >> b) & 1;
-            const uint64_t m = __ballot(bit);
-            peers &= bit ? m : ~m;
+    for (int base0 = i0; base0 < i1; base0 += 64 * kBatch) {
+        int ev[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            const int i = base0 + 64 * u + lane;
+            ev[u] = i < i1 ? ids[i] : 0;
         }
-        if (in) {
-            const int rank = __popcll(peers & below);
-            const int row = hist[e] + rank;
-            src[row] = i / k;
-            slot[i] = row;
-            entry[row] = i;
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            const int i = base0 + 64 * u + lane;
+            const bool in = i < i1;
+            const int e = ev[u];
+            uint64_t peers = __ballot(in);
+            for (int b = 0; b < nbits; ++b) {
+                const bool bit = (e >> b) & 1;
+                const uint64_t m = __ballot(bit);
+                peers &= bit ? m : ~m;
+            }
+            if (in) {
+                const int rank = __popcll(peers & below);
+                const int row = hist[e] + rank;
+                src[row] = i / k;
+                slot[i] = row;
+                entry[row] = i;
+            }
+            __builtin_amdgcn_wave_barrier();
+            if (in && (peers & below) == 0) hist[e] += __popcll(peers);
+            __builtin_amdgcn_wave_barrier();
         }
-        __builtin_amdgcn_wave_barrier();
-        if (in && (peers & below) == 0) hist[e] += __popcll(peers);
-        __builtin_amdgcn_wave_barrier();
     }
+}
+
+// ---------------------------------------------------------------- the permutation split over work-groups
+// The single work-group above writes every row itself, and its scattered stores (one cache line a lane) bound it.
+// The whole-layer path has a workspace, so it spreads the same permutation over blocks of kSeg entries: pass 1 counts
+// each block's experts (and bad ids), pass 2 gives every block its bases - the experts' exclusive prefix plus the
+// counts of the blocks before it - and ranks its entries as above, one 64-entry step a wave.  Rows, groups and
+// bounds come out identical to the single work-group's.
+constexpr int kSeg = 1024;
+
+__global__ __launch_bounds__(256) void route_hist_kernel(const int32_t* __restrict__ ids, int n, int n_expert,
+                                                         int32_t* __restrict__ ghist) {
+    extern __shared__ int s_h[];   // [n_expert + 1]: counts, then bad ids
+    const int tid = threadIdx.x;
+    for (int e = tid; e <= n_expert; e += 256) s_h[e] = 0;
+    __syncthreads();
+    const int i0 = blockIdx.x * kSeg;
+    int ev[kSeg / 256];
+#pragma unroll
+    for (int u = 0; u < kSeg / 256; ++u) {
+        const int i = i0 + 256 * u + tid;
+        ev[u] = i < n ? ids[i] : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < kSeg / 256; ++u) {
+        if (i0 + 256 * u + tid >= n) continue;
+        const int e = ev[u];
+        atomicAdd(&s_h[(e < 0 || e >= n_expert) ? n_expert : e], 1);
+    }
+    __syncthreads();
+    for (int e = tid; e <= n_expert; e += 256) ghist[(int64_t)blockIdx.x * (n_expert + 1) + e] = s_h[e];
+}
+
+__global__ __launch_bounds__(1024) void route_fill_kernel(
+    const int32_t* __restrict__ ids, int n, int k, int n_expert, int nbits, const int32_t* __restrict__ ghist, int nblk,
+    int32_t* __restrict__ src, int32_t* __restrict__ slot, int32_t* __restrict__ entry, int32_t* __restrict__ bounds,
+    int32_t* __restrict__ experts, int32_t* __restrict__ n_groups, const uint8_t* cache_base, long long blob,
+    unsigned long long* __restrict__ grp_ptr, int32_t* __restrict__ mtile, int cap_groups) {
+    extern __shared__ int s_w[];   // [16][n_expert]: each wave's counts, then its bases
+    __shared__ int s_wave[64];
+    __shared__ int s_bad;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int E = n_expert, blk = blockIdx.x;
+    const int i = blk * kSeg + tid;
+    const bool in = i < n;
+    const int ev = in ? ids[i] : 0;
+    if (tid == 0) s_bad = 0;
+    for (int x = tid; x < 16 * E; x += 1024) s_w[x] = 0;
+    __syncthreads();
+    if (tid < nblk && ghist[(int64_t)tid * (E + 1) + E] != 0) s_bad = 1;
+    __syncthreads();
+    if (s_bad) {   // a bad id anywhere: n_groups = -1 and nothing else written, as the single work-group does
+        if (blk == 0 && tid == 0) *n_groups = -1;
+        return;
+    }
+    const int e = in ? ev : 0;
+    uint64_t peers = __ballot(in);
+    for (int b = 0; b < nbits; ++b) {
+        const bool bit = (e >> b) & 1;
+        const uint64_t m = __ballot(bit);
+        peers &= bit ? m : ~m;
+    }
+    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    const int rank = __popcll(peers & below);
+    if (in && rank == 0) s_w[wave * E + e] = __popcll(peers);
+    __syncthreads();
+    int carry = 0, gcarry = 0, c128 = 0, c64 = 0;
+    for (int e0 = 0; e0 < E; e0 += 1024) {
+        const int ee = e0 + tid;
+        int tot = 0, pre = 0;
+        if (ee < E)
+            for (int b0 = 0; b0 < nblk; b0 += 8) {   // 8 loads in flight at a time
+                int c[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) c[u] = b0 + u < nblk ? ghist[(int64_t)(b0 + u) * (E + 1) + ee] : 0;
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    tot += c[u];
+                    if (b0 + u < blk) pre += c[u];
+                }
+            }
+        int sum_all;
+        const int st = block_exclusive_scan(tot, s_wave, &sum_all) + carry;
+        if (blk == 0) {   // the groups (experts ascending), and the m-tile prefixes of 128- and 64-row tiles
+            int g_all, t_all, u_all;
+            const int gi = block_exclusive_scan(tot > 0 ? 1 : 0, s_wave, &g_all) + gcarry;
+            const int m128 = block_exclusive_scan((tot + 127) / 128, s_wave, &t_all) + c128;
+            const int m64 = block_exclusive_scan((tot + 63) / 64, s_wave, &u_all) + c64;
+            if (ee < E && tot > 0) {
+                experts[gi] = ee;
+                bounds[gi] = st;
+                if (grp_ptr) grp_ptr[gi] = (unsigned long long)(uintptr_t)(cache_base + (size_t)ee * (size_t)blob);
+                if (mtile && gi < cap_groups) {
+                    mtile[gi] = m128;
+                    mtile[cap_groups + 1 + gi] = m64;
+                }
+            }
+            gcarry += g_all;
+            c128 += t_all;
+            c64 += u_all;
+        }
+        if (ee < E) {
+            int b = st + pre;
+            for (int w = 0; w < 16; ++w) {
+                const int c = s_w[w * E + ee];
+                s_w[w * E + ee] = b;
+                b += c;
+            }
+        }
+        carry += sum_all;
+    }
+    if (blk == 0 && tid == 0) {
+        bounds[gcarry] = n;
+        *n_groups = gcarry;
+        if (mtile && gcarry <= cap_groups) {
+            mtile[gcarry] = c128;
+            mtile[cap_groups + 1 + gcarry] = c64;
+        }
+    }
+    __syncthreads();
+    if (in) {
+        const int row = s_w[wave * E + e] + rank;
+        src[row] = i / k;
+        slot[i] = row;
+        entry[row] = i;
+    }
+}
+
+hipError_t launch_prefill_route_split(const int32_t* ids, int64_t n, int k, int n_expert, int32_t* src, int32_t* slot,
+                                      int32_t* entry, int32_t* bounds, int32_t* experts, int32_t* n_groups,
+                                      const uint8_t* cache_base, long long blob, unsigned long long* grp_ptr,
+                                      int32_t* ghist, int32_t* mtile, int cap_groups, hipStream_t s) {
+    int nbits = 1;
+    while ((1 << nbits) < n_expert) ++nbits;
+    const int nblk = (int)((n + kSeg - 1) / kSeg);
+    hipLaunchKernelGGL(route_hist_kernel, dim3(nblk), dim3(256), (size_t)(n_expert + 1) * sizeof(int), s, ids, (int)n,
+                       n_expert, ghist);
+    hipLaunchKernelGGL(route_fill_kernel, dim3(nblk), dim3(1024), (size_t)16 * n_expert * sizeof(int), s, ids, (int)n,
+                       k, n_expert, nbits, ghist, nblk, src, slot, entry, bounds, experts, n_groups, cache_base, blob,
+                       grp_ptr, mtile, cap_groups);
+    return hipGetLastError();
+}
+
+size_t prefill_route_split_scratch(int64_t n, int n_expert) {
+    return (size_t)((n + kSeg - 1) / kSeg) * (size_t)(n_expert + 1) * sizeof(int32_t);
 }
 
 hipError_t launch_resident_plan(const int32_t* ids, int n, int k, const int32_t* res, int n_expert,

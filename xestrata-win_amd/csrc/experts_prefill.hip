@@ -469,9 +469,17 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
             const int row = 32 * i + 8 * (q >> 2) + 4 * hf + (q & 3);
             if (row >= nrows) continue;
             if (DOWN) {
-                float* dst = a.parts + (int64_t)s_entry[row] * H + n0;
+                const int64_t o = (int64_t)s_entry[row] * H + n0;
+                if (a.parts_h) {
 #pragma unroll
-                for (int j = 0; j < 2; ++j) dst[cb[j] + (lane & 31)] = acc[i][j][q];
+                    for (int j = 0; j < 2; ++j) {
+                        const float v = __builtin_fminf(__builtin_fmaxf(acc[i][j][q], -65504.0f), 65504.0f);
+                        a.parts_h[o + cb[j] + (lane & 31)] = f2h(v);
+                    }
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) a.parts[o + cb[j] + (lane & 31)] = acc[i][j][q];
+                }
             } else {
                 // SwiGLU on the hardware exp2 and reciprocal (the f16 path's tolerance, not canon's bits), stored in
                 // the step order the down product reads
@@ -506,7 +514,9 @@ static hipError_t launch_gemm(const ExpertLayout& L, const PrefillArgs& a, hipSt
 hipError_t launch_prefill_experts(const ExpertLayout& L, const PrefillArgs& a, hipStream_t s) {
     const int64_t nc = a.n_tok * L.n_embd / 8;
     hipLaunchKernelGGL(to_f16_kernel, dim3((unsigned)((nc + 255) / 256)), dim3(256), 0, s, a.x, a.xb, nc);
-    hipLaunchKernelGGL(tile_map_kernel, dim3(1), dim3(1024), 0, s, a.bounds, a.n_groups, a.mtile, (int)a.cap_groups);
+    if (!a.mtile_ready)
+        hipLaunchKernelGGL(tile_map_kernel, dim3(1), dim3(1024), 0, s, a.bounds, a.n_groups, a.mtile,
+                           (int)a.cap_groups);
     hipError_t e = launch_gemm<false>(L, a, s);
     if (e != hipSuccess) return e;
     return launch_gemm<true>(L, a, s);

@@ -56,6 +56,14 @@ hipError_t launch_prefill_route(const int32_t* ids, int64_t n, int k, int n_expe
                                 int32_t* entry, int32_t* bounds, int32_t* experts, int32_t* n_groups,
                                 const uint8_t* cache_base, long long blob, unsigned long long* grp_ptr, hipStream_t s);
 
+// the same permutation over ceil(n / 1024) work-groups (ghist: prefill_route_split_scratch bytes), and, when mtile
+// is given, the m-tile prefixes launch_prefill_experts would compute (PrefillArgs::mtile_ready)
+hipError_t launch_prefill_route_split(const int32_t* ids, int64_t n, int k, int n_expert, int32_t* src, int32_t* slot,
+                                      int32_t* entry, int32_t* bounds, int32_t* experts, int32_t* n_groups,
+                                      const uint8_t* cache_base, long long blob, unsigned long long* grp_ptr,
+                                      int32_t* ghist, int32_t* mtile, int cap_groups, hipStream_t s);
+size_t prefill_route_split_scratch(int64_t n, int n_expert);
+
 // decode_layer.hip
 hipError_t launch_decode_route(const float* logits, const float* x, int n_tok, int n_expert, int k, int64_t n_embd,
                                int32_t* ids, float* weights, int32_t* plan, long long capx, uint32_t* skip,
@@ -95,6 +103,9 @@ hipError_t launch_decode_fused(const FusedArgs& a, const FusedPlan& P, hipStream
 hipError_t launch_combine(const float* parts, const float* weights, const float* shared, const float* shared_gate,
                           const float* residual, float* out, int64_t n_embd, int k, int n_tok, hipStream_t s);
 hipError_t launch_add_inplace(float* x, const float* y, int64_t n, hipStream_t s);
+// the combine over f16 parts, + residual (n_embd % 4 == 0)
+hipError_t launch_combine_h(const uint16_t* parts, const float* weights, const float* residual, float* out,
+                            int64_t n_embd, int k, int n_tok, hipStream_t s);
 
 // experts_prefill.hip
 struct PrefillArgs {
@@ -107,7 +118,9 @@ struct PrefillArgs {
     uint16_t* xb;                   // scratch: [n_tok, n_embd] f16 copy of x, in the GEMM's K order
     uint16_t* h;                    // scratch: [rows, n_ff] f16 SwiGLU output, in the GEMM's K order
     float* parts;                   // [n_tok * k, n_embd] routing-order outputs
+    uint16_t* parts_h;              // the same in f16 (saturated), written in place of parts when set
     int32_t* mtile;                 // scratch: [2, cap_groups + 1] m-tile prefixes of the groups (128-, 64-row tiles)
+    bool mtile_ready;               // mtile already holds them (launch_prefill_route_split wrote them)
     int32_t* err;
     int64_t n_tok, rows, cap_groups;
 };
