@@ -22,7 +22,7 @@ ROOT = pathlib.Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / "xestrata-win_amd"))
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, published
-BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, published
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 and fp16 MFMA, published
 METRIC = "MoE-layer decode µs/token + expert-weight HBM GB/s (% of peak); prefill TFLOP/s"
 
 
@@ -92,6 +92,26 @@ def pmc_run(torch, xm, copies):
         f"4 copies of {256 << 20} bytes; status {layer.status()}")
 
 
+def pmc_prefill(torch, xm):
+    """The workload of a rocprofv3 --pmc pass on the prompt path: 4 config-3 prefill layers (2048 tokens, Zipf(1.2)
+    routing), the grouped GEMMs' counters read per dispatch."""
+    import numpy as np
+    E, H, F, k, Tp = 128, 2048, 768, 8, 2048
+    arena, L = xm.build_arena(E, H, F, xm.Q4_K, xm.Q6_K, seed=0, copies=1)
+    rng = np.random.default_rng(3)
+    pop = -1.2 * np.log(np.arange(1, E + 1))[rng.permutation(E)]
+    zl = torch.from_numpy((pop[None, :] + rng.gumbel(size=(Tp, E))).astype(np.float32)).cuda()
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    xp = torch.randn(Tp, H, device="cuda", generator=gen).to(torch.bfloat16).float()
+    rp = torch.randn(Tp, H, device="cuda", generator=gen)
+    op = torch.empty(Tp, H, device="cuda")
+    layer = xm.MoeLayer(L, arena, E, k, Tp, prefill=True)
+    for _ in range(4):
+        layer(xp, zl, rp, op)
+    torch.cuda.synchronize()
+    log("pmc prefill run: 4 config-3 prefill layers")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -102,6 +122,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--pmc-run", action="store_true", help="only the short workload of a rocprofv3 --pmc pass")
+    ap.add_argument("--pmc-prefill", action="store_true", help="only 4 prefill layers, for a rocprofv3 --pmc pass")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -117,6 +138,9 @@ def main():
     torch.cuda.set_device(0)
     if args.pmc_run:
         pmc_run(torch, xm, args.copies)
+        return
+    if args.pmc_prefill:
+        pmc_prefill(torch, xm)
         return
     E, H, F, k = 128, 2048, 768, 8
     copies = args.copies
@@ -199,7 +223,8 @@ def main():
     tf = flops / (ms_p * 1e-3) / 1e12
     log(f"prefill T={Tp}: {ms_p * 1e3:.1f} us/layer, {tf:.1f} TFLOP/s")
     prefill = dict(tokens=Tp, us_per_layer=round(ms_p * 1e3, 1), tflops=round(tf, 2),
-                   frac_bf16_peak=round(tf / BF16_PEAK_TFLOPS, 4), tokens_per_s=round(Tp / (ms_p * 1e-3), 0),
+                   frac_mfma_peak=round(tf / BF16_PEAK_TFLOPS, 4), mfma="f16 operands, fp32 accumulate (dense peak "
+                   "2.5 PFLOP/s, as bf16)", tokens_per_s=round(Tp / (ms_p * 1e-3), 0),
                    flops_per_layer=flops, routing="Zipf alpha=1.2 (Gumbel-top-k)")
 
     # ---------------------------------------------------------------- the CPU baseline (the oracle, host cores)

@@ -132,10 +132,11 @@ __device__ __forceinline__ h2_t h2b(float v) {   // v rounded to f16, in both ha
     const _Float16 h = (_Float16)v;
     return (h2_t){h, h};
 }
-// (a & m) | o as one v_and_or_b32 (left to itself the compiler regroups nested ones into v_and, v_and, v_or3_b32)
+// (a & m) | o as one v_and_or_b32: the empty asm pins the result, else the compiler regroups nested ones into v_and,
+// v_and, v_or3_b32 (an instruction more)
 __device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t o) {
-    uint32_t r;
-    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(m), "v"(o));
+    uint32_t r = (a & m) | o;
+    asm("" : "+v"(r));
     return r;
 }
 
