@@ -125,6 +125,19 @@ __device__ __forceinline__ int add_dev(int32_t* p, int v) {
 // activations, polls), wave 3 writes h and parts from LDS.
 __device__ __forceinline__ void vm_drain() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// n16 16-byte chunks to LDS dst[0 .. n16) by one wave's DMA: the store wave's fetch of the first down slab, issued
+// once the gate/up slab is in (so it does not compete with it), complete at the store wave's vm_drain()
+template <typename Src>
+__device__ __forceinline__ void dma_wave_to_lds(uint8_t* dst, int n16, Src src) {
+    const int lane = threadIdx.x & 63;
+    for (int base = 0; base < n16; base += 64) {
+        const int i = base + lane;
+        if (i < n16)
+            __builtin_amdgcn_global_load_lds(src(i), (__attribute__((address_space(3))) void*)(dst + 16 * base), 16, 0,
+                                             2 /* nt */);
+    }
+}
+
 // n16 16-byte chunks to LDS dst[0 .. n16) by DMA (global_load_lds_dwordx4: a wave's instruction fills 64 consecutive
 // chunks at a wave-uniform LDS address), chunk i from src(i); issued by the load waves, complete at their vm_drain()
 template <typename Src>
@@ -374,6 +387,9 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
     const int n16a = rh * (int)L.gu_row / 16, n16d = rd * (int)L.d_row / 16;
     float* s_po = (float*)(lds + o.po);
     const bool loader = wave < kLoadWaves;
+    // with at most one gate/up unit a work-group, the store wave fetches the work-group's first down rows once the
+    // gate/up slab is in: they then land while the gate/up products run and h travels
+    const bool dn_early = n_gu <= (int)gridDim.x && wg < n_gu && wg < n_dn;
     for (int u1 = wg; u1 < n_gu; u1 += gridDim.x) {
         const int g = u1 / nu, j = u1 - g * nu;
         const uint8_t* blob = a.arena + (size_t)s_gexp[g] * (size_t)a.blob;
@@ -398,6 +414,12 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
                 vm_drain();   // the slab and the activations have landed
             }
             __syncthreads();
+            if (dn_early && !loader && u1 == wg && p == e0) {
+                const int gd = wg / nj, jd = wg - gd * nj;
+                const uint8_t* srcd =
+                    a.arena + (size_t)s_gexp[gd] * (size_t)a.blob + L.down_off + (size_t)jd * rd * L.d_row;
+                dma_wave_to_lds(slab_dn, n16d, [&](int i) { return (const void*)(srcd + 16 * (size_t)i); });
+            }
             const int c = lane & (lpr_g - 1);
             for (int rr = tid / lpr_g; rr < 2 * rh; rr += kFT / lpr_g) {
                 float acc[NE];
@@ -428,7 +450,8 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
         const int g = u2 / nj, j = u2 - g * nj;
         const uint8_t* srcd = a.arena + (size_t)s_gexp[g] * (size_t)a.blob + L.down_off + (size_t)j * rd * L.d_row;
         __syncthreads();   // the previous unit's readers of the slab are done
-        if (loader) dma_to_lds(slab_dn, n16d, [&](int i) { return (const void*)(srcd + 16 * (size_t)i); });
+        const bool fetched = dn_early && u2 == wg;
+        if (loader && !fetched) dma_to_lds(slab_dn, n16d, [&](int i) { return (const void*)(srcd + 16 * (size_t)i); });
         const int e0 = s_start[g], e1 = s_start[g + 1];
         for (int p = e0; p < e1; p += NE) {
             const int m = min(NE, e1 - p);
@@ -471,6 +494,8 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
                     }
                 }
                 vm_drain();   // the slab has landed
+            } else if (fetched && p == e0) {
+                vm_drain();   // the store wave's fetch of the slab has landed
             }
             __syncthreads();
             const int c = lane & (lpr_d - 1);
@@ -546,17 +571,42 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
 
 // ---------------------------------------------------------------- host side
 
+// compute units of the current device (cached per device)
+static int device_cus() {
+    static std::mutex mu;
+    static std::vector<std::pair<int, int>> seen;
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    std::lock_guard<std::mutex> lock(mu);
+    for (const auto& s : seen)
+        if (s.first == dev) return s.second;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    seen.emplace_back(dev, cus);
+    return cus;
+}
+
 bool fused_decode_plan(const ExpertLayout& L, int n_expert, int k, int n_tok, FusedPlan* P) {
     const int H = (int)L.n_embd, F = (int)L.n_ff, n = n_tok * k;
     if (n > kFMaxN || n_expert > 1024 || k > 64 || n_tok > 64) return false;
     const bool pair = (L.gu_type == kQ4_K && L.d_type == kQ6_K) || (L.gu_type == kQ8_0 && L.d_type == kQ8_0) ||
                       (L.gu_type == kIQ4_XS && L.d_type == kIQ4_XS) || (L.gu_type == kQ4_K && L.d_type == kQ4_K);
     if (!pair || H % 256 || F % 32) return false;
-    // h-slab rows: about 36 KB of gate + up rows, a multiple of 8 dividing n_ff
+    // h-slab rows: about 36 KB of gate + up rows, a multiple of 8 dividing n_ff (of 4 for one token, below)
     int rh = (int)((36864 / (2 * L.gu_row)) & ~7ll);
     if (rh < 8) rh = 8;
     while (rh > 8 && F % rh) rh -= 8;
     if (F % rh) return false;
+    // one token: its k groups' gate/up units as close to one a resident work-group (two a CU) as the slab allows -
+    // smaller slabs spread the weight stream over more CUs, and each work-group then also fetches its down rows
+    // while its gate/up products run
+    if (n_tok == 1) {
+        const int target = 2 * device_cus();
+        for (int r = 4; r < rh; r += 4)
+            if (F % r == 0 && (int64_t)k * (F / r) <= target) {
+                rh = r;
+                break;
+            }
+    }
     int rd = (int)((20480 / L.d_row) & ~7ll);
     if (rd < 8) rd = 8;
     if (rd > 64) rd = 64;
