@@ -422,7 +422,7 @@ int xs_add_inplace(float* x, const float* y, int64_t n, void* stream) {
 namespace {
 struct DecodeWs {
     int32_t* status;   // the error word, first in the workspace
-    int32_t* sync;     // the persistent layer's epoch and done counts (same 1024 bytes, from byte 64)
+    int32_t* sync;     // the persistent layer's call counters (same 4 KB head, from byte 128)
     unsigned long long *hx, *px;   // the persistent layer's tagged hand-over words (256 entries)
     int32_t* ids;
     float* w;
@@ -445,8 +445,8 @@ DecodeWs decode_ws(const xs_expert_layout_t* L, int n_expert, int k, int n_tok, 
     const long long capx = (long long)n_tok * k;
     size_t off = 0;
     auto take = [&](size_t b) { uint8_t* p = base ? base + off : nullptr; off += up256(b); return p; };
-    d.status = (int32_t*)take(1024);
-    d.sync = d.status ? d.status + 16 : nullptr;
+    d.status = (int32_t*)take(4096);
+    d.sync = d.status ? d.status + 32 : nullptr;
     const bool fused = fused_possible(L, n_expert, k);
     d.hx = (unsigned long long*)take(fused ? (size_t)256 * (size_t)L->n_ff * 8 : 0);
     d.px = (unsigned long long*)take(fused ? (size_t)256 * (size_t)L->n_embd * 8 : 0);

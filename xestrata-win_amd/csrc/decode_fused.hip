@@ -104,8 +104,8 @@ __device__ __forceinline__ void q8_1_256_to_act(const float* __restrict__ x, int
 // acknowledged before raising a flag waits behind the HBM write queue, which the weight stream starves.  So a value
 // handed over travels in a 64-bit word with the call's tag in its upper half, written and read with device-scope
 // relaxed atomics (coherent across XCDs by themselves: write-through stores, loads that refetch), and the reader
-// polls the words it needs until every one carries the tag.  Tags come from an epoch in the workspace that the last
-// work-group to finish advances, so no word needs resetting and a stale word never matches.
+// polls the words it needs until every one carries the tag.  Tags come from a call counter in the workspace that
+// every call advances by one epoch (done_call), so no word needs resetting and a stale word never matches.
 __device__ __forceinline__ void st_tag(unsigned long long* p, float v, unsigned int tag) {
     __hip_atomic_store(p, ((unsigned long long)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
@@ -180,29 +180,40 @@ __device__ __forceinline__ float lanes_sum(float v, int l) {
     return l == 8 ? lane0_sum<8>(v) : l == 4 ? lane0_sum<4>(v) : l == 2 ? lane0_sum<2>(v) : v;
 }
 
-// The work-group is done with the call.  Work-groups count themselves done in eight sub-counters (blockIdx % 8, 64
-// atomics an address instead of 512 on one), the last of a sub-count in a top counter, and the last of the top count
-// advances the epoch and clears the counters: every work-group read the epoch before it counted itself done.
-__device__ __forceinline__ void done_call(const FusedArgs& a, unsigned int tag) {
+// The work-group is done with the call: it adds its share of 2^20 to one of 16 64-bit call counters (the shares of a
+// grid sum to 2^20 whatever its size; 16 counters, 128 bytes apart, keep the device atomics on one address few), and
+// does not wait for the result.  The next call's epoch is (the counters' sum) >> 20: the kernel's end makes every
+// addition visible to the next launch, and no work-group has to learn it was the last (that took three dependent
+// device atomics at the end of every call).
+constexpr int kCounters = 16, kCounterStride = 32;   // counters, ints apart
+__device__ __forceinline__ void done_call(const FusedArgs& a, unsigned int) {
     if (threadIdx.x != 0) return;
-    const int G = (int)gridDim.x, sub = (int)blockIdx.x & 7;
-    const int in_sub = G / 8 + (sub < G % 8 ? 1 : 0);
-    const int subs = G < 8 ? G : 8;
-    if (add_dev(a.sync + 32 + 16 * sub, 1) != in_sub - 1) return;
-    __hip_atomic_store(a.sync + 32 + 16 * sub, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (add_dev(a.sync + 16, 1) != subs - 1) return;
-    __hip_atomic_store(a.sync + 16, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(a.sync, (int)tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned int G = gridDim.x, b = blockIdx.x;
+    const unsigned long long share = (1ull << 20) / G + (b < (1u << 20) % G ? 1ull : 0ull);
+    __hip_atomic_fetch_add((unsigned long long*)(a.sync + kCounterStride * (b % kCounters)), share, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+}
+// the epoch: lane i of a wave loads counter i (issued early, its latency behind the routing), and the wave's sum
+// gives it (on every lane) once the routing is done
+__device__ __forceinline__ unsigned long long load_counter(const FusedArgs& a) {
+    const int lane = threadIdx.x & 63;
+    return lane < kCounters ? __hip_atomic_load((unsigned long long*)(a.sync + kCounterStride * lane), __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT)
+                            : 0ull;
+}
+__device__ __forceinline__ int epoch_of(unsigned long long c) {
+#pragma unroll
+    for (int o = 1; o < kCounters; o <<= 1) c += __shfl_xor(c, o, 64);
+    return (int)(c >> 20);
 }
 
 template <int PER>
-__device__ __forceinline__ void route_tokens_wave(const FusedArgs& a, int* s_ids, float* s_w, int& epoch) {
+__device__ __forceinline__ void route_tokens_wave(const FusedArgs& a, int* s_ids, float* s_w,
+                                                  unsigned long long& ctr) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, E = a.n_expert, k = a.k;
     float lv[PER];
     if (wave < a.n_tok) load_logits_wave<PER>(a.logits + (int64_t)wave * E, E, lv);
-    if (tid == 0) {
-        epoch = __hip_atomic_load(a.sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    ctr = load_counter(a);
     for (int t = wave; t < a.n_tok; t += kFT / 64) {
         if (lane < k) {   // ranks a NaN row leaves unwritten stay invalid
             s_ids[t * k + lane] = -1;
@@ -247,16 +258,14 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
     }
 
     // ---- 1. routing, in every work-group (router.cpp:59-308 and verify_kernels.cpp:819-890's order, in LDS): up to
-    // three tokens on the whole work-group each, more on a wave each.  The logits loads go out first; thread 0 then
-    // reads the epoch, used only after the routing, so its latency hides behind it.
-    int epoch = 0;
+    // three tokens on the whole work-group each, more on a wave each.  The logits loads go out first; the call
+    // counters' loads follow, summed only after the routing, so their latency hides behind it.
+    unsigned long long ctr = 0;
     if (T <= 3 && E <= 256) {
         float lvp[3];
 #pragma unroll
         for (int t = 0; t < 3; ++t) lvp[t] = t < T && tid < E ? a.logits[(int64_t)t * E + tid] : 0.0f;
-        if (tid == 0) {
-            epoch = __hip_atomic_load(a.sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+        ctr = load_counter(a);
         if (tid < n) {   // ranks a NaN row leaves unwritten stay invalid
             s_ids[tid] = -1;
             s_w[tid] = 0.0f;
@@ -267,17 +276,20 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
                 route_topk_block(lvp[t], E, k, (unsigned long long*)(lds + o.key), s_excl, (double*)(lds + o.red),
                                  (int*)(lds + o.sel), s_ids + t * k, s_w + t * k);
     } else if (E <= 64) {
-        route_tokens_wave<1>(a, s_ids, s_w, epoch);
+        route_tokens_wave<1>(a, s_ids, s_w, ctr);
     } else if (E <= 128) {
-        route_tokens_wave<2>(a, s_ids, s_w, epoch);
+        route_tokens_wave<2>(a, s_ids, s_w, ctr);
     } else if (E <= 256) {
-        route_tokens_wave<4>(a, s_ids, s_w, epoch);
+        route_tokens_wave<4>(a, s_ids, s_w, ctr);
     } else if (E <= 512) {
-        route_tokens_wave<8>(a, s_ids, s_w, epoch);
+        route_tokens_wave<8>(a, s_ids, s_w, ctr);
     } else {
-        route_tokens_wave<16>(a, s_ids, s_w, epoch);
+        route_tokens_wave<16>(a, s_ids, s_w, ctr);
     }
-    if (tid == 0) s_misc[3] = epoch;
+    if (wave == 0) {
+        const int epoch = epoch_of(ctr);
+        if (lane == 0) s_misc[3] = epoch;
+    }
     __syncthreads();
     // the plan: groups = distinct experts in order of first occurrence, a group's entries ascending
     if (T == 1) {   // one token: its k experts are distinct, each a group of one entry, in rank order

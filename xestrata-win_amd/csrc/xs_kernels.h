@@ -90,8 +90,8 @@ struct FusedArgs {
     // hand-over words: a float's bits | the call's tag << 32 (tags never repeat, so no reset is needed)
     unsigned long long* hx; // [256, n_ff] SwiGLU outputs, plan order
     unsigned long long* px; // [256, n_embd] expert outputs, routing order
-    int32_t* sync;          // [0] the epoch (this call's tag - 1), [16] sub-counts done, [32 + 16 s] work-groups
-                            // done in sub-count s (8); zero before the first call
+    int32_t* sync;          // 16 64-bit call counters at sync + 32 i (2 KB, 8-byte aligned; 2^20 a call in all, this
+                            // call's tag - 1 = their sum >> 20), zero before the first call
     int32_t* err;
     int rh, rd, nu, nj, slab_gu_bytes, slab_dn_bytes;
     long long spin_ticks;   // bound of a wait, in wall-clock ticks
