@@ -541,6 +541,7 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
             const int64_t col = (int64_t)j * rd + r;
             const unsigned long long* pp = a.px + (int64_t)t * k * H + col;
             const float* ww = s_w + t * k;
+            const float res = a.residual[(int64_t)t * H + col];   // in flight while the parts are polled
             float sum = 0.0f;
             bool good = true;
             for (int e0 = 0; e0 < k; e0 += 16) {   // 16 parts in flight at once
@@ -575,7 +576,7 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
                     }
             }
             if (!good) atomicOr(a.err, 2);
-            a.out[(int64_t)t * H + col] = a.residual[(int64_t)t * H + col] + sum;
+            a.out[(int64_t)t * H + col] = res + sum;
         }
     }
     done_call(a, tag);
