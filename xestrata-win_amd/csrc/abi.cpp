@@ -544,6 +544,7 @@ int xs_moe_layer_decode(const xs_expert_layout_t* L, const uint8_t* arena, size_
         a.nj = P.nj;
         a.slab_gu_bytes = P.slab_gu;
         a.slab_dn_bytes = P.slab_dn;
+        a.ttab = P.ttab;
         a.spin_ticks = spin_ticks();
         return finish(stream, xs::launch_decode_fused(a, P, S(stream)), "moe_layer_decode");
     }

@@ -42,8 +42,9 @@ __host__ __device__ inline int up16(int v) { return (v + 15) & ~15; }
 // one entry's LDS activation of n values: int8 values | n / 32 fp32 scales | n / 16 int sums of 16
 __host__ __device__ inline int act_stride(int n) { return up16(n + n / 8 + n / 4); }
 
+// ttab: tokens of the LDS activation table of the pipelined gate/up path (0: none; it then also has no second slab)
 template <int NE>
-__host__ __device__ inline FusedLds fused_lds(int n_expert, int H, int F, int rh, int slab_gu, int slab_dn) {
+__host__ __device__ inline FusedLds fused_lds(int n_expert, int H, int F, int rh, int slab_gu, int slab_dn, int ttab) {
     FusedLds o;
     int at = 0;
     o.ids = at; at += up16(kFMaxN * 4);
@@ -62,8 +63,9 @@ __host__ __device__ inline FusedLds fused_lds(int n_expert, int H, int F, int rh
     o.gu = at; at += up16(NE * 2 * rh * 4);
     o.po = at; at += up16(NE * 64 * 4);
     o.slab_gu = at; at += up16(slab_gu);
+    if (ttab > 0) at += up16(slab_gu);   // a second gate/up slab: a unit is fetched while one computes
     o.slab_dn = at; at += up16(slab_dn);
-    o.act_g = at; at += NE * act_stride(H);
+    o.act_g = at; at += (ttab > NE ? ttab : NE) * act_stride(H);   // the passes' activations, or the token table
     o.act_d = at; at += NE * act_stride(F);
     o.total = at;
     return o;
@@ -124,6 +126,18 @@ __device__ __forceinline__ int add_dev(int32_t* p, int v) {
 // fills the memory queues.  So the waves that load never store a hand-over word: waves 0..2 fetch (weights by DMA,
 // activations, polls), wave 3 writes h and parts from LDS.
 __device__ __forceinline__ void vm_drain() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// wait until at most n of the wave's vector memory operations are outstanding (n wave-uniform; above 15, 15: a wait
+// for more than asked, never less)
+__device__ __forceinline__ void vm_wait_le(int n) {
+    switch (n < 15 ? n : 15) {
+#define XS_VMW(i) \
+    case i: asm volatile("s_waitcnt vmcnt(" #i ")" ::: "memory"); break;
+        XS_VMW(0) XS_VMW(1) XS_VMW(2) XS_VMW(3) XS_VMW(4) XS_VMW(5) XS_VMW(6) XS_VMW(7)
+        XS_VMW(8) XS_VMW(9) XS_VMW(10) XS_VMW(11) XS_VMW(12) XS_VMW(13) XS_VMW(14) XS_VMW(15)
+#undef XS_VMW
+        default: break;
+    }
+}
 
 // n16 16-byte chunks to LDS dst[0 .. n16) by one wave's DMA: the store wave's fetch of the first down slab, issued
 // once the gate/up slab is in (so it does not compete with it), complete at the store wave's vm_drain()
@@ -232,7 +246,7 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
     const ExpertLayout& L = a.L;
     const int H = (int)L.n_embd, F = (int)L.n_ff, k = a.k, T = a.n_tok, n = T * k, E = a.n_expert;
     const int rh = a.rh, rd = a.rd, nu = a.nu, nj = a.nj;
-    const FusedLds o = fused_lds<NE>(E, H, F, rh, a.slab_gu_bytes, a.slab_dn_bytes);
+    const FusedLds o = fused_lds<NE>(E, H, F, rh, a.slab_gu_bytes, a.slab_dn_bytes, a.ttab);
     int* s_ids = (int*)(lds + o.ids);
     float* s_w = (float*)(lds + o.w);
     int* s_excl = (int*)(lds + o.excl);
@@ -401,7 +415,81 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
     const bool loader = wave < kLoadWaves;
     // with at most one gate/up unit a work-group, the store wave fetches the work-group's first down rows once the
     // gate/up slab is in: they then land while the gate/up products run and h travels
-    const bool dn_early = n_gu <= (int)gridDim.x && wg < n_gu && wg < n_dn;
+    const bool piped = a.ttab > 0 && T <= a.ttab;   // the pipelined gate/up path below (4..16 tokens)
+    const bool dn_early = !piped && n_gu <= (int)gridDim.x && wg < n_gu && wg < n_dn;
+    if (piped) {
+        // 4..16 tokens, several units a work-group: every token's q8_1 activation once, into an LDS table, then the
+        // units' slabs double-buffered - unit i + 1's DMA flies while unit i computes.  The load waves issue nothing
+        // but those DMAs meanwhile, so waiting for unit i is vmcnt <= (unit i + 1's DMA instructions of the wave).
+        int8_t* ttab = (int8_t*)(lds + o.act_g);
+        for (int t = 0; t < T; ++t) {
+            const float* xr = a.x + (int64_t)t * H;
+            int8_t* q = ttab + t * act_stride(H);
+            for (int j8 = tid; j8 < H / 8; j8 += kFT)
+                q8_1_256_to_act(xr, j8, q, (float*)(q + H), (int*)(q + H + H / 8));
+        }
+        vm_drain();
+        uint8_t* slab2[2] = {slab_gu, slab_gu + up16(a.slab_gu_bytes)};
+        const int per_wave = loader && 2 * n16a > 64 * wave ? (2 * n16a - 64 * wave + kLT - 1) / kLT : 0;
+        auto dma_unit = [&](int u, uint8_t* dst) {
+            const int g = u / nu, j = u - g * nu;
+            const uint8_t* blob = a.arena + (size_t)s_gexp[g] * (size_t)a.blob;
+            const uint8_t* srcg = blob + (size_t)j * rh * L.gu_row;
+            const uint8_t* srcu = blob + L.up_off + (size_t)j * rh * L.gu_row;
+            dma_to_lds(dst, 2 * n16a, [&](int i) {
+                return (const void*)(i < n16a ? srcg + 16 * (size_t)i : srcu + 16 * (size_t)(i - n16a));
+            });
+        };
+        if (loader && wg < n_gu) dma_unit(wg, slab2[0]);
+        int it = 0;
+        for (int u1 = wg; u1 < n_gu; u1 += gridDim.x, ++it) {
+            const int g = u1 / nu, j = u1 - g * nu, next = u1 + (int)gridDim.x;
+            uint8_t* slab = slab2[it & 1];
+            __syncthreads();   // the previous unit's readers of the other slab and of s_gu are done
+            if (loader) {
+                if (next < n_gu) {
+                    dma_unit(next, slab2[(it + 1) & 1]);
+                    vm_wait_le(per_wave);
+                } else {
+                    vm_drain();
+                }
+            }
+            __syncthreads();   // this unit's slab is in
+            const int e0 = s_start[g], e1 = s_start[g + 1];
+            for (int p = e0; p < e1; p += NE) {
+                const int m = min(NE, e1 - p);
+                if (p > e0) __syncthreads();   // the previous pass's stores have read s_gu
+                Act at[NE];
+#pragma unroll
+                for (int e = 0; e < NE; ++e) {
+                    int8_t* q = ttab + (e < m ? s_tok[p + e] : 0) * act_stride(H);
+                    at[e] = Act{q, (const float*)(q + H), (const int*)(q + H + H / 8)};
+                }
+                const int c = lane & (lpr_g - 1);
+                for (int rr = tid / lpr_g; rr < 2 * rh; rr += kFT / lpr_g) {
+                    float acc[NE];
+#pragma unroll
+                    for (int e = 0; e < NE; ++e) acc[e] = 0.0f;
+                    for (int u = c; u < H / UG::kUnit; u += lpr_g)
+                        UG::template apply<NE>(slab, rr * (int)L.gu_row, u, at, m, acc);
+#pragma unroll
+                    for (int e = 0; e < NE; ++e) acc[e] = lanes_sum(acc[e], lpr_g);
+                    if (c == 0) {
+#pragma unroll
+                        for (int e = 0; e < NE; ++e)
+                            if (e < m) s_gu[e * 2 * rh + rr] = acc[e];
+                    }
+                }
+                __syncthreads();
+                if (!loader)
+                    for (int i = lane; i < m * rh; i += 64) {
+                        const int e = i / rh, r = i - e * rh;
+                        st_tag(a.hx + (int64_t)(p + e) * F + j * rh + r,
+                               canon_silu_mul(s_gu[e * 2 * rh + r], s_gu[e * 2 * rh + rh + r]), tag);
+                    }
+            }
+        }
+    } else
     for (int u1 = wg; u1 < n_gu; u1 += gridDim.x) {
         const int g = u1 / nu, j = u1 - g * nu;
         const uint8_t* blob = a.arena + (size_t)s_gexp[g] * (size_t)a.blob;
@@ -632,10 +720,15 @@ bool fused_decode_plan(const ExpertLayout& L, int n_expert, int k, int n_tok, Fu
     P->slab_gu = 2 * rh * (int)L.gu_row;
     P->slab_dn = rd * (int)L.d_row;
     P->ne = n_tok >= 4 ? 4 : n_tok >= 2 ? 2 : 1;
-    const FusedLds lo = P->ne == 1 ? fused_lds<1>(n_expert, H, F, rh, P->slab_gu, P->slab_dn)
-                        : P->ne == 2 ? fused_lds<2>(n_expert, H, F, rh, P->slab_gu, P->slab_dn)
-                                     : fused_lds<4>(n_expert, H, F, rh, P->slab_gu, P->slab_dn);
-    P->lds = lo.total;
+    auto lds_of = [&](int ttab) {
+        return (P->ne == 1 ? fused_lds<1>(n_expert, H, F, rh, P->slab_gu, P->slab_dn, ttab)
+                : P->ne == 2 ? fused_lds<2>(n_expert, H, F, rh, P->slab_gu, P->slab_dn, ttab)
+                             : fused_lds<4>(n_expert, H, F, rh, P->slab_gu, P->slab_dn, ttab)).total;
+    };
+    // 4..16 tokens: the pipelined gate/up path, if its token table and second slab fit
+    P->ttab = 0;
+    if (P->ne == 4 && n_tok <= 16 && lds_of(16) <= 160 * 1024) P->ttab = 16;
+    P->lds = lds_of(P->ttab);
     return P->lds <= 160 * 1024;
 }
 

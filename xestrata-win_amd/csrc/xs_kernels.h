@@ -75,6 +75,7 @@ struct FusedPlan {     // the fused decode layer's unit sizes (a function of the
     int nu, nj;        // gate/up units, down units a group
     int slab_gu, slab_dn;
     int ne, lds;       // entries a pass, dynamic LDS bytes
+    int ttab;          // tokens of the pipelined gate/up path's activation table (0: that path is off)
 };
 struct FusedArgs {
     ExpertLayout L;
@@ -93,7 +94,7 @@ struct FusedArgs {
     int32_t* sync;          // 16 64-bit call counters at sync + 32 i (2 KB, 8-byte aligned; 2^20 a call in all, this
                             // call's tag - 1 = their sum >> 20), zero before the first call
     int32_t* err;
-    int rh, rd, nu, nj, slab_gu_bytes, slab_dn_bytes;
+    int rh, rd, nu, nj, slab_gu_bytes, slab_dn_bytes, ttab;
     long long spin_ticks;   // bound of a wait, in wall-clock ticks
 };
 bool fused_decode_plan(const ExpertLayout& L, int n_expert, int k, int n_tok, FusedPlan* P);
