@@ -34,8 +34,7 @@ constexpr int kLoadWaves = 3;     // waves 0..2 issue every global load; wave 3 
 constexpr int kLT = 64 * kLoadWaves;
 
 struct FusedLds {                 // byte offsets in the dynamic LDS
-    int ids, w, excl, wave, first, gexp, start, dst, tok, misc, key, red, sel, gu, po, slab_gu, slab_dn, act_g, act_d,
-        total;
+    int ids, w, excl, wave, first, gexp, start, dst, tok, misc, gu, po, slab_gu, slab_dn, act_g, act_d, total;
 };
 
 __host__ __device__ inline int up16(int v) { return (v + 15) & ~15; }
@@ -57,9 +56,6 @@ __host__ __device__ inline FusedLds fused_lds(int n_expert, int H, int F, int rh
     o.dst = at; at += up16(kFMaxN * 4);
     o.tok = at; at += up16(kFMaxN * 4);
     o.misc = at; at += up16(96 * 4);
-    o.key = at; at += 256 * 8;
-    o.red = at; at += 16 * 8;
-    o.sel = at; at += 128 * 4;
     o.gu = at; at += up16(NE * 2 * rh * 4);
     o.po = at; at += up16(NE * 64 * 4);
     o.slab_gu = at; at += up16(slab_gu);
@@ -215,10 +211,14 @@ __device__ __forceinline__ unsigned long long load_counter(const FusedArgs& a) {
                                                 __HIP_MEMORY_SCOPE_AGENT)
                             : 0ull;
 }
-__device__ __forceinline__ int epoch_of(unsigned long long c) {
-#pragma unroll
-    for (int o = 1; o < kCounters; o <<= 1) c += __shfl_xor(c, o, 64);
-    return (int)(c >> 20);
+__device__ __forceinline__ int epoch_of(unsigned long long c) {   // lanes 0..15 (row 0) by DPP, read from lane 0
+    static_assert(kCounters == 16, "one 16-lane row of counters");
+    c += dpp_u64<kDppXor1, 0xF>(c);
+    c += dpp_u64<kDppXor2, 0xF>(c);
+    c += dpp_u64<kDppRor4, 0xF>(c);
+    c += dpp_u64<kDppRor8, 0xF>(c);
+    const unsigned int lo = __builtin_amdgcn_readlane((int)c, 0), hi = __builtin_amdgcn_readlane((int)(c >> 32), 0);
+    return (int)((((unsigned long long)hi << 32) | lo) >> 20);
 }
 
 template <int PER>
@@ -271,25 +271,18 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
         actd[e] = Act{qd, (const float*)(qd + F), (const int*)(qd + F + F / 8)};
     }
 
-    // ---- 1. routing, in every work-group (router.cpp:59-308 and verify_kernels.cpp:819-890's order, in LDS): up to
-    // three tokens on the whole work-group each, more on a wave each.  The logits loads go out first; the call
-    // counters' loads follow, summed only after the routing, so their latency hides behind it.
+    // ---- 1. routing, in every work-group (router.cpp:59-308 and verify_kernels.cpp:819-890's order, in LDS): a wave a
+    // token, waves t, t + 4, ...  The logits loads go out first; the call counters' loads follow, summed only after
+    // the routing, so their latency hides behind it.  With one token, waves 1..3 meanwhile quantize its activation
+    // (the gate/up units' q8_1 input, one scale a 256) into LDS, and wave 0 plans the call itself.
     unsigned long long ctr = 0;
-    if (T <= 3 && E <= 256) {
-        float lvp[3];
-#pragma unroll
-        for (int t = 0; t < 3; ++t) lvp[t] = t < T && tid < E ? a.logits[(int64_t)t * E + tid] : 0.0f;
-        ctr = load_counter(a);
-        if (tid < n) {   // ranks a NaN row leaves unwritten stay invalid
-            s_ids[tid] = -1;
-            s_w[tid] = 0.0f;
-        }
-#pragma unroll
-        for (int t = 0; t < 3; ++t)
-            if (t < T)
-                route_topk_block(lvp[t], E, k, (unsigned long long*)(lds + o.key), s_excl, (double*)(lds + o.red),
-                                 (int*)(lds + o.sel), s_ids + t * k, s_w + t * k);
-    } else if (E <= 64) {
+    const bool x_early = T == 1 && a.ttab == 0;
+    if (x_early && wave > 0) {
+        int8_t* q = (int8_t*)(lds + o.act_g);
+        for (int j8 = tid - 64; j8 < H / 8; j8 += kFT - 64)
+            q8_1_256_to_act(a.x, j8, q, (float*)(q + H), (int*)(q + H + H / 8));
+    }
+    if (E <= 64) {
         route_tokens_wave<1>(a, s_ids, s_w, ctr);
     } else if (E <= 128) {
         route_tokens_wave<2>(a, s_ids, s_w, ctr);
@@ -303,25 +296,28 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
     if (wave == 0) {
         const int epoch = epoch_of(ctr);
         if (lane == 0) s_misc[3] = epoch;
+        if (T == 1) {   // one token: its k experts are distinct, each a group of one entry, in rank order
+            const int ex = lane < k ? s_ids[lane] : 0;   // this lane's own rank (route_topk_wave_lv writes lane < k)
+            if (__ballot(lane < k && (ex < 0 || ex >= E))) {
+                if (lane == 0) s_misc[0] = -1;
+            } else {
+                if (lane < k) {
+                    s_gexp[lane] = ex;
+                    s_start[lane] = lane;
+                    s_dst[lane] = lane;
+                    s_tok[lane] = 0;
+                }
+                if (lane == 0) {
+                    s_start[k] = k;
+                    s_misc[0] = k;
+                }
+            }
+        }
     }
     __syncthreads();
     // the plan: groups = distinct experts in order of first occurrence, a group's entries ascending
-    if (T == 1) {   // one token: its k experts are distinct, each a group of one entry, in rank order
-        const int ex = tid < n ? s_ids[tid] : 0;
-        if (__syncthreads_or(tid < n && (ex < 0 || ex >= E))) {
-            if (tid == 0) s_misc[0] = -1;
-        } else {
-            if (tid < n) {
-                s_gexp[tid] = ex;
-                s_start[tid] = tid;
-                s_dst[tid] = tid;
-                s_tok[tid] = 0;
-            }
-            if (tid == 0) {
-                s_start[n] = n;
-                s_misc[0] = n;
-            }
-        }
+    if (T == 1) {
+        // planned above
     } else if (n <= 64) {   // one wave: uniform v_readlane loops, no work-group scan
         if (wave == 0) {
             const int ex = lane < n ? s_ids[lane] : -1;
@@ -393,7 +389,7 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
             }
         }
     }
-    __syncthreads();
+    if (T > 1) __syncthreads();
     const unsigned int tag = (unsigned int)s_misc[3] + 1u;
     if (s_misc[0] < 0) {   // a rank left unwritten (NaN logits): no output this call
         if (tid == 0) atomicOr(a.err, 4);
@@ -505,7 +501,7 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
             const int m = min(NE, e1 - p);
             if (p > e0) __syncthreads();   // the previous pass's readers of the activations are done
             if (loader) {
-                for (int e = 0; e < m; ++e) {    // the entries' tokens to q8_1, one scale a 256
+                for (int e = 0; e < (x_early ? 0 : m); ++e) {    // the entries' tokens to q8_1, one scale a 256
                     const float* xr = a.x + (int64_t)s_tok[p + e] * H;
                     int8_t* q = (int8_t*)(lds + o.act_g) + e * act_stride(H);
                     for (int j8 = tid; j8 < H / 8; j8 += kLT)

@@ -148,18 +148,21 @@ __device__ __forceinline__ unsigned long long dpp_u64(unsigned long long v) {
     const int hi = __builtin_amdgcn_update_dpp((int)(v >> 32), (int)(v >> 32), CTRL, ROWS, 0xF, false);
     return ((unsigned long long)(unsigned int)hi << 32) | (unsigned int)lo;
 }
-__device__ __forceinline__ unsigned long long max_u64(unsigned long long a, unsigned long long b) { return a > b ? a : b; }
-// the largest 64-bit key of the wave, uniform: rows by xor and rotation, then rows 0+1 into row 1, 2+3 into row 3 and
-// row 1 into row 3 (row_bcast), read from lane 63.  Branch-free: no exec-mask or scalar round trips on the way.
-__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
-    v = max_u64(v, dpp_u64<kDppXor1, 0xF>(v));
-    v = max_u64(v, dpp_u64<kDppXor2, 0xF>(v));
-    v = max_u64(v, dpp_u64<kDppRor4, 0xF>(v));
-    v = max_u64(v, dpp_u64<kDppRor8, 0xF>(v));
-    v = max_u64(v, dpp_u64<kDppBcast15, 0xA>(v));
-    v = max_u64(v, dpp_u64<kDppBcast31, 0xC>(v));
-    const unsigned int lo = __builtin_amdgcn_readlane((int)v, 63), hi = __builtin_amdgcn_readlane((int)(v >> 32), 63);
-    return ((unsigned long long)hi << 32) | lo;
+// the largest 32-bit unsigned value of the wave, uniform: rows by xor and rotation, then rows 0+1 into row 1, 2+3 into
+// row 3 and row 1 into row 3 (row_bcast), read from lane 63.  0 is the identity of the max, so each move fuses into one
+// v_max_u32_dpp (lanes of rows a move leaves out keep their value); no exec-mask or scalar round trips on the way.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint32_t max_dpp_u32(uint32_t v) {
+    return max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROWS, 0xF, true));
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max_dpp_u32<kDppXor1, 0xF>(v);
+    v = max_dpp_u32<kDppXor2, 0xF>(v);
+    v = max_dpp_u32<kDppRor4, 0xF>(v);
+    v = max_dpp_u32<kDppRor8, 0xF>(v);
+    v = max_dpp_u32<kDppBcast15, 0xA>(v);
+    v = max_dpp_u32<kDppBcast31, 0xC>(v);
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
 // max over each 16-lane row (every lane ends with its row's), over 32 lanes, over the wave (uniform); every lane of

@@ -59,28 +59,102 @@ __device__ void route_topk_wave_lv(const float (&lv)[PER], int n_expert, int k, 
         }
         inv = (float)(1.0 / sum);
     }
-    // candidates as 64-bit keys: the bits of p (non-negative, so ordered as unsigned) over the inverted index (a
-    // tie goes to the lower index); 0 = no candidate (NaN p never wins, taken experts drop out)
-    unsigned long long key[PER];
+    // k argmax passes (the reference's order: the larger p wins, a tie goes to the lower index; NaN never wins).  A
+    // candidate's p bits + 1 order as p does (p >= 0), 0 marks none; each pass is one 32-bit wave max and, for the
+    // tie, the lowest lane of the lowest slot holding it (slot j holds experts 64 j + lane).
+    uint32_t pv[PER];
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
         const int x = lane + 64 * j;
         const float p = x < n_expert ? (float)(ex[j] * (double)inv) : __int_as_float(0x7FC00000);
-        key[j] = p == p ? ((unsigned long long)__float_as_uint(p) << 32) | (unsigned int)~x : 0ull;
+        pv[j] = p == p ? __float_as_uint(p) + 1u : 0u;
     }
+    constexpr int kEq = 32, kNe = 33, kUge = 35;   // llvm.amdgcn.icmp predicates: the compare's lane mask, straight
     float my_w = 0.0f;
     int my_id = 0, nsel = 0;
-    for (int i = 0; i < k; ++i) {
-        unsigned long long best = key[0];
+    // Fast path, the same keys in the same order without k dependent passes: below the largest key, thresholds half a
+    // binade apart; at the highest one with at least k candidates at or above it, the M (<= 32) candidates there
+    // are moved to lanes 0..M-1 (ds_permute), each one's rank is the count of candidate keys above its own, and the k
+    // best move to the lanes of their ranks.  Otherwise (NaN p, k > 32, candidates too dense) the passes below.
+    int nvalid = 0;
+    uint32_t pm = 0u;
 #pragma unroll
-        for (int j = 1; j < PER; ++j) best = max_u64(best, key[j]);
-        best = wave_max_u64(best);
-        if (best == 0ull) break;   // every p left is NaN: ranks i.. keep the buffer's contents
+    for (int j = 0; j < PER; ++j) {
+        nvalid += __popcll(__builtin_amdgcn_uicmp(pv[j], 0u, kNe));
+        pm = pm > pv[j] ? pm : pv[j];
+    }
+    if (nvalid > k && k <= 32) {
+        pm = wave_max_u32(pm);
+        uint32_t c = 0u;
+        int M = 0;
 #pragma unroll
-        for (int j = 0; j < PER; ++j) key[j] = key[j] == best ? 0ull : key[j];
+        for (int st = 1; st <= 16; ++st) {
+            const uint32_t cs = pm > ((uint32_t)st << 22) ? pm - ((uint32_t)st << 22) : 1u;
+            int n = 0;
+#pragma unroll
+            for (int j = 0; j < PER; ++j) n += __popcll(__builtin_amdgcn_uicmp(pv[j], cs, kUge));
+            if (c == 0u && n >= k) {
+                c = cs;
+                M = n;
+            }
+        }
+        if (c != 0u && M <= 32) {
+            // candidate q of the ascending index order to lane q; lanes that are no candidate write lane 63
+            uint32_t cp = 0u, cx = 0u;
+            int base = 0;
+#pragma unroll
+            for (int j = 0; j < PER; ++j) {
+                const unsigned long long cm = __builtin_amdgcn_uicmp(pv[j], c, kUge);
+                const int nj = __popcll(cm);
+                if (nj == 0) continue;   // uniform
+                const uint32_t below =
+                    __builtin_amdgcn_mbcnt_hi((uint32_t)(cm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)cm, 0u));
+                const int to = pv[j] >= c ? base + (int)below : 63;
+                const uint32_t gp = (uint32_t)__builtin_amdgcn_ds_permute(4 * to, (int)pv[j]);
+                const uint32_t gx = (uint32_t)__builtin_amdgcn_ds_permute(4 * to, lane + 64 * j);
+                const bool mine = lane >= base && lane < base + nj;
+                cp = mine ? gp : cp;
+                cx = mine ? gx : cx;
+                base += nj;
+            }
+            // rank = candidates whose key (p bits over the inverted index) is above this lane's
+            const unsigned long long kq = ((unsigned long long)cp << 32) | (unsigned int)~cx;
+            int rank = 0;
+            for (int r = 0; r < M; ++r) {
+                const uint32_t hr = __builtin_amdgcn_readlane((int)cp, r), xr = __builtin_amdgcn_readlane((int)cx, r);
+                rank += (((unsigned long long)hr << 32) | (unsigned int)~xr) > kq ? 1 : 0;
+            }
+            const int to = lane < M && rank < k ? rank : 63;
+            const uint32_t wp = (uint32_t)__builtin_amdgcn_ds_permute(4 * to, (int)cp);
+            const uint32_t wx = (uint32_t)__builtin_amdgcn_ds_permute(4 * to, (int)cx);
+            if (lane < k) {
+                my_w = __uint_as_float(wp - 1u);
+                my_id = (int)wx;
+            }
+            nsel = k;
+        }
+    }
+    for (int i = nsel > 0 ? k : 0; i < k; ++i) {
+        uint32_t m = pv[0];
+#pragma unroll
+        for (int j = 1; j < PER; ++j) m = m > pv[j] ? m : pv[j];
+        const uint32_t best = wave_max_u32(m);
+        if (best == 0u) break;   // no candidate left (NaN p): ranks i.. keep the buffer's contents
+        // the lowest index holding it: the first slot with a lane at best, its lowest lane
+        unsigned long long e = 0ull;
+        int wj = 0;
+#pragma unroll
+        for (int j = PER - 1; j >= 0; --j) {
+            const unsigned long long ej = __builtin_amdgcn_uicmp(pv[j], best, kEq);
+            wj = ej ? j : wj;
+            e = ej ? ej : e;
+        }
+        const int wl = __builtin_ctzll(e);
+#pragma unroll
+        for (int j = 0; j < PER; ++j) pv[j] = j == wj && lane == wl ? 0u : pv[j];
         if (lane == i) {
-            my_w = __uint_as_float((unsigned int)(best >> 32));
-            my_id = (int)~(unsigned int)best;
+            my_w = __uint_as_float(best - 1u);
+            my_id = wl + 64 * wj;
         }
         nsel = i + 1;
     }
@@ -110,87 +184,6 @@ __device__ void route_topk_wave(const float* __restrict__ l, int n_expert, int k
     float lv[PER];
     load_logits_wave<PER>(l, n_expert, lv);
     route_topk_wave_lv<PER>(lv, n_expert, k, id_row, w_row);
-}
-
-// Softmax top-k of one token on a work-group of 256 threads (n_expert <= 256, expert tid on thread tid), bit for bit
-// route_topk_wave: the same max, exp, bracketed (else serial ascending) sum and p, the same renormalisation; the k
-// largest keys are found by counting, for every key, the keys above it - the four waves compare in parallel instead
-// of k dependent argmax passes on one wave.  lv: this thread's logit (ignored for tid >= n_expert).  Scratch in LDS:
-// s_key [256] u64, s_rank [256] int, s_red [16] double, s_sel [128] int.  Every thread calls it.  Ranks a NaN row
-// leaves unfilled are not written (id_row keeps what the caller put there).
-__device__ void route_topk_block(float lv, int n_expert, int k, unsigned long long* s_key, int* s_rank, double* s_red,
-                                 int* s_sel, int32_t* id_row, float* w_row) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const bool in = tid < n_expert;
-    const float m = wave_max(in ? lv : -INFINITY);
-    if (lane == 0) s_red[wave] = (double)m;
-    if (tid < k) s_sel[tid] = -1;
-    __syncthreads();
-    const float mx = fmaxf(fmaxf((float)s_red[0], (float)s_red[1]), fmaxf((float)s_red[2], (float)s_red[3]));
-    const double exv = in ? exp((double)lv - (double)mx) : 0.0;
-    const double ps = wave_sum_d(exv);
-    if (lane == 0) s_red[4 + wave] = ps;
-    __syncthreads();
-    const double part = (s_red[4] + s_red[5]) + (s_red[6] + s_red[7]);
-    const double lo = part * (1.0 - 0x1p-40), hi = part * (1.0 + 0x1p-40);
-    const float f_lo = (float)(1.0 / hi), f_hi = (float)(1.0 / lo);
-    float inv;
-    if (part >= 1.0 && hi < 1e300 && f_lo == f_hi) {
-        inv = f_lo;
-    } else {   // uniform over the work-group: the serial ascending sum
-        double* s_ex = (double*)s_key;
-        s_ex[tid] = exv;
-        __syncthreads();
-        if (tid == 0) {
-            double sum = 0.0;
-            for (int i = 0; i < n_expert; ++i) sum += s_ex[i];
-            s_red[8] = sum;
-        }
-        __syncthreads();
-        inv = (float)(1.0 / s_red[8]);
-        __syncthreads();
-    }
-    const float p = in ? (float)(exv * (double)inv) : 0.0f;
-    const unsigned long long key = in && p == p ? ((unsigned long long)__float_as_uint(p) << 32) | (unsigned int)~tid : 0ull;
-    s_key[tid] = key;   // 0 past n_expert: never above a key
-    __syncthreads();
-    int above = 0;
-    if (n_expert <= 128) {   // two threads a key, half the keys each
-        const int i = tid & 127, h = tid >> 7;
-        const unsigned long long mine = s_key[i];
-#pragma unroll 8
-        for (int j = 64 * h; j < 64 * h + 64; j += 2) {
-            const ulonglong2 kk = *(const ulonglong2*)(s_key + j);
-            above += (kk.x > mine ? 1 : 0) + (kk.y > mine ? 1 : 0);
-        }
-        s_rank[tid] = above;
-        __syncthreads();
-        if (tid < 128) above += s_rank[tid + 128];
-    } else {
-#pragma unroll 8
-        for (int j = 0; j < 256; j += 2) {
-            const ulonglong2 kk = *(const ulonglong2*)(s_key + j);
-            above += (kk.x > key ? 1 : 0) + (kk.y > key ? 1 : 0);
-        }
-    }
-    if (in && key != 0ull && above < k) {
-        s_sel[above] = tid;
-        s_sel[64 + above] = __float_as_int(p);
-    }
-    __syncthreads();
-    if (tid < k) {
-        double sum = 0.0;
-        bool full = true;
-        for (int q = 0; q < k; ++q) {
-            full = full && s_sel[q] >= 0;
-            sum += (double)__int_as_float(s_sel[64 + q]);
-        }
-        if (full) {
-            const double sc = fmax(sum, 6.103515625e-05);
-            id_row[tid] = s_sel[tid];
-            w_row[tid] = (float)((double)__int_as_float(s_sel[64 + tid]) / sc);
-        }
-    }
 }
 
 // exclusive scan of v over the work-group (blockDim.x threads, a multiple of 64, at most 1024); *total gets the sum
