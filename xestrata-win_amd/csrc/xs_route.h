@@ -69,13 +69,14 @@ __device__ void route_topk_wave_lv(const float (&lv)[PER], int n_expert, int k, 
         const float p = x < n_expert ? (float)(ex[j] * (double)inv) : __int_as_float(0x7FC00000);
         pv[j] = p == p ? __float_as_uint(p) + 1u : 0u;
     }
-    constexpr int kEq = 32, kNe = 33, kUge = 35;   // llvm.amdgcn.icmp predicates: the compare's lane mask, straight
+    constexpr int kEq = 32, kNe = 33, kUle = 37;   // llvm.amdgcn.icmp predicates: the compare's lane mask, straight
     float my_w = 0.0f;
     int my_id = 0, nsel = 0;
-    // Fast path, the same keys in the same order without k dependent passes: below the largest key, thresholds half a
-    // binade apart; at the highest one with at least k candidates at or above it, the M (<= 32) candidates there
-    // are moved to lanes 0..M-1 (ds_permute), each one's rank is the count of candidate keys above its own, and the k
-    // best move to the lanes of their ranks.  Otherwise (NaN p, k > 32, candidates too dense) the passes below.
+    // Fast path, the same keys in the same order without k dependent passes: each candidate's bucket is its distance
+    // below the largest key in half binades (2^22 in the bits, 15 for all further down); the k-th smallest bucket v
+    // (a 4-step bisection on ballot counts) bounds the k best, the M (<= 32) candidates in buckets <= v move to
+    // lanes 0..M-1 (ds_permute), each one's rank is the count of candidate keys above its own, and the k best move to
+    // the lanes of their ranks.  Otherwise (NaN p, k > 32, candidates too dense) the passes below.
     int nvalid = 0;
     uint32_t pm = 0u;
 #pragma unroll
@@ -85,31 +86,33 @@ __device__ void route_topk_wave_lv(const float (&lv)[PER], int n_expert, int k, 
     }
     if (nvalid > k && k <= 32) {
         pm = wave_max_u32(pm);
-        uint32_t c = 0u;
-        int M = 0;
+        uint32_t d[PER];
 #pragma unroll
-        for (int st = 1; st <= 16; ++st) {
-            const uint32_t cs = pm > ((uint32_t)st << 22) ? pm - ((uint32_t)st << 22) : 1u;
+        for (int j = 0; j < PER; ++j) d[j] = pv[j] == 0u ? 16u : min((pm - pv[j]) >> 22, 15u);
+        uint32_t v = 0u;   // the smallest bucket with >= k candidates at or below it (all valid ones are at <= 15)
+#pragma unroll
+        for (int b = 3; b >= 0; --b) {
+            const uint32_t c = v + (1u << b) - 1u;
             int n = 0;
 #pragma unroll
-            for (int j = 0; j < PER; ++j) n += __popcll(__builtin_amdgcn_uicmp(pv[j], cs, kUge));
-            if (c == 0u && n >= k) {
-                c = cs;
-                M = n;
-            }
+            for (int j = 0; j < PER; ++j) n += __popcll(__builtin_amdgcn_uicmp(d[j], c, kUle));
+            v = n < k ? v + (1u << b) : v;
         }
-        if (c != 0u && M <= 32) {
+        int M = 0;
+#pragma unroll
+        for (int j = 0; j < PER; ++j) M += __popcll(__builtin_amdgcn_uicmp(d[j], v, kUle));
+        if (M <= 32) {
             // candidate q of the ascending index order to lane q; lanes that are no candidate write lane 63
             uint32_t cp = 0u, cx = 0u;
             int base = 0;
 #pragma unroll
             for (int j = 0; j < PER; ++j) {
-                const unsigned long long cm = __builtin_amdgcn_uicmp(pv[j], c, kUge);
+                const unsigned long long cm = __builtin_amdgcn_uicmp(d[j], v, kUle);
                 const int nj = __popcll(cm);
                 if (nj == 0) continue;   // uniform
                 const uint32_t below =
                     __builtin_amdgcn_mbcnt_hi((uint32_t)(cm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)cm, 0u));
-                const int to = pv[j] >= c ? base + (int)below : 63;
+                const int to = d[j] <= v ? base + (int)below : 63;
                 const uint32_t gp = (uint32_t)__builtin_amdgcn_ds_permute(4 * to, (int)pv[j]);
                 const uint32_t gx = (uint32_t)__builtin_amdgcn_ds_permute(4 * to, lane + 64 * j);
                 const bool mine = lane >= base && lane < base + nj;
@@ -159,8 +162,20 @@ __device__ void route_topk_wave_lv(const float (&lv)[PER], int n_expert, int k, 
         nsel = i + 1;
     }
     if (nsel == k) {
+        // the sum of the k in rank order, in double.  With k <= 16 values within 2^25 of each other (all <= 1) every
+        // partial sum is exact (it is a multiple of the smallest value's ulp below 2^53 of them), so a tree over the
+        // lanes gives the serial sum bit for bit.
         double s = 0.0;
-        for (int i = 0; i < k; ++i) s += (double)readlane_f(my_w, i);
+        if (k <= 16 && readlane_f(my_w, k - 1) >= readlane_f(my_w, 0) * 0x1p-25f) {
+            double t = lane < k ? (double)my_w : 0.0;
+            t += dpp_d<kDppXor1>(t);
+            t += dpp_d<kDppXor2>(t);
+            t += dpp_d<kDppRor4>(t);
+            t += dpp_d<kDppRor8>(t);
+            s = readlane_d(t, 0);
+        } else {
+            for (int i = 0; i < k; ++i) s += (double)readlane_f(my_w, i);
+        }
         const double sc = fmax(s, 6.103515625e-05);
         if (lane < k) {
             id_row[lane] = my_id;
