@@ -135,6 +135,12 @@ __device__ __forceinline__ void vm_wait_le(int n) {
     }
 }
 
+// A work-group barrier for LDS hand-overs.  __syncthreads() is also a work-group release, which makes every wave wait
+// for all of its LDS DMA in flight (vmcnt(0)) - the next unit's rows fetched ahead on purpose included.  Where a wave
+// needs DMA data it waits for it itself (vm_drain, vm_wait_le) before the barrier; LDS reads and writes are complete at
+// lgkmcnt(0).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // n16 16-byte chunks to LDS dst[0 .. n16) by one wave's DMA: the store wave's fetch of the first down slab, issued
 // once the gate/up slab is in (so it does not compete with it), complete at the store wave's vm_drain()
 template <typename Src>
@@ -441,7 +447,7 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
         for (int u1 = wg; u1 < n_gu; u1 += gridDim.x, ++it) {
             const int g = u1 / nu, j = u1 - g * nu, next = u1 + (int)gridDim.x;
             uint8_t* slab = slab2[it & 1];
-            __syncthreads();   // the previous unit's readers of the other slab and of s_gu are done
+            lds_barrier();   // the previous unit's readers of the other slab and of s_gu are done
             if (loader) {
                 if (next < n_gu) {
                     dma_unit(next, slab2[(it + 1) & 1]);
@@ -450,11 +456,11 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
                     vm_drain();
                 }
             }
-            __syncthreads();   // this unit's slab is in
+            lds_barrier();   // this unit's slab is in
             const int e0 = s_start[g], e1 = s_start[g + 1];
             for (int p = e0; p < e1; p += NE) {
                 const int m = min(NE, e1 - p);
-                if (p > e0) __syncthreads();   // the previous pass's stores have read s_gu
+                if (p > e0) lds_barrier();   // the previous pass's stores have read s_gu
                 Act at[NE];
 #pragma unroll
                 for (int e = 0; e < NE; ++e) {
@@ -476,7 +482,7 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
                             if (e < m) s_gu[e * 2 * rh + rr] = acc[e];
                     }
                 }
-                __syncthreads();
+                lds_barrier();
                 if (!loader)
                     for (int i = lane; i < m * rh; i += 64) {
                         const int e = i / rh, r = i - e * rh;
@@ -499,7 +505,7 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
         const int e0 = s_start[g], e1 = s_start[g + 1];
         for (int p = e0; p < e1; p += NE) {
             const int m = min(NE, e1 - p);
-            if (p > e0) __syncthreads();   // the previous pass's readers of the activations are done
+            if (p > e0) lds_barrier();   // the previous pass's readers of the activations are done
             if (loader) {
                 for (int e = 0; e < (x_early ? 0 : m); ++e) {    // the entries' tokens to q8_1, one scale a 256
                     const float* xr = a.x + (int64_t)s_tok[p + e] * H;
@@ -531,7 +537,7 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
                         if (e < m) s_gu[e * 2 * rh + rr] = acc[e];
                 }
             }
-            __syncthreads();
+            lds_barrier();
             if (!loader)
                 for (int i = lane; i < m * rh; i += 64) {
                     const int e = i / rh, r = i - e * rh;
@@ -545,7 +551,7 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
     for (int u2 = wg; u2 < n_dn; u2 += gridDim.x) {
         const int g = u2 / nj, j = u2 - g * nj;
         const uint8_t* srcd = a.arena + (size_t)s_gexp[g] * (size_t)a.blob + L.down_off + (size_t)j * rd * L.d_row;
-        __syncthreads();   // the previous unit's readers of the slab are done
+        lds_barrier();   // the previous unit's readers of the slab are done
         const bool fetched = dn_early && u2 == wg;
         if (loader && !fetched) dma_to_lds(slab_dn, n16d, [&](int i) { return (const void*)(srcd + 16 * (size_t)i); });
         const int e0 = s_start[g], e1 = s_start[g + 1];
