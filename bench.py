@@ -151,14 +151,18 @@ def main():
     log(f"arena {copies * layer_bytes / 1e9:.2f} GB, blob {blob} B")
     gen = torch.Generator(device=dev).manual_seed(1)
 
+    inputs = {}
+
     def decode_run(T, steps, warmup):
-        """Time `steps` decode layer steps of T tokens (one graph = one step per copy); returns (ms/step, bytes/step)."""
+        """Time `steps` decode layer steps of T tokens (one graph = one step per copy); returns (ms/step, bytes/step,
+        steps timed).  The inputs stay in `inputs[T]` (logits [copies, T, E], x [T, H])."""
         n_logit_sets = copies
         logits = torch.randn(n_logit_sets, T, E, device=dev, generator=gen)
         x = torch.randn(T, H, device=dev, generator=gen).to(torch.bfloat16).float()
         res = torch.randn(T, H, device=dev, generator=gen)
         out = torch.empty(copies, T, H, device=dev)
         layer = xm.MoeLayer(L, arena, E, k, T)
+        inputs[T] = (logits, x)
         distinct = []
         for c in range(copies):
             ids = torch.topk(logits[c], k, dim=1).indices
@@ -235,8 +239,8 @@ def main():
         cores = min(16, os.cpu_count() or 1)
         blobs = list(arena[:E].cpu().numpy())
         ol = xo.layout(xm.Q4_K, xm.Q6_K, H, F)
-        lg = logits[0].cpu().numpy()
-        xx = x.cpu().numpy()
+        lg = inputs[1][0][0].cpu().numpy()        # the first copy's token, as timed on the GPU
+        xx = inputs[1][1].cpu().numpy()
         rr = np.zeros((1, H), np.float32)
         xo.moe_layer_decode(ol, blobs, k, xx, lg, rr, n_threads=cores)     # warm-up
         n = 0
