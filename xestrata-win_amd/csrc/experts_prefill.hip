@@ -384,8 +384,8 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
                 acc[i][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i], fb1, acc[i][1], 0, 0, 0);
             }
         };
-        dma_a(0, 0);
         if (T == kQ4_K) {
+            dma_a(0, 0);
             const int nb = K / 256;
             uint4 hdr[2], q[2][2];   // header of the block; the qs run of steps (even, odd)
 #pragma unroll
@@ -416,36 +416,61 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
                 }
             }
         } else if (T == kQ6_K) {
-            const int nb = K / 256;
-            Q6Raw r[2][2];   // the raw words of halves (even, odd), per row
+            // K is short here (n_ff: 12 steps at 768), so the loads of a step must be in flight two steps ahead.  The
+            // A tile goes through registers (loaded at step ks - 2, written to LDS at step ks - 1) rather than by LDS
+            // DMA: the wait for a register load is the compiler's own and exact, while a wait for "all but the newest
+            // n" on vmcnt cannot single out LDS DMA among ordinary loads.  The raw words of a half are loaded at the
+            // first step of the half before.  With 3 blocks a row (n_ff 768) everything is straight-line code.
+            uint4 areg[2][RT];   // A(ks) staging, slot ks & 1
+            auto load_a = [&](int ks, int slot) {
 #pragma unroll
-            for (int j = 0; j < 2; ++j) q6k_load(brow[j], 0, hf, r[0][j]);
-            for (int b = 0; b < nb; ++b) {
+                for (int i = 0; i < RT; ++i) areg[slot][i] = ldg16(asrc[i] + (size_t)ks * 128);
+            };
+            auto store_a = [&](int slot, int buf) {
+                uint8_t* dst = lds + buf * (kBM * 128) + wave * 8 * RT * 128 + 16 * lane;
 #pragma unroll
-                for (int n = 0; n < 2; ++n) {
+                for (int i = 0; i < RT; ++i) *(uint4*)(dst + i * 1024) = areg[slot][i];
+            };
+            auto q6loop = [&](auto nbc) {
+                constexpr int NBC = decltype(nbc)::value;
+                const int nb = NBC > 0 ? NBC : K / 256;
+                Q6Raw r[2][2];   // the raw words of halves (even, odd), per row
+                load_a(0, 0);
 #pragma unroll
-                    for (int t = 0; t < 2; ++t) {
-                        const int ks = 4 * b + 2 * n + t;
-                        step_sync();
-                        if (ks + 1 < nk) {
-                            dma_a(ks + 1, (ks + 1) & 1);
-                            if (t == 1) {   // the next half's words
-                                const int bn = n == 0 ? b : b + 1;
+                for (int j = 0; j < 2; ++j) q6k_load(brow[j], 0, hf, r[0][j]);
+                load_a(1, 1);
+                store_a(0, 0);
 #pragma unroll
-                                for (int j = 0; j < 2; ++j) q6k_load(brow[j] + 210 * bn, n ^ 1, hf, r[n ^ 1][j]);
+                for (int b = 0; b < nb; ++b) {
+#pragma unroll
+                    for (int n = 0; n < 2; ++n) {
+#pragma unroll
+                        for (int t = 0; t < 2; ++t) {
+                            const int ks = 4 * b + 2 * n + t;
+                            __syncthreads();   // A(ks) is in buffer ks & 1; step ks - 1 is done with the other
+                            if (ks + 1 < nk) store_a((ks + 1) & 1, (ks + 1) & 1);
+                            if (ks + 2 < nk) load_a(ks + 2, ks & 1);
+                            if (t == 0 && 2 * b + n + 1 < 2 * nb) {   // the next half's words
+                                const int h1 = 2 * b + n + 1;
+#pragma unroll
+                                for (int j = 0; j < 2; ++j)
+                                    q6k_load(brow[j] + 210 * (h1 >> 1), h1 & 1, hf, r[n ^ 1][j]);
                             }
-                        }
 #pragma unroll
-                        for (int kk = 0; kk < 4; ++kk) {
-                            const Q6Raw& ra = r[n][0];
-                            const Q6Raw& rb = r[n][1];
-                            mfma_step(ks, kk, q6k_frag(ra, t, kk, q6k_scale(ra, t, kk, hf), qc),
-                                      q6k_frag(rb, t, kk, q6k_scale(rb, t, kk, hf), qc));
+                            for (int kk = 0; kk < 4; ++kk) {
+                                const Q6Raw& ra = r[n][0];
+                                const Q6Raw& rb = r[n][1];
+                                mfma_step(ks, kk, q6k_frag(ra, t, kk, q6k_scale(ra, t, kk, hf), qc),
+                                          q6k_frag(rb, t, kk, q6k_scale(rb, t, kk, hf), qc));
+                            }
                         }
                     }
                 }
-            }
+            };
+            if (K == 768) q6loop(IntC<3>{});
+            else q6loop(IntC<0>{});
         } else {
+            dma_a(0, 0);
             for (int ks = 0; ks < nk; ++ks) {
                 step_sync();
                 if (ks + 1 < nk) dma_a(ks + 1, (ks + 1) & 1);
