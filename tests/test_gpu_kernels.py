@@ -83,6 +83,42 @@ def test_router_shapes(xm, xo, T, E, k):
     assert np.array_equal(t2n(w).view(np.uint32), rw.view(np.uint32))
 
 
+def _edge_logits(kind, T, E, rng):
+    if kind == "equal":           # every p equal: the tie order alone decides (too many candidates for the fast path)
+        return np.zeros((T, E), np.float32)
+    if kind == "near_equal":      # p within a few ulps: one crowded bucket
+        return (rng.standard_normal((T, E)) * 1e-6).astype(np.float32)
+    if kind == "few_large":       # k clear winners, the rest far below (a candidate set of exactly k)
+        lg = rng.standard_normal((T, E)).astype(np.float32) - 40.0
+        for t in range(T):
+            lg[t, rng.choice(E, 8, replace=False)] += 60.0
+        return lg
+    if kind == "underflow":       # exp underflows to 0 for most experts: zero p ranked by index
+        return np.tile(np.linspace(0.0, -3000.0, E, dtype=np.float32)[rng.permutation(E)], (T, 1))
+    if kind == "neg_inf":         # -inf logits: p = 0 exactly
+        lg = rng.standard_normal((T, E)).astype(np.float32)
+        lg[:, ::3] = -np.inf
+        return lg
+    if kind == "two_levels":      # two tied levels straddling rank k
+        lg = np.full((T, E), -1.0, np.float32)
+        lg[:, : E // 16 + 3] = 1.0
+        return lg
+    raise ValueError(kind)
+
+
+@pytest.mark.parametrize("kind", ["equal", "near_equal", "few_large", "underflow", "neg_inf", "two_levels"])
+@pytest.mark.parametrize("E,k", [(128, 8), (256, 8), (512, 10), (64, 6), (1024, 40)])
+def test_router_selection_edges(xm, xo, kind, E, k):
+    """Distributions that take each branch of the device selection (the bucket fast path, its fallback to k argmax
+    passes, ties at the k-th key, zero p, k above 32): ids and weights bit for bit against the oracle."""
+    rng = np.random.default_rng(E * 31 + k)
+    lg = _edge_logits(kind, 12, E, rng)
+    ids, w = xm.router_top10(torch.from_numpy(lg).to(DEV), k)
+    rids, rw = xo.router_top10(lg, k)
+    assert np.array_equal(t2n(ids), rids)
+    assert np.array_equal(t2n(w).view(np.uint32), rw.view(np.uint32))
+
+
 def test_router_zipf_prefill(xm, xo):
     """Config 3's skewed logits: log-Zipf(1.2) popularity plus per-token Gumbel noise."""
     rng = np.random.default_rng(3)
