@@ -182,6 +182,28 @@ size_t xs_moe_layer_decode_workspace_bytes(const xs_expert_layout_t* L, int n_ex
  * counterpart in the reference (its layer reports through host-side checks of each launch). */
 int32_t* xs_moe_layer_decode_status(void* workspace);
 
+/* A shared expert over a decode / verify window: every token through one dense expert in the native format (blob:
+ * [gate rows | up rows | down rows] of layout SL, 16-byte aligned), shared[t] = down(SwiGLU(gate x_t, up x_t)) on q8_1
+ * activations, canonical rows as the routed experts; with w_gate ([n_embd] fp32), gate_logit[t] = w_gate . x_t (the
+ * scalar gate the combine turns into 1 / (1 + exp(-g))).  Replaces the engine's shared-expert decode
+ * (src/core/plain_model.cpp:959-973: native_mmvq's Q8_0/Q4_K pair, native_swiglu_q8_1 and the F32 gate GEMV,
+ * include/strata/kernels/native_mmvq.hpp:45-52, 128-133).  n_tok <= 1024. */
+int xs_shared_expert_decode(const xs_expert_layout_t* SL, const uint8_t* blob, const float* x, int n_tok,
+                            const float* w_gate, float* shared, float* gate_logit, void* workspace,
+                            size_t workspace_bytes, void* stream);
+size_t xs_shared_expert_decode_workspace_bytes(const xs_expert_layout_t* SL, int n_tok);
+/* xs_moe_layer_decode with a shared expert: the shared expert (xs_shared_expert_decode) first, then the routed layer,
+ * whose combine adds the shared row once after the routed ones, times its gate's sigmoid when w_gate is given
+ * (native_moe_combine_multi's shared / shared_gate, native_moe.cpp:36-58; plain_model.cpp:951-988).  The workspace
+ * (xs_moe_layer_decode_shared_workspace_bytes, zeroed once) starts with the layer's own: its status word is
+ * xs_moe_layer_decode_status(workspace). */
+int xs_moe_layer_decode_shared(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_bytes, int n_expert,
+                               int k, const float* x, const float* logits, const float* residual, float* out,
+                               int n_tok, const xs_expert_layout_t* SL, const uint8_t* shared_blob,
+                               const float* w_gate, void* workspace, size_t workspace_bytes, void* stream);
+size_t xs_moe_layer_decode_shared_workspace_bytes(const xs_expert_layout_t* L, int n_expert, int k, int n_tok,
+                                                  const xs_expert_layout_t* SL);
+
 /* The whole prompt / verify MoE layer on the device (same arena): router -> permutation -> f16 MFMA grouped
  * experts -> combine -> residual.  The engine's prompt MoE section (src/prefill/plain_prompt.cpp:558-797). */
 int xs_moe_layer_prefill(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_bytes, int n_expert,

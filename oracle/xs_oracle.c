@@ -759,6 +759,49 @@ void xso_combine(const float* parts, const float* weights, const float* shared, 
     }
 }
 
+/* A shared expert over n_tok tokens: one group holding every token (the engine's shared-expert decode,
+ * src/core/plain_model.cpp:959-973, on the same canonical rows as the routed experts). */
+void xso_shared_expert(const xso_layout* SL, const uint8_t* blob, const float* x, int n_tok, float* shared,
+                       int n_threads) {
+    const int64_t H = SL->n_embd;
+    uint8_t* xq = (uint8_t*)malloc((size_t)(H / 32 * 36) * (size_t)n_tok);
+    int32_t* idx = (int32_t*)malloc(sizeof(int32_t) * (size_t)n_tok);
+    int32_t start[2] = {0, n_tok};
+    const uint8_t* blobs[1] = {blob};
+    for (int t = 0; t < n_tok; ++t) idx[t] = t;
+    xso_quantize_q8_1_rows(x, n_tok, H, xq);
+    xso_native_expert_grouped(SL, blobs, start, 1, idx, idx, xq, shared, NULL, NULL, NULL, n_threads);
+    free(xq); free(idx);
+}
+
+/* The decode layer with a shared expert: the routed layer's combine then + the shared row once (times
+ * 1 / (1 + exp(-gate_logit[t])) when given), then the residual (plain_model.cpp:951-988). */
+void xso_moe_layer_decode_shared(const xso_layout* L, const uint8_t* const* blobs_by_expert, int n_expert, int k,
+                                 const float* x, const float* logits, const float* residual, int n_tok,
+                                 const xso_layout* SL, const uint8_t* shared_blob, const float* gate_logit, float* out,
+                                 int n_threads) {
+    const int64_t H = L->n_embd, n = (int64_t)n_tok * k;
+    int32_t* ids = (int32_t*)malloc(sizeof(int32_t) * (size_t)n);
+    float* w = (float*)malloc(sizeof(float) * (size_t)n);
+    int32_t counts[4], *start = (int32_t*)malloc(sizeof(int32_t) * (size_t)(n + 1));
+    int32_t* dst = (int32_t*)malloc(sizeof(int32_t) * (size_t)n);
+    int32_t* tok = (int32_t*)malloc(sizeof(int32_t) * (size_t)n);
+    int32_t* gexp = (int32_t*)malloc(sizeof(int32_t) * (size_t)n);
+    uint8_t* xq = (uint8_t*)malloc((size_t)(H / 32 * 36) * (size_t)n_tok);
+    float* parts = (float*)malloc(sizeof(float) * (size_t)(n * H));
+    float* shared = (float*)malloc(sizeof(float) * (size_t)((int64_t)n_tok * H));
+    const uint8_t** gblob = (const uint8_t**)malloc(sizeof(void*) * (size_t)n);
+    xso_router_top10(logits, n_tok, n_expert, k, ids, w);
+    const int groups = xso_decode_plan(ids, (int)n, k, counts, start, dst, tok, gexp);
+    for (int g = 0; g < groups; ++g) gblob[g] = blobs_by_expert[gexp[g]];
+    xso_quantize_q8_1_rows(x, n_tok, H, xq);
+    xso_native_expert_grouped(L, gblob, start, groups, dst, tok, xq, parts, NULL, NULL, NULL, n_threads);
+    xso_shared_expert(SL, shared_blob, x, n_tok, shared, n_threads);
+    xso_combine(parts, w, shared, gate_logit, out, H, k, n_tok);
+    for (int64_t i = 0; i < (int64_t)n_tok * H; ++i) out[i] = residual[i] + out[i];
+    free(ids); free(w); free(start); free(dst); free(tok); free(gexp); free(xq); free(parts); free(shared); free(gblob);
+}
+
 /* ------------------------------------------------------------------------------------------------ float reference */
 
 /* src/kernels/native_expert_parity.cpp:104-130 */

@@ -96,6 +96,12 @@ void xso_expert_float(const xso_layout* L, const uint8_t* const* blobs, const fl
 void xso_moe_layer_decode(const xso_layout* L, const uint8_t* const* blobs_by_expert, int n_expert, int k,
                           const float* x, const float* logits, const float* residual, int n_tok, float* out,
                           int n_threads);
+void xso_shared_expert(const xso_layout* SL, const uint8_t* blob, const float* x, int n_tok, float* shared,
+                       int n_threads);
+void xso_moe_layer_decode_shared(const xso_layout* L, const uint8_t* const* blobs_by_expert, int n_expert, int k,
+                                 const float* x, const float* logits, const float* residual, int n_tok,
+                                 const xso_layout* SL, const uint8_t* shared_blob, const float* gate_logit, float* out,
+                                 int n_threads);
 
 #ifdef __cplusplus
 }

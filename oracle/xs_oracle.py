@@ -65,6 +65,9 @@ def lib():
         L.xso_combine.argtypes = [P, P, P, P, P, I64, I, I]
         L.xso_expert_float.argtypes = [ctypes.POINTER(Layout), P, P, P, I, P, I]
         L.xso_moe_layer_decode.argtypes = [ctypes.POINTER(Layout), P, I, I, P, P, P, I, P, I]
+        L.xso_shared_expert.argtypes = [ctypes.POINTER(Layout), P, P, I, P, I]
+        L.xso_moe_layer_decode_shared.argtypes = [ctypes.POINTER(Layout), P, I, I, P, P, P, I, ctypes.POINTER(Layout),
+                                                  P, P, P, I]
         L.xso_canon_silu_mul_n.argtypes = [P, P, I64, P]
         L.xso_canon_exp_n.argtypes = [P, I64, P]
         L.xso_canon_rcp_n.argtypes = [P, I64, P]
@@ -259,6 +262,31 @@ def moe_layer_decode(L, blobs_by_expert, k, x, logits, residual, n_threads=1):
     out = np.zeros_like(residual)
     lib().xso_moe_layer_decode(ctypes.byref(L), ctypes.cast(arr, P), len(keep), k, _a(x), _a(logits), _a(residual),
                                x.shape[0], _a(out), n_threads)
+    return out
+
+
+def shared_expert(SL, blob, x, n_threads=8):
+    """One shared expert over the tokens of x [T, n_embd] -> rows [T, n_embd]."""
+    x = np.ascontiguousarray(x, np.float32)
+    blob = np.ascontiguousarray(blob, np.uint8)
+    out = np.zeros((x.shape[0], SL.n_embd), np.float32)
+    lib().xso_shared_expert(ctypes.byref(SL), _a(blob), _a(x), x.shape[0], _a(out), n_threads)
+    return out
+
+
+def moe_layer_decode_shared(L, blobs_by_expert, k, x, logits, residual, SL, shared_blob, gate_logit=None,
+                            n_threads=8):
+    keep = [np.ascontiguousarray(b, np.uint8) for b in blobs_by_expert]
+    arr = (ctypes.c_void_p * len(keep))(*[b.ctypes.data for b in keep])
+    x = np.ascontiguousarray(x, np.float32)
+    logits = np.ascontiguousarray(logits, np.float32)
+    residual = np.ascontiguousarray(residual, np.float32)
+    sb = np.ascontiguousarray(shared_blob, np.uint8)
+    g = None if gate_logit is None else np.ascontiguousarray(gate_logit, np.float32)
+    out = np.zeros_like(residual)
+    lib().xso_moe_layer_decode_shared(ctypes.byref(L), ctypes.cast(arr, P), len(keep), k, _a(x), _a(logits),
+                                      _a(residual), x.shape[0], ctypes.byref(SL), _a(sb),
+                                      None if g is None else _a(g), _a(out), n_threads)
     return out
 
 

@@ -223,3 +223,58 @@ def test_decode_graph_replays(xm, c2_arena):
         torch.cuda.synchronize()
         assert torch.equal(out.view(torch.int32), eager.view(torch.int32)), r
     assert layer.status() == 0
+
+
+@pytest.fixture(scope="module")
+def c2_shared(xm):
+    """A Q8_0 shared expert beside config 2's routed ones (hidden 2048, F 512), and a gate vector."""
+    sh_arena, SL = xm.build_arena(1, 2048, 512, 8, 8, seed=22)
+    g = torch.Generator(device=DEV).manual_seed(23)
+    w_gate = torch.randn(2048, device=DEV, generator=g) * 0.02
+    return sh_arena, SL, w_gate
+
+
+def test_shared_expert_decode(xm, xo, c2_shared):
+    """xs_shared_expert_decode: every token through the one expert, rows bit for bit the oracle's (the same canonical
+    rows as the routed experts); the gate logit within 1e-5 of a float64 dot (the router-logit GEMV's bound)."""
+    sh_arena, SL, w_gate = c2_shared
+    T = 5
+    g = torch.Generator(device=DEV).manual_seed(24)
+    x = torch.randn(T, 2048, device=DEV, generator=g).to(torch.bfloat16).float()
+    shared, gate = xm.shared_expert_decode(SL, sh_arena[0], x, w_gate)
+    torch.cuda.synchronize()
+    want = xo.shared_expert(xo.layout(8, 8, 2048, 512), t2n(sh_arena[0]), t2n(x))
+    assert np.array_equal(t2n(shared).view(np.uint32), want.view(np.uint32))
+    ref = t2n(x).astype(np.float64) @ t2n(w_gate).astype(np.float64)
+    assert np.max(np.abs(t2n(gate) - ref)) <= 1e-5 * np.max(np.abs(t2n(x)) @ np.abs(t2n(w_gate)))
+
+
+@pytest.mark.parametrize("T", [1, 4, 16, 80])
+@pytest.mark.parametrize("gated", [False, True])
+def test_decode_shared_expert_layer(xm, xo, c2_arena, c2_shared, T, gated):
+    """xs_moe_layer_decode_shared at config 2 + a Q8_0 shared expert (one persistent launch up to 16 tokens, the
+    chained launches at 80): the routed combine, then the shared row once (times the sigmoid of its gate), then the
+    residual.  Ungated: bit for bit the oracle.  Gated: the gate's sigmoid uses each side's own expf, so within an ulp
+    or two (the gate logits given to the oracle are the device's, from xs_shared_expert_decode)."""
+    arena, L = c2_arena
+    sh_arena, SL, w_gate = c2_shared
+    E, k = 128, 8
+    g = torch.Generator(device=DEV).manual_seed(300 + T)
+    logits = torch.randn(T, E, device=DEV, generator=g)
+    x = torch.randn(T, 2048, device=DEV, generator=g).to(torch.bfloat16).float()
+    res = torch.randn(T, 2048, device=DEV, generator=g)
+    wg = w_gate if gated else None
+    layer = xm.MoeLayer(L, arena, E, k, T, shared=(SL, sh_arena[0], wg))
+    out = torch.empty_like(res)
+    layer(x, logits, res, out)
+    gate = xm.shared_expert_decode(SL, sh_arena[0], x, wg)[1] if gated else None
+    torch.cuda.synchronize()
+    assert layer.status() == 0
+    want = xo.moe_layer_decode_shared(xo.layout(12, 14, 2048, 768), [t2n(arena[e]) for e in range(E)], k, t2n(x),
+                                      t2n(logits), t2n(res), xo.layout(8, 8, 2048, 512), t2n(sh_arena[0]),
+                                      None if gate is None else t2n(gate))
+    got = t2n(out)
+    if gated:
+        assert np.max(np.abs(got - want)) <= 1e-6 * np.max(np.abs(want)), xo.rel_max(got, want)
+    else:
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), xo.rel_max(got, want)

@@ -417,6 +417,61 @@ int xs_add_inplace(float* x, const float* y, int64_t n, void* stream) {
     return finish(stream, xs::launch_add_inplace(x, y, n, S(stream)), "add_inplace");
 }
 
+// ---------------------------------------------------------------- a shared expert (decode)
+
+namespace {
+struct SharedWs {
+    void* xq;
+    unsigned long long* grp_ptr;
+    int32_t *start, *n_groups, *idx;
+    void* scratch;
+    size_t bytes;
+};
+SharedWs shared_ws(const xs_expert_layout_t* SL, int n_tok, uint8_t* base) {
+    SharedWs d;
+    size_t off = 0;
+    auto take = [&](size_t b) { uint8_t* p = base ? base + off : nullptr; off += up256(b); return p; };
+    d.xq = take((size_t)n_tok * (size_t)(SL->n_embd / 32) * 36);
+    d.grp_ptr = (unsigned long long*)take(8);
+    d.start = (int32_t*)take(8);
+    d.n_groups = (int32_t*)take(4);
+    d.idx = (int32_t*)take((size_t)n_tok * 4);
+    d.scratch = take(xs_native_expert_scratch_bytes(n_tok, SL->n_ff));
+    d.bytes = off;
+    return d;
+}
+}  // namespace
+
+size_t xs_shared_expert_decode_workspace_bytes(const xs_expert_layout_t* SL, int n_tok) {
+    if (!SL || n_tok <= 0) return 0;
+    return shared_ws(SL, n_tok, nullptr).bytes;
+}
+
+int xs_shared_expert_decode(const xs_expert_layout_t* SL, const uint8_t* blob, const float* x, int n_tok,
+                            const float* w_gate, float* shared, float* gate_logit, void* workspace,
+                            size_t workspace_bytes, void* stream) {
+    if (n_tok <= 0) return ok();
+    if (int r = check_layout(SL, "shared_expert_decode")) return r;
+    if (n_tok > 1024) return fail(XS_EINVAL, "shared_expert_decode: %d tokens is past 1024", n_tok);
+    if (!aligned(blob, 16) || !aligned(x, 4) || !aligned(shared, 4))
+        return fail(XS_EINVAL, "shared_expert_decode: the blob (16-byte aligned), x or shared is missing or misaligned");
+    if ((w_gate == nullptr) != (gate_logit == nullptr))
+        return fail(XS_EINVAL, "shared_expert_decode: w_gate and gate_logit go together");
+    if (!aligned(workspace, 256) || workspace_bytes < xs_shared_expert_decode_workspace_bytes(SL, n_tok))
+        return fail(XS_EINVAL, "shared_expert_decode: workspace missing, misaligned or short");
+    const SharedWs w = shared_ws(SL, n_tok, (uint8_t*)workspace);
+    if (int r = xs_quantize_q8_1_rows(x, n_tok, SL->n_embd, w.xq, stream)) return r;
+    if (int r = finish(stream, xs::launch_single_group_plan(w.grp_ptr, w.start, w.n_groups, w.idx, n_tok, blob,
+                                                            S(stream)),
+                       "shared_expert_decode"))
+        return r;
+    if (int r = grouped_impl(SL, w.grp_ptr, w.start, w.n_groups, w.idx, w.idx, 1, n_tok, w.xq, w.scratch, shared,
+                             stream, 0, n_tok))
+        return r;
+    if (w_gate) return xs_router_logits_f32(x, w_gate, gate_logit, n_tok, SL->n_embd, 1, stream);
+    return ok();
+}
+
 // ---------------------------------------------------------------- whole layers
 
 namespace {
@@ -501,9 +556,10 @@ size_t xs_moe_layer_decode_workspace_bytes(const xs_expert_layout_t* L, int n_ex
     return decode_ws(L, n_expert, k, n_tok, nullptr).bytes;
 }
 
-int xs_moe_layer_decode(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_bytes, int n_expert, int k,
-                        const float* x, const float* logits, const float* residual, float* out, int n_tok,
-                        void* workspace, size_t workspace_bytes, void* stream) {
+namespace {
+int layer_decode(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_bytes, int n_expert, int k,
+                 const float* x, const float* logits, const float* residual, float* out, int n_tok, void* workspace,
+                 size_t workspace_bytes, const float* shared, const float* shared_gate, void* stream) {
     if (n_tok <= 0) return ok();
     if (int r = check_layout(L, "moe_layer_decode")) return r;
     if (n_tok * k > 1024) return fail(XS_EINVAL, "moe_layer_decode: %d tokens x top-%d is past 1024 entries", n_tok, k);
@@ -546,6 +602,8 @@ int xs_moe_layer_decode(const xs_expert_layout_t* L, const uint8_t* arena, size_
         a.slab_dn_bytes = P.slab_dn;
         a.ttab = P.ttab;
         a.spin_ticks = spin_ticks();
+        a.shared = shared;
+        a.shared_gate = shared_gate;
         return finish(stream, xs::launch_decode_fused(a, P, S(stream)), "moe_layer_decode");
     }
     // routing, plan and activations in one launch (the reference's router_top10 + resident_plan + quantize_q8_1_rows)
@@ -558,7 +616,50 @@ int xs_moe_layer_decode(const xs_expert_layout_t* L, const uint8_t* arena, size_
     if (int r = grouped_impl(L, (const unsigned long long*)(w.plan + o_ptr), w.plan + o_start, w.plan, w.plan + o_dst,
                              w.plan + o_tok, cap_groups, capx, w.xq, w.scratch, w.parts, stream, 0, n_tok))
         return r;
-    return xs_moe_combine_residual(w.parts, w.w, nullptr, nullptr, residual, out, L->n_embd, k, n_tok, stream);
+    return xs_moe_combine_residual(w.parts, w.w, shared, shared_gate, residual, out, L->n_embd, k, n_tok, stream);
+}
+}  // namespace
+
+int xs_moe_layer_decode(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_bytes, int n_expert, int k,
+                        const float* x, const float* logits, const float* residual, float* out, int n_tok,
+                        void* workspace, size_t workspace_bytes, void* stream) {
+    return layer_decode(L, arena, blob_bytes, n_expert, k, x, logits, residual, out, n_tok, workspace, workspace_bytes,
+                        nullptr, nullptr, stream);
+}
+
+size_t xs_moe_layer_decode_shared_workspace_bytes(const xs_expert_layout_t* L, int n_expert, int k, int n_tok,
+                                                  const xs_expert_layout_t* SL) {
+    if (!L || !SL || k <= 0 || n_tok <= 0 || n_expert <= 0) return 0;
+    return decode_ws(L, n_expert, k, n_tok, nullptr).bytes + up256((size_t)n_tok * (size_t)L->n_embd * 4) +
+           up256((size_t)n_tok * 4) + shared_ws(SL, n_tok, nullptr).bytes;
+}
+
+int xs_moe_layer_decode_shared(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_bytes, int n_expert,
+                               int k, const float* x, const float* logits, const float* residual, float* out,
+                               int n_tok, const xs_expert_layout_t* SL, const uint8_t* shared_blob,
+                               const float* w_gate, void* workspace, size_t workspace_bytes, void* stream) {
+    if (n_tok <= 0) return ok();
+    if (int r = check_layout(L, "moe_layer_decode_shared")) return r;
+    if (int r = check_layout(SL, "moe_layer_decode_shared")) return r;
+    if (SL->n_embd != L->n_embd)
+        return fail(XS_EINVAL, "moe_layer_decode_shared: the shared expert's n_embd %lld is not the layer's %lld",
+                    (long long)SL->n_embd, (long long)L->n_embd);
+    if (!aligned(workspace, 256) ||
+        workspace_bytes < xs_moe_layer_decode_shared_workspace_bytes(L, n_expert, k, n_tok, SL))
+        return fail(XS_EINVAL, "moe_layer_decode_shared: workspace missing, misaligned or short");
+    // the layer's own workspace first (its head and tagged words at the offsets xs_moe_layer_decode uses), then the
+    // shared rows, the gate logits and the shared expert's workspace
+    const size_t lw = decode_ws(L, n_expert, k, n_tok, nullptr).bytes;
+    uint8_t* base = (uint8_t*)workspace;
+    float* shared = (float*)(base + lw);
+    float* gate = (float*)(base + lw + up256((size_t)n_tok * (size_t)L->n_embd * 4));
+    uint8_t* sws = base + lw + up256((size_t)n_tok * (size_t)L->n_embd * 4) + up256((size_t)n_tok * 4);
+    const size_t sbytes = shared_ws(SL, n_tok, nullptr).bytes;
+    if (int r = xs_shared_expert_decode(SL, shared_blob, x, n_tok, w_gate, shared, w_gate ? gate : nullptr, sws, sbytes,
+                                        stream))
+        return r;
+    return layer_decode(L, arena, blob_bytes, n_expert, k, x, logits, residual, out, n_tok, workspace, lw, shared,
+                        w_gate ? gate : nullptr, stream);
 }
 
 size_t xs_moe_layer_prefill_workspace_bytes(const xs_expert_layout_t* L, int n_expert, int k, int n_tok) {

@@ -14,7 +14,8 @@
 //   3. down units (a group, a slab of rd down rows): gather the entries' h, polling each word until it carries this
 //      call's tag, quantize it per 32 values in LDS, compute the rows into tagged `parts` words (routing order);
 //   4. combines (a token, a down slab), after the work-group's down units: poll the slab's columns of the token's k
-//      parts, add them in rank order, add the residual (native_moe_combine_multi + add_inplace).
+//      parts, add them in rank order, then a shared expert's row when given, add the residual
+//      (native_moe_combine_multi + add_inplace).
 // Waits only point backwards (down units on gate/up units, combines on down units, and a work-group finishes its
 // gate/up units before its down units and those before its combines), every work-group of the grid is resident at
 // once, and every wait is bounded: a wait past the bound sets the error word and moves on.
@@ -666,6 +667,11 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
                     }
             }
             if (!good) atomicOr(a.err, 2);
+            if (a.shared) {   // the shared expert's row, once, after the routed ones (times its gate's sigmoid)
+                float sv = a.shared[(int64_t)t * H + col];
+                if (a.shared_gate) sv = sv * (1.0f / (1.0f + expf(-a.shared_gate[t])));
+                sum = sum + sv;
+            }
             a.out[(int64_t)t * H + col] = res + sum;
         }
     }

@@ -317,4 +317,25 @@ hipError_t launch_prefill_route(const int32_t* ids, int64_t n, int k, int n_expe
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------- one group (a shared expert)
+
+__global__ void single_group_plan_kernel(unsigned long long* grp_ptr, int32_t* start, int32_t* n_groups, int32_t* idx,
+                                         int n, const uint8_t* blob) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) idx[i] = i;
+    if (i == 0) {
+        grp_ptr[0] = (unsigned long long)blob;
+        start[0] = 0;
+        start[1] = n;
+        *n_groups = 1;
+    }
+}
+
+hipError_t launch_single_group_plan(unsigned long long* grp_ptr, int32_t* start, int32_t* n_groups, int32_t* idx,
+                                    int n, const uint8_t* blob, hipStream_t s) {
+    hipLaunchKernelGGL(single_group_plan_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, grp_ptr, start,
+                       n_groups, idx, n, blob);
+    return hipGetLastError();
+}
+
 }  // namespace xs

@@ -96,9 +96,16 @@ struct FusedArgs {
     int32_t* err;
     int rh, rd, nu, nj, slab_gu_bytes, slab_dn_bytes, ttab;
     long long spin_ticks;   // bound of a wait, in wall-clock ticks
+    const float* shared;       // [n_tok, n_embd] the shared expert's rows, added once by the combine (NULL: none)
+    const float* shared_gate;  // [n_tok] its gate logits (NULL: ungated)
 };
 bool fused_decode_plan(const ExpertLayout& L, int n_expert, int k, int n_tok, FusedPlan* P);
 hipError_t launch_decode_fused(const FusedArgs& a, const FusedPlan& P, hipStream_t s);
+
+// the plan of one group of n entries (a shared expert over n tokens): grp_ptr[0] = blob, start = {0, n},
+// *n_groups = 1, idx[i] = i (the entries' destination rows and tokens)
+hipError_t launch_single_group_plan(unsigned long long* grp_ptr, int32_t* start, int32_t* n_groups, int32_t* idx,
+                                    int n, const uint8_t* blob, hipStream_t s);
 
 // combine.hip
 hipError_t launch_combine(const float* parts, const float* weights, const float* shared, const float* shared_gate,

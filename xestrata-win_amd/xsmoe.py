@@ -73,6 +73,10 @@ _SIGS = {
     "xs_moe_layer_decode_workspace_bytes": (SZ, [LP, I, I, I]),
     "xs_moe_layer_decode_status": (P, [P]),
     "xs_moe_layer_prefill": (I, [LP, P, SZ, I, I, P, P, P, P, I, P, SZ, P]),
+    "xs_shared_expert_decode": (I, [LP, P, P, I, P, P, P, P, SZ, P]),
+    "xs_shared_expert_decode_workspace_bytes": (SZ, [LP, I]),
+    "xs_moe_layer_decode_shared": (I, [LP, P, SZ, I, I, P, P, P, P, I, LP, P, P, P, SZ, P]),
+    "xs_moe_layer_decode_shared_workspace_bytes": (SZ, [LP, I, I, I, LP]),
     "xs_moe_layer_prefill_workspace_bytes": (SZ, [LP, I, I, I]),
 }
 
@@ -280,16 +284,37 @@ def moe_combine_residual(parts, weights, residual, output, n_embd, k, n_tok, sha
 
 # ------------------------------------------------------------------------------------------------ whole layers
 
+def shared_expert_decode(SL, blob, x, w_gate=None, stream=None):
+    """One shared expert over the tokens of x [T, n_embd] (blob: the expert's native bytes on the device) -> (shared
+    rows [T, n_embd], gate logits [T] or None)."""
+    T = x.shape[0]
+    ws_bytes = lib().xs_shared_expert_decode_workspace_bytes(ctypes.byref(SL), T)
+    ws = torch.zeros(ws_bytes + 256, dtype=torch.uint8, device=x.device)
+    shared = torch.empty(T, SL.n_embd, dtype=torch.float32, device=x.device)
+    gate = torch.empty(T, dtype=torch.float32, device=x.device) if w_gate is not None else None
+    _check(lib().xs_shared_expert_decode(ctypes.byref(SL), _p(blob), _p(x), T, _p(w_gate), _p(shared), _p(gate),
+                                         (ws.data_ptr() + 255) & ~255, ws_bytes, _stream(stream)))
+    return shared, gate
+
+
 class MoeLayer:
     """One MoE layer whose experts live in one HBM arena (expert e's native blob at arena + e * blob_bytes), with its
-    workspace allocated once, so calls allocate nothing (graph-capturable)."""
+    workspace allocated once, so calls allocate nothing (graph-capturable).  shared = (SL, blob, w_gate or None): a
+    shared expert added by the decode layer's combine (xs_moe_layer_decode_shared)."""
 
-    def __init__(self, L, arena, n_expert, k, max_tokens, prefill=False, device="cuda"):
+    def __init__(self, L, arena, n_expert, k, max_tokens, prefill=False, device="cuda", shared=None):
         self.L, self.arena, self.n_expert, self.k, self.max_tokens = L, arena, n_expert, k, max_tokens
         self.blob = L.bytes
         self.prefill = prefill
-        fn = lib().xs_moe_layer_prefill_workspace_bytes if prefill else lib().xs_moe_layer_decode_workspace_bytes
-        self.ws_bytes = fn(ctypes.byref(L), n_expert, k, max_tokens)
+        self.shared = shared
+        if shared is not None and prefill:
+            raise ValueError("a shared expert is supported on the decode layer")
+        if shared is not None:
+            self.ws_bytes = lib().xs_moe_layer_decode_shared_workspace_bytes(ctypes.byref(L), n_expert, k, max_tokens,
+                                                                             ctypes.byref(shared[0]))
+        else:
+            fn = lib().xs_moe_layer_prefill_workspace_bytes if prefill else lib().xs_moe_layer_decode_workspace_bytes
+            self.ws_bytes = fn(ctypes.byref(L), n_expert, k, max_tokens)
         # zeroed once: the decode layer's counters start at zero and every call leaves them there
         self.ws = torch.zeros(self.ws_bytes + 256, dtype=torch.uint8, device=device)
         self.ws_ptr = (self.ws.data_ptr() + 255) & ~255
@@ -304,6 +329,13 @@ class MoeLayer:
 
     def __call__(self, x, logits, residual, out, n_tok=None, arena=None, stream=None):
         n_tok = x.shape[0] if n_tok is None else n_tok
+        if self.shared is not None:
+            SL, sblob, w_gate = self.shared
+            _check(lib().xs_moe_layer_decode_shared(
+                ctypes.byref(self.L), _p(self.arena if arena is None else arena), self.blob, self.n_expert, self.k,
+                _p(x), _p(logits), _p(residual), _p(out), n_tok, ctypes.byref(SL), _p(sblob), _p(w_gate), self.ws_ptr,
+                self.ws_bytes, _stream(stream)))
+            return out
         fn = lib().xs_moe_layer_prefill if self.prefill else lib().xs_moe_layer_decode
         _check(fn(ctypes.byref(self.L), _p(self.arena if arena is None else arena), self.blob, self.n_expert, self.k,
                   _p(x), _p(logits), _p(residual), _p(out), n_tok, self.ws_ptr, self.ws_bytes, _stream(stream)))
