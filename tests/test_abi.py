@@ -16,7 +16,7 @@ def xm():
 
 
 def declared_symbols():
-    text = (ROOT / "include" / "xs_moe.h").read_text()
+    text = "".join(h.read_text() for h in sorted((ROOT / "include").glob("*.h")))
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"\b(xs_[a-z0-9_]+)\s*\(", text)))
 

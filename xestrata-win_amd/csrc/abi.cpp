@@ -86,6 +86,13 @@ size_t plan_words(long long capx) { return (size_t)(plan_ptr_off(capx) + 4 * cap
 
 }  // namespace
 
+namespace xs {
+int set_error(int code, const std::string& message) {
+    g_err = message;
+    return code;
+}
+}  // namespace xs
+
 extern "C" {
 
 const char* xs_last_error(void) { return g_err.c_str(); }

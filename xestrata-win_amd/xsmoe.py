@@ -37,10 +37,30 @@ class Layout(ctypes.Structure):
 
 
 _lib = None
+class PackInfo(ctypes.Structure):
+    """xs_pack_info_t: a pack's ExpertLayout totals (include/strata/kernels/cpu/expert_layout.hpp:21-49)."""
+    _fields_ = [("version", ctypes.c_int), ("has_gguf_off", ctypes.c_int), ("n_layers", ctypes.c_int64),
+                ("n_expert", ctypes.c_int64), ("max_blob", ctypes.c_uint64), ("total", ctypes.c_uint64)]
+
+
+class PackLayer(ctypes.Structure):
+    """xs_pack_layer_t: one layer's row of ExpertLayout (expert_layout.hpp:22-44)."""
+    _fields_ = [("gu_type", ctypes.c_int), ("d_type", ctypes.c_int), ("up_type", ctypes.c_int),
+                ("block", ctypes.c_int64), ("offset", ctypes.c_uint64), ("bytes", ctypes.c_uint64),
+                ("up_off", ctypes.c_uint64), ("down_off", ctypes.c_uint64), ("gguf_off", ctypes.c_uint64 * 3),
+                ("gguf_file", ctypes.c_char_p * 3)]
+
+
+class PackLoadStats(ctypes.Structure):
+    _fields_ = [("bytes", ctypes.c_uint64), ("layers", ctypes.c_uint64), ("seconds", ctypes.c_double)]
+
+
 P, I, I64, SZ, F = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t, ctypes.c_float
 LP = ctypes.POINTER(Layout)
 LL = ctypes.c_longlong
 U32 = ctypes.c_uint32
+U64 = ctypes.c_uint64
+S = ctypes.c_char_p
 
 _SIGS = {
     "xs_last_error": (ctypes.c_char_p, []),
@@ -78,6 +98,16 @@ _SIGS = {
     "xs_moe_layer_decode_shared": (I, [LP, P, SZ, I, I, P, P, P, P, I, LP, P, P, P, SZ, P]),
     "xs_moe_layer_decode_shared_workspace_bytes": (SZ, [LP, I, I, I, LP]),
     "xs_moe_layer_prefill_workspace_bytes": (SZ, [LP, I, I, I]),
+    # include/xs_pack.h
+    "xs_pack_layout_load": (I, [S, I64, I64, I64, I64, ctypes.POINTER(P)]),
+    "xs_pack_layout_from_gguf": (I, [S, ctypes.POINTER(I64), I64, I64, I64, I64, ctypes.POINTER(P)]),
+    "xs_pack_free": (None, [P]),
+    "xs_pack_info": (I, [P, ctypes.POINTER(PackInfo)]),
+    "xs_pack_layer": (I, [P, I64, ctypes.POINTER(PackLayer)]),
+    "xs_pack_blob_offset": (U64, [P, I64, I64]),
+    "xs_pack_check_gguf": (I, [P, S]),
+    "xs_pack_load_gguf": (I, [P, S, P, U64, I, ctypes.POINTER(PackLoadStats)]),
+    "xs_pack_load_gguf_layers": (I, [P, S, ctypes.POINTER(P), I, ctypes.POINTER(PackLoadStats)]),
 }
 
 
@@ -340,6 +370,72 @@ class MoeLayer:
         _check(fn(ctypes.byref(self.L), _p(self.arena if arena is None else arena), self.blob, self.n_expert, self.k,
                   _p(x), _p(logits), _p(residual), _p(out), n_tok, self.ws_ptr, self.ws_bytes, _stream(stream)))
         return out
+
+
+# ------------------------------------------------------------------------------------------------ native packs
+
+class Pack:
+    """A native pack's expert layout (include/xs_pack.h), the reference's ExpertLayout with expert_layout_load,
+    expert_layout_from_gguf, check_experts_gguf and load_experts_gguf (src/kernels/cpu/expert_layout.cpp:278-393,
+    src/core/expert_source.cpp:2706-2916).  The table lives in the library; load_gguf fills an HBM arena from the
+    model's shards in place."""
+
+    def __init__(self, handle):
+        self._h = P(handle)
+
+    @classmethod
+    def load(cls, pack_dir, n_layers, n_expert, n_embd, n_ff):
+        """native_experts.txt of pack_dir (expert_layout_load)."""
+        h = P()
+        _check(lib().xs_pack_layout_load(str(pack_dir).encode(), n_layers, n_expert, n_embd, n_ff, ctypes.byref(h)))
+        return cls(h.value)
+
+    @classmethod
+    def from_gguf(cls, gguf, moe_blocks, n_expert, n_embd, n_ff):
+        """The routed experts of a GGUF model read in place (expert_layout_from_gguf)."""
+        blocks = (I64 * len(moe_blocks))(*moe_blocks)
+        h = P()
+        _check(lib().xs_pack_layout_from_gguf(str(gguf).encode(), blocks, len(moe_blocks), n_expert, n_embd, n_ff,
+                                              ctypes.byref(h)))
+        return cls(h.value)
+
+    def __del__(self):
+        if getattr(self, "_h", None) and self._h.value and _lib is not None:
+            _lib.xs_pack_free(self._h)
+            self._h = P()
+
+    def info(self):
+        v = PackInfo()
+        _check(lib().xs_pack_info(self._h, ctypes.byref(v)))
+        return dict(version=v.version, has_gguf_off=bool(v.has_gguf_off), n_layers=v.n_layers, n_expert=v.n_expert,
+                    max_blob=v.max_blob, total=v.total)
+
+    def layer(self, l):
+        v = PackLayer()
+        _check(lib().xs_pack_layer(self._h, l, ctypes.byref(v)))
+        return dict(gu_type=v.gu_type, d_type=v.d_type, up_type=v.up_type, block=v.block, offset=v.offset,
+                    bytes=v.bytes, up_off=v.up_off, down_off=v.down_off, gguf_off=list(v.gguf_off),
+                    gguf_file=[f.decode() for f in v.gguf_file])
+
+    def blob_offset(self, l, e):
+        return lib().xs_pack_blob_offset(self._h, l, e)
+
+    def check_gguf(self, native_shard):
+        _check(lib().xs_pack_check_gguf(self._h, str(native_shard).encode()))
+
+    def load_gguf(self, native_shard, arena, threads=0):
+        """Fill `arena` (a uint8 tensor of at least info()['total'] bytes, on the GPU) from the shards."""
+        st = PackLoadStats()
+        _check(lib().xs_pack_load_gguf(self._h, str(native_shard).encode(), _p(arena), arena.numel() * arena.element_size(),
+                                       threads, ctypes.byref(st)))
+        return dict(bytes=st.bytes, layers=st.layers, seconds=st.seconds)
+
+    def load_gguf_layers(self, native_shard, layer_dst, threads=0):
+        """Fill one destination per layer (uint8 tensors of n_expert blobs each)."""
+        ptrs = (P * len(layer_dst))(*[_p(t) for t in layer_dst])
+        st = PackLoadStats()
+        _check(lib().xs_pack_load_gguf_layers(self._h, str(native_shard).encode(), ptrs, threads, ctypes.byref(st)))
+        return dict(bytes=st.bytes, layers=st.layers, seconds=st.seconds)
 
 
 # ------------------------------------------------------------------------------------------------ synthetic experts
