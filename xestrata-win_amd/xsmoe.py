@@ -108,6 +108,13 @@ _SIGS = {
     "xs_pack_check_gguf": (I, [P, S]),
     "xs_pack_load_gguf": (I, [P, S, P, U64, I, ctypes.POINTER(PackLoadStats)]),
     "xs_pack_load_gguf_layers": (I, [P, S, ctypes.POINTER(P), I, ctypes.POINTER(PackLoadStats)]),
+    # include/xs_tiers.h
+    "xs_wait_flag_ge": (I, [P, U32, I64, P, P]),
+    "xs_copy_i32_from_mapped": (I, [P, P, I64, P]),
+    "xs_copy_rows_from_mapped": (I, [P, P, I64, I64, P, P, P]),
+    "xs_fetch_blobs": (I, [P, P, P, I64, I, P]),
+    "xs_rebase_ptrs": (I, [P, P, P, I64, P]),
+    "xs_moe_hit_add": (I, [P, P, P, P, I64, I64, P]),
 }
 
 
@@ -370,6 +377,35 @@ class MoeLayer:
         _check(fn(ctypes.byref(self.L), _p(self.arena if arena is None else arena), self.blob, self.n_expert, self.k,
                   _p(x), _p(logits), _p(residual), _p(out), n_tok, self.ws_ptr, self.ws_bytes, _stream(stream)))
         return out
+
+
+# ------------------------------------------------------------------------------------------------ tier protocol
+# Host buffers are pinned torch tensors (pin_memory=True: hipHostMalloc, device-accessible at the same address);
+# device buffers are torch tensors on the GPU or raw addresses (ints).
+
+def wait_flag_ge(flag, value, limit_us=0, status=None, stream=None):
+    """Spin (bounded) until flag[0] >= value (include/xs_tiers.h; reference verify_kernels.cpp:783-788)."""
+    _check(lib().xs_wait_flag_ge(_p(flag), value, limit_us, _p(status), _stream(stream)))
+
+
+def copy_i32_from_mapped(dst, src, n, stream=None):
+    _check(lib().xs_copy_i32_from_mapped(_p(dst), _p(src), n, _stream(stream)))
+
+
+def copy_rows_from_mapped(dst, src, rows, width, hit_rows, count, stream=None):
+    _check(lib().xs_copy_rows_from_mapped(_p(dst), _p(src), rows, width, _p(hit_rows), _p(count), _stream(stream)))
+
+
+def fetch_blobs(src, n, dst, blob_bytes, cap, stream=None):
+    _check(lib().xs_fetch_blobs(_p(src), _p(n), _p(dst), blob_bytes, cap, _stream(stream)))
+
+
+def rebase_ptrs(ptr, n, base, blob_bytes, stream=None):
+    _check(lib().xs_rebase_ptrs(_p(ptr), _p(n), _p(base), blob_bytes, _stream(stream)))
+
+
+def moe_hit_add(parts, hit_out, dst, count, cap, n_embd, stream=None):
+    _check(lib().xs_moe_hit_add(_p(parts), _p(hit_out), _p(dst), _p(count), cap, n_embd, _stream(stream)))
 
 
 # ------------------------------------------------------------------------------------------------ native packs
