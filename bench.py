@@ -112,6 +112,80 @@ def pmc_prefill(torch, xm):
     log("pmc prefill run: 4 config-3 prefill layers")
 
 
+def set_logits(torch, n_sets, T, E, k, dev, gen):
+    """n_sets logit sets [n_sets, T, E]: i.i.d. N(0,1) plus +8 on set s's T*k experts (s*T*k .. mod E), so that the
+    steps of a rotation touch disjoint experts and no step finds its blobs still in the caches."""
+    lg = torch.randn(n_sets, T, E, device=dev, generator=gen)
+    for s in range(n_sets):
+        lg[s, :, (torch.arange(T * k, device=dev) + s * T * k) % E] += 8.0
+    return lg
+
+
+def time_steps(torch, calls, steps, warmup):
+    """calls: one zero-argument callable a step, captured as one graph round and replayed; ms per step."""
+    def one_round():
+        for c in calls:
+            c()
+    graph_time(torch, one_round, max(1, math.ceil(warmup / len(calls))))
+    ms, _ = graph_time(torch, one_round, max(1, math.ceil(steps / len(calls))))
+    return ms / len(calls)
+
+
+def distinct_experts(torch, lg, k):
+    return float(sum(len(torch.unique(torch.topk(lg[s], k, dim=1).indices)) for s in range(lg.shape[0])) / lg.shape[0])
+
+
+def other_configs(torch, xm, dev, gen, steps):
+    """Decode of configs 4 and 5 (reported beside the value, not the value): the layer per step, weights rotated so
+    that every step reads its experts from HBM."""
+    out = {}
+    # config 4: Qwen3-235B-A22B-shaped, IQ4_XS experts (hidden 4096, 128 experts, top-8, F 1536), batch 1 and 8
+    E, H, F, k, copies = 128, 4096, 1536, 8, 2
+    arena, L = xm.build_arena(E, H, F, xm.IQ4_XS, xm.IQ4_XS, seed=4, copies=copies)
+    for T in (1, 8):
+        n_sets = max(1, E // (T * k))
+        lg = set_logits(torch, n_sets, T, E, k, dev, gen)
+        x = torch.randn(T, H, device=dev, generator=gen).to(torch.bfloat16).float()
+        res = torch.randn(T, H, device=dev, generator=gen)
+        o = torch.empty(T, H, device=dev)
+        layer = xm.MoeLayer(L, arena, E, k, T)
+        calls = [(lambda c=c, s=s: layer(x, lg[s], res, o, arena=arena[c * E]))
+                 for s in range(n_sets) for c in range(copies)]
+        ms = time_steps(torch, calls, steps, len(calls))
+        b = distinct_experts(torch, lg, k) * L.bytes
+        out[f"config4_T{T}"] = dict(us_per_layer=round(ms * 1e3, 2), us_per_token=round(ms * 1e3 / T, 3),
+                                    expert_gbs=round(b / (ms * 1e-3) / 1e9, 1),
+                                    frac_hbm_peak=round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                                    expert_mb=round(b / 1e6, 1))
+        log(f"config 4 decode T={T}: {ms * 1e3:.2f} us/layer, {out[f'config4_T{T}']['expert_gbs']} GB/s")
+    del arena
+    torch.cuda.empty_cache()
+    # config 5: DeepSeek-V3-shaped (hidden 7168, 256 routed Q4_K experts, top-8, F 2048, one shared Q8_0 expert)
+    E, H, F, k = 256, 7168, 2048, 8
+    arena, L = xm.build_arena(E, H, F, xm.Q4_K, xm.Q4_K, seed=5)
+    sarena, SL = xm.build_arena(1, H, 2048, xm.Q8_0, xm.Q8_0, seed=55)
+    n_sets = E // k
+    lg = set_logits(torch, n_sets, 1, E, k, dev, gen)
+    x = torch.randn(1, H, device=dev, generator=gen).to(torch.bfloat16).float()
+    res = torch.randn(1, H, device=dev, generator=gen)
+    o = torch.empty(1, H, device=dev)
+    layer = xm.MoeLayer(L, arena, E, k, 1, shared=(SL, sarena[0], None))
+    ms = time_steps(torch, [(lambda s=s: layer(x, lg[s], res, o)) for s in range(n_sets)], steps, n_sets)
+    bias = torch.randn(E, device=dev, generator=gen) * 0.1
+    ms_r = time_steps(torch, [lambda: xm.router_grouped_sigmoid(lg[0], bias, 8, 4, k, 2.5)], steps, 8)
+    b = k * L.bytes + SL.bytes
+    out["config5_T1"] = dict(us_per_layer=round(ms * 1e3, 2), expert_gbs=round(b / (ms * 1e-3) / 1e9, 1),
+                             frac_hbm_peak=round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), expert_mb=round(b / 1e6, 1),
+                             routing="the layer's softmax top-8 (xs_moe_layer_decode_shared); the config's "
+                                     "group-limited sigmoid router (8 groups, top-4) timed alone below",
+                             sigmoid_router_us=round(ms_r * 1e3, 2))
+    log(f"config 5 decode T=1 (+ shared expert): {ms * 1e3:.2f} us/layer, {out['config5_T1']['expert_gbs']} GB/s; "
+        f"grouped sigmoid router alone {ms_r * 1e3:.2f} us")
+    del arena, sarena
+    torch.cuda.empty_cache()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -121,6 +195,7 @@ def main():
     ap.add_argument("--prefill-steps", type=int, default=10)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-others", action="store_true", help="skip configs 3 (verify), 4 and 5")
     ap.add_argument("--pmc-run", action="store_true", help="only the short workload of a rocprofv3 --pmc pass")
     ap.add_argument("--pmc-prefill", action="store_true", help="only 4 prefill layers, for a rocprofv3 --pmc pass")
     args = ap.parse_args()
@@ -210,6 +285,21 @@ def main():
     Tp = 2048
     rng = np.random.default_rng(3)
     pop = -1.2 * np.log(np.arange(1, E + 1))[rng.permutation(E)]
+    if not args.no_others:   # config 3's spec-verify batch: 4 tokens, Zipf(1.2) routing, one step per copy
+        zv = torch.from_numpy((pop[None, None, :] + rng.gumbel(size=(copies, 4, E))).astype(np.float32)).to(dev)
+        xv = torch.randn(4, H, device=dev, generator=gen).to(torch.bfloat16).float()
+        rv = torch.randn(4, H, device=dev, generator=gen)
+        ov = torch.empty(4, H, device=dev)
+        vlayer = xm.MoeLayer(L, arena, E, k, 4)
+        ms_v = time_steps(torch, [(lambda c=c: vlayer(xv, zv[c], rv, ov, arena=arena[c * E])) for c in range(copies)],
+                          max(copies, args.steps // 4), copies)
+        bv = distinct_experts(torch, zv, k) * blob
+        extra["config3_verify_T4_zipf"] = dict(us_per_layer=round(ms_v * 1e3, 2),
+                                                expert_gbs=round(bv / (ms_v * 1e-3) / 1e9, 1),
+                                                frac_hbm_peak=round(bv / (ms_v * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                                                distinct_experts=round(bv / blob, 2))
+        log(f"config 3 verify T=4 (Zipf): {ms_v * 1e3:.2f} us/layer, {extra['config3_verify_T4_zipf']['expert_gbs']} "
+            f"GB/s")
     zl = torch.from_numpy((pop[None, :] + rng.gumbel(size=(Tp, E))).astype(np.float32)).to(dev)
     xp = torch.randn(Tp, H, device=dev, generator=gen).to(torch.bfloat16).float()
     rp = torch.randn(Tp, H, device=dev, generator=gen)
@@ -230,6 +320,8 @@ def main():
                    frac_mfma_peak=round(tf / BF16_PEAK_TFLOPS, 4), mfma="f16 operands, fp32 accumulate (dense peak "
                    "2.5 PFLOP/s, as bf16)", tokens_per_s=round(Tp / (ms_p * 1e-3), 0),
                    flops_per_layer=flops, routing="Zipf alpha=1.2 (Gumbel-top-k)")
+
+    others = {} if args.no_others else other_configs(torch, xm, dev, gen, max(64, args.steps // 4))
 
     # ---------------------------------------------------------------- the CPU baseline (the oracle, host cores)
     cpu = None
@@ -290,6 +382,7 @@ def main():
                      "algorithmic_bytes_per_launch": round(roof_bytes), "avg_launch_us": round(roof_us, 3)},
         "decode_batches": extra,
         "prefill": prefill,
+        "other_configs": others,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -131,12 +131,22 @@ def test_router_zipf_prefill(xm, xo):
     assert np.array_equal(t2n(w).view(np.uint32), rw.view(np.uint32))
 
 
-def test_grouped_sigmoid_router(xm, xo):
-    rng = np.random.default_rng(11)
-    lg = (rng.standard_normal((64, 256)) * 2).astype(np.float32)
-    bias = (rng.standard_normal(256) * 0.1).astype(np.float32)
-    ids, w = xm.router_grouped_sigmoid(torch.from_numpy(lg).to(DEV), torch.from_numpy(bias).to(DEV), 8, 4, 8, 2.5)
-    rids, rw = xo.router_grouped_sigmoid(lg, bias, 8, 4, 8, 2.5)
+@pytest.mark.parametrize("E,G,TG,k,ties", [(256, 8, 4, 8, False), (256, 8, 4, 8, True), (64, 4, 2, 6, True),
+                                          (128, 8, 3, 8, False), (160, 5, 2, 8, True), (512, 8, 4, 8, False),
+                                          (72, 3, 2, 6, True), (1024, 64, 8, 16, False)])
+def test_grouped_sigmoid_router(xm, xo, E, G, TG, k, ties):
+    # the register form (groups on whole lanes: 256/8, 64/4, 128/8, 160/5 with idle lanes, 512/8, 1024/64) and the
+    # LDS form (72/3: 12 lanes a group); ties: logits on a 0.25 grid and no bias, so group scores and experts tie
+    rng = np.random.default_rng(E + G + k)
+    T = 37                                              # not a multiple of the 4 tokens a work-group
+    lg = (rng.standard_normal((T, E)) * 2).astype(np.float32)
+    bias = (rng.standard_normal(E) * 0.1).astype(np.float32)
+    if ties:
+        lg = (np.round(lg * 4) / 4).astype(np.float32)
+        bias = None
+    ids, w = xm.router_grouped_sigmoid(torch.from_numpy(lg).to(DEV), None if bias is None else
+                                       torch.from_numpy(bias).to(DEV), G, TG, k, 2.5)
+    rids, rw = xo.router_grouped_sigmoid(lg, bias, G, TG, k, 2.5)
     assert np.array_equal(t2n(ids), rids)
     assert np.array_equal(t2n(w).view(np.uint32), rw.view(np.uint32))
 

@@ -79,6 +79,87 @@ __global__ __launch_bounds__(64) void router_grouped_sigmoid_kernel(const float*
     }
 }
 
+// The same routing with the experts in registers, for shapes whose groups fall on whole lanes: lane l holds experts
+// l PER .. l PER + PER - 1, so a group of per = n_expert / n_group experts is lpg = per / PER adjacent lanes (a power
+// of two).  A group's two best c: each lane's two best, merged over the group's lanes by a xor butterfly (the pair of
+// largest values does not depend on the order they are met in); the groups' ranks by v_readlane (score, then the
+// lower group); the k best c by k argmax passes over the wave (better(): the same total order as above, so the same
+// picks, a taken expert's c set to -inf as above).  Four tokens a work-group, one a wave.
+template <int PER>
+__global__ __launch_bounds__(256) void router_grouped_sigmoid_wave_kernel(
+    const float* __restrict__ logits, const float* __restrict__ bias, int n_tokens, int n_expert, int n_group,
+    int topk_group, int k, float routed_scale, int32_t* __restrict__ ids, float* __restrict__ weights) {
+    const int lane = threadIdx.x & 63, t = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+    if (t >= n_tokens) return;
+    const float* l = logits + (int64_t)t * n_expert;
+    const int per = n_expert / n_group, lpg = per / PER, my_g = lane / lpg;
+    float s[PER], c[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        const int e = lane * PER + j;
+        const bool in = e < n_expert;
+        s[j] = in ? canon_rcp(1.0f + canon_exp(-l[e])) : 0.0f;
+        c[j] = in ? s[j] + (bias ? bias[e] : 0.0f) : -INFINITY;
+    }
+    float b1 = -INFINITY, b2 = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        const float v = c[j];
+        if (v > b1) { b2 = b1; b1 = v; }
+        else if (v > b2) b2 = v;
+    }
+    for (int o = 1; o < lpg; o <<= 1) {
+        const float o1 = __shfl_xor(b1, o, 64), o2 = __shfl_xor(b2, o, 64);
+        const float n1 = fmaxf(b1, o1), n2 = fmaxf(fminf(b1, o1), fmaxf(b2, o2));
+        b1 = n1;
+        b2 = n2;
+    }
+    const float gs = b1 + b2;
+    int rank = 0;
+    for (int g = 0; g < n_group; ++g) {
+        const float og = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gs), g * lpg));
+        rank += og > gs || (og == gs && g < my_g) ? 1 : 0;
+    }
+    const bool chosen = my_g < n_group && rank < topk_group;
+    if (!chosen) {
+#pragma unroll
+        for (int j = 0; j < PER; ++j) c[j] = -INFINITY;
+    }
+    // a pass: each lane's best candidate as an unsigned key of c (the float order; NaN and "none" 0, so never picked),
+    // the wave's largest key by DPP, its lowest lane by ballot (the lower lane holds the lower experts, and a lane's
+    // own ties keep its lower one): better()'s order
+    float my_w = 0.0f;
+    int my_id = 0;
+    for (int i = 0; i < k; ++i) {
+        uint32_t lk = 0u;
+        int lj = 0;
+        float ls = 0.0f;
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            const float v = c[j] + 0.0f;   // -0 as +0: equal floats, equal keys
+            const uint32_t b = __float_as_uint(v);
+            const uint32_t key = !chosen || lane * PER + j >= n_expert || v != v ? 0u
+                                 : (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+            if (key > lk) { lk = key; lj = j; ls = s[j]; }
+        }
+        const uint32_t m = wave_max_u32(lk);
+        if (m == 0u) break;
+        const int owner = (int)__builtin_ctzll(__ballot(lk == m));
+        const int bi = owner * PER + __builtin_amdgcn_readlane(lj, owner);
+        const float sv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ls), owner));
+#pragma unroll
+        for (int j = 0; j < PER; ++j)
+            if (lane == owner && j == lj) c[j] = -INFINITY;   // taken
+        if (lane == i) { my_w = sv; my_id = bi; }
+    }
+    float sum = 0.0f;
+    for (int i = 0; i < k; ++i) sum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_w), i));
+    if (lane < k) {
+        ids[(int64_t)t * k + lane] = my_id;
+        weights[(int64_t)t * k + lane] = my_w / sum * routed_scale;
+    }
+}
+
 // logits[t, e] = x[t] . w[e] in fp32 (the router GEMV, reference src/kernels/xe/bf16_gemv.cpp:495-517): a wave per
 // (expert, token), lanes over the row, then a butterfly
 __global__ __launch_bounds__(256) void logits_f32_kernel(const float* __restrict__ x, const float* __restrict__ w,
@@ -109,6 +190,23 @@ hipError_t launch_router_topk(const float* logits, int n_tokens, int n_expert, i
 hipError_t launch_router_grouped_sigmoid(const float* logits, const float* bias, int n_tokens, int n_expert,
                                          int n_group, int topk_group, int k, float routed_scale, int32_t* ids,
                                          float* weights, hipStream_t s) {
+    // the register form where the groups fall on whole lanes (lanes a group a power of two), else the LDS form
+    const int PER = n_expert <= 64 ? 1 : n_expert <= 128 ? 2 : n_expert <= 256 ? 4 : n_expert <= 512 ? 8 : 16;
+    const int per = n_group > 0 ? n_expert / n_group : 0;
+    const int lpg = per % PER == 0 ? per / PER : 0;
+    if (n_expert <= 1024 && n_group > 0 && per * n_group == n_expert && lpg > 0 && (lpg & (lpg - 1)) == 0) {
+        const dim3 g((unsigned)((n_tokens + 3) / 4)), b(256);
+        const auto args = [&](auto kern) {
+            hipLaunchKernelGGL(kern, g, b, 0, s, logits, bias, n_tokens, n_expert, n_group, topk_group, k, routed_scale,
+                               ids, weights);
+        };
+        if (PER == 1) args(router_grouped_sigmoid_wave_kernel<1>);
+        else if (PER == 2) args(router_grouped_sigmoid_wave_kernel<2>);
+        else if (PER == 4) args(router_grouped_sigmoid_wave_kernel<4>);
+        else if (PER == 8) args(router_grouped_sigmoid_wave_kernel<8>);
+        else args(router_grouped_sigmoid_wave_kernel<16>);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(router_grouped_sigmoid_kernel, dim3((unsigned)n_tokens), dim3(64), 0, s, logits, bias, n_expert,
                        n_group, topk_group, k, routed_scale, ids, weights);
     return hipGetLastError();
