@@ -172,7 +172,7 @@ def other_configs(torch, xm, dev, gen, steps):
     layer = xm.MoeLayer(L, arena, E, k, 1, shared=(SL, sarena[0], None))
     ms = time_steps(torch, [(lambda s=s: layer(x, lg[s], res, o)) for s in range(n_sets)], steps, n_sets)
     bias = torch.randn(E, device=dev, generator=gen) * 0.1
-    ms_r = time_steps(torch, [lambda: xm.router_grouped_sigmoid(lg[0], bias, 8, 4, k, 2.5)], steps, 8)
+    ms_r = time_steps(torch, [lambda: xm.router_grouped_sigmoid(lg[0], bias, 8, 4, k, 2.5)] * 32, steps, 32)
     b = k * L.bytes + SL.bytes
     out["config5_T1"] = dict(us_per_layer=round(ms * 1e3, 2), expert_gbs=round(b / (ms * 1e-3) / 1e9, 1),
                              frac_hbm_peak=round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), expert_mb=round(b / 1e6, 1),

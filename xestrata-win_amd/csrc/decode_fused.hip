@@ -419,7 +419,17 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
     // with at most one gate/up unit a work-group, the store wave fetches the work-group's first down rows once the
     // gate/up slab is in: they then land while the gate/up products run and h travels
     const bool piped = a.ttab > 0 && T <= a.ttab;   // the pipelined gate/up path below (4..16 tokens)
-    const bool dn_early = !piped && n_gu <= (int)gridDim.x && wg < n_gu && wg < n_dn;
+    // down units: with one token and more units than work-groups, a work-group takes a run of consecutive ones
+    // (mostly one expert's), so its entry's h is gathered and quantized once for the run rather than once a unit.
+    // (With more tokens a unit's cost is its group's entry count, and runs would load the work-groups unevenly: there
+    // the units go round the work-groups.)
+    const int G = (int)gridDim.x;
+    const bool runs = T == 1 && n_dn > G;
+    const int dq = n_dn / G, dr = n_dn - dq * G;
+    const int d_begin = runs ? wg * dq + min(wg, dr) : wg;
+    const int d_end = runs ? d_begin + dq + (wg < dr ? 1 : 0) : n_dn;
+    const int d_step = runs ? 1 : G;
+    const bool dn_early = !piped && n_gu <= G && wg < n_gu && d_begin < d_end;   // (round robin: d_begin = wg)
     if (piped) {
         // 4..16 tokens, several units a work-group: every token's q8_1 activation once, into an LDS table, then the
         // units' slabs double-buffered - unit i + 1's DMA flies while unit i computes.  The load waves issue nothing
@@ -518,7 +528,7 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
             }
             __syncthreads();
             if (dn_early && !loader && u1 == wg && p == e0) {
-                const int gd = wg / nj, jd = wg - gd * nj;
+                const int gd = d_begin / nj, jd = d_begin - gd * nj;
                 const uint8_t* srcd =
                     a.arena + (size_t)s_gexp[gd] * (size_t)a.blob + L.down_off + (size_t)jd * rd * L.d_row;
                 dma_wave_to_lds(slab_dn, n16d, [&](int i) { return (const void*)(srcd + 16 * (size_t)i); });
@@ -549,19 +559,24 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
     }
 
     // ---- 3. down units; the first one's rows are fetched once the gate/up rows are in (they go first)
-    for (int u2 = wg; u2 < n_dn; u2 += gridDim.x) {
+    int prev_g = -1;
+    for (int u2 = d_begin; u2 < d_end; u2 += d_step) {
         const int g = u2 / nj, j = u2 - g * nj;
         const uint8_t* srcd = a.arena + (size_t)s_gexp[g] * (size_t)a.blob + L.down_off + (size_t)j * rd * L.d_row;
         lds_barrier();   // the previous unit's readers of the slab are done
-        const bool fetched = dn_early && u2 == wg;
+        const bool fetched = dn_early && u2 == d_begin;
         if (loader && !fetched) dma_to_lds(slab_dn, n16d, [&](int i) { return (const void*)(srcd + 16 * (size_t)i); });
         const int e0 = s_start[g], e1 = s_start[g + 1];
         for (int p = e0; p < e1; p += NE) {
             const int m = min(NE, e1 - p);
             if (p > e0) __syncthreads();
             // h of the entries (polled until the gate/up units have written it) per 32 values to canonical q8_1
-            // (iq_kernels.cpp:2118-2133): 8 values a lane, a block on 4 neighbouring lanes
-            if (loader) {
+            // (iq_kernels.cpp:2118-2133): 8 values a lane, a block on 4 neighbouring lanes.  The previous unit's, when
+            // it was the same group's single pass: act_d holds it still.
+            const bool h_kept = g == prev_g && e1 - e0 <= NE;
+            if (loader && h_kept) {
+                vm_drain();   // the slab has landed
+            } else if (loader) {
                 const int c8n = F / 8;
                 for (int i0 = 0; i0 < m * c8n; i0 += kLT) {
                     const int i = i0 + tid;
@@ -623,6 +638,7 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
                     st_tag(a.px + (int64_t)s_dst[p + e] * H + j * rd + r, s_po[e * rd + r], tag);
                 }
         }
+        prev_g = g;
     }
 
     // ---- 4. combines: (token t, down slab j), the slab's columns of the token's k parts in rank order + residual
