@@ -124,6 +124,19 @@ def test_config4_iq4_xs(xm, xo, T):
     assert rel <= 1e-3 and moe_rel <= 1e-3, (rel, moe_rel)
 
 
+@pytest.mark.parametrize("k", [8, 6])
+def test_config5_shape_fused_decode(xm, xo, k):
+    """The fused layer at config 5's expert shape (hidden 7168, F 2048, Q4_K both sides), one token: far more units
+    than work-groups, so each work-group runs several gate/up units and a run of consecutive down units (its entry's
+    h gathered once a run); bit for bit with the oracle (softmax routing over 16 resident experts)."""
+    E = 16
+    arena, L = xm.build_arena(E, 7168, 2048, 12, 12, seed=57)
+    g = torch.Generator(device=DEV).manual_seed(58 + k)
+    logits = torch.randn(1, E, device=DEV, generator=g)
+    rel, moe_rel = decode_case(xm, xo, arena, L, E, k, 1, logits, 59)
+    assert rel <= 1e-3 and moe_rel <= 1e-3, (rel, moe_rel)
+
+
 def test_config5_deepseek_decode(xm, xo):
     """Config 5: hidden 7168, 256 routed Q4_K experts + 1 shared Q8_0, sigmoid + bias, 8 groups / top-4 / top-8, F
     2048, decode batch 1: the routed experts through the plan and the grouped kernels, the shared expert as one
