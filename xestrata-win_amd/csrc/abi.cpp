@@ -608,6 +608,7 @@ int layer_decode(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_
         a.slab_gu_bytes = P.slab_gu;
         a.slab_dn_bytes = P.slab_dn;
         a.ttab = P.ttab;
+        a.direct = P.direct;
         a.spin_ticks = spin_ticks();
         a.shared = shared;
         a.shared_gate = shared_gate;

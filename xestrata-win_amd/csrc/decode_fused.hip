@@ -429,7 +429,7 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
     const int d_begin = runs ? wg * dq + min(wg, dr) : wg;
     const int d_end = runs ? d_begin + dq + (wg < dr ? 1 : 0) : n_dn;
     const int d_step = runs ? 1 : G;
-    const bool dn_early = !piped && n_gu <= G && wg < n_gu && d_begin < d_end;   // (round robin: d_begin = wg)
+    const bool dn_early = !piped && !a.direct && n_gu <= G && wg < n_gu && d_begin < d_end;   // (round robin: d_begin = wg)
     if (piped) {
         // 4..16 tokens, several units a work-group: every token's q8_1 activation once, into an LDS table, then the
         // units' slabs double-buffered - unit i + 1's DMA flies while unit i computes.  The load waves issue nothing
@@ -509,7 +509,7 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
         const uint8_t* srcg = blob + (size_t)j * rh * L.gu_row;
         const uint8_t* srcu = blob + L.up_off + (size_t)j * rh * L.gu_row;
         __syncthreads();   // the previous unit's readers of the slab are done
-        if (loader)
+        if (loader && !a.direct)
             dma_to_lds(slab_gu, 2 * n16a, [&](int i) {
                 return (const void*)(i < n16a ? srcg + 16 * (size_t)i : srcu + 16 * (size_t)(i - n16a));
             });
@@ -538,8 +538,10 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
                 float acc[NE];
 #pragma unroll
                 for (int e = 0; e < NE; ++e) acc[e] = 0.0f;
+                // the row in the slab, or (direct) in the blob: gate rows, then up rows
+                const uint8_t* rb = !a.direct ? slab_gu : rr < rh ? srcg : srcu - (size_t)rh * L.gu_row;
                 for (int u = c; u < H / UG::kUnit; u += lpr_g)
-                    UG::template apply<NE>(slab_gu, rr * (int)L.gu_row, u, actg, m, acc);
+                    UG::template apply<NE>(rb, rr * (int)L.gu_row, u, actg, m, acc);
 #pragma unroll
                 for (int e = 0; e < NE; ++e) acc[e] = lanes_sum(acc[e], lpr_g);
                 if (c == 0) {
@@ -565,7 +567,8 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
         const uint8_t* srcd = a.arena + (size_t)s_gexp[g] * (size_t)a.blob + L.down_off + (size_t)j * rd * L.d_row;
         lds_barrier();   // the previous unit's readers of the slab are done
         const bool fetched = dn_early && u2 == d_begin;
-        if (loader && !fetched) dma_to_lds(slab_dn, n16d, [&](int i) { return (const void*)(srcd + 16 * (size_t)i); });
+        if (loader && !fetched && !a.direct)
+            dma_to_lds(slab_dn, n16d, [&](int i) { return (const void*)(srcd + 16 * (size_t)i); });
         const int e0 = s_start[g], e1 = s_start[g + 1];
         for (int p = e0; p < e1; p += NE) {
             const int m = min(NE, e1 - p);
@@ -621,8 +624,9 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
                 float acc[NE];
 #pragma unroll
                 for (int e = 0; e < NE; ++e) acc[e] = 0.0f;
+                const uint8_t* rb = a.direct ? srcd : slab_dn;
                 for (int u = c; u < F / UD::kUnit; u += lpr_d)
-                    UD::template apply<NE>(slab_dn, rr * (int)L.d_row, u, actd, m, acc);
+                    UD::template apply<NE>(rb, rr * (int)L.d_row, u, actd, m, acc);
 #pragma unroll
                 for (int e = 0; e < NE; ++e) acc[e] = lanes_sum(acc[e], lpr_d);
                 if (c == 0) {
@@ -737,12 +741,28 @@ bool fused_decode_plan(const ExpertLayout& L, int n_expert, int k, int n_tok, Fu
     if (rd > 64) rd = 64;
     while (rd > 8 && H % rd) rd -= 8;
     if (H % rd) return false;
+    // one token with more gate/up units than two work-groups a CU (large experts): the direct form - a unit's rows
+    // fill the work-group's lanes (each row's canonical lanes, 256 in all), every lane reads its blocks from HBM
+    // itself, and without slabs the LDS holds up to four work-groups a CU, whose loads hide each other's latency
+    // (only with at least 4 gate/up units a lane: fewer, and each lane's few dependent loads leave it idle - measured
+    // slower at hidden 4096, 2 a lane)
+    P->direct = 0;
+    const int ug = H / (L.gu_type == kQ8_0 ? 32 : 256);
+    if (n_tok == 1 && (int64_t)k * (F / rh) > 2 * device_cus() && ug / canon_lanes(ug) >= 4) {
+        const int lg = canon_lanes(ug), ld = canon_lanes(F / 32);
+        const int rh2 = 128 / lg, rd2 = 256 / ld;
+        if (F % rh2 == 0 && H % rd2 == 0 && rd2 <= 64) {
+            P->direct = 1;
+            rh = rh2;
+            rd = rd2;
+        }
+    }
     P->rh = rh;
     P->rd = rd;
     P->nu = F / rh;
     P->nj = H / rd;
-    P->slab_gu = 2 * rh * (int)L.gu_row;
-    P->slab_dn = rd * (int)L.d_row;
+    P->slab_gu = P->direct ? 0 : 2 * rh * (int)L.gu_row;
+    P->slab_dn = P->direct ? 0 : rd * (int)L.d_row;
     P->ne = n_tok >= 4 ? 4 : n_tok >= 2 ? 2 : 1;
     auto lds_of = [&](int ttab) {
         return (P->ne == 1 ? fused_lds<1>(n_expert, H, F, rh, P->slab_gu, P->slab_dn, ttab)
@@ -767,19 +787,19 @@ namespace {
 struct LaunchShape {   // per device and kernel: the attribute set and the resident work-groups
     int dev;
     const void* kern;
-    int lds, grid_max;
+    int lds, cap, grid_max;
 };
 std::mutex g_shape_mu;
 std::vector<LaunchShape> g_shapes;
 }  // namespace
 
-static hipError_t resident_grid(const void* kern, int lds, int* grid_max) {
+static hipError_t resident_grid(const void* kern, int lds, int cap, int* grid_max) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
     std::lock_guard<std::mutex> lock(g_shape_mu);
     for (const LaunchShape& s : g_shapes)
-        if (s.dev == dev && s.kern == kern && s.lds == lds) {
+        if (s.dev == dev && s.kern == kern && s.lds == lds && s.cap == cap) {
             *grid_max = s.grid_max;
             return hipSuccess;
         }
@@ -789,8 +809,8 @@ static hipError_t resident_grid(const void* kern, int lds, int* grid_max) {
     if ((e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return e;
     if ((e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, kFT, lds)) != hipSuccess) return e;
     if (occ < 1) return hipErrorInvalidConfiguration;
-    *grid_max = cus * (occ > 2 ? 2 : occ);
-    g_shapes.push_back(LaunchShape{dev, kern, lds, *grid_max});
+    *grid_max = cus * (occ > cap ? cap : occ);
+    g_shapes.push_back(LaunchShape{dev, kern, lds, cap, *grid_max});
     return hipSuccess;
 }
 
@@ -802,7 +822,7 @@ hipError_t launch_decode_fused(const FusedArgs& a, const FusedPlan& P, hipStream
     else kern = pick<kQ4_K, kQ4_K>(P.ne);
     // every work-group resident at once: the down units wait on the gate/up units of others
     int grid = 0;
-    hipError_t e = resident_grid(kern, P.lds, &grid);
+    hipError_t e = resident_grid(kern, P.lds, P.direct ? 4 : 2, &grid);
     if (e != hipSuccess) return e;
     const int cap = a.n_tok * a.k < a.n_expert ? a.n_tok * a.k : a.n_expert;
     const int need = cap * (P.nu > P.nj ? P.nu : P.nj);

@@ -76,6 +76,7 @@ struct FusedPlan {     // the fused decode layer's unit sizes (a function of the
     int slab_gu, slab_dn;
     int ne, lds;       // entries a pass, dynamic LDS bytes
     int ttab;          // tokens of the pipelined gate/up path's activation table (0: that path is off)
+    int direct;        // 1: one token, units read their rows from HBM straight into registers (no LDS slabs)
 };
 struct FusedArgs {
     ExpertLayout L;
@@ -94,7 +95,7 @@ struct FusedArgs {
     int32_t* sync;          // 16 64-bit call counters at sync + 32 i (2 KB, 8-byte aligned; 2^20 a call in all, this
                             // call's tag - 1 = their sum >> 20), zero before the first call
     int32_t* err;
-    int rh, rd, nu, nj, slab_gu_bytes, slab_dn_bytes, ttab;
+    int rh, rd, nu, nj, slab_gu_bytes, slab_dn_bytes, ttab, direct;
     long long spin_ticks;   // bound of a wait, in wall-clock ticks
     const float* shared;       // [n_tok, n_embd] the shared expert's rows, added once by the combine (NULL: none)
     const float* shared_gate;  // [n_tok] its gate logits (NULL: ungated)
