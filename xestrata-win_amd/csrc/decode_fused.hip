@@ -229,13 +229,13 @@ __device__ __forceinline__ int epoch_of(unsigned long long c) {   // lanes 0..15
 }
 
 template <int PER>
-__device__ __forceinline__ void route_tokens_wave(const FusedArgs& a, int* s_ids, float* s_w,
+__device__ __forceinline__ void route_tokens_wave(const FusedArgs& a, int T, int* s_ids, float* s_w,
                                                   unsigned long long& ctr) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, E = a.n_expert, k = a.k;
     float lv[PER];
-    if (wave < a.n_tok) load_logits_wave<PER>(a.logits + (int64_t)wave * E, E, lv);
+    if (wave < T) load_logits_wave<PER>(a.logits + (int64_t)wave * E, E, lv);
     ctr = load_counter(a);
-    for (int t = wave; t < a.n_tok; t += kFT / 64) {
+    for (int t = wave; t < T; t += kFT / 64) {
         if (lane < k) {   // ranks a NaN row leaves unwritten stay invalid
             s_ids[t * k + lane] = -1;
             s_w[t * k + lane] = 0.0f;
@@ -245,13 +245,17 @@ __device__ __forceinline__ void route_tokens_wave(const FusedArgs& a, int* s_ids
     }
 }
 
-template <int TG, int TD, int NE>
+// NE = 1 is launched for one token only (the plan's ne: 1 token -> 1, 2-3 -> 2, 4+ -> 4), so T = 1 there is a
+// constant and the multi-token planning and the pipelined gate/up path fold away; DIRECT (one token only) is the
+// form without slabs.  Each instance carries only its own paths: the kernel's code is large, and what an instance
+// does not run still costs instruction-cache room.
+template <int TG, int TD, int NE, bool DIRECT>
 __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];
     using UG = Unit<TG, true>;
     using UD = Unit<TD, false>;
     const ExpertLayout& L = a.L;
-    const int H = (int)L.n_embd, F = (int)L.n_ff, k = a.k, T = a.n_tok, n = T * k, E = a.n_expert;
+    const int H = (int)L.n_embd, F = (int)L.n_ff, k = a.k, T = NE == 1 ? 1 : a.n_tok, n = T * k, E = a.n_expert;
     const int rh = a.rh, rd = a.rd, nu = a.nu, nj = a.nj;
     const FusedLds o = fused_lds<NE>(E, H, F, rh, a.slab_gu_bytes, a.slab_dn_bytes, a.ttab);
     int* s_ids = (int*)(lds + o.ids);
@@ -290,15 +294,15 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
             q8_1_256_to_act(a.x, j8, q, (float*)(q + H), (int*)(q + H + H / 8));
     }
     if (E <= 64) {
-        route_tokens_wave<1>(a, s_ids, s_w, ctr);
+        route_tokens_wave<1>(a, T, s_ids, s_w, ctr);
     } else if (E <= 128) {
-        route_tokens_wave<2>(a, s_ids, s_w, ctr);
+        route_tokens_wave<2>(a, T, s_ids, s_w, ctr);
     } else if (E <= 256) {
-        route_tokens_wave<4>(a, s_ids, s_w, ctr);
+        route_tokens_wave<4>(a, T, s_ids, s_w, ctr);
     } else if (E <= 512) {
-        route_tokens_wave<8>(a, s_ids, s_w, ctr);
+        route_tokens_wave<8>(a, T, s_ids, s_w, ctr);
     } else {
-        route_tokens_wave<16>(a, s_ids, s_w, ctr);
+        route_tokens_wave<16>(a, T, s_ids, s_w, ctr);
     }
     if (wave == 0) {
         const int epoch = epoch_of(ctr);
@@ -418,7 +422,7 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
     const bool loader = wave < kLoadWaves;
     // with at most one gate/up unit a work-group, the store wave fetches the work-group's first down rows once the
     // gate/up slab is in: they then land while the gate/up products run and h travels
-    const bool piped = a.ttab > 0 && T <= a.ttab;   // the pipelined gate/up path below (4..16 tokens)
+    const bool piped = NE == 4 && a.ttab > 0 && T <= a.ttab;   // the pipelined gate/up path below (4..16 tokens)
     // down units: with one token and more units than work-groups, a work-group takes a run of consecutive ones
     // (mostly one expert's), so its entry's h is gathered and quantized once for the run rather than once a unit.
     // (With more tokens a unit's cost is its group's entry count, and runs would load the work-groups unevenly: there
@@ -429,7 +433,7 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
     const int d_begin = runs ? wg * dq + min(wg, dr) : wg;
     const int d_end = runs ? d_begin + dq + (wg < dr ? 1 : 0) : n_dn;
     const int d_step = runs ? 1 : G;
-    const bool dn_early = !piped && !a.direct && n_gu <= G && wg < n_gu && d_begin < d_end;   // (round robin: d_begin = wg)
+    const bool dn_early = !piped && !DIRECT && n_gu <= G && wg < n_gu && d_begin < d_end;   // (round robin: d_begin = wg)
     if (piped) {
         // 4..16 tokens, several units a work-group: every token's q8_1 activation once, into an LDS table, then the
         // units' slabs double-buffered - unit i + 1's DMA flies while unit i computes.  The load waves issue nothing
@@ -509,7 +513,7 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
         const uint8_t* srcg = blob + (size_t)j * rh * L.gu_row;
         const uint8_t* srcu = blob + L.up_off + (size_t)j * rh * L.gu_row;
         __syncthreads();   // the previous unit's readers of the slab are done
-        if (loader && !a.direct)
+        if (loader && !DIRECT)
             dma_to_lds(slab_gu, 2 * n16a, [&](int i) {
                 return (const void*)(i < n16a ? srcg + 16 * (size_t)i : srcu + 16 * (size_t)(i - n16a));
             });
@@ -534,22 +538,29 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
                 dma_wave_to_lds(slab_dn, n16d, [&](int i) { return (const void*)(srcd + 16 * (size_t)i); });
             }
             const int c = lane & (lpr_g - 1);
-            for (int rr = tid / lpr_g; rr < 2 * rh; rr += kFT / lpr_g) {
-                float acc[NE];
+            // the rows from the slab (LDS reads), or in the direct form from the blob (global reads): two loops, so
+            // that each one's loads have a known address space
+            auto gu_rows = [&](auto row_base) {
+                for (int rr = tid / lpr_g; rr < 2 * rh; rr += kFT / lpr_g) {
+                    float acc[NE];
 #pragma unroll
-                for (int e = 0; e < NE; ++e) acc[e] = 0.0f;
-                // the row in the slab, or (direct) in the blob: gate rows, then up rows
-                const uint8_t* rb = !a.direct ? slab_gu : rr < rh ? srcg : srcu - (size_t)rh * L.gu_row;
-                for (int u = c; u < H / UG::kUnit; u += lpr_g)
-                    UG::template apply<NE>(rb, rr * (int)L.gu_row, u, actg, m, acc);
+                    for (int e = 0; e < NE; ++e) acc[e] = 0.0f;
+                    const uint8_t* rb = row_base(rr);
+                    for (int u = c; u < H / UG::kUnit; u += lpr_g)
+                        UG::template apply<NE>(rb, rr * (int)L.gu_row, u, actg, m, acc);
 #pragma unroll
-                for (int e = 0; e < NE; ++e) acc[e] = lanes_sum(acc[e], lpr_g);
-                if (c == 0) {
+                    for (int e = 0; e < NE; ++e) acc[e] = lanes_sum(acc[e], lpr_g);
+                    if (c == 0) {
 #pragma unroll
-                    for (int e = 0; e < NE; ++e)
-                        if (e < m) s_gu[e * 2 * rh + rr] = acc[e];
+                        for (int e = 0; e < NE; ++e)
+                            if (e < m) s_gu[e * 2 * rh + rr] = acc[e];
+                    }
                 }
-            }
+            };
+            if (DIRECT)   // gate rows, then up rows
+                gu_rows([&](int rr) { return rr < rh ? srcg : srcu - (size_t)rh * L.gu_row; });
+            else
+                gu_rows([&](int) { return (const uint8_t*)slab_gu; });
             lds_barrier();
             if (!loader)
                 for (int i = lane; i < m * rh; i += 64) {
@@ -567,7 +578,7 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
         const uint8_t* srcd = a.arena + (size_t)s_gexp[g] * (size_t)a.blob + L.down_off + (size_t)j * rd * L.d_row;
         lds_barrier();   // the previous unit's readers of the slab are done
         const bool fetched = dn_early && u2 == d_begin;
-        if (loader && !fetched && !a.direct)
+        if (loader && !fetched && !DIRECT)
             dma_to_lds(slab_dn, n16d, [&](int i) { return (const void*)(srcd + 16 * (size_t)i); });
         const int e0 = s_start[g], e1 = s_start[g + 1];
         for (int p = e0; p < e1; p += NE) {
@@ -620,21 +631,24 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
             }
             __syncthreads();
             const int c = lane & (lpr_d - 1);
-            for (int rr = tid / lpr_d; rr < rd; rr += kFT / lpr_d) {
-                float acc[NE];
+            auto dn_rows = [&](const uint8_t* rb) {   // (the slab or, direct, the blob: as above, two instances)
+                for (int rr = tid / lpr_d; rr < rd; rr += kFT / lpr_d) {
+                    float acc[NE];
 #pragma unroll
-                for (int e = 0; e < NE; ++e) acc[e] = 0.0f;
-                const uint8_t* rb = a.direct ? srcd : slab_dn;
-                for (int u = c; u < F / UD::kUnit; u += lpr_d)
-                    UD::template apply<NE>(rb, rr * (int)L.d_row, u, actd, m, acc);
+                    for (int e = 0; e < NE; ++e) acc[e] = 0.0f;
+                    for (int u = c; u < F / UD::kUnit; u += lpr_d)
+                        UD::template apply<NE>(rb, rr * (int)L.d_row, u, actd, m, acc);
 #pragma unroll
-                for (int e = 0; e < NE; ++e) acc[e] = lanes_sum(acc[e], lpr_d);
-                if (c == 0) {
+                    for (int e = 0; e < NE; ++e) acc[e] = lanes_sum(acc[e], lpr_d);
+                    if (c == 0) {
 #pragma unroll
-                    for (int e = 0; e < NE; ++e)
-                        if (e < m) s_po[e * rd + rr] = acc[e];
+                        for (int e = 0; e < NE; ++e)
+                            if (e < m) s_po[e * rd + rr] = acc[e];
+                    }
                 }
-            }
+            };
+            if (DIRECT) dn_rows(srcd);
+            else dn_rows(slab_dn);
             __syncthreads();
             if (!loader)
                 for (int i = lane; i < m * rd; i += 64) {
@@ -777,10 +791,10 @@ bool fused_decode_plan(const ExpertLayout& L, int n_expert, int k, int n_tok, Fu
 }
 
 template <int TG, int TD>
-static void* pick(int ne) {
-    return ne == 1 ? (void*)moe_decode_fused_kernel<TG, TD, 1>
-         : ne == 2 ? (void*)moe_decode_fused_kernel<TG, TD, 2>
-                   : (void*)moe_decode_fused_kernel<TG, TD, 4>;
+static void* pick(int ne, bool direct) {
+    return ne == 1 ? (direct ? (void*)moe_decode_fused_kernel<TG, TD, 1, true> : (void*)moe_decode_fused_kernel<TG, TD, 1, false>)
+         : ne == 2 ? (void*)moe_decode_fused_kernel<TG, TD, 2, false>
+                   : (void*)moe_decode_fused_kernel<TG, TD, 4, false>;
 }
 
 namespace {
@@ -816,10 +830,11 @@ static hipError_t resident_grid(const void* kern, int lds, int cap, int* grid_ma
 
 hipError_t launch_decode_fused(const FusedArgs& a, const FusedPlan& P, hipStream_t s) {
     void* kern = nullptr;
-    if (a.L.gu_type == kQ4_K && a.L.d_type == kQ6_K) kern = pick<kQ4_K, kQ6_K>(P.ne);
-    else if (a.L.gu_type == kQ8_0) kern = pick<kQ8_0, kQ8_0>(P.ne);
-    else if (a.L.gu_type == kIQ4_XS) kern = pick<kIQ4_XS, kIQ4_XS>(P.ne);
-    else kern = pick<kQ4_K, kQ4_K>(P.ne);
+    const bool direct = P.direct && P.ne == 1;
+    if (a.L.gu_type == kQ4_K && a.L.d_type == kQ6_K) kern = pick<kQ4_K, kQ6_K>(P.ne, direct);
+    else if (a.L.gu_type == kQ8_0) kern = pick<kQ8_0, kQ8_0>(P.ne, direct);
+    else if (a.L.gu_type == kIQ4_XS) kern = pick<kIQ4_XS, kIQ4_XS>(P.ne, direct);
+    else kern = pick<kQ4_K, kQ4_K>(P.ne, direct);
     // every work-group resident at once: the down units wait on the gate/up units of others
     int grid = 0;
     hipError_t e = resident_grid(kern, P.lds, P.direct ? 4 : 2, &grid);
