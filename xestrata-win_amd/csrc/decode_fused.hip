@@ -249,7 +249,7 @@ __device__ __forceinline__ void route_tokens_wave(const FusedArgs& a, int T, int
 // constant and the multi-token planning and the pipelined gate/up path fold away; DIRECT (one token only) is the
 // form without slabs.  Each instance carries only its own paths: the kernel's code is large, and what an instance
 // does not run still costs instruction-cache room.
-template <int TG, int TD, int NE, bool DIRECT>
+template <int TG, int TD, int NE, bool DIRECT, int PER>
 __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];
     using UG = Unit<TG, true>;
@@ -293,17 +293,7 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
         for (int j8 = tid - 64; j8 < H / 8; j8 += kFT - 64)
             q8_1_256_to_act(a.x, j8, q, (float*)(q + H), (int*)(q + H + H / 8));
     }
-    if (E <= 64) {
-        route_tokens_wave<1>(a, T, s_ids, s_w, ctr);
-    } else if (E <= 128) {
-        route_tokens_wave<2>(a, T, s_ids, s_w, ctr);
-    } else if (E <= 256) {
-        route_tokens_wave<4>(a, T, s_ids, s_w, ctr);
-    } else if (E <= 512) {
-        route_tokens_wave<8>(a, T, s_ids, s_w, ctr);
-    } else {
-        route_tokens_wave<16>(a, T, s_ids, s_w, ctr);
-    }
+    route_tokens_wave<PER>(a, T, s_ids, s_w, ctr);   // PER = the experts a lane (64 PER >= E, chosen by the host)
     if (wave == 0) {
         const int epoch = epoch_of(ctr);
         if (lane == 0) s_misc[3] = epoch;
@@ -790,11 +780,22 @@ bool fused_decode_plan(const ExpertLayout& L, int n_expert, int k, int n_tok, Fu
     return P->lds <= 160 * 1024;
 }
 
+template <int TG, int TD, int PER>
+static void* pick_per(int ne, bool direct) {
+    return ne == 1 ? (direct ? (void*)moe_decode_fused_kernel<TG, TD, 1, true, PER>
+                             : (void*)moe_decode_fused_kernel<TG, TD, 1, false, PER>)
+         : ne == 2 ? (void*)moe_decode_fused_kernel<TG, TD, 2, false, PER>
+                   : (void*)moe_decode_fused_kernel<TG, TD, 4, false, PER>;
+}
+// the routing's experts a lane is a template parameter too: an instance holds one routing form, not five (they were
+// two thirds of its code)
 template <int TG, int TD>
-static void* pick(int ne, bool direct) {
-    return ne == 1 ? (direct ? (void*)moe_decode_fused_kernel<TG, TD, 1, true> : (void*)moe_decode_fused_kernel<TG, TD, 1, false>)
-         : ne == 2 ? (void*)moe_decode_fused_kernel<TG, TD, 2, false>
-                   : (void*)moe_decode_fused_kernel<TG, TD, 4, false>;
+static void* pick(int ne, bool direct, int n_expert) {
+    return n_expert <= 64    ? pick_per<TG, TD, 1>(ne, direct)
+         : n_expert <= 128   ? pick_per<TG, TD, 2>(ne, direct)
+         : n_expert <= 256   ? pick_per<TG, TD, 4>(ne, direct)
+         : n_expert <= 512   ? pick_per<TG, TD, 8>(ne, direct)
+                             : pick_per<TG, TD, 16>(ne, direct);
 }
 
 namespace {
@@ -831,10 +832,11 @@ static hipError_t resident_grid(const void* kern, int lds, int cap, int* grid_ma
 hipError_t launch_decode_fused(const FusedArgs& a, const FusedPlan& P, hipStream_t s) {
     void* kern = nullptr;
     const bool direct = P.direct && P.ne == 1;
-    if (a.L.gu_type == kQ4_K && a.L.d_type == kQ6_K) kern = pick<kQ4_K, kQ6_K>(P.ne, direct);
-    else if (a.L.gu_type == kQ8_0) kern = pick<kQ8_0, kQ8_0>(P.ne, direct);
-    else if (a.L.gu_type == kIQ4_XS) kern = pick<kIQ4_XS, kIQ4_XS>(P.ne, direct);
-    else kern = pick<kQ4_K, kQ4_K>(P.ne, direct);
+    const int E = a.n_expert;
+    if (a.L.gu_type == kQ4_K && a.L.d_type == kQ6_K) kern = pick<kQ4_K, kQ6_K>(P.ne, direct, E);
+    else if (a.L.gu_type == kQ8_0) kern = pick<kQ8_0, kQ8_0>(P.ne, direct, E);
+    else if (a.L.gu_type == kIQ4_XS) kern = pick<kIQ4_XS, kIQ4_XS>(P.ne, direct, E);
+    else kern = pick<kQ4_K, kQ4_K>(P.ne, direct, E);
     // every work-group resident at once: the down units wait on the gate/up units of others
     int grid = 0;
     hipError_t e = resident_grid(kern, P.lds, P.direct ? 4 : 2, &grid);
