@@ -246,11 +246,13 @@ __device__ __forceinline__ void route_tokens_wave(const FusedArgs& a, int T, int
 }
 
 // NE = 1 is launched for one token only (the plan's ne: 1 token -> 1, 2-3 -> 2, 4+ -> 4), so T = 1 there is a
-// constant and the multi-token planning and the pipelined gate/up path fold away; DIRECT (one token only) is the
-// form without slabs.  Each instance carries only its own paths: the kernel's code is large, and what an instance
-// does not run still costs instruction-cache room.
-template <int TG, int TD, int NE, bool DIRECT, int PER>
+// constant and the multi-token planning and the pipelined gate/up path fold away; MODE 1 is, for one token, the direct
+// form (no slabs) and, for 4+ tokens, the pipelined gate/up path (its token table in use), each without the other
+// path's code; MODE 0 otherwise.  Each instance carries only its own paths: the kernel's code is large, and what an
+// instance does not run still costs instruction-cache room.
+template <int TG, int TD, int NE, int MODE, int PER>
 __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
+    constexpr bool DIRECT = NE == 1 && MODE == 1;
     extern __shared__ __align__(16) uint8_t lds[];
     using UG = Unit<TG, true>;
     using UD = Unit<TD, false>;
@@ -412,7 +414,7 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
     const bool loader = wave < kLoadWaves;
     // with at most one gate/up unit a work-group, the store wave fetches the work-group's first down rows once the
     // gate/up slab is in: they then land while the gate/up products run and h travels
-    const bool piped = NE == 4 && a.ttab > 0 && T <= a.ttab;   // the pipelined gate/up path below (4..16 tokens)
+    const bool piped = NE == 4 && MODE == 1;   // the pipelined gate/up path below (4..16 tokens, the table in use)
     // down units: with one token and more units than work-groups, a work-group takes a run of consecutive ones
     // (mostly one expert's), so its entry's h is gathered and quantized once for the run rather than once a unit.
     // (With more tokens a unit's cost is its group's entry count, and runs would load the work-groups unevenly: there
@@ -781,21 +783,20 @@ bool fused_decode_plan(const ExpertLayout& L, int n_expert, int k, int n_tok, Fu
 }
 
 template <int TG, int TD, int PER>
-static void* pick_per(int ne, bool direct) {
-    return ne == 1 ? (direct ? (void*)moe_decode_fused_kernel<TG, TD, 1, true, PER>
-                             : (void*)moe_decode_fused_kernel<TG, TD, 1, false, PER>)
-         : ne == 2 ? (void*)moe_decode_fused_kernel<TG, TD, 2, false, PER>
-                   : (void*)moe_decode_fused_kernel<TG, TD, 4, false, PER>;
+static void* pick_per(int ne, int mode) {
+    return ne == 1 ? (mode ? (void*)moe_decode_fused_kernel<TG, TD, 1, 1, PER> : (void*)moe_decode_fused_kernel<TG, TD, 1, 0, PER>)
+         : ne == 2 ? (void*)moe_decode_fused_kernel<TG, TD, 2, 0, PER>
+                   : (mode ? (void*)moe_decode_fused_kernel<TG, TD, 4, 1, PER> : (void*)moe_decode_fused_kernel<TG, TD, 4, 0, PER>);
 }
 // the routing's experts a lane is a template parameter too: an instance holds one routing form, not five (they were
 // two thirds of its code)
 template <int TG, int TD>
-static void* pick(int ne, bool direct, int n_expert) {
-    return n_expert <= 64    ? pick_per<TG, TD, 1>(ne, direct)
-         : n_expert <= 128   ? pick_per<TG, TD, 2>(ne, direct)
-         : n_expert <= 256   ? pick_per<TG, TD, 4>(ne, direct)
-         : n_expert <= 512   ? pick_per<TG, TD, 8>(ne, direct)
-                             : pick_per<TG, TD, 16>(ne, direct);
+static void* pick(int ne, int mode, int n_expert) {
+    return n_expert <= 64    ? pick_per<TG, TD, 1>(ne, mode)
+         : n_expert <= 128   ? pick_per<TG, TD, 2>(ne, mode)
+         : n_expert <= 256   ? pick_per<TG, TD, 4>(ne, mode)
+         : n_expert <= 512   ? pick_per<TG, TD, 8>(ne, mode)
+                             : pick_per<TG, TD, 16>(ne, mode);
 }
 
 namespace {
@@ -831,12 +832,13 @@ static hipError_t resident_grid(const void* kern, int lds, int cap, int* grid_ma
 
 hipError_t launch_decode_fused(const FusedArgs& a, const FusedPlan& P, hipStream_t s) {
     void* kern = nullptr;
-    const bool direct = P.direct && P.ne == 1;
+    // the instance's mode: one token, the direct form; 4+ tokens, the pipelined path when its table takes them all
+    const int mode = P.ne == 1 ? (P.direct ? 1 : 0) : P.ne == 4 ? (P.ttab > 0 && a.n_tok <= P.ttab ? 1 : 0) : 0;
     const int E = a.n_expert;
-    if (a.L.gu_type == kQ4_K && a.L.d_type == kQ6_K) kern = pick<kQ4_K, kQ6_K>(P.ne, direct, E);
-    else if (a.L.gu_type == kQ8_0) kern = pick<kQ8_0, kQ8_0>(P.ne, direct, E);
-    else if (a.L.gu_type == kIQ4_XS) kern = pick<kIQ4_XS, kIQ4_XS>(P.ne, direct, E);
-    else kern = pick<kQ4_K, kQ4_K>(P.ne, direct, E);
+    if (a.L.gu_type == kQ4_K && a.L.d_type == kQ6_K) kern = pick<kQ4_K, kQ6_K>(P.ne, mode, E);
+    else if (a.L.gu_type == kQ8_0) kern = pick<kQ8_0, kQ8_0>(P.ne, mode, E);
+    else if (a.L.gu_type == kIQ4_XS) kern = pick<kIQ4_XS, kIQ4_XS>(P.ne, mode, E);
+    else kern = pick<kQ4_K, kQ4_K>(P.ne, mode, E);
     // every work-group resident at once: the down units wait on the gate/up units of others
     int grid = 0;
     hipError_t e = resident_grid(kern, P.lds, P.direct ? 4 : 2, &grid);
