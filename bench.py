@@ -378,7 +378,7 @@ def main():
         "frac_hbm_peak": round(gbs1 / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm", "achieved": round(roof_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(roof_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "moe_decode_fused_kernel<Q4_K, Q6_K, 1> (xs_moe_layer_decode, one launch a layer)",
+                     "kernel": "moe_decode_fused_kernel<Q4_K, Q6_K, 1, 0, 2> (xs_moe_layer_decode, one launch a layer)",
                      "algorithmic_bytes_per_launch": round(roof_bytes), "avg_launch_us": round(roof_us, 3)},
         "decode_batches": extra,
         "prefill": prefill,
