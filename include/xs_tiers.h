@@ -25,7 +25,7 @@ extern "C" {
 
 /* Spin until *flag >= value (flag: mapped host memory the host writes), then an acquire at system scope so the work
  * after it on the stream sees what the host wrote before the flag.  Bounded: after limit_us microseconds of the
- * device's wall clock (0: 10 s) the wait gives up and, when `status` (device int32) is given, sets *status = 1.
+ * device's wall clock (0: 10 s; at most an hour) the wait gives up and, when `status` (device int32) is given, sets *status = 1.
  * Replaces wait_flag_ge (include/strata/kernels/verify_kernels.hpp:65; src/kernels/xe/verify_kernels.cpp:783-788),
  * which waits without a bound. */
 int xs_wait_flag_ge(const uint32_t* flag, uint32_t value, int64_t limit_us, int32_t* status, void* stream);

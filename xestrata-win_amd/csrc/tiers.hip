@@ -114,7 +114,7 @@ int xs_wait_flag_ge(const uint32_t* flag, uint32_t value, int64_t limit_us, int3
     if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess ||
         khz <= 0)
         khz = 100000;
-    const long long us = limit_us > 0 ? (long long)limit_us : 10000000ll;
+    const long long us = limit_us > 0 ? (limit_us < 3600000000ll ? (long long)limit_us : 3600000000ll) : 10000000ll;
     const long long ticks = us * (long long)khz / 1000;
     hipLaunchKernelGGL(wait_flag_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, flag, value, ticks, status);
     return launched(stream, "wait_flag_ge");
