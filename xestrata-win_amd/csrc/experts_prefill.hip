@@ -21,7 +21,9 @@
 // 16-byte LDS read and a weight fragment is built from two quant words with no shuffles.
 //
 // Work-group: 4 waves over a 128-row x 256-weight-row tile; wave w owns 64 weight rows (two 32-column MFMA tiles)
-// and each lane dequantizes the fragments of its two weight rows in registers, one step ahead of their MFMAs.  The
+// and each lane dequantizes the fragments of its two weight rows in registers, one step ahead of their MFMAs.  Q6_K
+// down weights take a 128-row x 128-weight-row tile, one weight row a lane: a dequantized fragment then feeds four
+// MFMAs (against 64-row tiles' two), which halves the dequantization and the weight loads a product.  The
 // tile's activation rows reach LDS by DMA (global_load_lds_dwordx4, gathered through src for gate/up) into a double
 // buffer, chunk c of row r at slot c ^ (r & 7) (fragment reads of 8 neighbouring rows hit 8 bank groups).  Row tiles
 // of 32 past the group's rows are skipped.  A work-group's m-tile comes from a flat index over every group's
@@ -40,8 +42,12 @@ typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 constexpr int kBN = 256, kBK = 64;
-// row tiles of 32 a work-group: 4 for Q4_K weights, 2 where the weight words take more registers (Q6_K, others)
-__host__ __device__ constexpr int row_tiles(int t) { return t == kQ4_K ? 4 : 2; }
+// weight rows a lane dequantizes: one for Q6_K down weights (their raw words take the registers that a 128-row tile
+// needs), two otherwise (gate/up pairs a gate row with its up row)
+__host__ __device__ constexpr int lane_rows(bool down, int t) { return down && t == kQ6_K ? 1 : 2; }
+// row tiles of 32 a work-group: 4 for Q4_K weights and Q6_K down weights, 2 where the weight words of two rows a lane
+// take more registers (Q6_K gate/up, other formats)
+__host__ __device__ constexpr int row_tiles(bool down, int t) { return t == kQ4_K || (down && t == kQ6_K) ? 4 : 2; }
 
 // slot order inside an octet and octet order inside a step (an involution)
 __host__ __device__ constexpr int perm8(int i) { return (i == 1 || i == 5) ? i + 1 : (i == 2 || i == 6) ? i - 1 : i; }
@@ -286,6 +292,8 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
                                                               const int32_t* __restrict__ mtile, int mt_bound,
                                                               int n_tiles) {
     constexpr int kBM = 32 * RT;
+    constexpr int J = lane_rows(DOWN, T), BN = 128 * J;   // weight rows a lane; weight rows (output columns) a tile
+    static_assert(DOWN || J == 2, "gate/up pairs a gate row with its up row in each lane");
     extern __shared__ __align__(16) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, hf = lane >> 5;
     // work-group b runs on XCD x = b % 8.  With n-tiles a multiple of 8, XCD x takes n-tiles [x n8, x n8 + n8) of
@@ -318,7 +326,7 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
     const int H = (int)L.n_embd, F = (int)L.n_ff;
     const int K = DOWN ? F : H;
     const int nk = K / kBK;
-    const int n0 = nt * (DOWN ? kBN : kBN / 2);
+    const int n0 = nt * (DOWN ? BN : kBN / 2);
     const int wtype = DOWN ? L.d_type : L.gu_type;
     const int64_t wrb = DOWN ? L.d_row : L.gu_row;
 
@@ -340,23 +348,23 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
     auto dma_a = [&](int ks, int buf) {
         dma_rows<RT>(asrc, (size_t)ks * 128, lds + buf * (kBM * 128) + wave * 8 * RT * 128);
     };
-    // B: the lane's two weight rows (tile columns cb[j] + lane % 32); gate/up pairs a gate column with its up column
-    int cb[2];
-    cb[0] = DOWN ? 64 * wave : 32 * wave;
-    cb[1] = DOWN ? 64 * wave + 32 : 128 + 32 * wave;
-    const uint8_t* brow[2];
+    // B: the lane's J weight rows (tile columns cb[j] + lane % 32); gate/up pairs a gate column with its up column
+    int cb[J];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < J; ++j) cb[j] = DOWN ? 32 * J * wave + 32 * j : (j ? 128 + 32 * wave : 32 * wave);
+    const uint8_t* brow[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
         const int col = cb[j] + (lane & 31);
         const int wrow = DOWN ? n0 + col : (col < kBN / 2 ? n0 + col : F + n0 + (col - kBN / 2));
         brow[j] = (const uint8_t*)a.wptr[g] + (DOWN ? L.down_off : 0) + (int64_t)wrow * wrb;
     }
 
-    f32x16_t acc[RT][2];
+    f32x16_t acc[RT][J];
 #pragma unroll
     for (int i = 0; i < RT; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < J; ++j)
 #pragma unroll
             for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.0f;
 
@@ -371,25 +379,25 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
     // straight-line code that the scheduler interleaves with the next fragment's dequantization.
     auto kloop = [&](auto nrt_c) {
         constexpr int NRT = decltype(nrt_c)::value;
-        // fragment kk of step ks: B fragments fb0, fb1 against the live row tiles of the step's A buffer
-        auto mfma_step = [&](int ks, int kk, const f16x8_t& fb0, const f16x8_t& fb1) {
+        // fragment kk of step ks: the B fragments fb[0 .. J) against the live row tiles of the step's A buffer
+        auto mfma_step = [&](int ks, int kk, const f16x8_t (&fb)[J]) {
             const uint4* sA = (const uint4*)(lds + (ks & 1) * (kBM * 128));
             const int ch = 2 * kk + hf;
             f16x8_t fa[NRT];
 #pragma unroll
             for (int i = 0; i < NRT; ++i) fa[i] = __builtin_bit_cast(f16x8_t, sA[swz(32 * i + (lane & 31), ch)]);
 #pragma unroll
-            for (int i = 0; i < NRT; ++i) {
-                acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i], fb0, acc[i][0], 0, 0, 0);
-                acc[i][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i], fb1, acc[i][1], 0, 0, 0);
-            }
+            for (int i = 0; i < NRT; ++i)
+#pragma unroll
+                for (int j = 0; j < J; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i], fb[j], acc[i][j], 0, 0, 0);
         };
         if (T == kQ4_K) {
             dma_a(0, 0);
             const int nb = K / 256;
-            uint4 hdr[2], q[2][2];   // header of the block; the qs run of steps (even, odd)
+            uint4 hdr[J], q[2][J];   // header of the block; the qs run of steps (even, odd)
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
+            for (int j = 0; j < J; ++j) {
                 hdr[j] = ldg16(brow[j]);
                 q[0][j] = ldg16(brow[j] + 16 + 16 * hf);
             }
@@ -399,20 +407,26 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
                     const int ks = 4 * b + p;
                     step_sync();
                     // the step's scales first: at p = 3 the header registers then take the next block's header
-                    const Q4Step s0 = q4k_step(hdr[0], p), s1 = q4k_step(hdr[1], p);
+                    Q4Step sj[J];
+#pragma unroll
+                    for (int j = 0; j < J; ++j) sj[j] = q4k_step(hdr[j], p);
                     if (ks + 1 < nk) {
                         dma_a(ks + 1, (ks + 1) & 1);
                         const int bn = p == 3 ? b + 1 : b;   // the next step's block
 #pragma unroll
-                        for (int j = 0; j < 2; ++j) {
+                        for (int j = 0; j < J; ++j) {
                             const uint8_t* blk = brow[j] + 144 * bn;
                             if (p == 3) hdr[j] = ldg16(blk);
                             q[(p + 1) & 1][j] = ldg16(blk + 16 + 32 * ((p + 1) & 3) + 16 * hf);
                         }
                     }
 #pragma unroll
-                    for (int kk = 0; kk < 4; ++kk)
-                        mfma_step(ks, kk, q4k_frag(q[p & 1][0], kk, s0, qc), q4k_frag(q[p & 1][1], kk, s1, qc));
+                    for (int kk = 0; kk < 4; ++kk) {
+                        f16x8_t fb[J];
+#pragma unroll
+                        for (int j = 0; j < J; ++j) fb[j] = q4k_frag(q[p & 1][j], kk, sj[j], qc);
+                        mfma_step(ks, kk, fb);
+                    }
                 }
             }
         } else if (T == kQ6_K) {
@@ -434,10 +448,10 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
             auto q6loop = [&](auto nbc) {
                 constexpr int NBC = decltype(nbc)::value;
                 const int nb = NBC > 0 ? NBC : K / 256;
-                Q6Raw r[2][2];   // the raw words of halves (even, odd), per row
+                Q6Raw r[2][J];   // the raw words of halves (even, odd), per row
                 load_a(0, 0);
 #pragma unroll
-                for (int j = 0; j < 2; ++j) q6k_load(brow[j], 0, hf, r[0][j]);
+                for (int j = 0; j < J; ++j) q6k_load(brow[j], 0, hf, r[0][j]);
                 load_a(1, 1);
                 store_a(0, 0);
 #pragma unroll
@@ -453,15 +467,16 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
                             if (t == 0 && 2 * b + n + 1 < 2 * nb) {   // the next half's words
                                 const int h1 = 2 * b + n + 1;
 #pragma unroll
-                                for (int j = 0; j < 2; ++j)
+                                for (int j = 0; j < J; ++j)
                                     q6k_load(brow[j] + 210 * (h1 >> 1), h1 & 1, hf, r[n ^ 1][j]);
                             }
 #pragma unroll
                             for (int kk = 0; kk < 4; ++kk) {
-                                const Q6Raw& ra = r[n][0];
-                                const Q6Raw& rb = r[n][1];
-                                mfma_step(ks, kk, q6k_frag(ra, t, kk, q6k_scale(ra, t, kk, hf), qc),
-                                          q6k_frag(rb, t, kk, q6k_scale(rb, t, kk, hf), qc));
+                                f16x8_t fb[J];
+#pragma unroll
+                                for (int j = 0; j < J; ++j)
+                                    fb[j] = q6k_frag(r[n][j], t, kk, q6k_scale(r[n][j], t, kk, hf), qc);
+                                mfma_step(ks, kk, fb);
                             }
                         }
                     }
@@ -475,9 +490,12 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
                 step_sync();
                 if (ks + 1 < nk) dma_a(ks + 1, (ks + 1) & 1);
 #pragma unroll
-                for (int kk = 0; kk < 4; ++kk)
-                    mfma_step(ks, kk, generic_frag(brow[0], wtype, ks * kBK, kk, hf),
-                              generic_frag(brow[1], wtype, ks * kBK, kk, hf));
+                for (int kk = 0; kk < 4; ++kk) {
+                    f16x8_t fb[J];
+#pragma unroll
+                    for (int j = 0; j < J; ++j) fb[j] = generic_frag(brow[j], wtype, ks * kBK, kk, hf);
+                    mfma_step(ks, kk, fb);
+                }
             }
         }
     };
@@ -498,18 +516,18 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
                 const int64_t o = (int64_t)s_entry[row] * H + n0;
                 if (a.parts_h) {
 #pragma unroll
-                    for (int j = 0; j < 2; ++j) {
+                    for (int j = 0; j < J; ++j) {
                         const float v = __builtin_fminf(__builtin_fmaxf(acc[i][j][q], -65504.0f), 65504.0f);
                         a.parts_h[o + cb[j] + (lane & 31)] = f2h(v);
                     }
                 } else {
 #pragma unroll
-                    for (int j = 0; j < 2; ++j) a.parts[o + cb[j] + (lane & 31)] = acc[i][j][q];
+                    for (int j = 0; j < J; ++j) a.parts[o + cb[j] + (lane & 31)] = acc[i][j][q];
                 }
             } else {
                 // SwiGLU on the hardware exp2 and reciprocal (the f16 path's tolerance, not canon's bits), stored in
                 // the step order the down product reads
-                const float gv = acc[i][0][q], uv = acc[i][1][q];
+                const float gv = acc[i][0][q], uv = acc[i][J - 1][q];
                 const float e = __builtin_amdgcn_exp2f(-gv * 1.4426950408889634f);
                 float hv = gv * __builtin_amdgcn_rcpf(1.0f + e) * uv;
                 hv = __builtin_fminf(__builtin_fmaxf(hv, -65504.0f), 65504.0f);
@@ -522,17 +540,17 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
 
 template <bool DOWN>
 static hipError_t launch_gemm(const ExpertLayout& L, const PrefillArgs& a, hipStream_t s) {
-    const int n_tiles = DOWN ? (int)(L.n_embd / kBN) : (int)(L.n_ff / (kBN / 2));
     const int t = DOWN ? L.d_type : L.gu_type;
-    const int bm = 32 * row_tiles(t);
+    const int n_tiles = DOWN ? (int)(L.n_embd / (128 * lane_rows(DOWN, t))) : (int)(L.n_ff / (kBN / 2));
+    const int bm = 32 * row_tiles(DOWN, t);
     const int mt_bound = (int)((a.rows + bm - 1) / bm + a.cap_groups);
     const unsigned grid = (unsigned)(n_tiles % 8 == 0 ? mt_bound * n_tiles : 8 * ((mt_bound + 7) / 8) * n_tiles);
     const size_t lds = (size_t)2 * bm * 128 + (DOWN ? (size_t)bm * 4 : 0);
     const int32_t* mtile = a.mtile + (bm == 128 ? 0 : a.cap_groups + 1);
     void (*k)(ExpertLayout, PrefillArgs, const int32_t*, int, int) =
-        t == kQ4_K   ? grouped_mfma_kernel<DOWN, kQ4_K, row_tiles(kQ4_K)>
-        : t == kQ6_K ? grouped_mfma_kernel<DOWN, kQ6_K, row_tiles(kQ6_K)>
-                     : grouped_mfma_kernel<DOWN, 0, row_tiles(0)>;
+        t == kQ4_K   ? grouped_mfma_kernel<DOWN, kQ4_K, row_tiles(DOWN, kQ4_K)>
+        : t == kQ6_K ? grouped_mfma_kernel<DOWN, kQ6_K, row_tiles(DOWN, kQ6_K)>
+                     : grouped_mfma_kernel<DOWN, 0, row_tiles(DOWN, 0)>;
     hipLaunchKernelGGL(k, dim3(grid), dim3(256), lds, s, L, a, mtile, mt_bound, n_tiles);
     return hipGetLastError();
 }
