@@ -393,33 +393,48 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i], fb[j], acc[i][j], 0, 0, 0);
         };
         if (T == kQ4_K) {
-            dma_a(0, 0);
+            // The A rows of step ks + 1 go through registers (loaded at the start of step ks, written to LDS at its
+            // end), not by LDS DMA: a DMA in flight makes the compiler wait for every load (vmcnt(0)) before the
+            // step's first LDS read, which would serialise each step with its own prefetch.
+            uint4 areg[RT];
+            auto load_a = [&](int ks) {
+#pragma unroll
+                for (int i = 0; i < RT; ++i) areg[i] = ldg16(asrc[i] + (size_t)ks * 128);
+            };
+            auto store_a = [&](int buf) {
+                uint8_t* dst = lds + buf * (kBM * 128) + wave * 8 * RT * 128 + 16 * lane;
+#pragma unroll
+                for (int i = 0; i < RT; ++i) *(uint4*)(dst + i * 1024) = areg[i];
+            };
             const int nb = K / 256;
             uint4 hdr[J], q[2][J];   // header of the block; the qs run of steps (even, odd)
+            load_a(0);
 #pragma unroll
             for (int j = 0; j < J; ++j) {
                 hdr[j] = ldg16(brow[j]);
                 q[0][j] = ldg16(brow[j] + 16 + 16 * hf);
             }
+            store_a(0);
             for (int b = 0; b < nb; ++b) {
 #pragma unroll
                 for (int p = 0; p < 4; ++p) {
                     const int ks = 4 * b + p;
-                    step_sync();
+                    __syncthreads();   // A(ks) is in buffer ks & 1; step ks - 1 is done with the other
                     // the step's scales first: at p = 3 the header registers then take the next block's header
                     Q4Step sj[J];
 #pragma unroll
                     for (int j = 0; j < J; ++j) sj[j] = q4k_step(hdr[j], p);
-                    if (ks + 1 < nk) {
-                        dma_a(ks + 1, (ks + 1) & 1);
-                        const int bn = p == 3 ? b + 1 : b;   // the next step's block
+                    // the next step's loads, with no branch (the last step reloads its own block and A rows): a branch
+                    // around them would make the compiler's waits for the current words wait for these too
+                    load_a(min(ks + 1, nk - 1));
+                    const int bn = min(p == 3 ? b + 1 : b, nb - 1);   // the next step's block
 #pragma unroll
-                        for (int j = 0; j < J; ++j) {
-                            const uint8_t* blk = brow[j] + 144 * bn;
-                            if (p == 3) hdr[j] = ldg16(blk);
-                            q[(p + 1) & 1][j] = ldg16(blk + 16 + 32 * ((p + 1) & 3) + 16 * hf);
-                        }
+                    for (int j = 0; j < J; ++j) {
+                        const uint8_t* blk = brow[j] + 144 * bn;
+                        if (p == 3) hdr[j] = ldg16(blk);
+                        q[(p + 1) & 1][j] = ldg16(blk + 16 + 32 * ((p + 1) & 3) + 16 * hf);
                     }
+                    __builtin_amdgcn_sched_barrier(0);   // the loads stay ahead of the step's products
 #pragma unroll
                     for (int kk = 0; kk < 4; ++kk) {
                         f16x8_t fb[J];
@@ -427,6 +442,7 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
                         for (int j = 0; j < J; ++j) fb[j] = q4k_frag(q[p & 1][j], kk, sj[j], qc);
                         mfma_step(ks, kk, fb);
                     }
+                    store_a((ks + 1) & 1);   // after the last step no one reads it
                 }
             }
         } else if (T == kQ6_K) {
