@@ -181,6 +181,40 @@ def other_configs(torch, xm, dev, gen, steps):
                              sigmoid_router_us=round(ms_r * 1e3, 2))
     log(f"config 5 decode T=1 (+ shared expert): {ms * 1e3:.2f} us/layer, {out['config5_T1']['expert_gbs']} GB/s; "
         f"grouped sigmoid router alone {ms_r * 1e3:.2f} us")
+    # config 5 prefill, 1024 tokens: the routed layer (i.i.d. N(0,1) logits, softmax top-8) and the shared expert's
+    # products over every token (one group of 1024 rows through xs_moe_prefill_experts, Q8_0)
+    Tq = 1024
+    lq = torch.randn(Tq, E, device=dev, generator=gen)
+    xq = torch.randn(Tq, H, device=dev, generator=gen).to(torch.bfloat16).float()
+    rq = torch.randn(Tq, H, device=dev, generator=gen)
+    oq = torch.empty(Tq, H, device=dev)
+    qlayer = xm.MoeLayer(L, arena, E, k, Tq, prefill=True)
+    ms_q = time_steps(torch, [lambda: qlayer(xq, lq, rq, oq)] * 2, 4, 2)
+    i32 = dict(dtype=torch.int32, device=dev)
+    s_src = torch.arange(Tq, **i32)
+    s_bounds = torch.tensor([0, Tq], **i32)
+    s_ng = torch.ones(1, **i32)
+    s_ptr = torch.tensor([sarena[0].data_ptr()], dtype=torch.int64, device=dev)
+    s_scr = torch.empty(xm.moe_prefill_scratch_bytes(Tq, Tq, H, 2048), dtype=torch.uint8, device=dev)
+    s_out = torch.empty(Tq, H, device=dev)
+    ms_s = time_steps(torch, [lambda: xm.moe_prefill_experts(SL, xq, s_src, s_src, s_bounds, s_ng, s_ptr, 1, Tq, s_scr,
+                                                             s_out)] * 2, 4, 2)
+    fr, fs = 6.0 * Tq * k * H * F, 6.0 * Tq * H * 2048
+    tq = (fr + fs) / ((ms_q + ms_s) * 1e-3) / 1e12
+    # ~32 rows an expert: every routed expert's weights are streamed once, so the routed products are bound by HBM
+    # (114 FLOP a weight byte, under the ~310 of the MFMA ridge)
+    bq = distinct_experts(torch, lq[None], k) * L.bytes + SL.bytes
+    out["config5_prefill_T1024"] = dict(us_per_layer=round((ms_q + ms_s) * 1e3, 1), routed_us=round(ms_q * 1e3, 1),
+                                        shared_us=round(ms_s * 1e3, 1), tflops=round(tq, 2),
+                                        frac_mfma_peak=round(tq / BF16_PEAK_TFLOPS, 4),
+                                        gflops_per_layer=round((fr + fs) / 1e9, 1),
+                                        expert_gb=round(bq / 1e9, 3),
+                                        expert_gbs=round(bq / ((ms_q + ms_s) * 1e-3) / 1e9, 1),
+                                        frac_hbm_peak=round(bq / ((ms_q + ms_s) * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                                        bound="hbm (every expert streamed once at ~32 rows an expert)",
+                                        routing="i.i.d. N(0,1) logits, the layer's softmax top-8; the shared row's "
+                                                "add into the output (one [T, H] pass) is not included")
+    log(f"config 5 prefill T={Tq}: routed {ms_q * 1e3:.1f} us + shared {ms_s * 1e3:.1f} us, {tq:.1f} TFLOP/s")
     del arena, sarena
     torch.cuda.empty_cache()
     return out

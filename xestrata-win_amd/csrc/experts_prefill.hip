@@ -45,9 +45,11 @@ constexpr int kBN = 256, kBK = 64;
 // weight rows a lane dequantizes: one for Q6_K down weights (their raw words take the registers that a 128-row tile
 // needs), two otherwise (gate/up pairs a gate row with its up row)
 __host__ __device__ constexpr int lane_rows(bool down, int t) { return down && t == kQ6_K ? 1 : 2; }
-// row tiles of 32 a work-group: 4 for Q4_K weights and Q6_K down weights, 2 where the weight words of two rows a lane
-// take more registers (Q6_K gate/up, other formats)
-__host__ __device__ constexpr int row_tiles(bool down, int t) { return t == kQ4_K || (down && t == kQ6_K) ? 4 : 2; }
+// row tiles of 32 a work-group: 4 for Q4_K and Q8_0 weights and Q6_K down weights, 2 where the weight words of two
+// rows a lane take more registers (Q6_K gate/up, other formats)
+__host__ __device__ constexpr int row_tiles(bool down, int t) {
+    return t == kQ4_K || t == kQ8_0 || (down && t == kQ6_K) ? 4 : 2;
+}
 
 // slot order inside an octet and octet order inside a step (an involution)
 __host__ __device__ constexpr int perm8(int i) { return (i == 1 || i == 5) ? i + 1 : (i == 2 || i == 6) ? i - 1 : i; }
@@ -160,6 +162,7 @@ struct QConst {
     uint32_t nib[2];   // 4-bit code: 0x000F000F, 0x00F000F0
     uint32_t two[2];   // Q6_K 2-bit high part: 0x00300030, 0x03000300
     uint32_t mag[2];   // 0x64006400 (f16 1024), 0x4C004C00 (f16 16)
+    uint32_t byte;     // 8-bit code: 0x00FF00FF
 };
 __device__ __forceinline__ QConst make_qconst() {
     QConst c;
@@ -169,6 +172,7 @@ __device__ __forceinline__ QConst make_qconst() {
     c.two[1] = vreg<0x03000300u>();
     c.mag[0] = vreg<0x64006400u>();
     c.mag[1] = vreg<0x4C004C00u>();
+    c.byte = vreg<0x00FF00FFu>();
     return c;
 }
 
@@ -247,7 +251,23 @@ __device__ __forceinline__ f16x8_t q6k_frag(const Q6Raw& r, int t, int kk, h2_t 
     return __builtin_bit_cast(f16x8_t, make_uint4(w[0], w[1], w[2], w[3]));
 }
 
-// ---------------------------------------------------------------- other formats (Q8_0, IQ4_XS)
+// ---------------------------------------------------------------- Q8_0
+// Step ks (64 values) is blocks 2 ks, 2 ks + 1 of the row; lane hf takes codes 16 hf .. 16 hf + 15 of each (one
+// 16-byte load, 2-byte aligned) and the block's scale.  Fragment kk: block kk / 2, words (0, 1) / (2, 3) for kk % 2.
+// A code q becomes the f16 1152 + q (its byte with the sign bit flipped dropped into 0x6400), q = h - 1152 exactly,
+// and d q is rounded once - the bits of the reference's q * d (dequant.hpp:84-89) taken to f16.
+__device__ __forceinline__ f16x8_t q8_frag(const uint4& Q, int kk, uint32_t dbits, const QConst& qc) {
+    const uint32_t w0 = ((kk & 1) ? Q.z : Q.x) ^ 0x80808080u, w1 = ((kk & 1) ? Q.w : Q.y) ^ 0x80808080u;
+    const uint32_t m = qc.byte, o = qc.mag[0];
+    const uint32_t v[4] = {and_or(w0, m, o), and_or(w0 >> 8, m, o), and_or(w1, m, o), and_or(w1 >> 8, m, o)};
+    const h2_t d = h2((dbits & 0xFFFFu) * 0x10001u);
+    uint32_t r[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = u32((h2(v[i]) + (h2_t){-1152.0f16, -1152.0f16}) * d);
+    return __builtin_bit_cast(f16x8_t, make_uint4(r[0], r[1], r[2], r[3]));
+}
+
+// ---------------------------------------------------------------- other formats (IQ4_XS, and Q8_0 at other K)
 // values [o, o + 8) of the 32-value group g of the block at b, as the reference's host dequantizers give them
 // (dequant.hpp:84-89 Q8_0, 283-299 IQ4_XS)
 __device__ __forceinline__ void dequant8(int type, const uint8_t* b, int g, int o, float (&y)[8]) {
@@ -500,6 +520,55 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
             };
             if (K == 768) q6loop(IntC<3>{});
             else q6loop(IntC<0>{});
+        } else if (T == kQ8_0) {
+            // the Q4_K path's pipeline: A rows and raw words of step ks + 1 loaded at the start of step ks with no
+            // branch, A written to LDS at its end; steps in pairs so the word registers are named statically
+            uint4 areg[RT];
+            auto load_a = [&](int ks) {
+#pragma unroll
+                for (int i = 0; i < RT; ++i) areg[i] = ldg16(asrc[i] + (size_t)ks * 128);
+            };
+            auto store_a = [&](int buf) {
+                uint8_t* dst = lds + buf * (kBM * 128) + wave * 8 * RT * 128 + 16 * lane;
+#pragma unroll
+                for (int i = 0; i < RT; ++i) *(uint4*)(dst + i * 1024) = areg[i];
+            };
+            uint4 qv[2][2][J];       // codes of (step parity, block of the step, row)
+            uint32_t dv[2][2][J];    // their blocks' scales (f16 bits)
+            auto load_w = [&](int ks, auto slot_c) {
+                constexpr int SL = decltype(slot_c)::value;
+#pragma unroll
+                for (int j = 0; j < J; ++j)
+#pragma unroll
+                    for (int bb = 0; bb < 2; ++bb) {
+                        const uint8_t* blk = brow[j] + 34 * (2 * ks + bb);
+                        qv[SL][bb][j] = ldg16(blk + 2 + 16 * hf);
+                        dv[SL][bb][j] = ldg_u16(blk);
+                    }
+            };
+            auto q8_step = [&](int ks, auto slot_c) {
+                constexpr int SL = decltype(slot_c)::value;
+                __syncthreads();   // A(ks) is in buffer ks & 1; step ks - 1 is done with the other
+                const int kn = min(ks + 1, nk - 1);
+                load_a(kn);
+                load_w(kn, IntC<SL ^ 1>{});
+                __builtin_amdgcn_sched_barrier(0);   // the loads stay ahead of the step's products
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk) {
+                    f16x8_t fb[J];
+#pragma unroll
+                    for (int j = 0; j < J; ++j) fb[j] = q8_frag(qv[SL][kk >> 1][j], kk, dv[SL][kk >> 1][j], qc);
+                    mfma_step(ks, kk, fb);
+                }
+                store_a((ks + 1) & 1);   // after the last step no one reads it
+            };
+            load_a(0);
+            load_w(0, IntC<0>{});
+            store_a(0);
+            for (int ks = 0; ks < nk; ks += 2) {   // nk is even (K % 128 == 0 for this instance)
+                q8_step(ks, IntC<0>{});
+                q8_step(ks + 1, IntC<1>{});
+            }
         } else {
             dma_a(0, 0);
             for (int ks = 0; ks < nk; ++ks) {
@@ -558,7 +627,8 @@ template <bool DOWN>
 static hipError_t launch_gemm(const ExpertLayout& L, const PrefillArgs& a, hipStream_t s) {
     const int t = DOWN ? L.d_type : L.gu_type;
     const int n_tiles = DOWN ? (int)(L.n_embd / (128 * lane_rows(DOWN, t))) : (int)(L.n_ff / (kBN / 2));
-    const int bm = 32 * row_tiles(DOWN, t);
+    const bool q8_fast = (DOWN ? L.n_ff : L.n_embd) % 128 == 0;   // Q8_0's own path takes its K steps in pairs
+    const int bm = 32 * row_tiles(DOWN, q8_fast ? t : (t == kQ8_0 ? 0 : t));
     const int mt_bound = (int)((a.rows + bm - 1) / bm + a.cap_groups);
     const unsigned grid = (unsigned)(n_tiles % 8 == 0 ? mt_bound * n_tiles : 8 * ((mt_bound + 7) / 8) * n_tiles);
     const size_t lds = (size_t)2 * bm * 128 + (DOWN ? (size_t)bm * 4 : 0);
@@ -566,6 +636,7 @@ static hipError_t launch_gemm(const ExpertLayout& L, const PrefillArgs& a, hipSt
     void (*k)(ExpertLayout, PrefillArgs, const int32_t*, int, int) =
         t == kQ4_K   ? grouped_mfma_kernel<DOWN, kQ4_K, row_tiles(DOWN, kQ4_K)>
         : t == kQ6_K ? grouped_mfma_kernel<DOWN, kQ6_K, row_tiles(DOWN, kQ6_K)>
+        : t == kQ8_0 && q8_fast ? grouped_mfma_kernel<DOWN, kQ8_0, row_tiles(DOWN, kQ8_0)>
                      : grouped_mfma_kernel<DOWN, 0, row_tiles(DOWN, 0)>;
     hipLaunchKernelGGL(k, dim3(grid), dim3(256), lds, s, L, a, mtile, mt_bound, n_tiles);
     return hipGetLastError();
