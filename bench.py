@@ -30,8 +30,22 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def graph_time(torch, fn, replays):
-    """Capture fn() once in a HIP graph; replay `replays` times between two events; return ms per replay."""
+_FLUSH = []
+
+
+def flush_caches(torch):
+    """Read and write 1 GiB of unrelated memory (4x the 256 MB Infinity Cache): nothing a timed step reads is left
+    in the caches by the untimed runs before it."""
+    if not _FLUSH:
+        _FLUSH.append(torch.empty(1 << 29, dtype=torch.uint8, device="cuda").fill_(1))
+        _FLUSH.append(torch.empty(1 << 29, dtype=torch.uint8, device="cuda"))
+    _FLUSH[1].copy_(_FLUSH[0])
+    _FLUSH[0].copy_(_FLUSH[1])
+
+
+def graph_time(torch, fn, replays, flush=False):
+    """Capture fn() once in a HIP graph; replay `replays` times between two events (after flushing the caches when
+    asked); return ms per replay."""
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
@@ -43,6 +57,9 @@ def graph_time(torch, fn, replays):
         fn()
     g.replay()
     torch.cuda.synchronize()
+    if flush:
+        flush_caches(torch)
+        torch.cuda.synchronize()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     e0.record()
@@ -51,6 +68,16 @@ def graph_time(torch, fn, replays):
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / replays, g
+
+
+def run_graph(torch, calls):
+    """Capture the calls once, in order, as one HIP graph; replay it once between two events on the replay stream;
+    return the elapsed ms (each call's kernels run exactly once in the timed region)."""
+    def fn():
+        for c in calls:
+            c()
+    ms, _ = graph_time(torch, fn, 1, flush=True)
+    return ms
 
 
 TRAFFIC_FILE = ROOT / "profiles" / "moe_decode_fused_config2_traffic.md"
@@ -69,26 +96,27 @@ def read_traffic():
 
 
 def pmc_run(torch, xm, copies):
-    """The workload of a rocprofv3 --pmc pass: 32 config-2 decode layers at T=1 (one launch each, rotating over the
-    HBM copies) and, for calibration, 4 device-to-device copies of 256 MiB."""
+    """The workload of a rocprofv3 --pmc pass: the headline's rotation, one cycle of config-2 decode layers at T=1
+    (8 copies x 16 disjoint expert sets = 128 launches, each reading its 8 experts from HBM) and, for calibration,
+    4 device-to-device copies of 256 MiB."""
     E, H, F, k = 128, 2048, 768, 8
     arena, L = xm.build_arena(E, H, F, xm.Q4_K, xm.Q6_K, seed=0, copies=copies)
     gen = torch.Generator(device="cuda").manual_seed(1)
-    logits = torch.randn(copies, 1, E, device="cuda", generator=gen)
+    n_sets = E // k
+    logits = set_logits(torch, n_sets, 1, E, k, "cuda", gen)
     x = torch.randn(1, H, device="cuda", generator=gen).to(torch.bfloat16).float()
     res = torch.randn(1, H, device="cuda", generator=gen)
     out = torch.empty(1, H, device="cuda")
     layer = xm.MoeLayer(L, arena, E, k, 1)
-    for i in range(32):
-        c = i % copies
-        layer(x, logits[c], res, out, arena=arena[c * E])
+    for i in range(copies * n_sets):
+        c, s = i % copies, (i // copies) % n_sets
+        layer(x, logits[s], res, out, arena=arena[c * E])
     src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda").fill_(1)
     dst = torch.empty_like(src)
     for _ in range(4):
         dst.copy_(src)
     torch.cuda.synchronize()
-    distinct = [len(torch.unique(torch.topk(logits[c, 0], k).indices)) for c in range(copies)]
-    log(f"pmc run: 32 decode layers ({sum(distinct) / copies * L.bytes / 1e6:.2f} MB of expert weights each), "
+    log(f"pmc run: {copies * n_sets} decode layers ({k * L.bytes / 1e6:.2f} MB of expert weights each), "
         f"4 copies of {256 << 20} bytes; status {layer.status()}")
 
 
@@ -263,34 +291,39 @@ def main():
     inputs = {}
 
     def decode_run(T, steps, warmup):
-        """Time `steps` decode layer steps of T tokens (one graph = one step per copy); returns (ms/step, bytes/step,
-        steps timed).  The inputs stay in `inputs[T]` (logits [copies, T, E], x [T, H])."""
-        n_logit_sets = copies
-        logits = torch.randn(n_logit_sets, T, E, device=dev, generator=gen)
+        """Time exactly `steps` decode layer steps of T tokens after `warmup` untimed ones; returns (ms/step,
+        bytes/step).  Steps rotate over (copy, logit set) pairs, copy first, so consecutive steps read other copies
+        and, at T = 1, other experts: one token's 8 experts are the 8 boosted ones of its set (16 disjoint sets cover
+        all 128 experts), so a cycle of 8 copies x 16 sets reads all 3.13 GB once and no step finds its blobs in the
+        256 MB Infinity Cache.  T > 1: i.i.d. N(0,1) logits per set (uniform routing), 8 sets.  The warm-up takes the
+        pairs before the timed ones in the same cycle.  The inputs stay in `inputs[T]` (logits, x)."""
+        if T == 1:
+            n_sets = E // k
+            logits = set_logits(torch, n_sets, T, E, k, dev, gen)
+        else:
+            n_sets = copies
+            logits = torch.randn(n_sets, T, E, device=dev, generator=gen)
         x = torch.randn(T, H, device=dev, generator=gen).to(torch.bfloat16).float()
         res = torch.randn(T, H, device=dev, generator=gen)
-        out = torch.empty(copies, T, H, device=dev)
+        out = torch.empty(T, H, device=dev)
         layer = xm.MoeLayer(L, arena, E, k, T)
         inputs[T] = (logits, x)
-        distinct = []
-        for c in range(copies):
-            ids = torch.topk(logits[c], k, dim=1).indices
-            distinct.append(len(torch.unique(ids)))
+        cycle = [(i % copies, (i // copies) % n_sets) for i in range(copies * n_sets)]
 
-        def one_round():
-            for c in range(copies):
-                layer(x, logits[c], res, out[c], arena=arena[c * E])
+        def calls(first, n):
+            return [(lambda c=c, s=s: layer(x, logits[s], res, out, arena=arena[c * E]))
+                    for c, s in (cycle[(first + i) % len(cycle)] for i in range(n))]
 
-        replays = max(1, math.ceil(steps / copies))
-        wrep = max(1, math.ceil(warmup / copies))
-        graph_time(torch, one_round, wrep)                   # warm-up replays
-        ms, _ = graph_time(torch, one_round, replays)
-        ms_step = ms / copies
-        bytes_step = float(np.mean(distinct)) * blob
-        return ms_step, bytes_step, replays * copies
+        timed = calls(warmup, steps)
+        if warmup:
+            run_graph(torch, calls(0, warmup))
+        ms = run_graph(torch, timed) / steps
+        pairs = [cycle[(warmup + i) % len(cycle)] for i in range(steps)]
+        distinct = [len(torch.unique(torch.topk(logits[s], k, dim=1).indices)) for _, s in pairs]
+        return ms, float(np.mean(distinct)) * blob
 
     # ---------------------------------------------------------------- decode, batch 1 (the value)
-    ms1, bytes1, steps1 = decode_run(1, args.steps, args.warmup)
+    ms1, bytes1 = decode_run(1, args.steps, args.warmup)
     gbs1 = bytes1 / (ms1 * 1e-3) / 1e9
     log(f"decode T=1: {ms1 * 1e3:.2f} us/layer, {gbs1:.0f} GB/s expert weights")
 
@@ -303,12 +336,13 @@ def main():
     roof_gbs = roof_bytes / (roof_us * 1e-6) / 1e9
     traffic = read_traffic()
     log(f"fused decode kernel: {roof_us:.2f} us/launch, {roof_gbs:.0f} GB/s of {roof_bytes / 1e6:.2f} MB"
-        + (f", HBM traffic {traffic / 1e6:.2f} MB/launch (rocprofv3 --pmc)" if traffic else ""))
+        + (f", HBM traffic {traffic / 1e6:.2f} MB/launch (rocprofv3 --pmc, from {TRAFFIC_FILE.name})"
+           if traffic else ""))
 
     # ---------------------------------------------------------------- decode batches 4 and 16, verify 4
     extra = {}
     for T in (4, 16):
-        ms, b, _ = decode_run(T, max(copies, args.steps // 4), copies)
+        ms, b = decode_run(T, max(copies, args.steps // 4), copies)
         extra[f"T{T}"] = dict(us_per_layer=round(ms * 1e3, 2), us_per_token=round(ms * 1e3 / T, 3),
                               tokens_per_s=round(T / (ms * 1e-3), 1), expert_gbs=round(b / (ms * 1e-3) / 1e9, 1),
                               frac_hbm_peak=round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
@@ -394,7 +428,7 @@ def main():
         "value": round(gbs1, 1),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": steps1,
+        "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms1, 5),
         "higher_is_better": True,
@@ -412,6 +446,9 @@ def main():
         "frac_hbm_peak": round(gbs1 / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm", "achieved": round(roof_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(roof_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_source": f"{TRAFFIC_FILE.relative_to(ROOT)}: rocprofv3 --pmc FETCH_SIZE + WRITE_SIZE of "
+                                       "the same rotation (bench.py --pmc-run), scaled by a copy kernel of known size; "
+                                       "read from the committed summary, not measured in this run",
                      "kernel": "moe_decode_fused_kernel<Q4_K, Q6_K, 1, 0, 2> (xs_moe_layer_decode, one launch a layer)",
                      "algorithmic_bytes_per_launch": round(roof_bytes), "avg_launch_us": round(roof_us, 3)},
         "decode_batches": extra,

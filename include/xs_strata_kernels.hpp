@@ -4,6 +4,10 @@
 // src/prefill/plain_prompt.cpp:558-797) build against it unchanged.  A failing call throws
 // strata::core::DeviceError (a HIP error) or std::invalid_argument (geometry, alignment, overlap, a missing stream),
 // as the reference's entry points do.
+//
+// DeviceError is the engine's own class (include/strata/core/device.hpp:66): in an engine build that header is on
+// the include path and is included here.  A translation unit that declares the class itself before this header
+// defines XS_STRATA_HAVE_DEVICE_ERROR; only a build with neither gets the stand-alone definition below.
 #pragma once
 
 #include "xs_moe.h"
@@ -13,11 +17,16 @@
 #include <stdexcept>
 #include <string>
 
+#if __has_include("strata/core/device.hpp")
+#include "strata/core/device.hpp"
+#elif !defined(XS_STRATA_HAVE_DEVICE_ERROR)
 namespace strata::core {
-struct DeviceError : std::runtime_error {   // the reference's include/strata/core/runtime.hpp error type
+class DeviceError : public std::runtime_error {   // stand-alone builds only: the engine's is device.hpp's
+public:
     using std::runtime_error::runtime_error;
 };
 }  // namespace strata::core
+#endif
 
 namespace strata::kernels {
 

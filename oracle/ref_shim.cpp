@@ -5,6 +5,7 @@
 #include "strata/artifact/dequant.hpp"
 #include "strata/kernels/canon_math.hpp"
 
+#include <cmath>
 #include <cstdint>
 
 extern "C" {
@@ -35,9 +36,10 @@ void xsref_canon_silu_mul(const float* g, const float* u, int64_t n, float* h) {
     for (int64_t i = 0; i < n; ++i) h[i] = strata::kernels::canon::silu_mul(g[i], u[i]);
 }
 void xsref_canon_q8(const float* x, int64_t n, float* d, float* id, int8_t* q) {
-    // n values as one block: the scale of their largest magnitude, its inverse, and each value's int8
+    // n values as one block: the scale of their largest magnitude (fmax of fabs, as the kernels reduce it: a
+    // negative zero counts as +0), its inverse, and each value's int8
     float amax = 0.0f;
-    for (int64_t i = 0; i < n; ++i) amax = amax > (x[i] < 0 ? -x[i] : x[i]) ? amax : (x[i] < 0 ? -x[i] : x[i]);
+    for (int64_t i = 0; i < n; ++i) amax = std::fmax(amax, std::fabs(x[i]));
     *d = strata::kernels::canon::q8_scale(amax);
     *id = strata::kernels::canon::q8_inv(*d);
     for (int64_t i = 0; i < n; ++i) q[i] = strata::kernels::canon::q8_value(x[i], *id);

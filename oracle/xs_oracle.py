@@ -86,6 +86,7 @@ def ref():
         R.xsref_canon_exp.argtypes = [P, I64, P]
         R.xsref_canon_rcp.argtypes = [P, I64, P]
         R.xsref_canon_silu_mul.argtypes = [P, P, I64, P]
+        R.xsref_canon_q8.argtypes = [P, I64, P, P, P]
         _ref = R
     return _ref
 

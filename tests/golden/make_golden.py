@@ -67,6 +67,43 @@ def main():
     h = np.empty_like(g)
     R.xsref_canon_silu_mul(xo._a(g), xo._a(u), g.size, xo._a(h))
     out["silu_g"], out["silu_u"], out["silu_h"] = g, u, h
+    # canon q8_scale / q8_inv / q8_value over whole blocks (one scale a block): 256- and 32-value blocks of normal
+    # data at magnitudes from 1e-3 to 1e5, plus the edges - an all-zero block, amax below the 1e-30 inverse cut
+    # (1e-29 and 1e-28 / 127), amax past 65504 * 127 = 8.3e6 (the scale held at 65504 and the values at +-127),
+    # signed zeros, values at exact .5 steps of the scale
+    q8_x, q8_d, q8_id, q8_q, q8_n = [], [], [], [], []
+    def q8_block(v):
+        v = np.ascontiguousarray(v, np.float32)
+        d = np.zeros(1, np.float32)
+        i = np.zeros(1, np.float32)
+        q = np.zeros(v.size, np.int8)
+        R.xsref_canon_q8(xo._a(v), v.size, xo._a(d), xo._a(i), xo._a(q))
+        q8_x.append(v)
+        q8_d.append(d[0])
+        q8_id.append(i[0])
+        q8_q.append(q)
+        q8_n.append(v.size)
+    for n in (256, 32):
+        for mag in (1e-3, 0.02, 1.0, 30.0, 1e5):
+            for _ in range(24):
+                q8_block(rng.standard_normal(n) * mag)
+        q8_block(np.zeros(n))
+        q8_block(np.full(n, -0.0))
+        q8_block(rng.standard_normal(n) * 1e-29)
+        q8_block(np.linspace(-1.27e-28, 1.27e-28, n))
+        big = rng.standard_normal(n) * 1e3
+        big[3] = 9.0e6
+        q8_block(big)
+        big2 = rng.standard_normal(n) * 3e6
+        big2[0] = -2.0e7
+        q8_block(big2)
+        steps = (np.arange(n) - n // 2 + 0.5) * (127.0 / (n // 2 + 0.5))   # values near the .5 rounding edges
+        q8_block(steps)
+    out["q8_n"] = np.array(q8_n, np.int32)
+    out["q8_x"] = np.concatenate(q8_x)
+    out["q8_d"] = np.array(q8_d, np.float32)
+    out["q8_id"] = np.array(q8_id, np.float32)
+    out["q8_q"] = np.concatenate(q8_q)
     np.savez_compressed(HERE / "reference_vectors.npz", **out)
 
     with tempfile.TemporaryDirectory() as tmp:

@@ -1,0 +1,93 @@
+"""The engine-facing C++ header (include/xs_strata_kernels.hpp) compiles where the engine would include it, on the CPU:
+
+- stand-alone (no engine headers on the path: its own DeviceError);
+- in a translation unit that declares the engine's `class strata::core::DeviceError` itself first (the declaration
+  of include/strata/core/device.hpp:66) and says so with XS_STRATA_HAVE_DEVICE_ERROR;
+- beside the reference's real include/strata/core/device.hpp, where the reference tree is present (this container);
+
+and a program built against it links with libxsmoe.so and runs a host-only entry point (no GPU call)."""
+import pathlib
+import shutil
+import subprocess
+
+import pytest
+
+ROOT = pathlib.Path(__file__).resolve().parent.parent
+REF_INCLUDE = pathlib.Path("/root/reference/include")
+CXX = shutil.which("g++")
+
+USE = r"""
+#include "xs_strata_kernels.hpp"
+#include <cstdio>
+int main() {
+    namespace k = strata::kernels;
+    const k::NativeExpertLayout L = k::native_expert_layout(12, 14, 2048, 768);
+    std::printf("%zu %d\n", L.bytes, (int)k::native_expert_supported(12, 14, 2048, 768));
+    try {
+        k::native_expert_layout(12, 14, 2000, 768);
+    } catch (const std::invalid_argument&) {
+        std::printf("invalid\n");
+    }
+    try {
+        throw strata::core::DeviceError("device");
+    } catch (const std::runtime_error& e) {
+        std::printf("%s\n", e.what());
+    }
+    return 0;
+}
+"""
+
+ENGINE_DECL = r"""
+#include <stdexcept>
+namespace strata::core {
+class DeviceError : public std::runtime_error {
+public:
+    using std::runtime_error::runtime_error;
+};
+}  // namespace strata::core
+#define XS_STRATA_HAVE_DEVICE_ERROR 1
+"""
+
+ENGINE_HEADER = r"""
+#include "strata/core/device.hpp"
+"""
+
+pytestmark = pytest.mark.skipif(CXX is None, reason="g++ is not installed")
+
+
+def compile_only(tmp_path, prefix, extra=()):
+    src = tmp_path / "tu.cpp"
+    src.write_text(prefix + USE)
+    r = subprocess.run([CXX, "-std=c++17", "-fsyntax-only", "-Wall", "-Werror", "-I", str(ROOT / "include"), *extra,
+                        str(src)], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+
+
+def test_header_stand_alone(tmp_path):
+    compile_only(tmp_path, "")
+
+
+def test_header_after_engine_declaration(tmp_path):
+    compile_only(tmp_path, ENGINE_DECL)
+
+
+def test_header_beside_engine_device_hpp(tmp_path):
+    if not (REF_INCLUDE / "strata" / "core" / "device.hpp").exists():
+        pytest.skip("the reference tree is not present here")
+    compile_only(tmp_path, ENGINE_HEADER, ["-std=c++20", "-I", str(REF_INCLUDE)])
+    compile_only(tmp_path, "", ["-std=c++20", "-I", str(REF_INCLUDE)])   # device.hpp found by __has_include
+
+
+def test_links_and_runs_host_entry_points(tmp_path):
+    lib = ROOT / "xestrata-win_amd" / "libxsmoe.so"
+    if not lib.exists():
+        pytest.skip("libxsmoe.so is not built")
+    src = tmp_path / "prog.cpp"
+    src.write_text(USE)
+    exe = tmp_path / "prog"
+    r = subprocess.run([CXX, "-std=c++17", "-I", str(ROOT / "include"), str(src), "-o", str(exe), str(lib),
+                        f"-Wl,-rpath,{lib.parent}"], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    assert out.returncode == 0, out.stderr
+    assert out.stdout.split() == ["3059712", "1", "invalid", "device"]

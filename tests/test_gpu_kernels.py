@@ -52,6 +52,25 @@ def test_quantize_q8_1_rows(xm, xo, rows, cols):
     assert np.array_equal(got, want)
 
 
+@pytest.mark.parametrize("n", [256, 32])
+def test_quantize_q8_1_reference_canon_vectors(xm, xo, golden, n):
+    """q8_1 on the GPU against the reference's own canon q8_scale / q8_inv / q8_value (compiled from canon_math.hpp
+    into tests/golden/reference_vectors.npz): each n-value block as one row; codes bit for bit, the stored scale the
+    reference's d rounded to fp16 - including amax = 0, amax under the 1e-30 inverse cut, d held at 65504.  The block
+    sums equal the oracle's (whose sums are pinned in closed form, tests/test_oracle.py)."""
+    ref, _ = golden
+    sizes = ref["q8_n"]
+    at = np.concatenate([[0], np.cumsum(sizes)])
+    sel = np.flatnonzero(sizes == n)
+    x = np.stack([ref["q8_x"][at[b]:at[b + 1]] for b in sel])
+    got = t2n(xm.quantize_q8_1_rows(torch.from_numpy(x).to(DEV)))
+    q, d, _ = xo.q8_1_values(got)
+    assert np.array_equal(q.reshape(len(sel), n), np.stack([ref["q8_q"][at[b]:at[b + 1]] for b in sel]))
+    want_d = np.repeat(ref["q8_d"][sel], n // 32).astype(np.float16)
+    assert np.array_equal(d.astype(np.float16).view(np.uint16), want_d.view(np.uint16))
+    assert np.array_equal(got, xo.quantize_q8_1_rows(x))
+
+
 def router_cases(golden):
     _, seeded = golden
     return seeded["router_cases"]

@@ -265,6 +265,79 @@ def test_q8_1_contract(xo, cols):
     assert np.allclose(s, x.reshape(-1, 32).sum(1).astype(np.float16).astype(np.float32), rtol=2e-3, atol=1e-3)
 
 
+def _q8_blocks(golden):
+    """The reference's canon q8 vectors (oracle/_ref's xsref_canon_q8 over canon_math.hpp:94-108): per block its
+    values, scale d, inverse id and int8 codes."""
+    ref, _ = golden
+    n = ref["q8_n"]
+    at = np.concatenate([[0], np.cumsum(n)])
+    for b in range(n.size):
+        yield ref["q8_x"][at[b]:at[b + 1]], ref["q8_d"][b], ref["q8_id"][b], ref["q8_q"][at[b]:at[b + 1]]
+
+
+def test_q8_1_matches_reference_canon_vectors(xo, golden):
+    """The oracle's q8_1 blocks against the reference's own q8_scale / q8_inv / q8_value (compiled from
+    canon_math.hpp): a 256-value block is one row of 256 (one scale a 256, iq_kernels.cpp:1850-1879), a 32-value block
+    one row of 32 (per-32, :1209-1223).  Codes bit for bit; the stored scale is the reference's d rounded to fp16
+    (make_half2, RNE), including d held at 65504 past amax = 8.3e6 and the blocks below the 1e-30 inverse cut."""
+    seen = {"zero": 0, "clamped": 0, "tiny": 0}
+    for x, d, _id, q in _q8_blocks(golden):
+        y = xo.quantize_q8_1_rows(x.reshape(1, -1))
+        qq, dd, _ = xo.q8_1_values(y)
+        assert np.array_equal(qq.ravel(), q), (x.size, d)
+        assert np.array_equal(dd.astype(np.float16).view(np.uint16),
+                              np.full(x.size // 32, d, np.float32).astype(np.float16).view(np.uint16))
+        seen["zero"] += d == 0
+        seen["clamped"] += d == 65504.0
+        seen["tiny"] += 0 < d < 1e-29
+    assert seen["zero"] >= 4 and seen["clamped"] >= 4 and seen["tiny"] >= 2, seen
+
+
+def test_q8_1_matches_reference_live(xo):
+    """The same against oracle/_ref directly, on fresh blocks (this container only: skipped where the reference tree
+    was not compiled)."""
+    R = xo.ref()
+    if R is None:
+        pytest.skip("oracle/_ref is not built here")
+    rng = np.random.default_rng(77)
+    for n in (256, 32):
+        for _ in range(200):
+            x = (rng.standard_normal(n) * np.exp(rng.uniform(-8, 16))).astype(np.float32)
+            d, i, q = np.zeros(1, np.float32), np.zeros(1, np.float32), np.zeros(n, np.int8)
+            R.xsref_canon_q8(xo._a(x), n, xo._a(d), xo._a(i), xo._a(q))
+            qq, dd, _ = xo.q8_1_values(xo.quantize_q8_1_rows(x.reshape(1, -1)))
+            assert np.array_equal(qq.ravel(), q)
+            assert np.array_equal(dd, np.full(n // 32, d[0], np.float32).astype(np.float16).astype(np.float32))
+
+
+@pytest.mark.parametrize("cols", [256, 32])
+def test_q8_1_block_sum_closed_form(xo, cols):
+    """The fp16 sum of each block's 32 raw values (block_q8_1's s, the K-quants' min term), on values whose partial
+    sums are all exact in fp32 (multiples of 1/64 below 2^17), so that every summation order gives the exact sum: the
+    stored s must be that sum rounded to fp16 - and, past the largest finite half, held at +-65504 rather than inf
+    (q8_1_finite, src/kernels/xe/q8_1_finite.hpp:24).  A NaN-free block stays finite."""
+    rng = np.random.default_rng(cols + 5)
+    rows = []
+    for scale in (1.0, 40.0, 2000.0, 4000.0):                      # sums from ~10 to ~1e5
+        rows.append(np.round(rng.standard_normal(cols) * scale * 64) / 64)
+    rows.append(np.full(cols, 3000.0))                              # 96000 a block: held at 65504
+    rows.append(np.full(cols, -3000.0))
+    r = np.full(cols, 2047.0)
+    r[::32] = 2047.0 + 65504.0 - 32 * 2047.0 + 8.0                  # 65512: rounds to 65504 as a half anyway
+    rows.append(r)
+    r = np.zeros(cols)
+    r[::32] = 65519.0                                               # 65519: below the half rounding edge 65520
+    rows.append(r)
+    x = np.stack(rows).astype(np.float32)
+    exact = x.astype(np.float64).reshape(-1, 32).sum(1)
+    assert np.all(np.abs(x) < 2 ** 17) and np.all(np.abs(exact) < 2 ** 17)   # every partial sum exact
+    _, _, s = xo.q8_1_values(xo.quantize_q8_1_rows(x))
+    want = np.where(np.abs(exact) > 65504.0, np.sign(exact) * 65504.0, exact).astype(np.float16).astype(np.float32)
+    assert np.isfinite(s).all()
+    assert np.array_equal(s, want), np.flatnonzero(s != want)[:8]
+    assert (np.abs(s) == 65504.0).sum() >= 3 * (cols // 32)
+
+
 # ------------------------------------------------------------------------------------------------ row dots
 
 def random_rows(xo, t, rows, n, rng):

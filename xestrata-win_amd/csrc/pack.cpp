@@ -20,6 +20,8 @@
 
 #include <algorithm>
 #include <atomic>
+#include <cctype>
+#include <charconv>
 #include <chrono>
 #include <cstdio>
 #include <cstdlib>
@@ -31,6 +33,7 @@
 #include <set>
 #include <sstream>
 #include <string>
+#include <string_view>
 #include <thread>
 #include <vector>
 
@@ -475,7 +478,146 @@ int load(const xs_pack* P, const char* native_shard, uint8_t* const* layer_dst, 
     return XS_OK;
 }
 
-bool parse_u64(std::istringstream& ss, unsigned long long& v) { return (bool)(ss >> v); }
+// ---- native_experts.txt
+//
+// The file is lines of whitespace-separated fields.  A line starting with '#' is a comment; a comment can carry the
+// format's version tag (upstream Strata's "# strata native experts vN", N = 2..4, or XeStrata's "# xestrata native
+// experts xsN", N = 1, read as 4) and "(n_expert N" (the pack's expert count, which wins over the caller's: a pruned
+// model ships fewer).  Every other non-empty line is one MoE layer: layer, gate/up type, down type, arena offset, blob
+// bytes, then optionally the three tensors' absolute GGUF offsets (gate, up, down) and a shard column.  The reader
+// first turns the text into header facts and rows (read_manifest), then checks the rows against the geometry and
+// lays them into the table (xs_pack_layout_load).
+
+struct VersionTag {
+    const char* prefix;   // the comment's text up to the number
+    const char* label;    // how a refused version is named ("v5", "xs2")
+    int newest;           // the newest number this reader takes
+    bool upstream;        // the number is the version itself (else it reads as 4)
+};
+constexpr VersionTag kVersionTags[] = {
+    {"# strata native experts v", "v", 4, true},
+    {"# xestrata native experts xs", "xs", 1, false},
+};
+
+struct ManifestRow {
+    std::string text;               // the line, for messages
+    int64_t layer = -1;
+    int64_t gu = -1, d = -1;
+    uint64_t offset = 0, blob = 0;
+    bool has_gguf = false;
+    uint64_t gguf_off[3] = {0, 0, 0};
+    std::vector<std::string> shards;   // the shard column's fields as written (empty: no column)
+};
+
+struct Manifest {
+    int version = 0;
+    int64_t n_expert = 0;           // 0: no header gave it
+    std::vector<ManifestRow> rows;
+};
+
+std::vector<std::string_view> fields_of(std::string_view line) {
+    std::vector<std::string_view> f;
+    size_t i = 0;
+    while (i < line.size()) {
+        while (i < line.size() && std::isspace((unsigned char)line[i])) ++i;
+        size_t j = i;
+        while (j < line.size() && !std::isspace((unsigned char)line[j])) ++j;
+        if (j > i) f.push_back(line.substr(i, j - i));
+        i = j;
+    }
+    return f;
+}
+
+template <typename T>
+bool number_of(std::string_view s, T& v) {
+    const char* end = s.data() + s.size();
+    const auto r = std::from_chars(s.data(), end, v);
+    return r.ec == std::errc() && r.ptr == end;
+}
+
+// a comment line's facts: the version tag (an error for a version past what this reader takes) and n_expert
+bool read_comment(std::string_view line, Manifest& m, std::string& err) {
+    for (const VersionTag& t : kVersionTags) {
+        const std::string_view prefix(t.prefix);
+        if (line.substr(0, prefix.size()) != prefix) continue;
+        const std::string digits(line.substr(prefix.size()));
+        const int n = (int)std::strtol(digits.c_str(), nullptr, 10);
+        if (n > t.newest) {
+            err = std::string("native_experts.txt is ") + t.label + std::to_string(n) + ", newer than this reader "
+                  "knows (it takes upstream Strata's v2-v4 and XeStrata's xs1)";
+            return false;
+        }
+        m.version = t.upstream ? n : 4;
+    }
+    static constexpr std::string_view kCount = "(n_expert ";
+    const size_t at = line.find(kCount);
+    if (at != std::string_view::npos) {
+        m.n_expert = std::atoll(std::string(line.substr(at + kCount.size())).c_str());
+        if (m.n_expert <= 0) {
+            err = "native_experts.txt: a header with no experts: " + std::string(line);
+            return false;
+        }
+    }
+    return true;
+}
+
+// one layer line: five numbers, then either the three GGUF offsets and the shard column or nothing this reader uses
+bool read_row(std::string_view line, ManifestRow& r, std::string& err) {
+    const std::vector<std::string_view> f = fields_of(line);
+    r.text = std::string(line);
+    if (f.size() < 5 || !number_of(f[0], r.layer) || !number_of(f[1], r.gu) || !number_of(f[2], r.d) ||
+        !number_of(f[3], r.offset) || !number_of(f[4], r.blob)) {
+        err = "native_experts.txt: a malformed line: " + r.text;
+        return false;
+    }
+    r.has_gguf = f.size() >= 8 && number_of(f[5], r.gguf_off[0]) && number_of(f[6], r.gguf_off[1]) &&
+                 number_of(f[7], r.gguf_off[2]);
+    if (r.has_gguf)
+        for (size_t i = 8; i < f.size(); ++i) r.shards.emplace_back(f[i]);
+    return true;
+}
+
+bool read_manifest(std::istream& in, Manifest& m, std::string& err) {
+    for (std::string line; std::getline(in, line);) {
+        std::string_view v(line);
+        if (!v.empty() && v.back() == '\r') v.remove_suffix(1);
+        if (v.empty()) continue;
+        if (v.front() == '#') {
+            if (!read_comment(v, m, err)) return false;
+            continue;
+        }
+        m.rows.emplace_back();
+        if (!read_row(v, m.rows.back(), err)) return false;
+    }
+    return true;
+}
+
+// The shard column as three file names (gate, up, down; "" = the native shard).  Written as one name for all three
+// roles, as "gate,up,down" in one field (an empty field: the native shard), or as three fields ("-": the native
+// shard).  No column: no names.
+bool shard_names(const ManifestRow& r, std::vector<std::string>& names, std::string& err) {
+    names.clear();
+    if (r.shards.empty()) return true;
+    std::vector<std::string> parts = r.shards;
+    if (parts.size() == 1 && parts[0].find(',') != std::string::npos) {
+        std::vector<std::string> split(1);
+        for (const char c : parts[0]) {
+            if (c == ',') split.emplace_back();
+            else split.back() += c;
+        }
+        parts = std::move(split);
+    }
+    if (parts.size() == 1) parts = {parts[0], parts[0], parts[0]};
+    if (parts.size() != 3) {
+        err = "native_experts.txt: layer " + std::to_string(r.layer) + ": the shard column must be one name, "
+              "gate,up,down or three names, not: " + r.text;
+        return false;
+    }
+    for (std::string& s : parts)
+        if (s == "-") s.clear();
+    names = std::move(parts);
+    return true;
+}
 
 }  // namespace
 
@@ -492,85 +634,53 @@ int xs_pack_layout_load(const char* pack_dir, int64_t n_layers, int64_t n_expert
     if (!in)
         return fail(XS_EINVAL, "pack layout: " + path + " is missing: not a native pack (the Strata Q2_0 expert form "
                                "is not a format these kernels read)");
+    Manifest m;
+    std::string err;
+    if (!read_manifest(in, m, err)) return fail(XS_EINVAL, err);
+
     auto P = std::make_unique<xs_pack>();
+    P->version = m.version;
     P->n_layers = n_layers;
-    P->n_expert = n_expert;
+    P->n_expert = m.n_expert > 0 ? m.n_expert : n_expert;
     P->n_embd = n_embd;
     P->n_ff = n_ff;
     P->layer.assign((size_t)n_layers, xs_pack::Layer{});
-    std::string line;
-    static const char up_tag[] = "# strata native experts v", xs_tag[] = "# xestrata native experts xs";
-    while (std::getline(in, line)) {
-        if (!line.empty() && line.back() == '\r') line.pop_back();
-        if (line.empty()) continue;
-        if (line[0] == '#') {
-            const bool up = line.compare(0, sizeof up_tag - 1, up_tag) == 0;
-            const bool xs = line.compare(0, sizeof xs_tag - 1, xs_tag) == 0;
-            if (up || xs) {
-                const int v = (int)std::strtol(line.c_str() + (up ? sizeof up_tag : sizeof xs_tag) - 1, nullptr, 10);
-                P->version = up ? v : 4;
-                if (v > (up ? 4 : 1))
-                    return fail(XS_EINVAL, std::string("native_experts.txt is ") + (up ? "v" : "xs") +
-                                               std::to_string(v) + "; this reader takes upstream's v2-v4 and "
-                                               "XeStrata's xs1");
-            }
-            const size_t at = line.find("(n_expert ");
-            if (at != std::string::npos) P->n_expert = std::atoll(line.c_str() + at + 10);   // the header wins
-            if (P->n_expert <= 0) return fail(XS_EINVAL, "native_experts.txt: a header with no experts: " + line);
-            continue;
-        }
-        std::istringstream ss(line);
-        long long l = -1, gt = -1, dt = -1;
-        unsigned long long off = 0, blob = 0, go = 0, uo = 0, dox = 0;
-        if (!(ss >> l >> gt >> dt >> off >> blob) || l < 0 || l >= n_layers)
-            return fail(XS_EINVAL, "native_experts.txt: a malformed line: " + line);
-        xs_pack::Layer& L = P->layer[(size_t)l];
-        std::string err;
-        if (!blob_format((int)gt, (int)dt, (int)gt, n_embd, n_ff, L, err))
-            return fail(XS_EINVAL, "native_experts.txt: layer " + std::to_string(l) + ": " + err);
-        if (L.bytes != blob)
-            return fail(XS_EINVAL, "native_experts.txt: layer " + std::to_string(l) + " blob is " +
-                                       std::to_string(blob) + " B but its formats make " + std::to_string(L.bytes));
-        if (parse_u64(ss, go) && parse_u64(ss, uo) && parse_u64(ss, dox)) {   // v2 and later: the GGUF offsets
+    std::vector<char> seen((size_t)n_layers, 0);
+    for (const ManifestRow& r : m.rows) {
+        if (r.layer < 0 || r.layer >= n_layers)
+            return fail(XS_EINVAL, "native_experts.txt: a malformed line (layer out of range): " + r.text);
+        const std::string which = "native_experts.txt: layer " + std::to_string(r.layer);
+        if (seen[(size_t)r.layer]++) return fail(XS_EINVAL, which + " is listed twice");
+        xs_pack::Layer& L = P->layer[(size_t)r.layer];
+        if (!blob_format((int)r.gu, (int)r.d, (int)r.gu, n_embd, n_ff, L, err))
+            return fail(XS_EINVAL, which + ": " + err);
+        if (L.bytes != r.blob)
+            return fail(XS_EINVAL, which + " says " + std::to_string(r.blob) + " B a blob, but its formats make " +
+                                       std::to_string(L.bytes));
+        std::vector<std::string> names;
+        if (!shard_names(r, names, err)) return fail(XS_EINVAL, err);
+        if (r.has_gguf) {
             if (P->gguf_off.empty()) P->gguf_off.assign((size_t)(3 * n_layers), 0);
-            P->gguf_off[(size_t)(3 * l)] = go;
-            P->gguf_off[(size_t)(3 * l + 1)] = uo;
-            P->gguf_off[(size_t)(3 * l + 2)] = dox;
-            std::vector<std::string> files;
-            for (std::string f; ss >> f;) files.push_back(f);
-            if (files.size() == 1 && files[0].find(',') != std::string::npos) {
-                const std::string col = files[0];
-                files.clear();
-                size_t from = 0;
-                for (;;) {
-                    const size_t comma = col.find(',', from);
-                    files.push_back(col.substr(from, comma == std::string::npos ? std::string::npos : comma - from));
-                    if (comma == std::string::npos) break;
-                    from = comma + 1;
-                }
-            }
-            for (auto& f : files)
-                if (f == "-") f.clear();
-            if (files.size() == 1) files.assign(3, std::string(files[0]));
-            if (!files.empty() && files.size() != 3)
-                return fail(XS_EINVAL, "native_experts.txt: layer " + std::to_string(l) +
-                                           ": the shard column is one name, gate,up,down or three names, not: " + line);
-            if (!files.empty()) {
-                if (P->gguf_file.empty()) P->gguf_file.assign((size_t)(3 * n_layers), std::string());
-                for (int r = 0; r < 3; ++r) P->gguf_file[(size_t)(3 * l + r)] = files[(size_t)r];
-            }
+            std::copy(r.gguf_off, r.gguf_off + 3, P->gguf_off.begin() + 3 * r.layer);
         }
-        L.block = l;
-        L.offset = off;
-        P->max_blob = std::max<uint64_t>(P->max_blob, blob);
+        if (!names.empty()) {
+            if (P->gguf_file.empty()) P->gguf_file.assign((size_t)(3 * n_layers), std::string());
+            std::copy(names.begin(), names.end(), P->gguf_file.begin() + 3 * r.layer);
+        }
+        L.block = r.layer;
+        L.offset = r.offset;
+        P->max_blob = std::max<uint64_t>(P->max_blob, r.blob);
     }
-    uint64_t at = 0;
+    // the layers tile the arena from offset 0 in order, each n_expert blobs long
+    uint64_t next = 0;
     for (int64_t l = 0; l < n_layers; ++l) {
-        if (P->layer[(size_t)l].offset != at)
-            return fail(XS_EINVAL, "native_experts.txt: layer " + std::to_string(l) + " is missing or not contiguous");
-        at += P->layer[(size_t)l].bytes * (uint64_t)P->n_expert;
+        const xs_pack::Layer& L = P->layer[(size_t)l];
+        if (!seen[(size_t)l] || L.offset != next)
+            return fail(XS_EINVAL, "native_experts.txt: layer " + std::to_string(l) + " is missing or not contiguous "
+                                   "(expected at arena offset " + std::to_string(next) + ")");
+        next += L.bytes * (uint64_t)P->n_expert;
     }
-    P->total = at;
+    P->total = next;
     *out = P.release();
     return XS_OK;
 }
