@@ -182,6 +182,20 @@ size_t xs_moe_layer_decode_workspace_bytes(const xs_expert_layout_t* L, int n_ex
  * counterpart in the reference (its layer reports through host-side checks of each launch). */
 int32_t* xs_moe_layer_decode_status(void* workspace);
 
+/* xs_moe_layer_decode without a caller workspace, for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  No counterpart in the reference.  The layer
+ * runs in the library's own scratch: a fixed XS_NOALLOC_SCRATCH_BYTES array in device memory that each GPU holds
+ * from the library's load until the process ends, zero at load and left ready by every call.  Takes hidden sizes up to
+ * 8192 and expert widths up to 4096; a call whose tokens x top-k need more scratch than the array holds fails with
+ * XS_EINVAL.  status (optional, device int32): where the persistent layer ORs its error bits (those of
+ * xs_moe_layer_decode_status; the caller clears it).  Every call on a GPU shares that GPU's array: calls that overlap
+ * on one GPU (other streams, other threads) race, so a caller runs them one at a time.  The first call on each device
+ * looks the array's address up and must not be inside a graph capture.  Allocates nothing. */
+#define XS_NOALLOC_SCRATCH_BYTES ((size_t)48 << 20)
+int xs_moe_layer_decode_noalloc(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_bytes, int n_expert,
+                                int k, const float* x, const float* logits, const float* residual, float* out,
+                                int n_tok, int32_t* status, void* stream);
+
 /* A shared expert over a decode / verify window: every token through one dense expert in the native format (blob:
  * [gate rows | up rows | down rows] of layout SL, 16-byte aligned), shared[t] = down(SwiGLU(gate x_t, up x_t)) on q8_1
  * activations, canonical rows as the routed experts; with w_gate ([n_embd] fp32), gate_logit[t] = w_gate . x_t (the

@@ -502,16 +502,22 @@ bool fused_possible(const xs_expert_layout_t* L, int n_expert, int k) {
     xs::FusedPlan P;
     return xs::fused_decode_plan(to_layout(L), n_expert, k, 1, &P);
 }
-DecodeWs decode_ws(const xs_expert_layout_t* L, int n_expert, int k, int n_tok, uint8_t* base) {
+// fixed_tagged: the tagged words take the regions of the largest layout (xs::kScratchMaxFF, xs::kScratchMaxEmbd) at
+// the same offsets for every layout, so that a workspace shared by calls of different layouts (the library's own
+// scratch) has nothing but tagged words in those regions
+DecodeWs decode_ws(const xs_expert_layout_t* L, int n_expert, int k, int n_tok, uint8_t* base,
+                   bool fixed_tagged = false) {
     DecodeWs d;
     const long long capx = (long long)n_tok * k;
     size_t off = 0;
     auto take = [&](size_t b) { uint8_t* p = base ? base + off : nullptr; off += up256(b); return p; };
     d.status = (int32_t*)take(4096);
     d.sync = d.status ? d.status + 32 : nullptr;
-    const bool fused = fused_possible(L, n_expert, k);
-    d.hx = (unsigned long long*)take(fused ? (size_t)256 * (size_t)L->n_ff * 8 : 0);
-    d.px = (unsigned long long*)take(fused ? (size_t)256 * (size_t)L->n_embd * 8 : 0);
+    const bool fused = fixed_tagged || fused_possible(L, n_expert, k);
+    const int64_t hx_ff = fixed_tagged ? xs::kScratchMaxFF : L->n_ff;
+    const int64_t px_embd = fixed_tagged ? xs::kScratchMaxEmbd : L->n_embd;
+    d.hx = (unsigned long long*)take(fused ? (size_t)256 * (size_t)hx_ff * 8 : 0);
+    d.px = (unsigned long long*)take(fused ? (size_t)256 * (size_t)px_embd * 8 : 0);
     d.ids = (int32_t*)take((size_t)capx * 4);
     d.w = (float*)take((size_t)capx * 4);
     d.plan = (int32_t*)take(plan_words(capx) * 4);
@@ -564,17 +570,22 @@ size_t xs_moe_layer_decode_workspace_bytes(const xs_expert_layout_t* L, int n_ex
 }
 
 namespace {
+// status: where the persistent layer's error bits go (NULL: the workspace's status word); fixed_tagged: decode_ws's
 int layer_decode(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_bytes, int n_expert, int k,
                  const float* x, const float* logits, const float* residual, float* out, int n_tok, void* workspace,
-                 size_t workspace_bytes, const float* shared, const float* shared_gate, void* stream) {
+                 size_t workspace_bytes, const float* shared, const float* shared_gate, void* stream,
+                 int32_t* status = nullptr, bool fixed_tagged = false) {
     if (n_tok <= 0) return ok();
     if (int r = check_layout(L, "moe_layer_decode")) return r;
     if (n_tok * k > 1024) return fail(XS_EINVAL, "moe_layer_decode: %d tokens x top-%d is past 1024 entries", n_tok, k);
     if (blob_bytes < L->bytes || blob_bytes % 16 || !aligned(arena, 16))
         return fail(XS_EINVAL, "moe_layer_decode: the arena must hold 16-byte aligned blobs of at least %zu bytes", L->bytes);
-    if (!aligned(workspace, 256) || workspace_bytes < xs_moe_layer_decode_workspace_bytes(L, n_expert, k, n_tok))
+    const size_t need = fixed_tagged ? decode_ws(L, n_expert, k, n_tok, nullptr, true).bytes
+                                     : xs_moe_layer_decode_workspace_bytes(L, n_expert, k, n_tok);
+    if (!aligned(workspace, 256) || workspace_bytes < need)
         return fail(XS_EINVAL, "moe_layer_decode: workspace missing, misaligned or short");
-    const DecodeWs w = decode_ws(L, n_expert, k, n_tok, (uint8_t*)workspace);
+    if (status && !aligned(status, 4)) return fail(XS_EINVAL, "moe_layer_decode: the status word is misaligned");
+    const DecodeWs w = decode_ws(L, n_expert, k, n_tok, (uint8_t*)workspace, fixed_tagged);
     const long long capx = (long long)n_tok * k;
     if (n_expert > 1024 || k > 64 || k > n_expert)
         return fail(XS_EINVAL, "moe_layer_decode: %d experts, top-%d (the router takes up to 1024 and 64)", n_expert, k);
@@ -600,7 +611,7 @@ int layer_decode(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_
         a.hx = w.hx;
         a.px = w.px;
         a.sync = w.sync;
-        a.err = w.status;
+        a.err = status ? status : w.status;
         a.rh = P.rh;
         a.rd = P.rd;
         a.nu = P.nu;
@@ -634,6 +645,23 @@ int xs_moe_layer_decode(const xs_expert_layout_t* L, const uint8_t* arena, size_
     return layer_decode(L, arena, blob_bytes, n_expert, k, x, logits, residual, out, n_tok, workspace, workspace_bytes,
                         nullptr, nullptr, stream);
 }
+
+}  // extern "C"
+
+namespace xs {
+size_t layer_decode_fixed_bytes(const xs_expert_layout_t* L, int n_expert, int k, int n_tok) {
+    if (!L || k <= 0 || n_tok <= 0 || n_expert <= 0) return 0;
+    return decode_ws(L, n_expert, k, n_tok, nullptr, true).bytes;
+}
+int layer_decode_fixed(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_bytes, int n_expert, int k,
+                       const float* x, const float* logits, const float* residual, float* out, int n_tok,
+                       void* scratch, size_t scratch_bytes, int32_t* status, void* stream) {
+    return layer_decode(L, arena, blob_bytes, n_expert, k, x, logits, residual, out, n_tok, scratch, scratch_bytes,
+                        nullptr, nullptr, stream, status, true);
+}
+}  // namespace xs
+
+extern "C" {
 
 size_t xs_moe_layer_decode_shared_workspace_bytes(const xs_expert_layout_t* L, int n_expert, int k, int n_tok,
                                                   const xs_expert_layout_t* SL) {

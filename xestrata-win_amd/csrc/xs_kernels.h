@@ -135,4 +135,9 @@ struct PrefillArgs {
 };
 hipError_t launch_prefill_experts(const ExpertLayout& L, const PrefillArgs& a, hipStream_t s);
 
+// the decode layer over a workspace whose tagged hand-over words sit in fixed regions sized for the largest layout
+// (abi.cpp; the library's own scratch of noalloc.hip): hidden sizes up to kScratchMaxEmbd, expert widths up to
+// kScratchMaxFF
+constexpr int64_t kScratchMaxEmbd = 8192, kScratchMaxFF = 4096;
+
 }  // namespace xs

@@ -92,6 +92,7 @@ _SIGS = {
     "xs_moe_layer_decode": (I, [LP, P, SZ, I, I, P, P, P, P, I, P, SZ, P]),
     "xs_moe_layer_decode_workspace_bytes": (SZ, [LP, I, I, I]),
     "xs_moe_layer_decode_status": (P, [P]),
+    "xs_moe_layer_decode_noalloc": (I, [LP, P, SZ, I, I, P, P, P, P, I, P, P]),
     "xs_moe_layer_prefill": (I, [LP, P, SZ, I, I, P, P, P, P, I, P, SZ, P]),
     "xs_shared_expert_decode": (I, [LP, P, P, I, P, P, P, P, SZ, P]),
     "xs_shared_expert_decode_workspace_bytes": (SZ, [LP, I]),
@@ -320,6 +321,16 @@ def moe_combine_residual(parts, weights, residual, output, n_embd, k, n_tok, sha
 
 
 # ------------------------------------------------------------------------------------------------ whole layers
+
+def moe_layer_decode_noalloc(L, arena, n_expert, k, x, logits, residual, out, status=None, blob_bytes=None,
+                             stream=None):
+    """The decode layer in the library's own device scratch (xs_moe_layer_decode_noalloc): no workspace, nothing
+    allocated.  status: an optional int32 device tensor the call ORs its error bits into."""
+    _check(lib().xs_moe_layer_decode_noalloc(ctypes.byref(L), _p(arena), L.bytes if blob_bytes is None else blob_bytes,
+                                             n_expert, k, _p(x), _p(logits), _p(residual), _p(out), x.shape[0],
+                                             _p(status), _stream(stream)))
+    return out
+
 
 def shared_expert_decode(SL, blob, x, w_gate=None, stream=None):
     """One shared expert over the tokens of x [T, n_embd] (blob: the expert's native bytes on the device) -> (shared
