@@ -80,7 +80,7 @@ def run_graph(torch, calls):
     return ms
 
 
-TRAFFIC_FILE = ROOT / "profiles" / "moe_decode_fused_config2_traffic.md"
+TRAFFIC_FILE = ROOT / "profiles" / "moe_decode_t1_config2_traffic.md"
 
 
 def read_traffic():
@@ -328,7 +328,7 @@ def main():
     log(f"decode T=1: {ms1 * 1e3:.2f} us/layer, {gbs1:.0f} GB/s expert weights")
 
     # ---------------------------------------------------------------- the dominant kernel: the fused decode layer
-    # At T <= 64 the layer is one launch (moe_decode_fused_kernel), so the per-step time above is that kernel's average
+    # At T = 1 the layer is one launch (moe_decode_t1_kernel), so the per-step time above is that kernel's average
     # launch duration: events on the stream the graph replays on bracket the replays.  Algorithmic bytes per launch =
     # the distinct experts' blob bytes.
     roof_bytes = bytes1
@@ -449,7 +449,8 @@ def main():
                      "traffic_source": f"{TRAFFIC_FILE.relative_to(ROOT)}: rocprofv3 --pmc FETCH_SIZE + WRITE_SIZE of "
                                        "the same rotation (bench.py --pmc-run), scaled by a copy kernel of known size; "
                                        "read from the committed summary, not measured in this run",
-                     "kernel": "moe_decode_fused_kernel<Q4_K, Q6_K, 1, 0, 2> (xs_moe_layer_decode, one launch a layer)",
+                     "kernel": "moe_decode_t1_kernel<Q4_K, Q6_K, 2, 2048, 768, 8> (xs_moe_layer_decode at one token, "
+                               "one launch a layer)",
                      "algorithmic_bytes_per_launch": round(roof_bytes), "avg_launch_us": round(roof_us, 3)},
         "decode_batches": extra,
         "prefill": prefill,

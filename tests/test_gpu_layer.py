@@ -291,3 +291,38 @@ def test_decode_shared_expert_layer(xm, xo, c2_arena, c2_shared, T, gated):
         assert np.max(np.abs(got - want)) <= 1e-6 * np.max(np.abs(want)), xo.rel_max(got, want)
     else:
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), xo.rel_max(got, want)
+
+
+def test_decode_one_token_probability_tie(xm, xo, c2_arena):
+    """One token whose two best experts have logits one float ulp apart (the larger at the higher index) and
+    probabilities that round to one float: the exact routing ranks the lower index first (router.cpp's tie rule), the
+    logits' order the other one, so the one-token kernel's speculative fetch misses and is redone.  Bit for bit the
+    oracle, and the ids in the exact order."""
+    arena, L = c2_arena
+    E, k = 128, 8
+    rng = np.random.default_rng(5)
+    lg = (np.full((1, E), -10.0) + rng.standard_normal((1, E)) * 0.1).astype(np.float32)
+    lg[0, 12] = np.float32(0.25)
+    lg[0, 37] = np.nextafter(np.float32(0.25), np.float32(1))
+    rids, _ = xo.router_top10(lg, k)
+    assert rids[0, 0] == 12 and rids[0, 1] == 37          # the tie the test is about
+    logits = torch.from_numpy(lg).to(DEV)
+    rel, moe_rel = decode_case(xm, xo, arena, L, E, k, 1, logits, 5)
+    assert rel <= 1e-3 and moe_rel <= 1e-3, (rel, moe_rel)
+
+
+def test_decode_one_token_nan_routing(xm, c2_arena):
+    """One token with fewer than k numbers among its logits: the router leaves ranks unwritten, the layer writes no
+    output and sets bit 2 (value 4) of the status word."""
+    arena, L = c2_arena
+    E, k = 128, 8
+    logits = torch.full((1, E), float("nan"), device=DEV)
+    logits[0, :5] = torch.arange(5, device=DEV, dtype=torch.float32)
+    x = torch.randn(1, L.n_embd, device=DEV)
+    res = torch.randn(1, L.n_embd, device=DEV)
+    out = torch.full_like(res, 7.0)
+    layer = xm.MoeLayer(L, arena, E, k, 1)
+    layer(x, logits, res, out)
+    torch.cuda.synchronize()
+    assert layer.status() & 4
+    assert torch.all(out == 7.0)

@@ -623,6 +623,11 @@ int layer_decode(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_
         a.spin_ticks = spin_ticks();
         a.shared = shared;
         a.shared_gate = shared_gate;
+        if (n_tok == 1) {   // the one-token kernel where the layout fits it
+            bool used = false;
+            const hipError_t e1 = xs::launch_decode_t1(a, S(stream), &used);
+            if (used || e1 != hipSuccess) return finish(stream, e1, "moe_layer_decode");
+        }
         return finish(stream, xs::launch_decode_fused(a, P, S(stream)), "moe_layer_decode");
     }
     // routing, plan and activations in one launch (the reference's router_top10 + resident_plan + quantize_q8_1_rows)

@@ -102,6 +102,10 @@ struct FusedArgs {
 };
 bool fused_decode_plan(const ExpertLayout& L, int n_expert, int k, int n_tok, FusedPlan* P);
 hipError_t launch_decode_fused(const FusedArgs& a, const FusedPlan& P, hipStream_t s);
+// decode_t1.hip: the one-token layer (a.n_tok == 1) with the down units over every expert and the combine inside them;
+// *used = false (nothing launched) when the layout is not one it takes, and the caller launches launch_decode_fused.
+// Needs the same workspace (a.hx holds the q8_1 h words).
+hipError_t launch_decode_t1(const FusedArgs& a, hipStream_t s, bool* used);
 
 // the plan of one group of n entries (a shared expert over n tokens): grp_ptr[0] = blob, start = {0, n},
 // *n_groups = 1, idx[i] = i (the entries' destination rows and tokens)

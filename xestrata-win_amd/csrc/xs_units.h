@@ -273,7 +273,7 @@ struct Unit<kIQ4_XS, S256> {
 };
 
 // L = min(8, the largest power of two dividing the unit count): the canonical lane count
-__host__ __device__ inline int canon_lanes(int units) {
+__host__ __device__ constexpr int canon_lanes(int units) {
     int l = 8;
     while (l > 1 && units % l) l >>= 1;
     return l;
