@@ -166,6 +166,7 @@ def distinct_experts(torch, lg, k):
 def other_configs(torch, xm, dev, gen, steps):
     """Decode of configs 4 and 5 (reported beside the value, not the value): the layer per step, weights rotated so
     that every step reads its experts from HBM."""
+    import numpy as np
     out = {}
     # config 4: Qwen3-235B-A22B-shaped, IQ4_XS experts (hidden 4096, 128 experts, top-8, F 1536), batch 1 and 8
     E, H, F, k, copies = 128, 4096, 1536, 8, 2
@@ -188,61 +189,59 @@ def other_configs(torch, xm, dev, gen, steps):
         log(f"config 4 decode T={T}: {ms * 1e3:.2f} us/layer, {out[f'config4_T{T}']['expert_gbs']} GB/s")
     del arena
     torch.cuda.empty_cache()
-    # config 5: DeepSeek-V3-shaped (hidden 7168, 256 routed Q4_K experts, top-8, F 2048, one shared Q8_0 expert)
+    # config 5: DeepSeek-V3-shaped (hidden 7168, 256 routed Q4_K experts, top-8, F 2048, one shared Q8_0 expert),
+    # routed by its own group-limited sigmoid router (bias, 8 groups, top-4, routed scale 2.5), the shared expert's
+    # row added by the combine: one call a layer (xs_moe_layer_decode_ex / xs_moe_layer_prefill_ex)
     E, H, F, k = 256, 7168, 2048, 8
     arena, L = xm.build_arena(E, H, F, xm.Q4_K, xm.Q4_K, seed=5)
     sarena, SL = xm.build_arena(1, H, 2048, xm.Q8_0, xm.Q8_0, seed=55)
+    bias = torch.randn(E, device=dev, generator=gen) * 0.1
+    router = xm.grouped_sigmoid_router(bias, 8, 4, 2.5)
     n_sets = E // k
-    lg = set_logits(torch, n_sets, 1, E, k, dev, gen)
+    # logits whose group-limited top-8 are disjoint from set to set: +8 on set s's 8 experts, one in each of its 4
+    # groups' top pairs (experts s*8 .. s*8+7 lie in groups (s*8 .. s*8+7) // 32, two a group at most)
+    lg = torch.randn(n_sets, 1, E, device=dev, generator=gen)
+    for st in range(n_sets):
+        lg[st, :, torch.arange(8, device=dev) * 32 + st] += 8.0
     x = torch.randn(1, H, device=dev, generator=gen).to(torch.bfloat16).float()
     res = torch.randn(1, H, device=dev, generator=gen)
     o = torch.empty(1, H, device=dev)
-    layer = xm.MoeLayer(L, arena, E, k, 1, shared=(SL, sarena[0], None))
-    ms = time_steps(torch, [(lambda s=s: layer(x, lg[s], res, o)) for s in range(n_sets)], steps, n_sets)
-    bias = torch.randn(E, device=dev, generator=gen) * 0.1
+    layer = xm.MoeLayer(L, arena, E, k, 1, shared=(SL, sarena[0], None), router=router)
+    ms = time_steps(torch, [(lambda st=st: layer(x, lg[st], res, o)) for st in range(n_sets)], steps, n_sets)
     ms_r = time_steps(torch, [lambda: xm.router_grouped_sigmoid(lg[0], bias, 8, 4, k, 2.5)] * 32, steps, 32)
-    b = k * L.bytes + SL.bytes
+    distinct = float(np.mean([len(torch.unique(xm.router_grouped_sigmoid(lg[st], bias, 8, 4, k, 2.5)[0]))
+                              for st in range(n_sets)]))
+    b = distinct * L.bytes + SL.bytes
     out["config5_T1"] = dict(us_per_layer=round(ms * 1e3, 2), expert_gbs=round(b / (ms * 1e-3) / 1e9, 1),
                              frac_hbm_peak=round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), expert_mb=round(b / 1e6, 1),
-                             routing="the layer's softmax top-8 (xs_moe_layer_decode_shared); the config's "
-                                     "group-limited sigmoid router (8 groups, top-4) timed alone below",
-                             sigmoid_router_us=round(ms_r * 1e3, 2))
-    log(f"config 5 decode T=1 (+ shared expert): {ms * 1e3:.2f} us/layer, {out['config5_T1']['expert_gbs']} GB/s; "
-        f"grouped sigmoid router alone {ms_r * 1e3:.2f} us")
-    # config 5 prefill, 1024 tokens: the routed layer (i.i.d. N(0,1) logits, softmax top-8) and the shared expert's
-    # products over every token (one group of 1024 rows through xs_moe_prefill_experts, Q8_0)
+                             routing="the group-limited sigmoid router (bias, 8 groups, top-4, k 8, scale 2.5) inside "
+                                     "the one-call layer (its own launch, included); the shared expert's row added",
+                             router_alone_us=round(ms_r * 1e3, 2))
+    log(f"config 5 decode T=1 (sigmoid router + shared expert, one call): {ms * 1e3:.2f} us/layer, "
+        f"{out['config5_T1']['expert_gbs']} GB/s; the router alone {ms_r * 1e3:.2f} us")
+    # config 5 prefill, 1024 tokens: the whole prompt layer in one call - router, permutation, routed experts, the
+    # shared expert over every token, the combine with the shared row, the residual
     Tq = 1024
     lq = torch.randn(Tq, E, device=dev, generator=gen)
     xq = torch.randn(Tq, H, device=dev, generator=gen).to(torch.bfloat16).float()
     rq = torch.randn(Tq, H, device=dev, generator=gen)
     oq = torch.empty(Tq, H, device=dev)
-    qlayer = xm.MoeLayer(L, arena, E, k, Tq, prefill=True)
+    qlayer = xm.MoeLayer(L, arena, E, k, Tq, prefill=True, shared=(SL, sarena[0], None), router=router)
     ms_q = time_steps(torch, [lambda: qlayer(xq, lq, rq, oq)] * 2, 4, 2)
-    i32 = dict(dtype=torch.int32, device=dev)
-    s_src = torch.arange(Tq, **i32)
-    s_bounds = torch.tensor([0, Tq], **i32)
-    s_ng = torch.ones(1, **i32)
-    s_ptr = torch.tensor([sarena[0].data_ptr()], dtype=torch.int64, device=dev)
-    s_scr = torch.empty(xm.moe_prefill_scratch_bytes(Tq, Tq, H, 2048), dtype=torch.uint8, device=dev)
-    s_out = torch.empty(Tq, H, device=dev)
-    ms_s = time_steps(torch, [lambda: xm.moe_prefill_experts(SL, xq, s_src, s_src, s_bounds, s_ng, s_ptr, 1, Tq, s_scr,
-                                                             s_out)] * 2, 4, 2)
     fr, fs = 6.0 * Tq * k * H * F, 6.0 * Tq * H * 2048
-    tq = (fr + fs) / ((ms_q + ms_s) * 1e-3) / 1e12
-    # ~32 rows an expert: every routed expert's weights are streamed once, so the routed products are bound by HBM
-    # (114 FLOP a weight byte, under the ~310 of the MFMA ridge)
-    bq = distinct_experts(torch, lq[None], k) * L.bytes + SL.bytes
-    out["config5_prefill_T1024"] = dict(us_per_layer=round((ms_q + ms_s) * 1e3, 1), routed_us=round(ms_q * 1e3, 1),
-                                        shared_us=round(ms_s * 1e3, 1), tflops=round(tq, 2),
+    tq = (fr + fs) / (ms_q * 1e-3) / 1e12
+    ids_q, _ = xm.router_grouped_sigmoid(lq, bias, 8, 4, k, 2.5)
+    bq = len(torch.unique(ids_q)) * L.bytes + SL.bytes
+    out["config5_prefill_T1024"] = dict(us_per_layer=round(ms_q * 1e3, 1), tflops=round(tq, 2),
                                         frac_mfma_peak=round(tq / BF16_PEAK_TFLOPS, 4),
                                         gflops_per_layer=round((fr + fs) / 1e9, 1),
                                         expert_gb=round(bq / 1e9, 3),
-                                        expert_gbs=round(bq / ((ms_q + ms_s) * 1e-3) / 1e9, 1),
-                                        frac_hbm_peak=round(bq / ((ms_q + ms_s) * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                                        expert_gbs=round(bq / (ms_q * 1e-3) / 1e9, 1),
+                                        frac_hbm_peak=round(bq / (ms_q * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                                         bound="hbm (every expert streamed once at ~32 rows an expert)",
-                                        routing="i.i.d. N(0,1) logits, the layer's softmax top-8; the shared row's "
-                                                "add into the output (one [T, H] pass) is not included")
-    log(f"config 5 prefill T={Tq}: routed {ms_q * 1e3:.1f} us + shared {ms_s * 1e3:.1f} us, {tq:.1f} TFLOP/s")
+                                        routing="the group-limited sigmoid router; the shared row added by the "
+                                                "combine; one call")
+    log(f"config 5 prefill T={Tq} (one call): {ms_q * 1e3:.1f} us, {tq:.1f} TFLOP/s")
     del arena, sarena
     torch.cuda.empty_cache()
     return out

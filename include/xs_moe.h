@@ -218,12 +218,48 @@ int xs_moe_layer_decode_shared(const xs_expert_layout_t* L, const uint8_t* arena
 size_t xs_moe_layer_decode_shared_workspace_bytes(const xs_expert_layout_t* L, int n_expert, int k, int n_tok,
                                                   const xs_expert_layout_t* SL);
 
+/* How a layer routes its tokens.  XS_ROUTER_SOFTMAX: the softmax top-k of the logits, renormalised
+ * (router_top10, include/strata/kernels/router_top10.hpp:20-21).  XS_ROUTER_GROUPED_SIGMOID: DeepSeek-V3's routing
+ * (xs_router_grouped_sigmoid: sigmoid scores, selection by score + bias, the topk_group best of n_group groups, weights
+ * normalised over the k and times routed_scale); no counterpart in the reference, whose layer wires router_top10
+ * (src/core/plain_model.cpp:955-956). */
+#define XS_ROUTER_SOFTMAX 0
+#define XS_ROUTER_GROUPED_SIGMOID 1
+typedef struct xs_router_cfg {
+    int kind;
+    const float* bias;    /* grouped sigmoid: [n_expert] selection bias, or NULL */
+    int n_group, topk_group;
+    float routed_scale;
+} xs_router_cfg_t;
+
+/* The decode layer with either router and an optional shared expert (SL NULL: none; w_gate NULL: ungated): the
+ * engine's whole decode MoE section (src/core/plain_model.cpp:951-988) in one call.  router NULL is the softmax.  With
+ * the grouped sigmoid router the routing is its own launch ahead of the layer, whose kernels then take its ids and
+ * weights.  workspace: xs_moe_layer_decode_ex_workspace_bytes, 256-byte aligned, zeroed once (as
+ * xs_moe_layer_decode's, whose status word it starts with). */
+int xs_moe_layer_decode_ex(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_bytes, int n_expert, int k,
+                           const float* x, const float* logits, const float* residual, float* out, int n_tok,
+                           const xs_router_cfg_t* router, const xs_expert_layout_t* SL, const uint8_t* shared_blob,
+                           const float* w_gate, void* workspace, size_t workspace_bytes, void* stream);
+size_t xs_moe_layer_decode_ex_workspace_bytes(const xs_expert_layout_t* L, int n_expert, int k, int n_tok,
+                                              const xs_expert_layout_t* SL);
+
 /* The whole prompt / verify MoE layer on the device (same arena): router -> permutation -> f16 MFMA grouped
  * experts -> combine -> residual.  The engine's prompt MoE section (src/prefill/plain_prompt.cpp:558-797). */
 int xs_moe_layer_prefill(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_bytes, int n_expert,
                          int k, const float* x, const float* logits, const float* residual, float* out, int n_tok,
                          void* workspace, size_t workspace_bytes, void* stream);
 size_t xs_moe_layer_prefill_workspace_bytes(const xs_expert_layout_t* L, int n_expert, int k, int n_tok);
+/* The prompt layer with either router and an optional shared expert: every token through the shared expert (one group
+ * of the f16 MFMA GEMMs, rows in fp32) and the combine adding its row once after the routed ones, times the sigmoid of
+ * its gate logit w_gate . x when w_gate is given - the reference's prompt layer (src/prefill/plain_prompt.cpp:
+ * 788-797: the shared SwiGLU and down projection, then native_moe_combine_multi with shared and sh_g). */
+int xs_moe_layer_prefill_ex(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_bytes, int n_expert, int k,
+                            const float* x, const float* logits, const float* residual, float* out, int n_tok,
+                            const xs_router_cfg_t* router, const xs_expert_layout_t* SL, const uint8_t* shared_blob,
+                            const float* w_gate, void* workspace, size_t workspace_bytes, void* stream);
+size_t xs_moe_layer_prefill_ex_workspace_bytes(const xs_expert_layout_t* L, int n_expert, int k, int n_tok,
+                                               const xs_expert_layout_t* SL);
 
 #ifdef __cplusplus
 }

@@ -205,3 +205,105 @@ def test_config5_prefill_shared_expert(xm, c5_arena):
     want = torch_reference_prefill(xm, sh, SL, x, ids, 1)
     rel = float((out - want).abs().max() / want.abs().max())
     assert rel <= 2e-2, rel
+
+
+# ------------------------------------------------------------------------------------------------ config 5 in one call
+
+def oracle_grouped_layer(xo, arena, L, E, k, x, logits, bias, res, shared=None, gate=None, n_group=8, topk_group=4,
+                         scale=2.5):
+    """The oracle's composition of a decode layer routed by the grouped sigmoid router: router, plan, grouped experts,
+    the shared expert as one group of every token, the combine (+ the shared row, times sigmoid(gate) if given),
+    the residual."""
+    T, H = x.shape
+    rids, rw = xo.router_grouped_sigmoid(logits, bias, n_group, topk_group, k, scale)
+    p = xo.decode_plan(rids, k)
+    oxq = xo.quantize_q8_1_rows(x)
+    blobs = [t2n(arena[e]) for e in p["experts"]]
+    oparts = xo.native_expert_grouped(xo.layout(L.gu_type, L.d_type, H, L.n_ff), blobs, p["start"], p["dst"], p["tok"],
+                                      oxq, T * k)
+    osh = None
+    if shared is not None:
+        SL, sblob = shared
+        idx = np.arange(T, dtype=np.int32)
+        osh = xo.native_expert_grouped(xo.layout(SL.gu_type, SL.d_type, H, SL.n_ff), [t2n(sblob)],
+                                       np.array([0, T], np.int32), idx, idx, oxq, T)
+    return rids, (res + xo.combine(oparts, rw, osh, gate, H, k, T)).astype(np.float32)
+
+
+@pytest.mark.parametrize("T,gated", [(1, False), (1, True), (4, False)])
+def test_config5_decode_one_call(xm, xo, c5_arena, T, gated):
+    """Config 5's whole decode layer as one call (xs_moe_layer_decode_ex): the group-limited sigmoid router with bias
+    (8 groups, top-4, k 8, routed scale 2.5) over 256 Q4_K experts plus the Q8_0 shared expert.  Ungated: bit for bit
+    the oracle's composition; gated: within 1e-6 relative (each side's own expf in the sigmoid)."""
+    arena, L, sh, SL, w_gate = c5_arena
+    E, k, H = 256, 8, 7168
+    g = torch.Generator(device=DEV).manual_seed(70 + T)
+    x = torch.randn(T, H, device=DEV, generator=g).to(torch.bfloat16).float()
+    res = torch.randn(T, H, device=DEV, generator=g)
+    logits = torch.randn(T, E, device=DEV, generator=g)
+    bias = torch.randn(E, device=DEV, generator=g) * 0.1
+    router = xm.grouped_sigmoid_router(bias, 8, 4, 2.5)
+    wg = w_gate if gated else None
+    layer = xm.MoeLayer(L, arena, E, k, T, shared=(SL, sh[0], wg), router=router)
+    out = torch.empty_like(res)
+    print(f"[case] config 5 decode one call T={T} gated={gated}", flush=True)
+    layer(x, logits, res, out)
+    gate = xm.shared_expert_decode(SL, sh[0], x, wg)[1] if gated else None
+    torch.cuda.synchronize()
+    layer.check()
+    _, want = oracle_grouped_layer(xo, arena, L, E, k, t2n(x), t2n(logits), t2n(bias), t2n(res), (SL, sh[0]),
+                                   None if gate is None else t2n(gate))
+    got = t2n(out)
+    if gated:
+        assert np.max(np.abs(got - want)) <= 1e-6 * np.max(np.abs(want)), xo.rel_max(got, want)
+    else:
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), xo.rel_max(got, want)
+
+
+def test_grouped_router_chained_decode(xm, xo, c2_arena):
+    """The grouped sigmoid router on config 2's experts (128 = 8 groups of 16, top-4 groups, k 8) at 40 tokens: 320
+    entries, past the persistent kernel, so the chained path plans the given ids (resident plan) and runs the grouped
+    kernels and the combine.  Bit for bit the oracle's composition, no shared expert."""
+    arena, L = c2_arena
+    E, k, T, H = 128, 8, 40, 2048
+    g = torch.Generator(device=DEV).manual_seed(77)
+    x = torch.randn(T, H, device=DEV, generator=g).to(torch.bfloat16).float()
+    res = torch.randn(T, H, device=DEV, generator=g)
+    logits = torch.randn(T, E, device=DEV, generator=g)
+    bias = torch.randn(E, device=DEV, generator=g) * 0.1
+    layer = xm.MoeLayer(L, arena, E, k, T, router=xm.grouped_sigmoid_router(bias, 8, 4, 1.0))
+    out = torch.empty_like(res)
+    layer(x, logits, res, out)
+    torch.cuda.synchronize()
+    layer.check()
+    _, want = oracle_grouped_layer(xo, arena, L, E, k, t2n(x), t2n(logits), t2n(bias), t2n(res), scale=1.0)
+    got = t2n(out)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), xo.rel_max(got, want)
+
+
+@pytest.mark.parametrize("gated", [False, True])
+def test_config5_prefill_one_call(xm, c5_arena, gated):
+    """Config 5's prompt layer as one call (xs_moe_layer_prefill_ex): 1024 tokens, the grouped sigmoid router, the 256
+    routed Q4_K experts and the Q8_0 shared expert through the f16 MFMA GEMMs, the shared row added by the combine
+    (times sigmoid(w_gate . x) when gated).  Against the fp32 reference: max|a - b| / max|ref| <= 2e-2."""
+    arena, L, sh, SL, w_gate = c5_arena
+    E, k, T, H = 256, 8, 1024, 7168
+    g = torch.Generator(device=DEV).manual_seed(90)
+    x = torch.randn(T, H, device=DEV, generator=g).to(torch.bfloat16).float()
+    res = torch.randn(T, H, device=DEV, generator=g)
+    logits = torch.randn(T, E, device=DEV, generator=g)
+    bias = torch.randn(E, device=DEV, generator=g) * 0.1
+    wg = w_gate if gated else None
+    layer = xm.MoeLayer(L, arena, E, k, T, prefill=True, shared=(SL, sh[0], wg),
+                        router=xm.grouped_sigmoid_router(bias, 8, 4, 2.5))
+    out = torch.empty_like(res)
+    print(f"[case] config 5 prefill one call gated={gated}", flush=True)
+    layer(x, logits, res, out)
+    ids, w = xm.router_grouped_sigmoid(logits, bias, 8, 4, k, 2.5)
+    parts = torch_reference_prefill(xm, arena, L, x, ids, E)
+    shared = torch_reference_prefill(xm, sh, SL, x, torch.zeros(T, 1, dtype=torch.int32, device=DEV), 1)
+    if gated:
+        shared = shared * torch.sigmoid(x @ w_gate)[:, None]
+    moe = (parts.reshape(T, k, -1) * w[:, :, None]).sum(1) + shared
+    rel = float(((out - res) - moe).abs().max() / moe.abs().max())
+    assert rel <= 2e-2, rel

@@ -570,11 +570,36 @@ size_t xs_moe_layer_decode_workspace_bytes(const xs_expert_layout_t* L, int n_ex
 }
 
 namespace {
+// How a layer routes its tokens: the softmax top-k of the logits (router_top10), or DeepSeek-V3's group-limited
+// sigmoid (xs_router_grouped_sigmoid's arguments)
+struct Route {
+    int kind = XS_ROUTER_SOFTMAX;
+    const float* bias = nullptr;
+    int n_group = 1, topk_group = 1;
+    float scale = 1.0f;
+};
+int route_of(const xs_router_cfg_t* cfg, int n_expert, int k, Route* r, const char* who) {
+    *r = Route{};
+    if (!cfg || cfg->kind == XS_ROUTER_SOFTMAX) return XS_OK;
+    if (cfg->kind != XS_ROUTER_GROUPED_SIGMOID) return fail(XS_EINVAL, "%s: router kind %d is unknown", who, cfg->kind);
+    if (cfg->n_group <= 0 || cfg->n_group > 64 || n_expert % cfg->n_group || cfg->topk_group <= 0 ||
+        cfg->topk_group > cfg->n_group || k > (n_expert / cfg->n_group) * cfg->topk_group ||
+        (cfg->bias && !aligned(cfg->bias, 4)))
+        return fail(XS_EINVAL, "%s: grouped sigmoid router: %d experts, %d groups, top %d groups, k %d", who, n_expert,
+                    cfg->n_group, cfg->topk_group, k);
+    r->kind = cfg->kind;
+    r->bias = cfg->bias;
+    r->n_group = cfg->n_group;
+    r->topk_group = cfg->topk_group;
+    r->scale = cfg->routed_scale;
+    return XS_OK;
+}
+
 // status: where the persistent layer's error bits go (NULL: the workspace's status word); fixed_tagged: decode_ws's
 int layer_decode(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_bytes, int n_expert, int k,
                  const float* x, const float* logits, const float* residual, float* out, int n_tok, void* workspace,
                  size_t workspace_bytes, const float* shared, const float* shared_gate, void* stream,
-                 int32_t* status = nullptr, bool fixed_tagged = false) {
+                 int32_t* status = nullptr, bool fixed_tagged = false, const Route& route = Route{}) {
     if (n_tok <= 0) return ok();
     if (int r = check_layout(L, "moe_layer_decode")) return r;
     if (n_tok * k > 1024) return fail(XS_EINVAL, "moe_layer_decode: %d tokens x top-%d is past 1024 entries", n_tok, k);
@@ -592,6 +617,11 @@ int layer_decode(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_
     if (!aligned(logits, 4) || !aligned(x, 4) || !aligned(residual, 4) || !aligned(out, 4))
         return fail(XS_EINVAL, "moe_layer_decode: a span is missing or misaligned");
     const xs::ExpertLayout XL = to_layout(L);
+    const bool pre = route.kind == XS_ROUTER_GROUPED_SIGMOID;
+    if (pre)   // the other router first, into the workspace's ids and weights
+        if (int r = xs_router_grouped_sigmoid(logits, route.bias, n_tok, n_expert, route.n_group, route.topk_group, k,
+                                              route.scale, w.ids, w.w, stream))
+            return r;
     xs::FusedPlan P;
     if (xs::fused_decode_plan(XL, n_expert, k, n_tok, &P)) {
         // the whole layer in one persistent launch
@@ -623,6 +653,8 @@ int layer_decode(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_
         a.spin_ticks = spin_ticks();
         a.shared = shared;
         a.shared_gate = shared_gate;
+        a.pre_ids = pre ? w.ids : nullptr;
+        a.pre_w = pre ? w.w : nullptr;
         if (n_tok == 1) {   // the one-token kernel where the layout fits it
             bool used = false;
             const hipError_t e1 = xs::launch_decode_t1(a, S(stream), &used);
@@ -630,10 +662,18 @@ int layer_decode(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_
         }
         return finish(stream, xs::launch_decode_fused(a, P, S(stream)), "moe_layer_decode");
     }
-    // routing, plan and activations in one launch (the reference's router_top10 + resident_plan + quantize_q8_1_rows)
-    hipError_t e = xs::launch_decode_route(logits, x, n_tok, n_expert, k, L->n_embd, w.ids, w.w, w.plan, capx, w.skip,
-                                           arena, (long long)blob_bytes, w.xq, S(stream));
-    if (e != hipSuccess) return hip_status(e, "moe_layer_decode");
+    if (pre) {   // the plan of the given ids, then the activations
+        if (int r = xs_resident_plan(w.ids, (int)capx, k, nullptr, n_expert, arena, nullptr, (long long)blob_bytes,
+                                     w.plan, capx, w.skip, 1u, stream))
+            return r;
+        if (int r = xs_quantize_q8_1_rows(x, n_tok, L->n_embd, w.xq, stream)) return r;
+    } else {
+        // routing, plan and activations in one launch (the reference's router_top10 + resident_plan +
+        // quantize_q8_1_rows)
+        hipError_t e = xs::launch_decode_route(logits, x, n_tok, n_expert, k, L->n_embd, w.ids, w.w, w.plan, capx,
+                                               w.skip, arena, (long long)blob_bytes, w.xq, S(stream));
+        if (e != hipSuccess) return hip_status(e, "moe_layer_decode");
+    }
     const int64_t cap_groups = capx < n_expert ? capx : n_expert;
     long long o_start, o_dst, o_tok, o_ptr;
     xs_plan_offsets(capx, &o_start, &o_dst, &o_tok, &o_ptr, nullptr);
@@ -675,19 +715,26 @@ size_t xs_moe_layer_decode_shared_workspace_bytes(const xs_expert_layout_t* L, i
            up256((size_t)n_tok * 4) + shared_ws(SL, n_tok, nullptr).bytes;
 }
 
-int xs_moe_layer_decode_shared(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_bytes, int n_expert,
-                               int k, const float* x, const float* logits, const float* residual, float* out,
-                               int n_tok, const xs_expert_layout_t* SL, const uint8_t* shared_blob,
-                               const float* w_gate, void* workspace, size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+// the decode layer with an optional shared expert (SL NULL: none) and either router
+int layer_decode_shared(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_bytes, int n_expert, int k,
+                        const float* x, const float* logits, const float* residual, float* out, int n_tok,
+                        const Route& route, const xs_expert_layout_t* SL, const uint8_t* shared_blob,
+                        const float* w_gate, void* workspace, size_t workspace_bytes, void* stream, const char* who) {
     if (n_tok <= 0) return ok();
-    if (int r = check_layout(L, "moe_layer_decode_shared")) return r;
-    if (int r = check_layout(SL, "moe_layer_decode_shared")) return r;
+    if (int r = check_layout(L, who)) return r;
+    if (!SL)
+        return layer_decode(L, arena, blob_bytes, n_expert, k, x, logits, residual, out, n_tok, workspace,
+                            workspace_bytes, nullptr, nullptr, stream, nullptr, false, route);
+    if (int r = check_layout(SL, who)) return r;
     if (SL->n_embd != L->n_embd)
-        return fail(XS_EINVAL, "moe_layer_decode_shared: the shared expert's n_embd %lld is not the layer's %lld",
+        return fail(XS_EINVAL, "%s: the shared expert's n_embd %lld is not the layer's %lld", who,
                     (long long)SL->n_embd, (long long)L->n_embd);
     if (!aligned(workspace, 256) ||
         workspace_bytes < xs_moe_layer_decode_shared_workspace_bytes(L, n_expert, k, n_tok, SL))
-        return fail(XS_EINVAL, "moe_layer_decode_shared: workspace missing, misaligned or short");
+        return fail(XS_EINVAL, "%s: workspace missing, misaligned or short", who);
     // the layer's own workspace first (its head and tagged words at the offsets xs_moe_layer_decode uses), then the
     // shared rows, the gate logits and the shared expert's workspace
     const size_t lw = decode_ws(L, n_expert, k, n_tok, nullptr).bytes;
@@ -700,7 +747,35 @@ int xs_moe_layer_decode_shared(const xs_expert_layout_t* L, const uint8_t* arena
                                         stream))
         return r;
     return layer_decode(L, arena, blob_bytes, n_expert, k, x, logits, residual, out, n_tok, workspace, lw, shared,
-                        w_gate ? gate : nullptr, stream);
+                        w_gate ? gate : nullptr, stream, nullptr, false, route);
+}
+}  // namespace
+
+extern "C" {
+
+int xs_moe_layer_decode_shared(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_bytes, int n_expert,
+                               int k, const float* x, const float* logits, const float* residual, float* out,
+                               int n_tok, const xs_expert_layout_t* SL, const uint8_t* shared_blob,
+                               const float* w_gate, void* workspace, size_t workspace_bytes, void* stream) {
+    if (!SL) return fail(XS_EINVAL, "moe_layer_decode_shared: no shared expert");
+    return layer_decode_shared(L, arena, blob_bytes, n_expert, k, x, logits, residual, out, n_tok, Route{}, SL,
+                               shared_blob, w_gate, workspace, workspace_bytes, stream, "moe_layer_decode_shared");
+}
+
+size_t xs_moe_layer_decode_ex_workspace_bytes(const xs_expert_layout_t* L, int n_expert, int k, int n_tok,
+                                              const xs_expert_layout_t* SL) {
+    return SL ? xs_moe_layer_decode_shared_workspace_bytes(L, n_expert, k, n_tok, SL)
+              : xs_moe_layer_decode_workspace_bytes(L, n_expert, k, n_tok);
+}
+
+int xs_moe_layer_decode_ex(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_bytes, int n_expert, int k,
+                           const float* x, const float* logits, const float* residual, float* out, int n_tok,
+                           const xs_router_cfg_t* router, const xs_expert_layout_t* SL, const uint8_t* shared_blob,
+                           const float* w_gate, void* workspace, size_t workspace_bytes, void* stream) {
+    Route rt;
+    if (int r = route_of(router, n_expert, k, &rt, "moe_layer_decode_ex")) return r;
+    return layer_decode_shared(L, arena, blob_bytes, n_expert, k, x, logits, residual, out, n_tok, rt, SL, shared_blob,
+                               w_gate, workspace, workspace_bytes, stream, "moe_layer_decode_ex");
 }
 
 size_t xs_moe_layer_prefill_workspace_bytes(const xs_expert_layout_t* L, int n_expert, int k, int n_tok) {
@@ -708,31 +783,115 @@ size_t xs_moe_layer_prefill_workspace_bytes(const xs_expert_layout_t* L, int n_e
     return prefill_ws(L, n_expert, k, n_tok, nullptr).bytes;
 }
 
-int xs_moe_layer_prefill(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_bytes, int n_expert,
-                         int k, const float* x, const float* logits, const float* residual, float* out, int n_tok,
-                         void* workspace, size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+// the prompt layer's shared expert: its single group's plan, its scratch, its fp32 rows and gate logits
+struct SharedPrefillWs {
+    unsigned long long* grp_ptr;
+    int32_t *start, *n_groups, *idx;
+    void* scratch;
+    float* rows;
+    float* gate;
+    size_t bytes;
+};
+SharedPrefillWs shared_prefill_ws(const xs_expert_layout_t* SL, int n_tok, uint8_t* base) {
+    SharedPrefillWs d;
+    size_t off = 0;
+    auto take = [&](size_t b) { uint8_t* p = base ? base + off : nullptr; off += up256(b); return p; };
+    d.grp_ptr = (unsigned long long*)take(8);
+    d.start = (int32_t*)take(8);
+    d.n_groups = (int32_t*)take(4);
+    d.idx = (int32_t*)take((size_t)n_tok * 4);
+    d.scratch = take(xs_moe_prefill_scratch_bytes(n_tok, n_tok, SL->n_embd, SL->n_ff));
+    d.rows = (float*)take((size_t)n_tok * (size_t)SL->n_embd * 4);
+    d.gate = (float*)take((size_t)n_tok * 4);
+    d.bytes = off;
+    return d;
+}
+
+int layer_prefill(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_bytes, int n_expert, int k,
+                  const float* x, const float* logits, const float* residual, float* out, int n_tok, const Route& route,
+                  const xs_expert_layout_t* SL, const uint8_t* shared_blob, const float* w_gate, void* workspace,
+                  size_t workspace_bytes, void* stream, const char* who) {
     if (n_tok <= 0) return ok();
-    if (int r = check_layout(L, "moe_layer_prefill")) return r;
+    if (int r = check_layout(L, who)) return r;
     if (blob_bytes < L->bytes || blob_bytes % 16 || !aligned(arena, 16))
-        return fail(XS_EINVAL, "moe_layer_prefill: the arena must hold 16-byte aligned blobs of at least %zu bytes", L->bytes);
-    if (!aligned(workspace, 256) || workspace_bytes < xs_moe_layer_prefill_workspace_bytes(L, n_expert, k, n_tok))
-        return fail(XS_EINVAL, "moe_layer_prefill: workspace missing, misaligned or short");
+        return fail(XS_EINVAL, "%s: the arena must hold 16-byte aligned blobs of at least %zu bytes", who, L->bytes);
+    if (SL) {
+        if (int r = check_layout(SL, who)) return r;
+        if (SL->n_embd != L->n_embd || !aligned(shared_blob, 16))
+            return fail(XS_EINVAL, "%s: the shared expert (n_embd %lld, blob 16-byte aligned) does not fit the layer",
+                        who, (long long)SL->n_embd);
+    }
+    if (!aligned(workspace, 256) || workspace_bytes < xs_moe_layer_prefill_ex_workspace_bytes(L, n_expert, k, n_tok, SL))
+        return fail(XS_EINVAL, "%s: workspace missing, misaligned or short", who);
     const PrefillWs w = prefill_ws(L, n_expert, k, n_tok, (uint8_t*)workspace);
     const int64_t n = (int64_t)n_tok * k;
-    if (int r = xs_router_top10(logits, n_tok, n_expert, k, w.ids, w.w, stream)) return r;
+    if (route.kind == XS_ROUTER_GROUPED_SIGMOID) {
+        if (int r = xs_router_grouped_sigmoid(logits, route.bias, n_tok, n_expert, route.n_group, route.topk_group, k,
+                                              route.scale, w.ids, w.w, stream))
+            return r;
+    } else if (int r = xs_router_top10(logits, n_tok, n_expert, k, w.ids, w.w, stream)) {
+        return r;
+    }
     const int64_t cap_groups = n < n_expert ? n : n_expert;
     if (int r = finish(stream,
                        xs::launch_prefill_route_split(w.ids, n, k, n_expert, w.src, w.slot, w.entry, w.bounds,
                                                       w.experts, w.n_groups, arena, (long long)blob_bytes, w.grp_ptr,
                                                       w.ghist, prefill_mtile(w.scratch, n_tok, n, L), (int)cap_groups,
                                                       S(stream)),
-                       "moe_layer_prefill"))
+                       who))
         return r;
     if (int r = prefill_experts(L, x, n_tok, w.src, w.entry, w.bounds, w.n_groups, w.grp_ptr, cap_groups, n, w.scratch,
                                 nullptr, w.parts, true, stream))
         return r;
-    return finish(stream, xs::launch_combine_h(w.parts, w.w, residual, out, L->n_embd, k, n_tok, S(stream)),
-                  "moe_layer_prefill");
+    const float* shared = nullptr;
+    const float* gate = nullptr;
+    if (SL) {   // every token through the shared expert (one group), its rows in fp32; its gate's logits
+        const SharedPrefillWs sw = shared_prefill_ws(SL, n_tok, (uint8_t*)workspace + w.bytes);
+        if (int r = finish(stream, xs::launch_single_group_plan(sw.grp_ptr, sw.start, sw.n_groups, sw.idx, n_tok,
+                                                                shared_blob, S(stream)),
+                           who))
+            return r;
+        if (int r = prefill_experts(SL, x, n_tok, sw.idx, sw.idx, sw.start, sw.n_groups, sw.grp_ptr, 1, n_tok,
+                                    sw.scratch, sw.rows, nullptr, false, stream))
+            return r;
+        if (w_gate) {
+            if (int r = xs_router_logits_f32(x, w_gate, sw.gate, n_tok, SL->n_embd, 1, stream)) return r;
+            gate = sw.gate;
+        }
+        shared = sw.rows;
+    }
+    return finish(stream,
+                  xs::launch_combine_h(w.parts, w.w, shared, gate, residual, out, L->n_embd, k, n_tok, S(stream)), who);
+}
+}  // namespace
+
+extern "C" {
+
+int xs_moe_layer_prefill(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_bytes, int n_expert,
+                         int k, const float* x, const float* logits, const float* residual, float* out, int n_tok,
+                         void* workspace, size_t workspace_bytes, void* stream) {
+    return layer_prefill(L, arena, blob_bytes, n_expert, k, x, logits, residual, out, n_tok, Route{}, nullptr, nullptr,
+                         nullptr, workspace, workspace_bytes, stream, "moe_layer_prefill");
+}
+
+size_t xs_moe_layer_prefill_ex_workspace_bytes(const xs_expert_layout_t* L, int n_expert, int k, int n_tok,
+                                               const xs_expert_layout_t* SL) {
+    if (!L || k <= 0 || n_tok <= 0 || n_expert <= 0) return 0;
+    const size_t base = prefill_ws(L, n_expert, k, n_tok, nullptr).bytes;
+    return SL ? base + shared_prefill_ws(SL, n_tok, nullptr).bytes : base;
+}
+
+int xs_moe_layer_prefill_ex(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_bytes, int n_expert, int k,
+                            const float* x, const float* logits, const float* residual, float* out, int n_tok,
+                            const xs_router_cfg_t* router, const xs_expert_layout_t* SL, const uint8_t* shared_blob,
+                            const float* w_gate, void* workspace, size_t workspace_bytes, void* stream) {
+    Route rt;
+    if (int r = route_of(router, n_expert, k, &rt, "moe_layer_prefill_ex")) return r;
+    return layer_prefill(L, arena, blob_bytes, n_expert, k, x, logits, residual, out, n_tok, rt, SL, shared_blob,
+                         w_gate, workspace, workspace_bytes, stream, "moe_layer_prefill_ex");
 }
 
 }  // extern "C"

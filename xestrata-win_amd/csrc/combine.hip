@@ -45,6 +45,8 @@ __global__ __launch_bounds__(256) void add_inplace_kernel(float* __restrict__ x,
 // 4 columns a thread (8-byte part reads, 16-byte residual and output accesses).
 __global__ __launch_bounds__(256) void combine_h_kernel(const uint16_t* __restrict__ parts,
                                                         const float* __restrict__ weights,
+                                                        const float* __restrict__ shared,
+                                                        const float* __restrict__ shared_gate,
                                                         const float* __restrict__ residual, float* __restrict__ out,
                                                         int64_t n_embd, int k) {
     const int64_t t = blockIdx.y;
@@ -61,14 +63,24 @@ __global__ __launch_bounds__(256) void combine_h_kernel(const uint16_t* __restri
         if (e == 0) sum = prod;
         else sum = make_float4(sum.x + prod.x, sum.y + prod.y, sum.z + prod.z, sum.w + prod.w);
     }
+    if (shared) {   // the shared expert's row, once, after the routed ones (times its gate's sigmoid)
+        float4 sv = *(const float4*)(shared + t * n_embd + c);
+        if (shared_gate) {
+            const float gs = 1.0f / (1.0f + expf(-shared_gate[t]));
+            sv = make_float4(sv.x * gs, sv.y * gs, sv.z * gs, sv.w * gs);
+        }
+        sum = make_float4(sum.x + sv.x, sum.y + sv.y, sum.z + sv.z, sum.w + sv.w);
+    }
     const float4 r = *(const float4*)(residual + t * n_embd + c);
     *(float4*)(out + t * n_embd + c) = make_float4(r.x + sum.x, r.y + sum.y, r.z + sum.z, r.w + sum.w);
 }
 
-hipError_t launch_combine_h(const uint16_t* parts, const float* weights, const float* residual, float* out,
-                            int64_t n_embd, int k, int n_tok, hipStream_t s) {
+hipError_t launch_combine_h(const uint16_t* parts, const float* weights, const float* shared,
+                            const float* shared_gate, const float* residual, float* out, int64_t n_embd, int k,
+                            int n_tok, hipStream_t s) {
     const dim3 grid((unsigned)((n_embd / 4 + 255) / 256), (unsigned)n_tok);
-    hipLaunchKernelGGL(combine_h_kernel, grid, dim3(256), 0, s, parts, weights, residual, out, n_embd, k);
+    hipLaunchKernelGGL(combine_h_kernel, grid, dim3(256), 0, s, parts, weights, shared, shared_gate, residual, out,
+                       n_embd, k);
     return hipGetLastError();
 }
 

@@ -232,6 +232,15 @@ template <int PER>
 __device__ __forceinline__ void route_tokens_wave(const FusedArgs& a, int T, int* s_ids, float* s_w,
                                                   unsigned long long& ctr) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, E = a.n_expert, k = a.k;
+    if (a.pre_ids) {   // routed already (another router): the tokens' ids and weights as given
+        ctr = load_counter(a);
+        for (int t = wave; t < T; t += kFT / 64)
+            if (lane < k) {
+                s_ids[t * k + lane] = a.pre_ids[t * k + lane];
+                s_w[t * k + lane] = a.pre_w[t * k + lane];
+            }
+        return;
+    }
     float lv[PER];
     if (wave < T) load_logits_wave<PER>(a.logits + (int64_t)wave * E, E, lv);
     ctr = load_counter(a);

@@ -99,6 +99,10 @@ struct FusedArgs {
     long long spin_ticks;   // bound of a wait, in wall-clock ticks
     const float* shared;       // [n_tok, n_embd] the shared expert's rows, added once by the combine (NULL: none)
     const float* shared_gate;  // [n_tok] its gate logits (NULL: ungated)
+    // routing already done by another router (DeepSeek's group-limited sigmoid): ids / weights [n_tok, k] in rank
+    // order, read instead of routing the logits (NULL: the softmax top-k of the logits)
+    const int32_t* pre_ids = nullptr;
+    const float* pre_w = nullptr;
 };
 bool fused_decode_plan(const ExpertLayout& L, int n_expert, int k, int n_tok, FusedPlan* P);
 hipError_t launch_decode_fused(const FusedArgs& a, const FusedPlan& P, hipStream_t s);
@@ -117,8 +121,9 @@ hipError_t launch_combine(const float* parts, const float* weights, const float*
                           const float* residual, float* out, int64_t n_embd, int k, int n_tok, hipStream_t s);
 hipError_t launch_add_inplace(float* x, const float* y, int64_t n, hipStream_t s);
 // the combine over f16 parts, + residual (n_embd % 4 == 0)
-hipError_t launch_combine_h(const uint16_t* parts, const float* weights, const float* residual, float* out,
-                            int64_t n_embd, int k, int n_tok, hipStream_t s);
+hipError_t launch_combine_h(const uint16_t* parts, const float* weights, const float* shared,
+                            const float* shared_gate, const float* residual, float* out, int64_t n_embd, int k,
+                            int n_tok, hipStream_t s);
 
 // experts_prefill.hip
 struct PrefillArgs {

@@ -51,12 +51,31 @@ class PackLayer(ctypes.Structure):
                 ("gguf_file", ctypes.c_char_p * 3)]
 
 
+class RouterCfg(ctypes.Structure):
+    """xs_router_cfg_t: how a layer routes (XS_ROUTER_SOFTMAX, or XS_ROUTER_GROUPED_SIGMOID with its bias, groups and
+    routed scale)."""
+    _fields_ = [("kind", ctypes.c_int), ("bias", ctypes.c_void_p), ("n_group", ctypes.c_int),
+                ("topk_group", ctypes.c_int), ("routed_scale", ctypes.c_float)]
+
+
+ROUTER_SOFTMAX, ROUTER_GROUPED_SIGMOID = 0, 1
+
+
+def grouped_sigmoid_router(bias, n_group, topk_group, routed_scale):
+    """DeepSeek-V3's routing for a layer: (RouterCfg, bias tensor kept alive with it)."""
+    cfg = RouterCfg(ROUTER_GROUPED_SIGMOID, None if bias is None else bias.data_ptr(), n_group, topk_group,
+                    float(routed_scale))
+    cfg._keep = bias
+    return cfg
+
+
 class PackLoadStats(ctypes.Structure):
     _fields_ = [("bytes", ctypes.c_uint64), ("layers", ctypes.c_uint64), ("seconds", ctypes.c_double)]
 
 
 P, I, I64, SZ, F = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t, ctypes.c_float
 LP = ctypes.POINTER(Layout)
+RP = ctypes.c_void_p
 LL = ctypes.c_longlong
 U32 = ctypes.c_uint32
 U64 = ctypes.c_uint64
@@ -99,6 +118,10 @@ _SIGS = {
     "xs_moe_layer_decode_shared": (I, [LP, P, SZ, I, I, P, P, P, P, I, LP, P, P, P, SZ, P]),
     "xs_moe_layer_decode_shared_workspace_bytes": (SZ, [LP, I, I, I, LP]),
     "xs_moe_layer_prefill_workspace_bytes": (SZ, [LP, I, I, I]),
+    "xs_moe_layer_decode_ex": (I, [LP, P, SZ, I, I, P, P, P, P, I, RP, LP, P, P, P, SZ, P]),
+    "xs_moe_layer_decode_ex_workspace_bytes": (SZ, [LP, I, I, I, LP]),
+    "xs_moe_layer_prefill_ex": (I, [LP, P, SZ, I, I, P, P, P, P, I, RP, LP, P, P, P, SZ, P]),
+    "xs_moe_layer_prefill_ex_workspace_bytes": (SZ, [LP, I, I, I, LP]),
     # include/xs_pack.h
     "xs_pack_layout_load": (I, [S, I64, I64, I64, I64, ctypes.POINTER(P)]),
     "xs_pack_layout_from_gguf": (I, [S, ctypes.POINTER(I64), I64, I64, I64, I64, ctypes.POINTER(P)]),
@@ -348,18 +371,23 @@ def shared_expert_decode(SL, blob, x, w_gate=None, stream=None):
 class MoeLayer:
     """One MoE layer whose experts live in one HBM arena (expert e's native blob at arena + e * blob_bytes), with its
     workspace allocated once, so calls allocate nothing (graph-capturable).  shared = (SL, blob, w_gate or None): a
-    shared expert added by the decode layer's combine (xs_moe_layer_decode_shared)."""
+    shared expert added by the combine; router: None (the softmax top-k) or a RouterCfg (grouped_sigmoid_router)."""
 
-    def __init__(self, L, arena, n_expert, k, max_tokens, prefill=False, device="cuda", shared=None):
+    def __init__(self, L, arena, n_expert, k, max_tokens, prefill=False, device="cuda", shared=None, router=None):
         self.L, self.arena, self.n_expert, self.k, self.max_tokens = L, arena, n_expert, k, max_tokens
         self.blob = L.bytes
         self.prefill = prefill
         self.shared = shared
-        if shared is not None and prefill:
-            raise ValueError("a shared expert is supported on the decode layer")
-        if shared is not None:
+        self.router = router
+        # the _ex entry points take a router and a shared expert on either path; the plain ones keep their own
+        self.ex = router is not None or (prefill and shared is not None)
+        SLp = ctypes.byref(shared[0]) if shared is not None else None
+        if self.ex:
+            fn = lib().xs_moe_layer_prefill_ex_workspace_bytes if prefill else lib().xs_moe_layer_decode_ex_workspace_bytes
+            self.ws_bytes = fn(ctypes.byref(L), n_expert, k, max_tokens, SLp)
+        elif shared is not None:
             self.ws_bytes = lib().xs_moe_layer_decode_shared_workspace_bytes(ctypes.byref(L), n_expert, k, max_tokens,
-                                                                             ctypes.byref(shared[0]))
+                                                                             SLp)
         else:
             fn = lib().xs_moe_layer_prefill_workspace_bytes if prefill else lib().xs_moe_layer_decode_workspace_bytes
             self.ws_bytes = fn(ctypes.byref(L), n_expert, k, max_tokens)
@@ -375,18 +403,35 @@ class MoeLayer:
         torch.cuda.synchronize(self.ws.device)
         return int(self.ws[off:off + 4].view(torch.int32).item())
 
+    def check(self):
+        """Synchronize and raise XsError when the status word is not 0 (a bounded wait of the persistent layer ran
+        out - its output is not valid - or a token's router produced fewer than k experts); the word is cleared."""
+        st = self.status()
+        if st:
+            off = self.ws_ptr - self.ws.data_ptr()
+            self.ws[off:off + 4].zero_()
+            raise XsError(XS_EDEVICE, f"moe layer: status word {st:#x} (2: a bounded wait ran out, 4: NaN routing)")
+
     def __call__(self, x, logits, residual, out, n_tok=None, arena=None, stream=None):
         n_tok = x.shape[0] if n_tok is None else n_tok
+        arena = self.arena if arena is None else arena
+        if self.ex:
+            SL, sblob, w_gate = self.shared if self.shared is not None else (None, None, None)
+            fn = lib().xs_moe_layer_prefill_ex if self.prefill else lib().xs_moe_layer_decode_ex
+            _check(fn(ctypes.byref(self.L), _p(arena), self.blob, self.n_expert, self.k, _p(x), _p(logits),
+                      _p(residual), _p(out), n_tok, None if self.router is None else ctypes.addressof(self.router),
+                      None if SL is None else ctypes.byref(SL), _p(sblob), _p(w_gate), self.ws_ptr, self.ws_bytes,
+                      _stream(stream)))
+            return out
         if self.shared is not None:
             SL, sblob, w_gate = self.shared
             _check(lib().xs_moe_layer_decode_shared(
-                ctypes.byref(self.L), _p(self.arena if arena is None else arena), self.blob, self.n_expert, self.k,
-                _p(x), _p(logits), _p(residual), _p(out), n_tok, ctypes.byref(SL), _p(sblob), _p(w_gate), self.ws_ptr,
-                self.ws_bytes, _stream(stream)))
+                ctypes.byref(self.L), _p(arena), self.blob, self.n_expert, self.k, _p(x), _p(logits), _p(residual),
+                _p(out), n_tok, ctypes.byref(SL), _p(sblob), _p(w_gate), self.ws_ptr, self.ws_bytes, _stream(stream)))
             return out
         fn = lib().xs_moe_layer_prefill if self.prefill else lib().xs_moe_layer_decode
-        _check(fn(ctypes.byref(self.L), _p(self.arena if arena is None else arena), self.blob, self.n_expert, self.k,
-                  _p(x), _p(logits), _p(residual), _p(out), n_tok, self.ws_ptr, self.ws_bytes, _stream(stream)))
+        _check(fn(ctypes.byref(self.L), _p(arena), self.blob, self.n_expert, self.k, _p(x), _p(logits),
+                  _p(residual), _p(out), n_tok, self.ws_ptr, self.ws_bytes, _stream(stream)))
         return out
 
 
