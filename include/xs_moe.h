@@ -95,6 +95,31 @@ int xs_iq_dequant_f32(int type, const void* src, int64_t n, float* dst, void* st
 /* The same values rounded to bf16 (nearest even): the prompt path's dequantizer.  Replaces dequant_f16 /
  * iq_dequant_f16 (include/strata/kernels/dequant_bf16.hpp:23-25, iq_kernels.hpp:29), which produce FP16. */
 int xs_iq_dequant_bf16(int type, const void* src, int64_t n, uint16_t* dst, void* stream);
+/* The same values rounded to FP16 (nearest even; IEEE half bits): the reference's iq_dequant_f16
+ * (include/strata/kernels/iq_kernels.hpp:29, the FP16 prompt fallback's weights). */
+int xs_iq_dequant_f16(int type, const void* src, int64_t n, uint16_t* dst, void* stream);
+
+/* The int8 activations of the reference's MMQ products (include/strata/kernels/iq_mmq.hpp:33-50;
+ * src/kernels/xe/iq_mmq.cpp:1264-1341), byte for byte: rows of `cols` values (a multiple of 32; 2 cols when `dup`,
+ * every block twice) as int8 q[rows][oc] | float d[rows][oc/32] | float d*sum(q)[rows][oc/32] (the sums written only
+ * when `sums`).  d = amax / 127, q = round-half-away(v / d).  xs_iq_mmq_act_bytes replaces iq_mmq_act_bytes;
+ * xs_iq_mmq_type_sums / _dup replace iq_mmq_type_sums / iq_mmq_type_dup (iq_mmq.hpp:33-38). */
+size_t xs_iq_mmq_act_bytes(int64_t rows, int64_t cols);
+int xs_iq_mmq_type_sums(int type);
+int xs_iq_mmq_type_dup(int type);
+/* Row i of xq from row ids[i] of x (row i when ids is NULL), ld floats a row of x.  Replaces iq_mmq_quantize
+ * (iq_mmq.hpp:39-41) and prefill::mmq::quantize (include/strata/prefill/moe_mmq.hpp:46-49). */
+int xs_iq_mmq_quantize(const float* x, const int32_t* ids, void* xq, int64_t cols, int64_t ld, int64_t rows, int sums,
+                       int dup, void* stream);
+/* Token t's row quantized once, stored at rows slot[t * k_used + j] of xq (tokens * k_used rows).  Replaces
+ * iq_mmq_quantize_scatter (iq_mmq.hpp:42-47) and prefill::mmq::quantize_scatter (moe_mmq.hpp:50-55). */
+int xs_iq_mmq_quantize_scatter(const float* x, const int32_t* slot, void* xq, int64_t cols, int64_t ld,
+                               int64_t tokens, int k_used, int sums, int dup, void* stream);
+/* h[r, j] = g / (1 + exp(-g)) * u over rows of 2 n_ff floats (gate, up interleaved 2j / 2j+1, or split j / n_ff+j).
+ * Replaces prefill::mmq::swiglu (moe_mmq.hpp:106-108; src/prefill/moe_mmq.cpp:128-136). */
+int xs_mmq_swiglu(const float* gu, float* h, int64_t rows, int64_t n_ff, int interleaved, void* stream);
+/* dst[i] = i, i < n.  Replaces prefill::mmq::iota (moe_mmq.hpp:110; moe_mmq.cpp:138-140). */
+int xs_mmq_iota(int32_t* dst, int64_t n, void* stream);
 
 /* This library's quantizer: n floats (a whole number of blocks) to `type` blocks.  No reference counterpart (the
  * reference's tests call ggml_quantize_chunk, src/kernels/native_expert_parity.cpp:483-487). */
@@ -113,10 +138,39 @@ int xs_router_top10(const float* logits, int n_tokens, int n_expert, int k, int3
 int xs_router_grouped_sigmoid(const float* logits, const float* bias, int n_tokens, int n_expert, int n_group,
                               int topk_group, int k, float routed_scale, int32_t* ids, float* weights, void* stream);
 
-/* Router logits logits[t, e] = x[t] . w[e] in fp32 (w: n_expert rows of n_embd floats).  Replaces the F32 router
- * GEMV f32_gemv_fp32_mmvf_multi / f32_gemm_rows (src/kernels/xe/bf16_gemv.cpp:464-517). */
+/* Router logits logits[t, e] = x[t] . w[e] in fp32 (w: n_expert rows of n_embd floats, n_embd even): up to 8 tokens
+ * in the decode GEMV's order (xs_f32_gemv_fp32_mmvf_multi), more in the prompt GEMM's (xs_f32_gemm_rows), so the
+ * logits are the reference's bits (src/core/plain_model.cpp:955 and src/prefill/plain_prompt.cpp:561). */
 int xs_router_logits_f32(const float* x, const float* w, float* logits, int n_tokens, int64_t n_embd, int n_expert,
                          void* stream);
+
+/* The reference's projection kernels, each in its own summation order (bit for bit its logits):
+ * y[t * ldy + o] = x[t * ldx + .] . w[o * n_in + .].
+ * - mmvf: B threads a row (the candidate of 32..256 with the fewest pair iterations), two ordered FMAs a pair, a
+ *   32-lane xor butterfly, then one over the B/32 partials; 1..8 tokens, n_in even, x 8-byte aligned.  Replace
+ *   f32_gemv_fp32_mmvf(_multi) and bf16_gemv_fp32_mmvf(_multi) (src/kernels/xe/bf16_gemv.cpp:91-147, 440-517).
+ * - gemm_rows: one FMA chain a logit over k = 0.. n_in - 1 (then zeros to a multiple of 16), any token count.
+ *   Replaces f32_gemm_rows (bf16_gemv.cpp:475-502; the prompt path's router and shared gate). */
+int xs_f32_gemv_fp32_mmvf_multi(const float* x, int64_t ldx, const float* w, float* y, int64_t ldy, int64_t n_in,
+                                int64_t n_out, int n_tok, void* stream);
+int xs_bf16_gemv_fp32_mmvf_multi(const float* x, int64_t ldx, const uint16_t* w, float* y, int64_t ldy, int64_t n_in,
+                                 int64_t n_out, int n_tok, void* stream);
+int xs_f32_gemm_rows(const float* x, int64_t ldx, const float* w, float* y, int64_t ldy, int64_t n_in, int64_t n_out,
+                     int64_t n_tok, void* stream);
+/* f32 -> bf16 bits, nearest even, a NaN kept and quieted.  Replaces f32_to_bf16_bulk
+ * (include/strata/kernels/elementwise.hpp:71; bf16_bits.hpp:39-45). */
+int xs_f32_to_bf16_bulk(const float* x, uint16_t* y, int64_t n, void* stream);
+/* bf16 x against bf16 rows: bf16_gemv (32 lanes a row for n_out >= 64, one chain a row below) and bf16_gemv_split
+ * (32 threads: the same 32-lane rows; another power of two: lane chains then a shared-memory tree).  Replace
+ * bf16_gemv / bf16_gemv_split (include/strata/kernels/bf16_gemv.hpp:30-39; bf16_gemv.cpp:50-77, 300-339). */
+int xs_bf16_gemv(const uint16_t* x, const uint16_t* w, float* y, int64_t n_in, int64_t n_out, void* stream);
+int xs_bf16_gemv_split(const uint16_t* x, const uint16_t* w, float* y, int64_t n_in, int64_t n_out,
+                       int threads_per_row, void* stream);
+/* The BF16 router projection of the engine's moe_route: native -> bf16_gemv_fp32_mmvf (f32 x); else x rounded to
+ * x_bf16, then bf16_gemv_split at 32 threads (split) or bf16_gemv.  x_bf16 NULL with split: the rounding is done
+ * inside the GEMV (the same bits, one launch, no bf16 copy).  Replaces project_bf16 (src/core/layer.cpp:100-107). */
+int xs_project_bf16(const float* x, uint16_t* x_bf16, const uint16_t* w, float* out, int64_t n_in, int64_t n_out,
+                    int split, int native, void* stream);
 
 /* The decode / verify-window plan built on the device when every routed expert is resident, in the host pool's
  * layout (counts | start | dst | tok | pad | ptr | ptr2 | start2, capx entries): distinct experts in routing order,
@@ -158,6 +212,12 @@ int xs_native_moe_combine(const float* parts, const float* weights, const float*
                           int64_t n_embd, int64_t k, void* stream);
 int xs_native_moe_combine_multi(const float* parts, const float* weights, const float* shared, float* output,
                                 int64_t n_embd, int64_t k, int n_tok, void* stream, const float* shared_gate);
+/* combine_multi with the tier path's hit rows folded in: entries dst[0, *count) (entry = token * k + rank) read
+ * parts + hits, the sum moe_hit_add would leave, before their product.  Replaces native_moe_combine_multi_hits
+ * (include/strata/kernels/native_moe.hpp:27-32; src/kernels/xe/native_moe.cpp:67-110). */
+int xs_native_moe_combine_multi_hits(const float* parts, const float* hits, const int32_t* dst, const int32_t* count,
+                                     const float* weights, const float* shared, float* output, int64_t n_embd,
+                                     int64_t k, int n_tok, void* stream, const float* shared_gate);
 /* The combine with the residual add fused: output = residual + combine (output may equal residual).  The reference
  * runs native_moe_combine_multi then add_inplace (src/core/plain_model.cpp:985-987). */
 int xs_moe_combine_residual(const float* parts, const float* weights, const float* shared, const float* shared_gate,
@@ -181,6 +241,11 @@ size_t xs_moe_layer_decode_workspace_bytes(const xs_expert_layout_t* L, int n_ex
  * output.  Bits stay set until the caller clears the word; the workspace itself needs no reset after an error.  No
  * counterpart in the reference (its layer reports through host-side checks of each launch). */
 int32_t* xs_moe_layer_decode_status(void* workspace);
+/* The checked contract of the persistent layer: synchronises `stream`, reads the status word; 0 -> XS_OK; else clears
+ * it and returns XS_EDEVICE with the bits named (an expired bounded wait means other work held CUs the layer's
+ * work-groups needed, and that call's output is not to be used).  Call it at the next synchronisation point after
+ * a layer call (or a run of them).  Not to be called inside a graph capture.  No counterpart in the reference. */
+int xs_moe_status_check(int32_t* status, void* stream);
 
 /* xs_moe_layer_decode without a caller workspace, for callers that cannot allocate device memory (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc).  No counterpart in the reference.  The layer

@@ -109,6 +109,29 @@ inline void iq_dequant_f32(int ggml_type, const void* src, int64_t n, float* dst
     detail::check(xs_iq_dequant_f32(ggml_type, src, n, dst, stream));
 }
 
+/// include/strata/kernels/iq_kernels.hpp:32 (IEEE half bits)
+inline void iq_dequant_f16(int ggml_type, const void* src, int64_t n, uint16_t* dst, void* stream) {
+    detail::check(xs_iq_dequant_f16(ggml_type, src, n, dst, stream));
+}
+
+/// include/strata/kernels/iq_mmq.hpp:33 (the int8 activations' bytes)
+inline size_t iq_mmq_act_bytes(int64_t rows, int64_t cols) { return xs_iq_mmq_act_bytes(rows, cols); }
+/// include/strata/kernels/iq_mmq.hpp:35
+inline bool iq_mmq_type_sums(int ggml_type) { return xs_iq_mmq_type_sums(ggml_type) != 0; }
+/// include/strata/kernels/iq_mmq.hpp:38
+inline bool iq_mmq_type_dup(int ggml_type) { return xs_iq_mmq_type_dup(ggml_type) != 0; }
+/// include/strata/kernels/iq_mmq.hpp:39-41; the reference's sycl::queue& is the stream here, and the call is
+/// asynchronous on it (the reference returns the event)
+inline void iq_mmq_quantize(void* stream, const float* x, const int32_t* ids, void* xq, int64_t cols, int64_t ld,
+                            int64_t rows, bool sums, bool dup = false) {
+    detail::check(xs_iq_mmq_quantize(x, ids, xq, cols, ld, rows, sums, dup, stream));
+}
+/// include/strata/kernels/iq_mmq.hpp:46-47
+inline void iq_mmq_quantize_scatter(void* stream, const float* x, const int32_t* slot, void* xq, int64_t cols,
+                                    int64_t ld, int64_t tokens, int k_used, bool sums, bool dup = false) {
+    detail::check(xs_iq_mmq_quantize_scatter(x, slot, xq, cols, ld, tokens, k_used, sums, dup, stream));
+}
+
 /// include/strata/kernels/iq_kernels.hpp:90-93
 inline void native_expert_grouped(const NativeExpertLayout& L, const unsigned long long* grp_ptr,
                                   const int32_t* grp_start, const int32_t* n_groups, const int32_t* ent_dst,
@@ -151,9 +174,83 @@ inline void native_moe_combine_multi(const float* parts, const float* weights, c
     detail::check(xs_native_moe_combine_multi(parts, weights, shared, output, n_embd, k, n_tok, stream, shared_gate));
 }
 
+/// include/strata/kernels/native_moe.hpp:30-32
+inline void native_moe_combine_multi_hits(const float* parts, const float* hits, const int32_t* dst,
+                                          const int32_t* count, const float* weights, const float* shared,
+                                          float* output, int64_t n_embd, int64_t k, int n_tok, void* stream,
+                                          const float* shared_gate = nullptr) {
+    if (!stream)
+        throw std::invalid_argument("native MoE combine (hits) requires a stream, width, 1..15 experts, tokens, hits");
+    detail::check(xs_native_moe_combine_multi_hits(parts, hits, dst, count, weights, shared, output, n_embd, k, n_tok,
+                                                   stream, shared_gate));
+}
+/// include/strata/kernels/native_moe.hpp:29: this library always fuses the hit add
+inline bool native_moe_fuse_hits() { return true; }
+
 /// src/core/plain_model.cpp:987 (add_inplace)
 inline void add_inplace(float* x, const float* y, int64_t n, void* stream) {
     detail::check(xs_add_inplace(x, y, n, stream));
 }
 
+/// The whole decode MoE layer (the engine's moe_route + moe_finish, src/core/plain_model.cpp:951-988) in one call,
+/// every expert resident in `arena`.  Asynchronous: the persistent form's co-residency is a checked contract, so the
+/// caller runs moe_layer_check(workspace, stream) at its next synchronisation point, which throws
+/// core::DeviceError when a bounded wait expired (the layer's work-groups were not all resident) or a router row was
+/// NaN; that call's output is then not to be used.
+inline void moe_layer_decode(const NativeExpertLayout& L, const uint8_t* arena, size_t blob_bytes, int n_expert, int k,
+                             const float* x, const float* logits, const float* residual, float* out, int n_tok,
+                             void* workspace, size_t workspace_bytes, void* stream) {
+    if (!stream) throw std::invalid_argument("moe_layer_decode requires an explicit stream");
+    const xs_expert_layout_t c = detail::to_c(L);
+    detail::check(xs_moe_layer_decode(&c, arena, blob_bytes, n_expert, k, x, logits, residual, out, n_tok, workspace,
+                                      workspace_bytes, stream));
+}
+inline size_t moe_layer_decode_workspace_bytes(const NativeExpertLayout& L, int n_expert, int k, int n_tok) {
+    const xs_expert_layout_t c = detail::to_c(L);
+    return xs_moe_layer_decode_workspace_bytes(&c, n_expert, k, n_tok);
+}
+/// Synchronises `stream` and throws core::DeviceError when the decode workspace's status word is set (then cleared).
+inline void moe_layer_check(void* workspace, void* stream) {
+    detail::check(xs_moe_status_check(xs_moe_layer_decode_status(workspace), stream));
+}
+/// The prompt / verify layer (src/prefill/plain_prompt.cpp:558-797) in one call.
+inline void moe_layer_prefill(const NativeExpertLayout& L, const uint8_t* arena, size_t blob_bytes, int n_expert,
+                              int k, const float* x, const float* logits, const float* residual, float* out, int n_tok,
+                              void* workspace, size_t workspace_bytes, void* stream) {
+    if (!stream) throw std::invalid_argument("moe_layer_prefill requires an explicit stream");
+    const xs_expert_layout_t c = detail::to_c(L);
+    detail::check(xs_moe_layer_prefill(&c, arena, blob_bytes, n_expert, k, x, logits, residual, out, n_tok, workspace,
+                                       workspace_bytes, stream));
+}
+inline size_t moe_layer_prefill_workspace_bytes(const NativeExpertLayout& L, int n_expert, int k, int n_tok) {
+    const xs_expert_layout_t c = detail::to_c(L);
+    return xs_moe_layer_prefill_workspace_bytes(&c, n_expert, k, n_tok);
+}
+
 }  // namespace strata::kernels
+
+namespace strata::prefill::mmq {
+
+/// include/strata/prefill/moe_mmq.hpp:41-43
+inline size_t q8_bytes(int64_t rows, int64_t cols) { return xs_iq_mmq_act_bytes(rows, cols); }
+/// include/strata/prefill/moe_mmq.hpp:46-49
+inline void quantize(const float* x, const int32_t* ids, void* xq, int ggml_type, int64_t cols, int64_t ld,
+                     int64_t rows, void* stream) {
+    kernels::detail::check(xs_iq_mmq_quantize(x, ids, xq, cols, ld, rows, xs_iq_mmq_type_sums(ggml_type),
+                                              xs_iq_mmq_type_dup(ggml_type), stream));
+}
+/// include/strata/prefill/moe_mmq.hpp:50-55 (src, the gathered form's map, is not needed by the scatter)
+inline void quantize_scatter(const float* x, const int32_t* slot, const int32_t* /*src*/, void* xq, int ggml_type,
+                             int64_t cols, int64_t ld, int64_t tokens, int k_used, void* stream) {
+    kernels::detail::check(xs_iq_mmq_quantize_scatter(x, slot, xq, cols, ld, tokens, k_used,
+                                                      xs_iq_mmq_type_sums(ggml_type), xs_iq_mmq_type_dup(ggml_type),
+                                                      stream));
+}
+/// include/strata/prefill/moe_mmq.hpp:106-108
+inline void swiglu(const float* gu, float* h, int64_t rows, int64_t n_ff, bool interleaved, void* stream) {
+    kernels::detail::check(xs_mmq_swiglu(gu, h, rows, n_ff, interleaved, stream));
+}
+/// include/strata/prefill/moe_mmq.hpp:110
+inline void iota(int32_t* dst, int64_t n, void* stream) { kernels::detail::check(xs_mmq_iota(dst, n, stream)); }
+
+}  // namespace strata::prefill::mmq

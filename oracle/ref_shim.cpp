@@ -1,9 +1,10 @@
 // oracle/ref_shim.cpp - C entry points over the reference's own header-only host code, compiled (by oracle/Makefile,
-// into oracle/_ref/) from include/strata/artifact/dequant.hpp, include/strata/kernels/canon_math.hpp and
-// include/strata/artifact/gguf_reader.hpp where they lie in the reference tree.  TEST INFRASTRUCTURE: it validates
+// into oracle/_ref/) from include/strata/artifact/dequant.hpp, include/strata/kernels/canon_math.hpp,
+// include/strata/kernels/bf16_bits.hpp and include/strata/artifact/gguf_reader.hpp where they lie in the reference tree.  TEST INFRASTRUCTURE: it validates
 // oracle/xs_oracle.c's restatement and writes tests/golden's vectors; it is never part of the product.
 #include "strata/artifact/dequant.hpp"
 #include "strata/kernels/canon_math.hpp"
+#include "strata/kernels/bf16_bits.hpp"
 
 #include <cmath>
 #include <cstdint>
@@ -34,6 +35,9 @@ void xsref_canon_rcp(const float* x, int64_t n, float* y) {
 }
 void xsref_canon_silu_mul(const float* g, const float* u, int64_t n, float* h) {
     for (int64_t i = 0; i < n; ++i) h[i] = strata::kernels::canon::silu_mul(g[i], u[i]);
+}
+void xsref_bf16_from_f32(const float* x, int64_t n, uint16_t* y) {
+    for (int64_t i = 0; i < n; ++i) y[i] = strata::kernels::bf16_from_f32(x[i]);
 }
 void xsref_canon_q8(const float* x, int64_t n, float* d, float* id, int8_t* q) {
     // n values as one block: the scale of their largest magnitude (fmax of fabs, as the kernels reduce it: a

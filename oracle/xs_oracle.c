@@ -867,3 +867,93 @@ void xso_moe_layer_decode(const xso_layout* L, const uint8_t* const* blobs_by_ex
     for (int64_t i = 0; i < (int64_t)n_tok * H; ++i) out[i] = residual[i] + out[i];
     free(ids); free(w); free(start); free(dst); free(tok); free(gexp); free(xq); free(parts); free(gblob);
 }
+
+/* ------------------------------------------------------------------------------------------------ router projections */
+
+static float bf(uint16_t b) { return u2f((uint32_t)b << 16); }
+
+/* the 32-lane xor butterfly of warp_sum (src/kernels/xe/bf16_gemv.cpp:43-46): v[l] += v[l ^ off], off 16 .. 1, all
+ * lanes at once; lane 0's value */
+static float butterfly32_sum(float* v) {
+    for (int off = 16; off > 0; off >>= 1) {
+        float n[32];
+        for (int l = 0; l < 32; ++l) n[l] = v[l] + v[l ^ off];
+        memcpy(v, n, sizeof n);
+    }
+    return v[0];
+}
+
+/* mmvf_block_size (bf16_gemv.cpp:213-225) */
+int xso_mmvf_block(int64_t n_in) {
+    int best = 32;
+    int64_t best_it = (n_in + 63) / 64;
+    for (int c = 64; c <= 256; c += 32) {
+        const int64_t it = (n_in + 2 * c - 1) / (2 * c);
+        if (it < best_it) { best_it = it; best = c; }
+    }
+    return best;
+}
+
+/* launch_mmvf (bf16_gemv.cpp:91-147): w_bf16 non-NULL selects the BF16 weights, else w_f32 */
+void xso_mmvf(const float* x, int64_t ldx, const float* w_f32, const uint16_t* w_bf16, float* y, int64_t ldy,
+              int64_t n_in, int64_t n_out, int n_tok) {
+    const int B = xso_mmvf_block(n_in);
+    const int64_t pairs = n_in / 2;
+    float* acc = (float*)malloc(sizeof(float) * (size_t)B);
+    for (int64_t o = 0; o < n_out; ++o)
+        for (int k = 0; k < n_tok; ++k) {
+            for (int t = 0; t < B; ++t) {
+                float a = 0.0f;
+                for (int64_t p = t; p < pairs; p += B) {
+                    const float w0 = w_bf16 ? bf(w_bf16[o * n_in + 2 * p]) : w_f32[o * n_in + 2 * p];
+                    const float w1 = w_bf16 ? bf(w_bf16[o * n_in + 2 * p + 1]) : w_f32[o * n_in + 2 * p + 1];
+                    a = fmaf(w0, x[k * ldx + 2 * p], a);
+                    a = fmaf(w1, x[k * ldx + 2 * p + 1], a);
+                }
+                acc[t] = a;
+            }
+            float part[32] = {0};
+            for (int g = 0; g < B / 32; ++g) {
+                float v[32];
+                memcpy(v, acc + 32 * g, sizeof v);
+                part[g] = butterfly32_sum(v);
+            }
+            y[k * ldy + o] = B > 32 ? butterfly32_sum(part) : part[0];
+        }
+    free(acc);
+}
+
+/* f32_gemm_rows (bf16_gemv.cpp:475-502): acc = fma(x[t][k], w[o][k], acc), k up to the next multiple of 16 (zeros) */
+void xso_gemm_rows(const float* x, int64_t ldx, const float* w, float* y, int64_t ldy, int64_t n_in, int64_t n_out,
+                   int64_t n_tok) {
+    const int64_t k_end = (n_in + 15) / 16 * 16;
+    for (int64_t t = 0; t < n_tok; ++t)
+        for (int64_t o = 0; o < n_out; ++o) {
+            float a = 0.0f;
+            for (int64_t k = 0; k < k_end; ++k)
+                a = k < n_in ? fmaf(x[t * ldx + k], w[o * n_in + k], a) : fmaf(0.0f, 0.0f, a);
+            y[t * ldy + o] = a;
+        }
+}
+
+/* bf16 x . bf16 rows: form 0 launch_warp (bf16_gemv.cpp:62-77), 1 launch_naive (50-60), 2 the split tree at tpr
+ * threads (318-339).  Products of bf16 values are exact in f32, so fmaf and the reference's `acc += a * b` agree. */
+void xso_bf16_gemv(const uint16_t* x, const uint16_t* w, float* y, int64_t n_in, int64_t n_out, int form, int tpr) {
+    const int lanes = form == 0 ? 32 : form == 1 ? 1 : tpr;
+    float* acc = (float*)malloc(sizeof(float) * (size_t)lanes);
+    for (int64_t o = 0; o < n_out; ++o) {
+        for (int l = 0; l < lanes; ++l) {
+            float a = 0.0f;
+            for (int64_t i = l; i < n_in; i += lanes) a = fmaf(bf(x[i]), bf(w[o * n_in + i]), a);
+            acc[l] = a;
+        }
+        if (form == 0) y[o] = butterfly32_sum(acc);
+        else if (form == 1) y[o] = acc[0];
+        else {
+            for (int off = lanes >> 1; off > 0; off >>= 1)
+                for (int l = 0; l < off; ++l) acc[l] = acc[l] + acc[l + off];
+            y[o] = acc[0];
+        }
+    }
+    free(acc);
+}

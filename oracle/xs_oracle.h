@@ -103,6 +103,14 @@ void xso_moe_layer_decode_shared(const xso_layout* L, const uint8_t* const* blob
                                  const xso_layout* SL, const uint8_t* shared_blob, const float* gate_logit, float* out,
                                  int n_threads);
 
+/* ---- the router projections in the reference's orders (src/kernels/xe/bf16_gemv.cpp) */
+int xso_mmvf_block(int64_t n_in);
+void xso_mmvf(const float* x, int64_t ldx, const float* w_f32, const uint16_t* w_bf16, float* y, int64_t ldy,
+              int64_t n_in, int64_t n_out, int n_tok);
+void xso_gemm_rows(const float* x, int64_t ldx, const float* w, float* y, int64_t ldy, int64_t n_in, int64_t n_out,
+                   int64_t n_tok);
+void xso_bf16_gemv(const uint16_t* x, const uint16_t* w, float* y, int64_t n_in, int64_t n_out, int form, int tpr);
+
 #ifdef __cplusplus
 }
 #endif

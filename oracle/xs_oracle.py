@@ -71,6 +71,10 @@ def lib():
         L.xso_canon_silu_mul_n.argtypes = [P, P, I64, P]
         L.xso_canon_exp_n.argtypes = [P, I64, P]
         L.xso_canon_rcp_n.argtypes = [P, I64, P]
+        L.xso_mmvf_block.argtypes = [I64]
+        L.xso_mmvf.argtypes = [P, I64, P, P, P, I64, I64, I64, I]
+        L.xso_gemm_rows.argtypes = [P, I64, P, P, I64, I64, I64, I64]
+        L.xso_bf16_gemv.argtypes = [P, P, P, I64, I64, I, I]
         _lib = L
     return _lib
 
@@ -87,6 +91,7 @@ def ref():
         R.xsref_canon_rcp.argtypes = [P, I64, P]
         R.xsref_canon_silu_mul.argtypes = [P, P, I64, P]
         R.xsref_canon_q8.argtypes = [P, I64, P, P, P]
+        R.xsref_bf16_from_f32.argtypes = [P, I64, P]
         _ref = R
     return _ref
 
@@ -289,6 +294,78 @@ def moe_layer_decode_shared(L, blobs_by_expert, k, x, logits, residual, SL, shar
                                       _a(residual), x.shape[0], ctypes.byref(SL), _a(sb),
                                       None if g is None else _a(g), _a(out), n_threads)
     return out
+
+
+def bf16_from_f32(x):
+    """include/strata/kernels/bf16_bits.hpp:39-45 (uint16 bits): nearest even on bit 16, a NaN kept with bit 6 set."""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + ((u >> 16) & 1) + 0x7FFF) & 0xFFFF0000) >> 16
+    return np.where(nan, (u >> 16) | 64, r).astype(np.uint16)
+
+
+def mmvf(x, w, n_tok=None):
+    """The decode GEMV's order (bf16_gemv.cpp:91-147): x [n_tok, n_in] f32, w [n_out, n_in] f32 or bf16 bits
+    (uint16) -> [n_tok, n_out]."""
+    x = np.ascontiguousarray(x, np.float32)
+    n_tok = x.shape[0] if n_tok is None else n_tok
+    n_out, n_in = w.shape
+    y = np.zeros((n_tok, n_out), np.float32)
+    if w.dtype == np.uint16:
+        lib().xso_mmvf(_a(x), x.shape[1], None, _a(np.ascontiguousarray(w)), _a(y), n_out, n_in, n_out, n_tok)
+    else:
+        lib().xso_mmvf(_a(x), x.shape[1], _a(np.ascontiguousarray(w, np.float32)), None, _a(y), n_out, n_in, n_out,
+                       n_tok)
+    return y
+
+
+def gemm_rows(x, w):
+    """The prompt GEMM's order (bf16_gemv.cpp:475-502)."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    y = np.zeros((x.shape[0], w.shape[0]), np.float32)
+    lib().xso_gemm_rows(_a(x), x.shape[1], _a(w), _a(y), w.shape[0], x.shape[1], w.shape[0], x.shape[0])
+    return y
+
+
+def bf16_gemv(x_bits, w_bits, form, tpr=32):
+    """bf16 x . bf16 rows in launch_warp (form 0), launch_naive (1) or the split tree (2) order."""
+    w_bits = np.ascontiguousarray(w_bits, np.uint16)
+    y = np.zeros(w_bits.shape[0], np.float32)
+    lib().xso_bf16_gemv(_a(np.ascontiguousarray(x_bits, np.uint16)), _a(w_bits), _a(y), w_bits.shape[1],
+                        w_bits.shape[0], form, tpr)
+    return y
+
+
+def mmq_quantize(x, ids, cols, rows, sums, dup=False):
+    """The int8 MMQ activations (src/kernels/xe/iq_mmq.cpp:1264-1302, iq_mmq_act_bytes and iq_mmq_quantize) as the
+    bytes the reference lays out: int8 q[rows][oc] | f32 d[rows][oc/32] | f32 d*sum(q)[rows][oc/32] (zeros where
+    `sums` is off), oc = 2 cols with `dup` (each block twice).  Per block: d = amax / 127 and id = 1 / d (0 when
+    amax == 0) in float32 (IEEE division), q = round half away from zero of fl(v * id) (sycl::round)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    src = np.arange(rows) if ids is None else np.asarray(ids, dtype=np.int64)
+    v = x[src, :cols].reshape(rows, cols // 32, 32)
+    amax = np.max(np.abs(v), axis=2)
+    with np.errstate(divide="ignore"):
+        d = (amax / np.float32(127.0)).astype(np.float32)
+        idv = np.where(amax > 0, np.float32(1.0) / np.where(d > 0, d, np.float32(1.0)), np.float32(0.0))
+    prod = (v * idv.astype(np.float32)[:, :, None]).astype(np.float32).astype(np.float64)
+    q = (np.sign(prod) * np.floor(np.abs(prod) + 0.5)).astype(np.int64)
+    s = (d * q.sum(axis=2).astype(np.float32)).astype(np.float32)
+    rep = 2 if dup else 1
+    q8 = np.repeat(q.astype(np.int8), rep, axis=1).reshape(rows, cols * rep)
+    dd = np.repeat(d, rep, axis=1)
+    ss = np.repeat(s, rep, axis=1) if sums else np.zeros_like(dd)
+    return np.concatenate([q8.view(np.uint8).ravel(), dd.view(np.uint8).ravel(), ss.view(np.uint8).ravel()])
+
+
+def mmq_quantize_parts(buf, rows, oc):
+    """Split mmq_quantize's bytes into (q int8 [rows, oc], d f32 [rows, oc/32], s f32 [rows, oc/32])."""
+    nb = oc // 32
+    q = buf[:rows * oc].view(np.int8).reshape(rows, oc)
+    d = buf[rows * oc:rows * oc + 4 * rows * nb].view(np.float32).reshape(rows, nb)
+    s = buf[rows * oc + 4 * rows * nb:rows * oc + 8 * rows * nb].view(np.float32).reshape(rows, nb)
+    return q, d, s
 
 
 def rel_max(a, b):

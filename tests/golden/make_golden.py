@@ -104,6 +104,19 @@ def main():
     out["q8_d"] = np.array(q8_d, np.float32)
     out["q8_id"] = np.array(q8_id, np.float32)
     out["q8_q"] = np.concatenate(q8_q)
+    # bf16_from_f32 (bf16_bits.hpp): random magnitudes, exact ties on both parities, the carry into the exponent, the
+    # largest finite values (rounding to inf), NaNs whose rounding add would carry, infinities, zeros, subnormals
+    rb = np.random.default_rng(20261202)
+    bits = np.concatenate([
+        (rb.standard_normal(4096) * np.exp(rb.uniform(-40, 40, 4096))).astype(np.float32).view(np.uint32),
+        np.array([0x3F808000, 0x3F818000, 0xBF808000, 0xBF818000, 0x3F7FFFFF, 0x3F7F8000, 0x7F7FFFFF, 0x7F7F8000,
+                  0xFF7FFFFF, 0x7F7F7FFF, 0x7FFFFFFF, 0x7F800001, 0xFFC00001, 0x7FC00000, 0xFF800001, 0x7F800000,
+                  0xFF800000, 0x00000000, 0x80000000, 0x00008000, 0x00018000, 0x00000001, 0x807FFFFF], np.uint32),
+        rb.integers(0, 2**32, 1024, dtype=np.uint64).astype(np.uint32)])
+    bx = bits.view(np.float32)
+    by = np.zeros(bx.size, np.uint16)
+    R.xsref_bf16_from_f32(xo._a(bx), bx.size, xo._a(by))
+    out["bf16_x"], out["bf16_y"] = bx, by
     np.savez_compressed(HERE / "reference_vectors.npz", **out)
 
     with tempfile.TemporaryDirectory() as tmp:

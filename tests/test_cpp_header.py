@@ -19,8 +19,30 @@ CXX = shutil.which("g++")
 USE = r"""
 #include "xs_strata_kernels.hpp"
 #include <cstdio>
-int main() {
+// every wrapper of the prompt and layer surface, compiled and linked; main calls it only with a stream, never here
+void surface(void* stream) {
     namespace k = strata::kernels;
+    namespace m = strata::prefill::mmq;
+    const k::NativeExpertLayout L = k::native_expert_layout(12, 14, 2048, 768);
+    k::iq_dequant_f16(12, nullptr, 256, nullptr, stream);
+    k::iq_mmq_quantize(stream, nullptr, nullptr, nullptr, 256, 256, 1, k::iq_mmq_type_sums(12), k::iq_mmq_type_dup(12));
+    k::iq_mmq_quantize_scatter(stream, nullptr, nullptr, nullptr, 256, 256, 1, 8, true);
+    m::quantize(nullptr, nullptr, nullptr, 12, 256, 256, 1, stream);
+    m::quantize_scatter(nullptr, nullptr, nullptr, nullptr, 12, 256, 256, 1, 8, stream);
+    m::swiglu(nullptr, nullptr, 1, 768, false, stream);
+    m::iota(nullptr, 16, stream);
+    k::native_moe_combine_multi_hits(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 2048, 8, 1, stream);
+    const size_t ws = k::moe_layer_decode_workspace_bytes(L, 128, 8, 1);
+    k::moe_layer_decode(L, nullptr, L.bytes, 128, 8, nullptr, nullptr, nullptr, nullptr, 1, nullptr, ws, stream);
+    k::moe_layer_check(nullptr, stream);
+    k::moe_layer_prefill(L, nullptr, L.bytes, 128, 8, nullptr, nullptr, nullptr, nullptr, 64, nullptr,
+                         k::moe_layer_prefill_workspace_bytes(L, 128, 8, 64), stream);
+    std::printf("%zu %d\n", m::q8_bytes(4, 256), (int)k::native_moe_fuse_hits());
+}
+
+int main(int argc, char** argv) {
+    namespace k = strata::kernels;
+    if (argc > 1) surface(argv[1]);
     const k::NativeExpertLayout L = k::native_expert_layout(12, 14, 2048, 768);
     std::printf("%zu %d\n", L.bytes, (int)k::native_expert_supported(12, 14, 2048, 768));
     try {

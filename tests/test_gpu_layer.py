@@ -326,3 +326,7 @@ def test_decode_one_token_nan_routing(xm, c2_arena):
     torch.cuda.synchronize()
     assert layer.status() & 4
     assert torch.all(out == 7.0)
+    with pytest.raises(xm.XsError, match="fewer than k experts"):   # the checked contract: raises, then clears
+        layer.check()
+    assert layer.status() == 0
+    layer.check()

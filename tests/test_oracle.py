@@ -469,3 +469,167 @@ def test_combine_replay(xo):
                 s = (s + sh[t]).astype(np.float32)
             want[t] = s
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+# ------------------------------------------------------------------------------------------------ int8 MMQ activations
+
+def _mmq_blocks(rows=64, cols=256, seed=7):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((rows, cols)).astype(np.float32) * np.float32(0.05)
+    x[0, :32] = 0.0                                   # an all-zero block: d = 0, id = 0, q = 0
+    x[1, 40] = 3.0e4                                  # one outlier owns its block
+    x[2, :32] = np.linspace(-1, 1, 32, dtype=np.float32)
+    x[3, :32] = -7.5e-20                              # a tiny block (below ~3.7e-37 the inverse overflows to inf and
+                                                      # the reference's float -> int conversion is undefined)
+    return x
+
+
+def test_mmq_quantize_round_to_nearest_bound(xo):
+    """Every code is a nearest integer to v / d, computed in float64 (|v - q d| <= d/2, up to the one float32
+    rounding of v * id); |q| <= 127 and the block's largest |v| takes |q| = 127; a zero block is all zeros.  A
+    wrong scale (128, 255), a truncation for the rounding or a wrong block index fails this."""
+    x = _mmq_blocks()
+    rows, cols = x.shape
+    q, d, s = xo.mmq_quantize_parts(xo.mmq_quantize(x, None, cols, rows, True), rows, cols)
+    v = x.reshape(rows, cols // 32, 32).astype(np.float64)
+    qq = q.reshape(rows, cols // 32, 32).astype(np.float64)
+    dd = d.astype(np.float64)[:, :, None]
+    assert np.all(np.abs(qq) <= 127)
+    err = np.abs(v - qq * dd)
+    assert np.all(err <= dd * (0.5 + 1e-5) + 1e-45)
+    amax = np.abs(v).max(axis=2)
+    live = amax > 0
+    assert np.all(np.abs(qq).max(axis=2)[live] == 127)
+    assert np.all(qq[~live] == 0) and np.all(d[~live] == 0)
+    np.testing.assert_array_equal(d, amax.astype(np.float32) / np.float32(127))
+
+
+def test_mmq_quantize_halves_round_away(xo):
+    """sycl::round takes halves away from zero: with amax = 127 the scale is 1 and the inverse 1, so 2.5 -> 3,
+    -2.5 -> -3, 0.5 -> 1, -126.5 -> -127 (a half-to-even rounding would give 2, -2, 0, -126)."""
+    x = np.zeros((1, 32), np.float32)
+    x[0, :5] = [127.0, 2.5, -2.5, 0.5, -126.5]
+    q, d, s = xo.mmq_quantize_parts(xo.mmq_quantize(x, None, 32, 1, True), 1, 32)
+    assert d[0, 0] == 1.0
+    assert list(q[0, :5]) == [127, 3, -3, 1, -127]
+    assert s[0, 0] == np.float32(127 + 3 - 3 + 1 - 127)
+
+
+def test_mmq_quantize_sums_ids_dup_layout(xo):
+    """The block sum is d times the codes' sum in float32; rows come from ids; with dup each block (codes, scale,
+    sum) appears twice in a row of 2 cols; without sums that part stays zero; the byte count is
+    iq_mmq_act_bytes = rows * oc + 8 * rows * oc / 32."""
+    x = _mmq_blocks(16, 128, 9)
+    ids = np.array([5, 0, 15, 5, 3], np.int64)
+    buf = xo.mmq_quantize(x, ids, 128, 5, True)
+    assert buf.size == 5 * 128 + 8 * 5 * 4
+    q, d, s = xo.mmq_quantize_parts(buf, 5, 128)
+    whole_q, whole_d, whole_s = xo.mmq_quantize_parts(xo.mmq_quantize(x, None, 128, 16, True), 16, 128)
+    np.testing.assert_array_equal(q, whole_q[ids])
+    np.testing.assert_array_equal(d, whole_d[ids])
+    np.testing.assert_array_equal(s, (d * q.reshape(5, 4, 32).astype(np.int64).sum(axis=2).astype(np.float32)))
+    qd, dd, sd = xo.mmq_quantize_parts(xo.mmq_quantize(x, ids, 128, 5, True, dup=True), 5, 256)
+    np.testing.assert_array_equal(qd.reshape(5, 4, 2, 32)[:, :, 1], q.reshape(5, 4, 32))
+    np.testing.assert_array_equal(qd.reshape(5, 4, 2, 32)[:, :, 0], q.reshape(5, 4, 32))
+    np.testing.assert_array_equal(dd.reshape(5, 4, 2)[:, :, 1], d)
+    np.testing.assert_array_equal(sd.reshape(5, 4, 2)[:, :, 0], s)
+    _, _, s0 = xo.mmq_quantize_parts(xo.mmq_quantize(x, ids, 128, 5, False), 5, 128)
+    assert not s0.any()
+
+
+# ------------------------------------------------------------------------------------------------ router projections
+
+def test_bf16_from_f32_reference_vectors(xo, golden):
+    """The oracle's f32 -> bf16 against the reference's own bf16_from_f32 (bf16_bits.hpp, compiled into the committed
+    vectors): ties to even on both parities, the carry into the exponent, rounding to inf, NaNs kept quiet."""
+    ref, _ = golden
+    assert np.array_equal(xo.bf16_from_f32(ref["bf16_x"]), ref["bf16_y"])
+
+
+def test_bf16_from_f32_reference_live(xo):
+    R = xo.ref()
+    if R is None:
+        pytest.skip("oracle/_ref is not built (no reference tree)")
+    x = np.random.default_rng(3).integers(0, 2**32, 1 << 16, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    y = np.zeros(x.size, np.uint16)
+    R.xsref_bf16_from_f32(xo._a(x), x.size, xo._a(y))
+    assert np.array_equal(xo.bf16_from_f32(x), y)
+
+
+def _int_operands(rng, n_tok, n_out, n_in):
+    """Small integers: every partial sum is exact in f32, so any summation order gives the integer dot product."""
+    x = rng.integers(-8, 9, (n_tok, n_in)).astype(np.float32)
+    w = rng.integers(-8, 9, (n_out, n_in)).astype(np.float32)
+    return x, w, (x.astype(np.int64) @ w.astype(np.int64).T).astype(np.float32)
+
+
+@pytest.mark.parametrize("n_tok,n_out,n_in", [(1, 7, 64), (3, 5, 192), (8, 4, 2048), (2, 3, 7168), (1, 2, 1000)])
+def test_projection_orders_exact_on_integers(xo, n_tok, n_out, n_in):
+    """Where every sum is exact, each order returns the integer dot product: a wrong index, a transposed operand, a
+    dropped pair or tail, a wrong stride fails this."""
+    x, w, want = _int_operands(np.random.default_rng(n_in), n_tok, n_out, n_in)
+    if n_in % 2 == 0:
+        np.testing.assert_array_equal(xo.mmvf(x, w), want)
+        wb = xo.bf16_from_f32(w)                       # small integers are exact in bf16
+        np.testing.assert_array_equal(xo.mmvf(x, wb), want)
+    np.testing.assert_array_equal(xo.gemm_rows(x, w), want)
+    xb = xo.bf16_from_f32(x[0])
+    wb = xo.bf16_from_f32(w)
+    for form, tpr in ((0, 32), (1, 1), (2, 64), (2, 256)):
+        np.testing.assert_array_equal(xo.bf16_gemv(xb, wb, form, tpr), want[0])
+
+
+def test_projection_orders_close_to_fp64(xo):
+    """Random operands: within the summation error bound n * eps * sum |x w| of the float64 dot products."""
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((4, 2048)).astype(np.float32)
+    w = rng.standard_normal((16, 2048)).astype(np.float32)
+    exact = x.astype(np.float64) @ w.astype(np.float64).T
+    bound = 2048 * 2.0 ** -24 * (np.abs(x).astype(np.float64) @ np.abs(w).astype(np.float64).T)
+    for got in (xo.mmvf(x, w), xo.gemm_rows(x, w)):
+        assert np.all(np.abs(got - exact) <= bound)
+
+
+def _spike(n_in, lanes_at):
+    """x = 1, w zero but for 2^24 at element 0 and 1 at the given elements."""
+    x = np.ones((1, n_in), np.float32)
+    w = np.zeros((1, n_in), np.float32)
+    w[0, 0] = 2.0 ** 24
+    for i in lanes_at:
+        w[0, i] = 1.0
+    return x, w
+
+
+def test_projection_order_known_answers(xo):
+    """The reductions' shapes, from values where the order decides the bits (2^24 + 1 rounds back to 2^24, 2^24 + 2
+    is exact):
+    - mmvf at n_in 64 (B = 32, one pair a thread): ones at the pairs of threads 8 and 24 meet first in the xor
+      butterfly (offset 16) and reach thread 0 as 2 -> 2^24 + 2; a sequential or an upward (1, 2, ..., 16) butterfly
+      gives 2^24;
+    - mmvf at n_in 2048 (B = 256, 8 groups of 32): ones in groups 2 and 6 meet in the partials' butterfly at offset
+      4 -> 2^24 + 2;
+    - gemm_rows: one chain in k order -> 2^24;
+    - bf16 warp (lanes l, l + 32, ...): the same butterfly as mmvf -> 2^24 + 2; naive: one chain -> 2^24; the tree at
+      64 threads pairs t with t + 32, then 16, ...: ones at threads 8 and 40 meet first -> 2^24 + 2."""
+    x, w = _spike(64, [16, 48])                       # pairs 8 and 24 (elements 16 and 48)
+    assert xo.lib().xso_mmvf_block(64) == 32
+    assert xo.mmvf(x, w)[0, 0] == 2.0 ** 24 + 2
+    x, w = _spike(2048, [2 * 64, 2 * 192])            # threads 64 and 192: groups 2 and 6
+    assert xo.lib().xso_mmvf_block(2048) == 256
+    assert xo.mmvf(x, w)[0, 0] == 2.0 ** 24 + 2
+    x, w = _spike(64, [1, 2])
+    assert xo.gemm_rows(x, w)[0, 0] == 2.0 ** 24
+    x, w = _spike(128, [8, 24])                       # warp lanes 8 and 24
+    xb, wb = xo.bf16_from_f32(x[0]), xo.bf16_from_f32(w)
+    assert xo.bf16_gemv(xb, wb, 0)[0] == 2.0 ** 24 + 2
+    assert xo.bf16_gemv(xb, wb, 1)[0] == 2.0 ** 24
+    x, w = _spike(128, [8, 40])
+    xb, wb = xo.bf16_from_f32(x[0]), xo.bf16_from_f32(w)
+    assert xo.bf16_gemv(xb, wb, 2, 64)[0] == 2.0 ** 24 + 2
+
+
+def test_mmvf_block_size_known_answers(xo):
+    """mmvf_block_size: the fewest pair iterations, the smaller size on a tie: 64 -> 32, 192 -> 96, 448 -> 224,
+    2048 -> 256, 7168 -> 256, 2 -> 32."""
+    for n_in, b in ((64, 32), (192, 96), (448, 224), (2048, 256), (7168, 256), (2, 32)):
+        assert xo.lib().xso_mmvf_block(n_in) == b, n_in

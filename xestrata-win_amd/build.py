@@ -26,7 +26,8 @@ FLAGS = [
     "-Wall", "-Wno-unused-function", "-Wno-unused-variable", "-Wno-unused-but-set-variable",
 ]
 SOURCES = ["formats.hip", "quant_act.hip", "experts_decode.hip", "experts_prefill.hip", "router.hip", "dispatch.hip",
-           "combine.hip", "decode_layer.hip", "decode_fused.hip", "decode_t1.hip", "tiers.hip", "noalloc.hip", "abi.cpp", "pack.cpp"]
+           "combine.hip", "decode_layer.hip", "decode_fused.hip", "decode_t1.hip", "tiers.hip", "noalloc.hip", "mmq.hip", "gemv.hip",
+           "abi.cpp", "pack.cpp"]
 
 
 def _compile(src: pathlib.Path) -> pathlib.Path:

@@ -152,6 +152,51 @@ int xs_quantize_q8_1_rows(const float* x, int64_t n_rows, int64_t n_cols, void* 
     return finish(stream, xs::launch_quantize_q8_1_rows(x, n_rows, n_cols, y, S(stream)), "quantize_q8_1_rows");
 }
 
+size_t xs_iq_mmq_act_bytes(int64_t rows, int64_t cols) {
+    return rows > 0 && cols > 0 ? (size_t)(rows * cols + 2 * rows * (cols / 32) * 4) : 0;
+}
+int xs_iq_mmq_type_sums(int type) { return type == 12 /* Q4_K */ || type == 13 /* Q5_K */; }
+int xs_iq_mmq_type_dup(int type) { return type == 10 /* Q2_K */; }
+
+int xs_iq_mmq_quantize(const float* x, const int32_t* ids, void* xq, int64_t cols, int64_t ld, int64_t rows, int sums,
+                       int dup, void* stream) {
+    if (rows <= 0) return ok();
+    if (cols <= 0 || cols % 32 || ld < cols || ld % 4)
+        return fail(XS_EINVAL, "iq_mmq_quantize: %lld columns (a multiple of 32), %lld floats a row", (long long)cols,
+                    (long long)ld);
+    if (!aligned(x, 16) || !aligned(xq, 4) || (ids && !aligned(ids, 4)))
+        return fail(XS_EINVAL, "iq_mmq_quantize: a span is missing or misaligned");
+    return finish(stream, xs::launch_mmq_quantize(x, ids, xq, cols, ld, rows, rows, 1, false, sums, dup, S(stream)),
+                  "iq_mmq_quantize");
+}
+
+int xs_iq_mmq_quantize_scatter(const float* x, const int32_t* slot, void* xq, int64_t cols, int64_t ld,
+                               int64_t tokens, int k_used, int sums, int dup, void* stream) {
+    if (tokens <= 0) return ok();
+    if (cols <= 0 || cols % 32 || ld < cols || ld % 4 || k_used < 1)
+        return fail(XS_EINVAL, "iq_mmq_quantize_scatter: %lld columns (a multiple of 32), %lld floats a row, k %d",
+                    (long long)cols, (long long)ld, k_used);
+    if (!aligned(x, 16) || !aligned(xq, 4) || !aligned(slot, 4))
+        return fail(XS_EINVAL, "iq_mmq_quantize_scatter: a span is missing or misaligned");
+    return finish(stream,
+                  xs::launch_mmq_quantize(x, slot, xq, cols, ld, tokens, tokens * k_used, k_used, true, sums, dup,
+                                          S(stream)),
+                  "iq_mmq_quantize_scatter");
+}
+
+int xs_mmq_swiglu(const float* gu, float* h, int64_t rows, int64_t n_ff, int interleaved, void* stream) {
+    if (rows <= 0) return ok();
+    if (n_ff <= 0 || !aligned(gu, 4) || !aligned(h, 4))
+        return fail(XS_EINVAL, "mmq swiglu: %lld values a row, or a span is missing", (long long)n_ff);
+    return finish(stream, xs::launch_mmq_swiglu(gu, h, rows, n_ff, interleaved != 0, S(stream)), "mmq swiglu");
+}
+
+int xs_mmq_iota(int32_t* dst, int64_t n, void* stream) {
+    if (n <= 0) return ok();
+    if (!aligned(dst, 4) || n > INT32_MAX) return fail(XS_EINVAL, "mmq iota: a span is missing or too long");
+    return finish(stream, xs::launch_iota(dst, n, S(stream)), "mmq iota");
+}
+
 namespace {
 int grouped_args(const xs_expert_layout_t* L, const unsigned long long* grp_ptr, const int32_t* grp_start,
                  const int32_t* n_groups, const int32_t* ent_dst, const int32_t* ent_tok, int64_t cap_groups,
@@ -236,14 +281,21 @@ int xs_iq_dequant_f32(int type, const void* src, int64_t n, float* dst, void* st
     if (n <= 0) return ok();
     if (!type_qk(type) || n % type_qk(type)) return fail(XS_EINVAL, "iq_dequant_f32: type %d, %lld values", type, (long long)n);
     if (!src || !aligned(dst, 4)) return fail(XS_EINVAL, "iq_dequant_f32: a span is missing or misaligned");
-    return finish(stream, xs::launch_dequant(type, src, n, dst, false, S(stream)), "iq_dequant_f32");
+    return finish(stream, xs::launch_dequant(type, src, n, dst, xs::kDequantF32, S(stream)), "iq_dequant_f32");
 }
 
 int xs_iq_dequant_bf16(int type, const void* src, int64_t n, uint16_t* dst, void* stream) {
     if (n <= 0) return ok();
     if (!type_qk(type) || n % type_qk(type)) return fail(XS_EINVAL, "iq_dequant_bf16: type %d, %lld values", type, (long long)n);
     if (!src || !aligned(dst, 2)) return fail(XS_EINVAL, "iq_dequant_bf16: a span is missing or misaligned");
-    return finish(stream, xs::launch_dequant(type, src, n, dst, true, S(stream)), "iq_dequant_bf16");
+    return finish(stream, xs::launch_dequant(type, src, n, dst, xs::kDequantBf16, S(stream)), "iq_dequant_bf16");
+}
+
+int xs_iq_dequant_f16(int type, const void* src, int64_t n, uint16_t* dst, void* stream) {
+    if (n <= 0) return ok();
+    if (!type_qk(type) || n % type_qk(type)) return fail(XS_EINVAL, "iq_dequant_f16: type %d, %lld values", type, (long long)n);
+    if (!src || !aligned(dst, 2)) return fail(XS_EINVAL, "iq_dequant_f16: a span is missing or misaligned");
+    return finish(stream, xs::launch_dequant(type, src, n, dst, xs::kDequantF16, S(stream)), "iq_dequant_f16");
 }
 
 int xs_quantize_rows(int type, const float* x, int64_t n, void* y, void* stream) {
@@ -281,9 +333,88 @@ int xs_router_grouped_sigmoid(const float* logits, const float* bias, int n_toke
 int xs_router_logits_f32(const float* x, const float* w, float* logits, int n_tokens, int64_t n_embd, int n_expert,
                          void* stream) {
     if (n_tokens <= 0 || n_expert <= 0) return ok();
-    if (n_embd <= 0 || !aligned(x, 4) || !aligned(w, 4) || !aligned(logits, 4))
-        return fail(XS_EINVAL, "router_logits_f32: bad geometry or span");
-    return finish(stream, xs::launch_logits_f32(x, w, logits, n_tokens, n_embd, n_expert, S(stream)), "router_logits_f32");
+    if (n_tokens <= 8) return xs_f32_gemv_fp32_mmvf_multi(x, n_embd, w, logits, n_expert, n_embd, n_expert, n_tokens, stream);
+    return xs_f32_gemm_rows(x, n_embd, w, logits, n_expert, n_embd, n_expert, n_tokens, stream);
+}
+
+namespace {
+int mmvf_args(const float* x, int64_t ldx, const void* w, const float* y, int64_t ldy, int64_t n_in, int64_t n_out,
+              int n_tok, const char* what) {
+    if (n_tok < 1 || n_tok > 8 || n_in <= 0 || (n_in & 1) || n_in > INT32_MAX || n_out <= 0 || n_out > INT32_MAX ||
+        (ldx & 1) || ldx < n_in || ldy < (n_tok > 1 ? n_out : 1))
+        return fail(XS_EINVAL, "%s: 1..8 rows, even n_in/ldx, aligned pointers", what);
+    if (!aligned(x, 8) || !aligned(w, 4) || !aligned(y, 4)) return fail(XS_EINVAL, "%s: null or misaligned pointer", what);
+    return XS_OK;
+}
+}  // namespace
+
+int xs_f32_gemv_fp32_mmvf_multi(const float* x, int64_t ldx, const float* w, float* y, int64_t ldy, int64_t n_in,
+                                int64_t n_out, int n_tok, void* stream) {
+    if (int r = mmvf_args(x, ldx, w, y, ldy, n_in, n_out, n_tok, "f32_gemv_fp32_mmvf_multi")) return r;
+    if (!aligned(w, 8)) return fail(XS_EINVAL, "f32_gemv_fp32_mmvf_multi: null or misaligned pointer");
+    return finish(stream, xs::launch_mmvf<float>(x, ldx, w, y, ldy, n_in, n_out, n_tok, S(stream)),
+                  "f32_gemv_fp32_mmvf_multi");
+}
+
+int xs_bf16_gemv_fp32_mmvf_multi(const float* x, int64_t ldx, const uint16_t* w, float* y, int64_t ldy, int64_t n_in,
+                                 int64_t n_out, int n_tok, void* stream) {
+    if (int r = mmvf_args(x, ldx, w, y, ldy, n_in, n_out, n_tok, "bf16_gemv_fp32_mmvf_multi")) return r;
+    return finish(stream, xs::launch_mmvf<uint16_t>(x, ldx, w, y, ldy, n_in, n_out, n_tok, S(stream)),
+                  "bf16_gemv_fp32_mmvf_multi");
+}
+
+int xs_f32_gemm_rows(const float* x, int64_t ldx, const float* w, float* y, int64_t ldy, int64_t n_in, int64_t n_out,
+                     int64_t n_tok, void* stream) {
+    if (n_in <= 0 || n_out <= 0 || n_tok <= 0) return ok();
+    if (!aligned(x, 4) || !aligned(w, 4) || !aligned(y, 4) || ldx < n_in || ldy < n_out || n_tok > 65535 * 64)
+        return fail(XS_EINVAL, "f32_gemm_rows: null pointer or bad strides");
+    return finish(stream, xs::launch_gemm_rows(x, ldx, w, y, ldy, n_in, n_out, n_tok, S(stream)), "f32_gemm_rows");
+}
+
+int xs_f32_to_bf16_bulk(const float* x, uint16_t* y, int64_t n, void* stream) {
+    if (n <= 0) return ok();
+    if (!aligned(x, 4) || !aligned(y, 2)) return fail(XS_EINVAL, "f32_to_bf16_bulk: null or misaligned pointer");
+    return finish(stream, xs::launch_to_bf16(x, y, n, S(stream)), "f32_to_bf16_bulk");
+}
+
+int xs_bf16_gemv(const uint16_t* x, const uint16_t* w, float* y, int64_t n_in, int64_t n_out, void* stream) {
+    if (n_in <= 0 || n_out <= 0) return ok();
+    if (!aligned(x, 2) || !aligned(w, 2) || !aligned(y, 4)) return fail(XS_EINVAL, "bf16_gemv: null or misaligned pointer");
+    return finish(stream,
+                  xs::launch_bf16_gemv(x, false, w, y, n_in, n_out, n_out >= 64 ? xs::kBf16Warp : xs::kBf16Naive, 32,
+                                       S(stream)),
+                  "bf16_gemv");
+}
+
+int xs_bf16_gemv_split(const uint16_t* x, const uint16_t* w, float* y, int64_t n_in, int64_t n_out,
+                       int threads_per_row, void* stream) {
+    if (n_in <= 0 || n_out <= 0) return ok();
+    if (!aligned(x, 2) || !aligned(w, 2) || !aligned(y, 4))
+        return fail(XS_EINVAL, "bf16_gemv_split: null or misaligned pointer");
+    if (threads_per_row == 32)
+        return finish(stream, xs::launch_bf16_gemv(x, false, w, y, n_in, n_out, xs::kBf16Warp, 32, S(stream)),
+                      "bf16_gemv_split(warp)");
+    if (threads_per_row <= 0 || (threads_per_row & (threads_per_row - 1)) || threads_per_row > 1024)
+        return fail(XS_EDEVICE, "bf16_gemv_split: threads_per_row %d must be a power of two (32 selects the "
+                    "warp-per-row path)", threads_per_row);
+    return finish(stream, xs::launch_bf16_gemv(x, false, w, y, n_in, n_out, xs::kBf16Tree, threads_per_row, S(stream)),
+                  "bf16_gemv_split");
+}
+
+int xs_project_bf16(const float* x, uint16_t* x_bf16, const uint16_t* w, float* out, int64_t n_in, int64_t n_out,
+                    int split, int native, void* stream) {
+    if (n_in <= 0 || n_out <= 0) return ok();
+    if (native) return xs_bf16_gemv_fp32_mmvf_multi(x, n_in, w, out, n_out, n_in, n_out, 1, stream);
+    if (!x_bf16) {   // converted on the fly: the same bits as the two launches, with no bf16 copy of x
+        if (!aligned(x, 4) || !aligned(w, 2) || !aligned(out, 4) || (!split && n_out < 64))
+            return fail(XS_EINVAL, "project_bf16: a span is missing or misaligned (the on-the-fly form is the row-split "
+                        "one)");
+        return finish(stream, xs::launch_bf16_gemv(x, true, w, out, n_in, n_out, xs::kBf16Warp, 32, S(stream)),
+                      "project_bf16");
+    }
+    if (int r = xs_f32_to_bf16_bulk(x, x_bf16, n_in, stream)) return r;
+    return split ? xs_bf16_gemv_split(x_bf16, w, out, n_in, n_out, 32, stream)
+                 : xs_bf16_gemv(x_bf16, w, out, n_in, n_out, stream);
 }
 
 void xs_plan_offsets(long long capx, long long* start, long long* dst, long long* tok, long long* ptr,
@@ -401,6 +532,24 @@ int xs_native_moe_combine(const float* parts, const float* weights, const float*
     if (n_embd <= 0 || n_embd > 0x7fffffff || k < 1 || k > 15)
         return fail(XS_EINVAL, "native MoE combine requires a positive width and 1..15 experts");
     return xs_native_moe_combine_multi(parts, weights, shared, output, n_embd, k, 1, stream, nullptr);
+}
+
+int xs_native_moe_combine_multi_hits(const float* parts, const float* hits, const int32_t* dst, const int32_t* count,
+                                     const float* weights, const float* shared, float* output, int64_t n_embd,
+                                     int64_t k, int n_tok, void* stream, const float* shared_gate) {
+    if (n_tok <= 0) return ok();
+    if (n_embd <= 0 || k < 1 || k > 15 || (shared_gate && !shared) || !hits || !dst || !count)
+        return fail(XS_EINVAL, "native MoE combine (hits) requires a width, 1..15 experts, tokens, hits (k %lld)",
+                    (long long)k);
+    if (!aligned(parts, 4) || !aligned(hits, 4) || !aligned(weights, 4) || !aligned(output, 4) || !aligned(dst, 4) ||
+        !aligned(count, 4))
+        return fail(XS_EINVAL, "native MoE combine (hits): a span is missing or misaligned");
+    const size_t pb = (size_t)n_tok * (size_t)k * (size_t)n_embd * 4, ob = (size_t)n_tok * (size_t)n_embd * 4;
+    if (overlap(output, ob, parts, pb) || overlap(output, ob, hits, pb) || (shared && overlap(output, ob, shared, ob)))
+        return fail(XS_EINVAL, "native MoE combine (hits): the output overlaps an input");
+    return finish(stream, xs::launch_combine_hits(parts, hits, dst, count, weights, shared, shared_gate, output, n_embd,
+                                                  (int)k, n_tok, S(stream)),
+                  "native_moe_combine_multi_hits");
 }
 
 int xs_moe_combine_residual(const float* parts, const float* weights, const float* shared, const float* shared_gate,
@@ -562,6 +711,25 @@ PrefillWs prefill_ws(const xs_expert_layout_t* L, int n_expert, int k, int n_tok
 
 int32_t* xs_moe_layer_decode_status(void* workspace) {
     return workspace ? (int32_t*)workspace : nullptr;
+}
+
+int xs_moe_status_check(int32_t* status, void* stream) {
+    if (!aligned(status, 4)) return fail(XS_EINVAL, "moe status check: the status word is missing or misaligned");
+    hipStream_t s = S(stream);
+    int32_t word = 0;
+    hipError_t e = hipMemcpyAsync(&word, status, 4, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return fail(XS_EDEVICE, "moe status check: %s", hipGetErrorString(e));
+    if (word == 0) return ok();
+    const int32_t zero = 0;
+    e = hipMemcpyAsync(status, &zero, 4, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return fail(XS_EDEVICE, "moe status check: %s", hipGetErrorString(e));
+    return fail(XS_EDEVICE, "moe layer: status 0x%x:%s%s%s", (unsigned)word,
+                (word & 2) ? " a bounded wait of the persistent layer expired (its work-groups were not all resident)"
+                           : "",
+                (word & 4) ? " a token's router produced fewer than k experts (NaN logits; no output written)" : "",
+                (word & ~6) ? " a blob was misaligned" : "");
 }
 
 size_t xs_moe_layer_decode_workspace_bytes(const xs_expert_layout_t* L, int n_expert, int k, int n_tok) {
@@ -858,7 +1026,8 @@ int layer_prefill(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob
                                     sw.scratch, sw.rows, nullptr, false, stream))
             return r;
         if (w_gate) {
-            if (int r = xs_router_logits_f32(x, w_gate, sw.gate, n_tok, SL->n_embd, 1, stream)) return r;
+            // the prompt path's gate GEMM order (f32_gemm_rows) at every token count
+            if (int r = xs_f32_gemm_rows(x, SL->n_embd, w_gate, sw.gate, 1, SL->n_embd, 1, n_tok, stream)) return r;
             gate = sw.gate;
         }
         shared = sw.rows;

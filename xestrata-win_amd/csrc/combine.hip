@@ -75,6 +75,55 @@ __global__ __launch_bounds__(256) void combine_h_kernel(const uint16_t* __restri
     *(float4*)(out + t * n_embd + c) = make_float4(r.x + sum.x, r.y + sum.y, r.z + sum.z, r.w + sum.w);
 }
 
+// native_moe_combine_multi with moe_hit_add folded in (the reference's native_moe_combine_multi_hits,
+// src/kernels/xe/native_moe.cpp:67-110): a work-group of token t marks which of its k entries are listed in
+// dst[0, *count), and those read parts + hits (the sum moe_hit_add leaves in place) before their product
+__global__ __launch_bounds__(256) void combine_hits_kernel(const float* __restrict__ parts, const float* __restrict__ hits,
+                                                           const int32_t* __restrict__ dst,
+                                                           const int32_t* __restrict__ count,
+                                                           const float* __restrict__ weights,
+                                                           const float* __restrict__ shared,
+                                                           const float* __restrict__ shared_gate,
+                                                           float* __restrict__ out, int64_t n_embd, int k) {
+    __shared__ int hit[16];
+    const int64_t t = blockIdx.y;
+    const int tid = threadIdx.x;
+    if (tid < 16) hit[tid] = 0;
+    __syncthreads();
+    const int n_hit = *count, lo = (int)(t * k);
+    for (int i = tid; i < n_hit; i += blockDim.x) {
+        const int e = dst[i] - lo;
+        if (e >= 0 && e < k) hit[e] = 1;
+    }
+    __syncthreads();
+    const int64_t c = (int64_t)blockIdx.x * blockDim.x + tid;
+    if (c >= n_embd) return;
+    const float* p = parts + t * k * n_embd + c;
+    const float* hp = hits + t * k * n_embd + c;
+    const float* w = weights + t * k;
+    float sum = 0.0f;
+    for (int e = 0; e < k; ++e) {
+        const float pe = hit[e] ? p[(int64_t)e * n_embd] + hp[(int64_t)e * n_embd] : p[(int64_t)e * n_embd];
+        const float prod = pe * w[e];
+        sum = e == 0 ? prod : sum + prod;
+    }
+    if (shared) {
+        float sv = shared[t * n_embd + c];
+        if (shared_gate) sv = sv * (1.0f / (1.0f + expf(-shared_gate[t])));
+        sum = sum + sv;
+    }
+    out[t * n_embd + c] = sum;
+}
+
+hipError_t launch_combine_hits(const float* parts, const float* hits, const int32_t* dst, const int32_t* count,
+                               const float* weights, const float* shared, const float* shared_gate, float* out,
+                               int64_t n_embd, int k, int n_tok, hipStream_t s) {
+    const dim3 grid((unsigned)((n_embd + 255) / 256), (unsigned)n_tok);
+    hipLaunchKernelGGL(combine_hits_kernel, grid, dim3(256), 0, s, parts, hits, dst, count, weights, shared,
+                       shared_gate, out, n_embd, k);
+    return hipGetLastError();
+}
+
 hipError_t launch_combine_h(const uint16_t* parts, const float* weights, const float* shared,
                             const float* shared_gate, const float* residual, float* out, int64_t n_embd, int k,
                             int n_tok, hipStream_t s) {

@@ -176,6 +176,11 @@ template <>
 __device__ __forceinline__ void put<float>(float* y, int i, float v) { y[i] = v; }
 template <>
 __device__ __forceinline__ void put<uint16_t>(uint16_t* y, int i, float v) { y[i] = f2bf(v); }
+struct f16_out {   // an f16 output (the bits of a half), told apart from the bf16 one by type
+    uint16_t bits;
+};
+template <>
+__device__ __forceinline__ void put<f16_out>(f16_out* y, int i, float v) { y[i].bits = f2h(v); }
 
 template <typename Out>
 __global__ void dequant_kernel(int type, const uint8_t* __restrict__ src, int64_t n32, Out* __restrict__ dst) {
@@ -197,12 +202,14 @@ hipError_t launch_quantize_rows(int type, const float* x, int64_t n, void* y, hi
     return hipGetLastError();
 }
 
-hipError_t launch_dequant(int type, const void* src, int64_t n, void* dst, bool bf16, hipStream_t s) {
+hipError_t launch_dequant(int type, const void* src, int64_t n, void* dst, int out, hipStream_t s) {
     const int64_t n32 = n / 32;
     if (n32 <= 0) return hipSuccess;
     const dim3 grid((unsigned)((n32 + 255) / 256));
-    if (bf16)
+    if (out == kDequantBf16)
         hipLaunchKernelGGL(dequant_kernel<uint16_t>, grid, dim3(256), 0, s, type, (const uint8_t*)src, n32, (uint16_t*)dst);
+    else if (out == kDequantF16)
+        hipLaunchKernelGGL(dequant_kernel<f16_out>, grid, dim3(256), 0, s, type, (const uint8_t*)src, n32, (f16_out*)dst);
     else
         hipLaunchKernelGGL(dequant_kernel<float>, grid, dim3(256), 0, s, type, (const uint8_t*)src, n32, (float*)dst);
     return hipGetLastError();

@@ -160,22 +160,6 @@ __global__ __launch_bounds__(256) void router_grouped_sigmoid_wave_kernel(
     }
 }
 
-// logits[t, e] = x[t] . w[e] in fp32 (the router GEMV, reference src/kernels/xe/bf16_gemv.cpp:495-517): a wave per
-// (expert, token), lanes over the row, then a butterfly
-__global__ __launch_bounds__(256) void logits_f32_kernel(const float* __restrict__ x, const float* __restrict__ w,
-                                                         float* __restrict__ logits, int n_tokens, int64_t n_embd,
-                                                         int n_expert) {
-    const int wave = (int)(blockIdx.x * 4 + (threadIdx.x >> 6)), lane = threadIdx.x & 63;
-    if (wave >= n_expert * n_tokens) return;
-    const int e = wave % n_expert, t = wave / n_expert;
-    const float* wr = w + (int64_t)e * n_embd;
-    const float* xr = x + (int64_t)t * n_embd;
-    float acc = 0.0f;
-    for (int64_t i = lane; i < n_embd; i += 64) acc = __builtin_fmaf(wr[i], xr[i], acc);
-    acc = group_sum<64>(acc);
-    if (lane == 0) logits[(int64_t)t * n_expert + e] = acc;
-}
-
 hipError_t launch_router_topk(const float* logits, int n_tokens, int n_expert, int k, int32_t* ids, float* weights,
                               hipStream_t s) {
     const dim3 g((unsigned)n_tokens), b(64);
@@ -209,14 +193,6 @@ hipError_t launch_router_grouped_sigmoid(const float* logits, const float* bias,
     }
     hipLaunchKernelGGL(router_grouped_sigmoid_kernel, dim3((unsigned)n_tokens), dim3(64), 0, s, logits, bias, n_expert,
                        n_group, topk_group, k, routed_scale, ids, weights);
-    return hipGetLastError();
-}
-
-hipError_t launch_logits_f32(const float* x, const float* w, float* logits, int n_tokens, int64_t n_embd,
-                             int n_expert, hipStream_t s) {
-    const int64_t waves = (int64_t)n_tokens * n_expert;
-    hipLaunchKernelGGL(logits_f32_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, x, w, logits, n_tokens,
-                       n_embd, n_expert);
     return hipGetLastError();
 }
 

@@ -15,7 +15,9 @@ struct ExpertLayout {   // one native expert blob: [gate rows | up rows | down r
 
 // formats.hip
 hipError_t launch_quantize_rows(int type, const float* x, int64_t n, void* y, hipStream_t s);
-hipError_t launch_dequant(int type, const void* src, int64_t n, void* dst, bool bf16, hipStream_t s);
+// out: kDequantF32 (float), kDequantBf16 (bf16 bits, nearest even), kDequantF16 (half bits, nearest even)
+enum : int { kDequantF32 = 0, kDequantBf16 = 1, kDequantF16 = 2 };
+hipError_t launch_dequant(int type, const void* src, int64_t n, void* dst, int out, hipStream_t s);
 
 // quant_act.hip
 hipError_t launch_quantize_q8_1_rows(const float* x, int64_t n_rows, int64_t n_cols, void* y, hipStream_t s);
@@ -45,8 +47,6 @@ hipError_t launch_router_topk(const float* logits, int n_tokens, int n_expert, i
 hipError_t launch_router_grouped_sigmoid(const float* logits, const float* bias, int n_tokens, int n_expert,
                                          int n_group, int topk_group, int k, float routed_scale, int32_t* ids,
                                          float* weights, hipStream_t s);
-hipError_t launch_logits_f32(const float* x, const float* w, float* logits, int n_tokens, int64_t n_embd,
-                             int n_expert, hipStream_t s);
 
 // dispatch.hip
 hipError_t launch_resident_plan(const int32_t* ids, int n, int k, const int32_t* res, int n_expert,
@@ -121,6 +121,28 @@ hipError_t launch_combine(const float* parts, const float* weights, const float*
                           const float* residual, float* out, int64_t n_embd, int k, int n_tok, hipStream_t s);
 hipError_t launch_add_inplace(float* x, const float* y, int64_t n, hipStream_t s);
 // the combine over f16 parts, + residual (n_embd % 4 == 0)
+// gemv.hip: the router projections in the reference's summation orders
+int mmvf_block(int64_t n_in);
+template <typename W>
+hipError_t launch_mmvf(const float* x, int64_t ldx, const W* w, float* y, int64_t ldy, int64_t n_in, int64_t n_out,
+                       int n_tok, hipStream_t s);
+hipError_t launch_gemm_rows(const float* x, int64_t ldx, const float* w, float* y, int64_t ldy, int64_t n_in,
+                            int64_t n_out, int64_t n_tok, hipStream_t s);
+enum : int { kBf16Warp = 0, kBf16Naive = 1, kBf16Tree = 2 };
+hipError_t launch_bf16_gemv(const void* x, bool x_f32, const uint16_t* w, float* y, int64_t n_in, int64_t n_out,
+                            int form, int tpr, hipStream_t s);
+hipError_t launch_to_bf16(const float* x, uint16_t* y, int64_t n, hipStream_t s);
+
+// mmq.hip: the int8 MMQ activations (map: ids of the gathered form, slot of the scatter form), SwiGLU rows, iota
+hipError_t launch_mmq_quantize(const float* x, const int32_t* map, void* xq, int64_t cols, int64_t ld, int64_t n_src,
+                               int64_t rows, int k_used, bool scatter, bool sums, bool dup, hipStream_t s);
+hipError_t launch_mmq_swiglu(const float* gu, float* h, int64_t rows, int64_t n_ff, bool interleaved, hipStream_t s);
+hipError_t launch_iota(int32_t* dst, int64_t n, hipStream_t s);
+
+// combine_multi with moe_hit_add folded in: entries dst[0 .. *count) read parts + hits
+hipError_t launch_combine_hits(const float* parts, const float* hits, const int32_t* dst, const int32_t* count,
+                               const float* weights, const float* shared, const float* shared_gate, float* out,
+                               int64_t n_embd, int k, int n_tok, hipStream_t s);
 hipError_t launch_combine_h(const uint16_t* parts, const float* weights, const float* shared,
                             const float* shared_gate, const float* residual, float* out, int64_t n_embd, int k,
                             int n_tok, hipStream_t s);

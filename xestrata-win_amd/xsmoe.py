@@ -95,6 +95,22 @@ _SIGS = {
     "xs_native_expert_grouped": (I, [LP, P, P, P, P, P, I64, I64, P, P, P, P, I64]),
     "xs_iq_dequant_f32": (I, [I, P, I64, P, P]),
     "xs_iq_dequant_bf16": (I, [I, P, I64, P, P]),
+    "xs_iq_dequant_f16": (I, [I, P, I64, P, P]),
+    "xs_moe_status_check": (I, [P, P]),
+    "xs_f32_gemv_fp32_mmvf_multi": (I, [P, I64, P, P, I64, I64, I64, I, P]),
+    "xs_bf16_gemv_fp32_mmvf_multi": (I, [P, I64, P, P, I64, I64, I64, I, P]),
+    "xs_f32_gemm_rows": (I, [P, I64, P, P, I64, I64, I64, I64, P]),
+    "xs_f32_to_bf16_bulk": (I, [P, P, I64, P]),
+    "xs_bf16_gemv": (I, [P, P, P, I64, I64, P]),
+    "xs_bf16_gemv_split": (I, [P, P, P, I64, I64, I, P]),
+    "xs_project_bf16": (I, [P, P, P, P, I64, I64, I, I, P]),
+    "xs_iq_mmq_act_bytes": (ctypes.c_size_t, [I64, I64]),
+    "xs_iq_mmq_type_sums": (I, [I]),
+    "xs_iq_mmq_type_dup": (I, [I]),
+    "xs_iq_mmq_quantize": (I, [P, P, P, I64, I64, I64, I, I, P]),
+    "xs_iq_mmq_quantize_scatter": (I, [P, P, P, I64, I64, I64, I, I, I, P]),
+    "xs_mmq_swiglu": (I, [P, P, I64, I64, I, P]),
+    "xs_mmq_iota": (I, [P, I64, P]),
     "xs_quantize_rows": (I, [I, P, I64, P, P]),
     "xs_router_top10": (I, [P, I, I, I, P, P, P]),
     "xs_router_grouped_sigmoid": (I, [P, P, I, I, I, I, I, F, P, P, P]),
@@ -107,6 +123,7 @@ _SIGS = {
     "xs_native_moe_combine": (I, [P, P, P, P, I64, I64, P]),
     "xs_native_moe_combine_multi": (I, [P, P, P, P, I64, I64, I, P, P]),
     "xs_moe_combine_residual": (I, [P, P, P, P, P, P, I64, I64, I, P]),
+    "xs_native_moe_combine_multi_hits": (I, [P, P, P, P, P, P, P, I64, I64, I, P, P]),
     "xs_add_inplace": (I, [P, P, I64, P]),
     "xs_moe_layer_decode": (I, [LP, P, SZ, I, I, P, P, P, P, I, P, SZ, P]),
     "xs_moe_layer_decode_workspace_bytes": (SZ, [LP, I, I, I]),
@@ -220,6 +237,13 @@ def iq_dequant_bf16(t, src, n, out=None, stream=None):
     return out
 
 
+def iq_dequant_f16(t, src, n, out=None, stream=None):
+    if out is None:
+        out = torch.empty(n, dtype=torch.float16, device=src.device)
+    _check(lib().xs_iq_dequant_f16(t, _p(src), n, _p(out), _stream(stream)))
+    return out
+
+
 # ------------------------------------------------------------------------------------------------ activations
 
 def quantize_q8_1_rows(x, out=None, stream=None):
@@ -330,11 +354,115 @@ def moe_prefill_experts(L, x, src, entry, bounds, n_groups, grp_ptr, cap_groups,
                                         _stream(stream)))
 
 
+# ------------------------------------------------------------------------------------------------ router projections
+
+def f32_gemv_fp32_mmvf_multi(x, w, n_tok=None, out=None, stream=None):
+    """logits [n_tok, n_out] = x [n_tok, n_in] . w [n_out, n_in]^T in the decode GEMV's order (1..8 tokens)."""
+    n_tok = x.shape[0] if n_tok is None else n_tok
+    n_out, n_in = w.shape
+    if out is None:
+        out = torch.empty(n_tok, n_out, dtype=torch.float32, device=x.device)
+    fn = lib().xs_bf16_gemv_fp32_mmvf_multi if w.dtype in (torch.int16, torch.bfloat16) else \
+        lib().xs_f32_gemv_fp32_mmvf_multi
+    _check(fn(_p(x), x.stride(0), _p(w), _p(out), out.stride(0), n_in, n_out, n_tok, _stream(stream)))
+    return out
+
+
+def f32_gemm_rows(x, w, out=None, stream=None):
+    """The prompt path's GEMM order: one FMA chain a logit."""
+    n_tok, n_in = x.shape
+    n_out = w.shape[0]
+    if out is None:
+        out = torch.empty(n_tok, n_out, dtype=torch.float32, device=x.device)
+    _check(lib().xs_f32_gemm_rows(_p(x), x.stride(0), _p(w), _p(out), out.stride(0), n_in, n_out, n_tok,
+                                  _stream(stream)))
+    return out
+
+
+def f32_to_bf16_bulk(x, out=None, stream=None):
+    if out is None:
+        out = torch.empty(x.numel(), dtype=torch.int16, device=x.device)
+    _check(lib().xs_f32_to_bf16_bulk(_p(x), _p(out), x.numel(), _stream(stream)))
+    return out
+
+
+def bf16_gemv(x, w, out=None, threads_per_row=None, stream=None):
+    """x bf16 bits [n_in], w bf16 bits [n_out, n_in]: bf16_gemv, or bf16_gemv_split at threads_per_row."""
+    n_out, n_in = w.shape
+    if out is None:
+        out = torch.empty(n_out, dtype=torch.float32, device=w.device)
+    if threads_per_row is None:
+        _check(lib().xs_bf16_gemv(_p(x), _p(w), _p(out), n_in, n_out, _stream(stream)))
+    else:
+        _check(lib().xs_bf16_gemv_split(_p(x), _p(w), _p(out), n_in, n_out, threads_per_row, _stream(stream)))
+    return out
+
+
+def project_bf16(x, w, split=True, native=False, x_bf16=None, out=None, stream=None):
+    n_out, n_in = w.shape
+    if out is None:
+        out = torch.empty(n_out, dtype=torch.float32, device=w.device)
+    _check(lib().xs_project_bf16(_p(x), _p(x_bf16), _p(w), _p(out), n_in, n_out, int(split), int(native),
+                                 _stream(stream)))
+    return out
+
+
+# ------------------------------------------------------------------------------------------------ int8 MMQ staging
+
+def iq_mmq_act_bytes(rows, cols):
+    return lib().xs_iq_mmq_act_bytes(rows, cols)
+
+
+def iq_mmq_type_sums(t):
+    return bool(lib().xs_iq_mmq_type_sums(t))
+
+
+def iq_mmq_type_dup(t):
+    return bool(lib().xs_iq_mmq_type_dup(t))
+
+
+def iq_mmq_quantize(x, ids, cols, ld, rows, sums, dup=False, out=None, stream=None):
+    """int8 MMQ activations (xs_iq_mmq_quantize): a uint8 device tensor of iq_mmq_act_bytes(rows, oc) bytes."""
+    if out is None:
+        out = torch.zeros(iq_mmq_act_bytes(rows, 2 * cols if dup else cols), dtype=torch.uint8, device=x.device)
+    _check(lib().xs_iq_mmq_quantize(_p(x), _p(ids), _p(out), cols, ld, rows, int(sums), int(dup), _stream(stream)))
+    return out
+
+
+def iq_mmq_quantize_scatter(x, slot, cols, ld, tokens, k_used, sums, dup=False, out=None, stream=None):
+    if out is None:
+        out = torch.zeros(iq_mmq_act_bytes(tokens * k_used, 2 * cols if dup else cols), dtype=torch.uint8,
+                          device=x.device)
+    _check(lib().xs_iq_mmq_quantize_scatter(_p(x), _p(slot), _p(out), cols, ld, tokens, k_used, int(sums), int(dup),
+                                            _stream(stream)))
+    return out
+
+
+def mmq_swiglu(gu, rows, n_ff, interleaved, out=None, stream=None):
+    if out is None:
+        out = torch.empty(rows, n_ff, dtype=torch.float32, device=gu.device)
+    _check(lib().xs_mmq_swiglu(_p(gu), _p(out), rows, n_ff, int(interleaved), _stream(stream)))
+    return out
+
+
+def mmq_iota(n, out=None, device="cuda", stream=None):
+    if out is None:
+        out = torch.empty(n, dtype=torch.int32, device=device)
+    _check(lib().xs_mmq_iota(_p(out), n, _stream(stream)))
+    return out
+
+
 # ------------------------------------------------------------------------------------------------ combine
 
 def native_moe_combine_multi(parts, weights, shared, output, n_embd, k, n_tok, shared_gate=None, stream=None):
     _check(lib().xs_native_moe_combine_multi(_p(parts), _p(weights), _p(shared), _p(output), n_embd, k, n_tok,
                                              _stream(stream), _p(shared_gate)))
+
+
+def native_moe_combine_multi_hits(parts, hits, dst, count, weights, shared, output, n_embd, k, n_tok,
+                                  shared_gate=None, stream=None):
+    _check(lib().xs_native_moe_combine_multi_hits(_p(parts), _p(hits), _p(dst), _p(count), _p(weights), _p(shared),
+                                                  _p(output), n_embd, k, n_tok, _stream(stream), _p(shared_gate)))
 
 
 def moe_combine_residual(parts, weights, residual, output, n_embd, k, n_tok, shared=None, shared_gate=None,
@@ -406,11 +534,8 @@ class MoeLayer:
     def check(self):
         """Synchronize and raise XsError when the status word is not 0 (a bounded wait of the persistent layer ran
         out - its output is not valid - or a token's router produced fewer than k experts); the word is cleared."""
-        st = self.status()
-        if st:
-            off = self.ws_ptr - self.ws.data_ptr()
-            self.ws[off:off + 4].zero_()
-            raise XsError(XS_EDEVICE, f"moe layer: status word {st:#x} (2: a bounded wait ran out, 4: NaN routing)")
+        if not self.prefill:
+            _check(lib().xs_moe_status_check(self.ws_ptr, None))
 
     def __call__(self, x, logits, residual, out, n_tok=None, arena=None, stream=None):
         n_tok = x.shape[0] if n_tok is None else n_tok
