@@ -247,6 +247,86 @@ def other_configs(torch, xm, dev, gen, steps):
     return out
 
 
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(torch, xm, np, arena, L, E, H, F, k, dev, gen, max_threads=16):
+    """The reference's CPU/host decode path (oracle/cpu_path.cpp: ggml's Q8_K / Q8_0 activations, the multi-token
+    AVX2 rows, g / (1 + exp(-g)) u, the rank-order combine) on this box's host cores: one pinned thread a physical
+    core, at most 16 (the box's CPU share), timed as the best of 5 means of 10 calls with the expert sets rotated so
+    the weights come from DRAM.  Config 2 at one token (the headline's workload) and config 1 (its own 4 tokens, and
+    1); each with the largest difference to the GPU's output of the same call, relative to the GPU's largest
+    magnitude of the MoE part."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import xs_oracle as xo
+    threads = xo.cpu().xscpu_init(max_threads)
+
+    def rel(cpu_out, gpu_out, res):
+        moe = gpu_out - res
+        return float(np.max(np.abs(cpu_out - gpu_out)) / np.max(np.abs(moe)))
+
+    # config 2, T = 1: one host copy of the layer (128 experts, 392 MB), the 16 disjoint 8-expert sets of the GPU
+    # rotation, so 16 calls read every expert once
+    host = arena[:E].reshape(-1).cpu().numpy()
+    ol = xo.layout(xm.Q4_K, xm.Q6_K, H, F)
+    n_sets = E // k
+    lg = set_logits(torch, n_sets, 1, E, k, dev, gen)
+    x = torch.randn(1, H, device=dev, generator=gen).to(torch.bfloat16).float()
+    res = torch.randn(1, H, device=dev, generator=gen)
+    us2 = xo.cpu_time(ol, host, L.bytes, E, k, x.cpu().numpy(), lg.cpu().numpy(), res.cpu().numpy())
+    out = torch.empty(1, H, device=dev)
+    xm.MoeLayer(L, arena, E, k, 1)(x, lg[0], res, out)
+    c_out = xo.cpu_layer_decode(ol, host, L.bytes, E, k, x.cpu().numpy(), lg[0].cpu().numpy(), res.cpu().numpy())
+    r2 = rel(c_out, out.cpu().numpy(), res.cpu().numpy())
+    gbs2 = k * L.bytes / (us2 * 1e-6) / 1e9
+    log(f"cpu baseline config 2 T=1: {us2:.1f} us/token, {gbs2:.2f} GB/s on {threads} threads; rel to GPU {r2:.2e}")
+    # config 1: hidden 1024, 8 Q8_0 experts, top-2, F 512, fp32 router N(0, 0.02), N(0,1) activations, seed 0; 32
+    # copies of the 13 MB layer in host memory, as 256 experts of which a call's logits enable one copy's 8
+    E1, H1, F1, k1, copies = 8, 1024, 512, 2, 32
+    arena1, L1 = xm.build_arena(E1, H1, F1, xm.Q8_0, xm.Q8_0, seed=0)
+    ol1 = xo.layout(xm.Q8_0, xm.Q8_0, H1, F1)
+    host1 = np.tile(arena1[:E1].reshape(-1).cpu().numpy(), copies)
+    g0 = torch.Generator().manual_seed(0)
+    wr = torch.randn(E1, H1, generator=g0) * 0.02
+    c1 = {}
+    for T in (4, 1):
+        x1 = torch.randn(T, H1, generator=g0)
+        res1 = torch.randn(T, H1, generator=g0)
+        lg1 = xm.router_logits_f32(x1.to(dev), wr.to(dev))                   # the decode GEMV's order
+        sets = np.full((copies, T, E1 * copies), -1e30, np.float32)
+        for c in range(copies):
+            sets[c, :, c * E1:(c + 1) * E1] = lg1.cpu().numpy()
+        us1 = xo.cpu_time(ol1, host1, L1.bytes, E1 * copies, k1, x1.numpy(), sets, res1.numpy())
+        o1 = torch.empty(T, H1, device=dev)
+        xm.MoeLayer(L1, arena1, E1, k1, T)(x1.to(dev), lg1, res1.to(dev), o1)
+        co1 = xo.cpu_layer_decode(ol1, host1, L1.bytes, E1, k1, x1.numpy(), lg1.cpu().numpy(), res1.numpy())
+        r1 = rel(co1, o1.cpu().numpy(), res1.numpy())
+        ids = torch.topk(lg1, k1, dim=1).indices
+        b1 = len(torch.unique(ids)) * L1.bytes
+        c1[f"T{T}"] = dict(us_per_layer=round(us1, 2), us_per_token=round(us1 / T, 2),
+                           expert_gbs=round(b1 / (us1 * 1e-6) / 1e9, 2), rel_to_gpu=float(f"{r1:.3e}"))
+        log(f"cpu baseline config 1 T={T}: {us1:.1f} us/layer, {c1[f'T{T}']['expert_gbs']} GB/s; rel to GPU "
+            f"{r1:.2e}")
+    del arena1
+    return dict(value=round(1e6 / us2, 1), unit="tokens/s", cores=threads, kind="port",
+                sample="config 2, one token a call: the best of 5 means of 10 calls (after 2), the calls rotating "
+                       "over the 16 disjoint 8-expert sets of one 392 MB host copy (every 16 calls read all 128 "
+                       "experts from DRAM); config 1 likewise over 32 host copies of its 13 MB layer",
+                us_per_token=round(us2, 1), expert_gbs=round(gbs2, 2), rel_to_gpu=float(f"{r2:.3e}"),
+                cpu_model=cpu_model(), threads="one a physical core, pinned, at most 16 (the box's CPU share)",
+                path="oracle/cpu_path.cpp: Q8_K activations, AVX2 multi-token Q4_K/Q6_K rows, SwiGLU "
+                     "g/(1+exp(-g))*u, h re-quantized to Q8_K, rank-order combine (src/kernels/cpu/"
+                     "native_expert.cpp, iq_avx2_rows.inl); the float accumulation order is this file's",
+                config1=c1)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -390,37 +470,8 @@ def main():
 
     others = {} if args.no_others else other_configs(torch, xm, dev, gen, max(64, args.steps // 4))
 
-    # ---------------------------------------------------------------- the CPU baseline (the oracle, host cores)
-    cpu = None
-    if not args.no_cpu:
-        sys.path.insert(0, str(ROOT / "oracle"))
-        import xs_oracle as xo
-        cores = min(16, os.cpu_count() or 1)
-        blobs = list(arena[:E].cpu().numpy())
-        ol = xo.layout(xm.Q4_K, xm.Q6_K, H, F)
-        lg = inputs[1][0][0].cpu().numpy()        # the first copy's token, as timed on the GPU
-        xx = inputs[1][1].cpu().numpy()
-        rr = np.zeros((1, H), np.float32)
-        xo.moe_layer_decode(ol, blobs, k, xx, lg, rr, n_threads=cores)     # warm-up
-        n = 0
-        t0 = time.perf_counter()
-        while time.perf_counter() - t0 < args.cpu_seconds:
-            xo.moe_layer_decode(ol, blobs, k, xx, lg, rr, n_threads=cores)
-            n += 1
-        dt = (time.perf_counter() - t0) / n
-        model = "unknown"
-        try:
-            for line in open("/proc/cpuinfo"):
-                if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
-                    break
-        except OSError:
-            pass
-        cpu = dict(value=round(1.0 / dt, 3), unit="tokens/s", cores=cores, kind="port",
-                   sample=f"{n} single-token config-2 decode layers (oracle/xs_oracle.c, {cores} OpenMP threads) in "
-                          f"{n * dt:.1f} s", us_per_token=round(dt * 1e6, 1),
-                   expert_gbs=round(k * blob / dt / 1e9, 3), cpu_model=model)
-        log(f"cpu baseline: {dt * 1e3:.1f} ms/token on {cores} threads")
+    # ---------------------------------------------------------------- the CPU baseline (the reference's CPU path)
+    cpu = None if args.no_cpu else cpu_baseline(torch, xm, np, arena, L, E, H, F, k, dev, gen)
 
     line = {
         "metric": METRIC,

@@ -10,6 +10,7 @@ import numpy as np
 HERE = pathlib.Path(__file__).resolve().parent
 LIB = HERE / "liboracle.so"
 REF = HERE / "_ref" / "libxsref.so"
+CPU = HERE / "libxscpu.so"
 
 Q8_0, Q4_K, Q6_K, IQ4_XS = 8, 12, 14, 23
 BLOCK_VALUES = {Q8_0: 32, Q4_K: 256, Q6_K: 256, IQ4_XS: 256}
@@ -94,6 +95,81 @@ def ref():
         R.xsref_bf16_from_f32.argtypes = [P, I64, P]
         _ref = R
     return _ref
+
+
+_cpu = None
+
+
+def cpu():
+    """oracle/libxscpu.so: the reference's CPU decode path restated for AVX2 (bench.py's cpu_baseline)."""
+    global _cpu
+    if _cpu is None:
+        if not CPU.exists():
+            subprocess.run(["make", "-s", "-C", str(HERE), "libxscpu.so"], check=True)
+        C = ctypes.CDLL(str(CPU))
+        C.xscpu_init.argtypes = [I]
+        C.xscpu_init.restype = I
+        C.xscpu_quantize_q8_k.argtypes = [P, I64, P]
+        C.xscpu_quantize_q8_0.argtypes = [P, I64, P]
+        C.xscpu_row_dot.argtypes = [I, P, I64, P]
+        C.xscpu_row_dot.restype = F
+        lay = [I, I, I64, I64, I64, I64, I64, I64, P, I64, I, I]
+        C.xscpu_layer_decode.argtypes = lay + [P, P, P, I, P]
+        C.xscpu_layer_decode.restype = I
+        C.xscpu_time.argtypes = lay + [P, P, I, P, I, P, I, I]
+        C.xscpu_time.restype = ctypes.c_double
+        _cpu = C
+    return _cpu
+
+
+def cpu_q8_k(x):
+    """ggml's Q8_K blocks of x (292 bytes a 256 values) as (d f32 [nb], qs int8 [nb, 256], bsums int16 [nb, 16])."""
+    x = np.ascontiguousarray(x, np.float32).ravel()
+    nb = x.size // 256
+    y = np.zeros(nb * 292, np.uint8)
+    cpu().xscpu_quantize_q8_k(_a(x), x.size, _a(y))
+    b = y.reshape(nb, 292)
+    return b[:, :4].copy().view(np.float32).ravel(), b[:, 4:260].copy().view(np.int8), \
+        b[:, 260:].copy().view(np.int16), y
+
+
+def cpu_q8_0(x):
+    """Q8_0 activations (the fp16 scale as a float, 36 bytes a 32 values) as (d [nb], qs [nb, 32], raw bytes)."""
+    x = np.ascontiguousarray(x, np.float32).ravel()
+    nb = x.size // 32
+    y = np.zeros(nb * 36, np.uint8)
+    cpu().xscpu_quantize_q8_0(_a(x), x.size, _a(y))
+    b = y.reshape(nb, 36)
+    return b[:, :4].copy().view(np.float32).ravel(), b[:, 4:].copy().view(np.int8), y
+
+
+def _cpu_layout_args(L, arena, blob, n_expert, k):
+    return (L.gu_type, L.d_type, L.n_embd, L.n_ff, L.gu_row, L.d_row, L.up_off, L.down_off, _a(arena), blob,
+            n_expert, k)
+
+
+def cpu_layer_decode(L, arena, blob, n_expert, k, x, logits, residual):
+    """out = residual + MoE(x) on the CPU path (n_tok <= 8); arena: uint8 [n_expert * blob]."""
+    x = np.ascontiguousarray(x, np.float32)
+    logits = np.ascontiguousarray(logits, np.float32)
+    residual = np.ascontiguousarray(residual, np.float32)
+    out = np.zeros_like(residual)
+    r = cpu().xscpu_layer_decode(*_cpu_layout_args(L, arena, blob, n_expert, k), _a(x), _a(logits), _a(residual),
+                                 x.shape[0], _a(out))
+    if r:
+        raise ValueError("cpu path: unsupported layer")
+    return out
+
+
+def cpu_time(L, arena, blob, n_expert, k, x, logit_sets, residual, reps=10, trials=5):
+    """Microseconds a layer call: the best of `trials` means of `reps` calls, logits rotating over the sets."""
+    x = np.ascontiguousarray(x, np.float32)
+    logit_sets = np.ascontiguousarray(logit_sets, np.float32)
+    residual = np.ascontiguousarray(residual, np.float32)
+    out = np.zeros_like(residual)
+    n_sets = logit_sets.shape[0]
+    return cpu().xscpu_time(*_cpu_layout_args(L, arena, blob, n_expert, k), _a(x), _a(logit_sets), n_sets,
+                            _a(residual), x.shape[0], _a(out), reps, trials)
 
 
 def _a(x):
