@@ -25,7 +25,7 @@ FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function", "-Wno-unused-variable", "-Wno-unused-but-set-variable",
 ]
-SOURCES = ["formats.hip", "quant_act.hip", "experts_decode.hip", "experts_prefill.hip", "router.hip", "dispatch.hip",
+SOURCES = ["formats.hip", "quant_act.hip", "experts_decode.hip", "experts_stream.hip", "experts_prefill.hip", "router.hip", "dispatch.hip",
            "combine.hip", "decode_layer.hip", "decode_fused.hip", "decode_t1.hip", "tiers.hip", "noalloc.hip", "mmq.hip", "gemv.hip",
            "abi.cpp", "pack.cpp"]
 

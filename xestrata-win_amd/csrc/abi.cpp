@@ -218,6 +218,8 @@ int grouped_args(const xs_expert_layout_t* L, const unsigned long long* grp_ptr,
     a->gate = (float*)scratch;
     a->up = (float*)((uint8_t*)scratch + fa);
     a->hq = (uint8_t*)scratch + 3 * fa;
+    a->hact = (uint8_t*)scratch + 2 * fa;
+    a->cap_entries_hint = cap_entries;
     a->out = out;
     a->err = xs_native_expert_status(scratch, cap_entries, L->n_ff);
     a->cap_groups = cap_groups;
@@ -239,8 +241,14 @@ int grouped_impl(const xs_expert_layout_t* L, const unsigned long long* grp_ptr,
         return r;
     a.max_entries = max_entries;
     const xs::ExpertLayout XL = to_layout(L);
-    hipError_t e = xs::launch_native_gu(XL, a, S(stream));
-    if (e == hipSuccess) e = xs::launch_native_down(XL, a, S(stream));
+    hipError_t e;
+    if (xs::stream_usable(XL, max_entries, cap_groups, cap_entries)) {   // the weight-stream kernels (the same bits)
+        e = xs::launch_stream_gu(XL, a, S(stream));
+        if (e == hipSuccess) e = xs::launch_stream_down(XL, a, S(stream));
+    } else {
+        e = xs::launch_native_gu(XL, a, S(stream));
+        if (e == hipSuccess) e = xs::launch_native_down(XL, a, S(stream));
+    }
     return finish(stream, e, "native_expert_grouped");
 }
 }  // namespace
@@ -791,7 +799,11 @@ int layer_decode(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_
                                               route.scale, w.ids, w.w, stream))
             return r;
     xs::FusedPlan P;
-    if (xs::fused_decode_plan(XL, n_expert, k, n_tok, &P)) {
+    // 2..16 tokens of a wide layer (hidden >= 4096): the chained path on the weight-stream kernels, measured faster
+    // there than the persistent layer (config 4 at 8 tokens: 565 -> ~250 us); narrower layers keep the persistent one
+    const bool streamed = n_tok >= 2 && L->n_embd >= 4096 &&
+                          xs::stream_usable(XL, n_tok, capx < n_expert ? capx : n_expert, capx);
+    if (!streamed && xs::fused_decode_plan(XL, n_expert, k, n_tok, &P)) {
         // the whole layer in one persistent launch
         xs::FusedArgs a;
         a.L = XL;

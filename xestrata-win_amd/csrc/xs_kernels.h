@@ -37,9 +37,15 @@ struct GroupedArgs {
     int32_t* err;  // device word: set non-zero when a blob address is not 16-byte aligned
     int64_t cap_groups, grid_groups;
     int max_entries;   // the most entries a group can have (the call's token count), 0 when not known
+    void* hact;        // scratch: the down stream's h activations (int8 values, scales, sums of 16)
+    int64_t cap_entries_hint;   // the entries the scratch was sized for
 };
 hipError_t launch_native_gu(const ExpertLayout& L, const GroupedArgs& a, hipStream_t s);
 hipError_t launch_native_down(const ExpertLayout& L, const GroupedArgs& a, hipStream_t s);
+// experts_stream.hip: the same products as a weight stream (2..16 tokens, the four formats)
+bool stream_usable(const ExpertLayout& L, int n_tok, int64_t cap_groups, int64_t cap_entries);
+hipError_t launch_stream_gu(const ExpertLayout& L, const GroupedArgs& a, hipStream_t s);
+hipError_t launch_stream_down(const ExpertLayout& L, const GroupedArgs& a, hipStream_t s);
 
 // router.hip
 hipError_t launch_router_topk(const float* logits, int n_tokens, int n_expert, int k, int32_t* ids, float* weights,
