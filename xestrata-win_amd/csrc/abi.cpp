@@ -466,11 +466,11 @@ int xs_prefill_route(const int32_t* ids, int64_t n_entries, int k, int n_expert,
 size_t xs_moe_prefill_scratch_bytes(int64_t n_tok, int64_t rows, int64_t n_embd, int64_t n_ff) {
     if (n_tok <= 0 || rows <= 0) return 256;
     return up256((size_t)n_tok * (size_t)n_embd * 2) + up256((size_t)rows * (size_t)n_ff * 2) +
-           up256((size_t)(rows + 1) * 8) + 256;
+           up256((size_t)xs::tile_table_words(rows, rows) * 4) + 256;   // (cap_groups <= rows)
 }
 
 namespace {
-// the m-tile prefixes inside the experts' scratch: after the f16 copy of x and h
+// the m-tile table inside the experts' scratch: after the f16 copy of x and h
 int32_t* prefill_mtile(void* scratch, int64_t n_tok, int64_t rows, const xs_expert_layout_t* L) {
     return (int32_t*)((uint8_t*)scratch + up256((size_t)n_tok * (size_t)L->n_embd * 2) +
                       up256((size_t)rows * (size_t)L->n_ff * 2));

@@ -7,8 +7,10 @@
 //   1. Wave 0 of every work-group routes the token exactly (softmax over all experts in double, top-k, renormalised:
 //      router.cpp:59-145's arithmetic, xs_route.h).  Meanwhile waves 1-3 take the top-k of the raw logits - the same
 //      experts in the same order unless two probabilities round to one float - and at once issue the LDS DMA of the
-//      work-group's gate/up rows and down rows for those experts; waves 4-7 quantize x to q8_1 (one scale a 256).
-//      When the exact routing disagrees with the speculation, the DMA is drained and issued again.
+//      work-group's gate/up rows for those experts; waves 4-7 quantize x to q8_1 (one scale a 256).  When the exact
+//      routing disagrees with the speculation, the DMA is drained and issued again.  The down rows are fetched once
+//      the gate/up rows are in (or right after routing by a work-group with no gate/up unit), so that the gate/up
+//      rows, which every output waits on, have the memory system to themselves.
 //   2. A gate/up unit is one expert's 32 SwiGLU outputs (32 gate rows + 32 up rows), fetched in two halves; each half
 //      is computed as it lands.  For Q4_K the integer sums of a block are split over four lanes (exact), then the
 //      block scales are applied in the canonical order and the canonical butterfly taken.  h = SwiGLU(gate, up) is
@@ -41,6 +43,8 @@ constexpr int kT1 = 1024;          // threads a work-group: 16 waves, 4 a SIMD
 constexpr int kT1Waves = kT1 / 64;
 constexpr int kSpecWaves = 3;      // waves 1..3: speculative routing and the weight DMA
 constexpr int kStoreWave = kT1Waves - 1;   // the wave that writes the hand-over words (and loads nothing after x)
+constexpr int kDnWave0 = 4, kDnWaves = 4;   // waves 4..7: the DMA of the down rows (they quantize x before it and
+                                            // decode the rows after it; they neither poll nor write h)
 constexpr int kHWords = 9;         // tagged words a 32-value q8_1 block of h: 8 x four codes, 1 scale
 // Every work-group polls every block of h with device-scope loads, which go past the L2 to the memory channel that
 // owns the line, and reads of one line queue there one after another: with the whole grid on each line a poll took
@@ -112,22 +116,23 @@ __device__ __forceinline__ void t1_vm_wait_le(int n) {
     }
 }
 
-// n16 16-byte chunks to LDS dst[0 .. n16) by the DMA of waves 1..kSpecWaves (global_load_lds_dwordx4: one instruction
-// of a wave fills 64 consecutive chunks at a wave-uniform LDS address)
-template <typename Src>
+// n16 16-byte chunks to LDS dst[0 .. n16) by the DMA of waves W0 .. W0 + NW - 1 (global_load_lds_dwordx4: one
+// instruction of a wave fills 64 consecutive chunks at a wave-uniform LDS address)
+template <int W0, int NW, typename Src>
 __device__ __forceinline__ void t1_dma(uint8_t* dst, int n16, Src src) {
-    const int lane = threadIdx.x & 63, r = (threadIdx.x >> 6) - 1;
-    for (int base = 64 * r; base < n16; base += 64 * kSpecWaves) {
+    const int lane = threadIdx.x & 63, r = (threadIdx.x >> 6) - W0;
+    for (int base = 64 * r; base < n16; base += 64 * NW) {
         const int i = base + lane;
         if (i < n16)
             __builtin_amdgcn_global_load_lds(src(i), (__attribute__((address_space(3))) void*)(dst + 16 * base), 16, 0,
                                              2 /* nt */);
     }
 }
-// the number of DMA instructions t1_dma issues in this wave for n16 chunks
+// the number of DMA instructions t1_dma<W0, NW> issues in this wave for n16 chunks
+template <int W0, int NW>
 __device__ __forceinline__ int t1_dma_count(int n16) {
-    const int r = (threadIdx.x >> 6) - 1;
-    return n16 > 64 * r ? (n16 - 64 * r + 64 * kSpecWaves - 1) / (64 * kSpecWaves) : 0;
+    const int r = (threadIdx.x >> 6) - W0;
+    return n16 > 64 * r ? (n16 - 64 * r + 64 * NW - 1) / (64 * NW) : 0;
 }
 
 // The top-k of the raw logits, in order (larger first, the lower index on a tie; NaN never wins): exp is monotone, so
@@ -225,19 +230,20 @@ __global__ __launch_bounds__(kT1) void moe_decode_t1_kernel(FusedArgs a) {
         return Act{q, (const float*)(q + F), (const int*)(q + F + F / 8)};
     };
     const bool spec_wave = wave >= 1 && wave <= kSpecWaves;
+    const bool dn_wave = wave >= kDnWave0 && wave < kDnWave0 + kDnWaves;
     const bool has_gu = b < k * nu;   // (the host makes the grid at least the unit counts)
     const int g_gu = has_gu ? b / nu : 0, j_gu = has_gu ? b - g_gu * nu : 0;
     const int j_dn = b;               // down unit: rows j_dn * rd .. + rd of every expert
     const bool has_dn = j_dn < a.nj;
     constexpr int n16_half = 32 * gu_row / 16, n16_dn = rd * d_row / 16;
     static_assert((16 * gu_row) % 16 == 0 && (rd * d_row) % 16 == 0, "16-byte DMA chunks");
-    // this wave's DMA instructions of each part (wave-uniform): gate/up half B, the down rows
-    const int n_b = __builtin_amdgcn_readfirstlane(has_gu ? t1_dma_count(n16_half) : 0);
-    const int n_d = __builtin_amdgcn_readfirstlane(has_dn ? k * t1_dma_count(n16_dn) : 0);
+    // this wave's DMA instructions of gate/up half B (wave-uniform)
+    const int n_b = __builtin_amdgcn_readfirstlane(has_gu ? t1_dma_count<1, kSpecWaves>(n16_half) : 0);
 
     // the DMA of this work-group's rows for the experts id_of(0 .. k) (rank order; id_of(i) wave-uniform): the slab
-    // holds half A (gate rows 0..15, up rows 0..15 of the unit's 32) then half B (rows 16..31 of each); then each
-    // expert's down rows
+    // holds half A (gate rows 0..15, up rows 0..15 of the unit's 32) then half B (rows 16..31 of each).  The down rows
+    // are fetched apart (issue_dn), once the gate/up rows have landed: fetched together, the down rows' bytes share
+    // the memory system with the gate/up rows that every output waits on, and all of them land late.
     auto issue = [&](auto id_of) {
         if (has_gu) {
             const uint8_t* blob = a.arena + (size_t)id_of(g_gu) * (size_t)a.blob;
@@ -245,16 +251,19 @@ __global__ __launch_bounds__(kT1) void moe_decode_t1_kernel(FusedArgs a) {
                 const uint8_t* sg = blob + ((size_t)j_gu * 32 + 16 * hh) * gu_row;
                 const uint8_t* su = blob + L.up_off + ((size_t)j_gu * 32 + 16 * hh) * gu_row;
                 const int n16g = n16_half / 2;
-                t1_dma(slab_gu + hh * 32 * gu_row, n16_half, [&](int i) {
+                t1_dma<1, kSpecWaves>(slab_gu + hh * 32 * gu_row, n16_half, [&](int i) {
                     return (const void*)(i < n16g ? sg + 16 * (size_t)i : su + 16 * (size_t)(i - n16g));
                 });
             }
         }
+    };
+    auto issue_dn = [&](auto id_of) {
         if (has_dn)
             for (int e = 0; e < k; ++e) {
                 const uint8_t* sd =
                     a.arena + (size_t)id_of(e) * (size_t)a.blob + L.down_off + (size_t)j_dn * rd * d_row;
-                t1_dma(slab_dn + e * rd * d_row, n16_dn, [&](int i) { return (const void*)(sd + 16 * (size_t)i); });
+                t1_dma<kDnWave0, kDnWaves>(slab_dn + e * rd * d_row, n16_dn,
+                                           [&](int i) { return (const void*)(sd + 16 * (size_t)i); });
             }
     };
 
@@ -324,6 +333,8 @@ __global__ __launch_bounds__(kT1) void moe_decode_t1_kernel(FusedArgs a) {
         t1_vm_drain();
         issue([&](int i) { return s_ids[i]; });
     }
+    // a work-group with no gate/up unit fetches its down rows now; the others once their gate/up rows are in
+    if (!has_gu && dn_wave) issue_dn([&](int i) { return s_ids[i]; });
     if (b == 0 && tid < k) {
         a.ids[tid] = s_ids[tid];
         a.weights[tid] = s_w[tid];
@@ -337,7 +348,7 @@ __global__ __launch_bounds__(kT1) void moe_decode_t1_kernel(FusedArgs a) {
             // the canonical order (lane c's blocks c, c + L, ..: fma(d d8, s1), fma(-dmin d8, s2)) and the lanes'
             // butterfly (acc[c] += acc[c ^ o], o = L/2 .. 1)
             for (int hh = 0; hh < 2; ++hh) {
-                if (spec_wave) t1_vm_wait_le(hh == 0 ? n_b + n_d : n_d);
+                if (spec_wave) t1_vm_wait_le(hh == 0 ? n_b : 0);
                 t1_lds_barrier();
                 const uint8_t* half = slab_gu + hh * 32 * gu_row;
                 for (int t = tid; t < 32 * nbx * 4; t += kT1) {
@@ -390,7 +401,7 @@ __global__ __launch_bounds__(kT1) void moe_decode_t1_kernel(FusedArgs a) {
                 }
             }
         } else {
-            if (spec_wave) t1_vm_wait_le(n_d);   // the gate/up rows have landed (the down rows may still fly)
+            if (spec_wave) t1_vm_drain();   // the gate/up rows have landed
             t1_lds_barrier();
             constexpr int lprc = canon_lanes(H / UG::kUnit);
             const int c = lane & (lprc - 1);
@@ -406,6 +417,7 @@ __global__ __launch_bounds__(kT1) void moe_decode_t1_kernel(FusedArgs a) {
             }
         }
         t1_lds_barrier();
+        if (dn_wave) issue_dn([&](int i) { return s_ids[i]; });   // the gate/up rows are in and done with
         if (wave == kStoreWave) {
             // lane i < 32: h_i = SwiGLU(gate_i, up_i); the block's scale from the 32 |h|; codes; 9 tagged words
             const float h = lane < 32 ? canon_silu_mul(s_gu[lane], s_gu[32 + lane]) : 0.0f;
@@ -428,9 +440,10 @@ __global__ __launch_bounds__(kT1) void moe_decode_t1_kernel(FusedArgs a) {
 
     // ---- 3. the down unit: rows j_dn * rd .. + rd of all k experts, combined in rank order, + residual
     if (has_dn) {
-        if (spec_wave) t1_vm_drain();   // the down rows have landed (every wave reads them after this barrier)
+        if (dn_wave) t1_vm_drain();   // the down rows have landed (every wave reads them after this barrier; polling
+                                      // h while they land measured slower: the polls slow the rows and the h stores)
         t1_lds_barrier();
-        uint8_t* dec = slab_gu;         // (the gate/up rows are done with)
+        uint8_t* dec = slab_gu;         // (the gate/up rows were done with at the barrier before the h hand-over)
         constexpr int dstr = t1_dec_stride(F);
         const int nblk = k * nu;
         // waves 0 .. kPollWaves - 1 poll h while the others decode the down rows

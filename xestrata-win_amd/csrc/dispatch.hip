@@ -211,7 +211,8 @@ __global__ __launch_bounds__(1024) void route_fill_kernel(
     const int rank = __popcll(peers & below);
     if (in && rank == 0) s_w[wave * E + e] = __popcll(peers);
     __syncthreads();
-    int carry = 0, gcarry = 0, c128 = 0, c64 = 0;
+    int carry = 0, gcarry = 0, f128 = 0, p128 = 0, f64 = 0, p64 = 0;
+    const int64_t cap128 = tile_cap(n, 128, cap_groups), cap64 = tile_cap(n, 64, cap_groups);
     for (int e0 = 0; e0 < E; e0 += 1024) {
         const int ee = e0 + tid;
         int tot = 0, pre = 0;
@@ -228,23 +229,27 @@ __global__ __launch_bounds__(1024) void route_fill_kernel(
             }
         int sum_all;
         const int st = block_exclusive_scan(tot, s_wave, &sum_all) + carry;
-        if (blk == 0) {   // the groups (experts ascending), and the m-tile prefixes of 128- and 64-row tiles
-            int g_all, t_all, u_all;
+        if (blk == 0) {   // the groups (experts ascending), and the m-tile table of 128- and 64-row tiles
+            int g_all, a0, a1, a2, a3;
             const int gi = block_exclusive_scan(tot > 0 ? 1 : 0, s_wave, &g_all) + gcarry;
-            const int m128 = block_exclusive_scan((tot + 127) / 128, s_wave, &t_all) + c128;
-            const int m64 = block_exclusive_scan((tot + 63) / 64, s_wave, &u_all) + c64;
+            const int b128 = block_exclusive_scan(tot / 128, s_wave, &a0) + f128;
+            const int q128 = block_exclusive_scan(tot % 128 ? 1 : 0, s_wave, &a1) + p128;
+            const int b64 = block_exclusive_scan(tot / 64, s_wave, &a2) + f64;
+            const int q64 = block_exclusive_scan(tot % 64 ? 1 : 0, s_wave, &a3) + p64;
             if (ee < E && tot > 0) {
                 experts[gi] = ee;
                 bounds[gi] = st;
                 if (grp_ptr) grp_ptr[gi] = (unsigned long long)(uintptr_t)(cache_base + (size_t)ee * (size_t)blob);
                 if (mtile && gi < cap_groups) {
-                    mtile[gi] = m128;
-                    mtile[cap_groups + 1 + gi] = m64;
+                    write_group_tiles(tile_list(mtile, n, cap_groups, 128), gi, st, tot, 128, b128, q128, cap128);
+                    write_group_tiles(tile_list(mtile, n, cap_groups, 64), gi, st, tot, 64, b64, q64, cap64);
                 }
             }
             gcarry += g_all;
-            c128 += t_all;
-            c64 += u_all;
+            f128 += a0;
+            p128 += a1;
+            f64 += a2;
+            p64 += a3;
         }
         if (ee < E) {
             int b = st + pre;
@@ -259,9 +264,11 @@ __global__ __launch_bounds__(1024) void route_fill_kernel(
     if (blk == 0 && tid == 0) {
         bounds[gcarry] = n;
         *n_groups = gcarry;
-        if (mtile && gcarry <= cap_groups) {
-            mtile[gcarry] = c128;
-            mtile[cap_groups + 1 + gcarry] = c64;
+        if (mtile) {
+            mtile[0] = f128;
+            mtile[1] = p128;
+            mtile[2] = f64;
+            mtile[3] = p64;
         }
     }
     __syncthreads();

@@ -42,6 +42,12 @@ typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 constexpr int kBN = 256, kBK = 64;
+// the epilogue's staging tile in LDS: output rows of 128 values, 16 bytes of padding a row (the two half-waves write
+// rows 4 apart, which the padding puts 16 banks apart); f16 rows take a whole 128-row tile, fp32 rows 64 at a time
+constexpr int kStageF16 = 128 * 2 + 16, kStageF32 = 128 * 4 + 16;
+constexpr int kStageBytes = 128 * kStageF16 > 64 * kStageF32 ? 128 * kStageF16 : 64 * kStageF32;
+// bytes of LDS before the routing entries of a down tile: the A double buffer or the staging tile, the larger
+__host__ __device__ constexpr int entry_offset(int bm) { return 2 * bm * 128 > kStageBytes ? 2 * bm * 128 : kStageBytes; }
 // weight rows a lane dequantizes: one for Q6_K down weights (their raw words take the registers that a 128-row tile
 // needs), two otherwise (gate/up pairs a gate row with its up row)
 __host__ __device__ constexpr int lane_rows(bool down, int t) { return down && t == kQ6_K ? 1 : 2; }
@@ -73,38 +79,51 @@ __global__ __launch_bounds__(256) void to_f16_kernel(const float* __restrict__ x
                                       sat_f16x2(v1.y, v1.w));
 }
 
-// m-tile prefixes for 128- and 64-row tiles: mt[g] = sum over groups before g of ceil(rows / 128), mt[n_groups] =
-// the total; the same for 64 at mt + cap_groups + 1
+// the m-tile table (tile_list) of the groups in bounds: one work-group, the groups 1024 at a time; each thread
+// writes its group's tiles of both maps
 __global__ __launch_bounds__(1024) void tile_map_kernel(const int32_t* __restrict__ bounds,
                                                         const int32_t* __restrict__ n_groups, int32_t* __restrict__ mt,
-                                                        int cap_groups) {
-    __shared__ int s_wave[16];
-    __shared__ int s_carry;
+                                                        int64_t rows, int cap_groups) {
+    __shared__ int s_wave[16][4];
+    __shared__ int s_carry[4];
     const int ng = min(*n_groups, cap_groups);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    for (int pass = 0; pass < 2; ++pass) {
-        const int bm = pass ? 64 : 128;
-        int32_t* mtile = mt + pass * (cap_groups + 1);
-        if (tid == 0) s_carry = 0;
-        __syncthreads();
-        for (int g0 = 0; g0 <= ng; g0 += 1024) {
-            const int g = g0 + tid;
-            const int t = g < ng ? (bounds[g + 1] - bounds[g] + bm - 1) / bm : 0;
-            int inc = t;
+    const int64_t cap128 = tile_cap(rows, 128, cap_groups), cap64 = tile_cap(rows, 64, cap_groups);
+    int32_t* l128 = tile_list(mt, rows, cap_groups, 128);
+    int32_t* l64 = tile_list(mt, rows, cap_groups, 64);
+    if (tid < 4) s_carry[tid] = 0;
+    __syncthreads();
+    for (int g0 = 0; g0 < max(ng, 0); g0 += 1024) {
+        const int g = g0 + tid;
+        const int start = g < ng ? bounds[g] : 0, n = g < ng ? bounds[g + 1] - start : 0;
+        int c[4] = {n / 128, n % 128 ? 1 : 0, n / 64, n % 64 ? 1 : 0}, inc[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {   // inclusive wave scans of the four counts
+            inc[m] = c[m];
             for (int o = 1; o < 64; o <<= 1) {
-                const int y = __shfl_up(inc, o, 64);
-                if (lane >= o) inc += y;
+                const int y = __shfl_up(inc[m], o, 64);
+                if (lane >= o) inc[m] += y;
             }
-            if (lane == 63) s_wave[wave] = inc;
-            __syncthreads();
-            int before = s_carry;
-            for (int w = 0; w < wave; ++w) before += s_wave[w];
-            if (g <= ng) mtile[g] = before + inc - t;
-            __syncthreads();
-            if (tid == 1023) s_carry = before + inc;
-            __syncthreads();
+            if (lane == 63) s_wave[wave][m] = inc[m];
         }
+        __syncthreads();
+        int before[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            before[m] = s_carry[m] + inc[m] - c[m];
+            for (int w = 0; w < wave; ++w) before[m] += s_wave[w][m];
+        }
+        if (g < ng) {
+            write_group_tiles(l128, g, start, n, 128, before[0], before[1], cap128);
+            write_group_tiles(l64, g, start, n, 64, before[2], before[3], cap64);
+        }
+        __syncthreads();
+        if (tid == 1023)
+#pragma unroll
+            for (int m = 0; m < 4; ++m) s_carry[m] = before[m] + c[m];
+        __syncthreads();
     }
+    if (tid < 4) mt[tid] = s_carry[tid];
 }
 
 // Loads through a global-address-space pointer.  Blob addresses come from memory (the group table), so the compiler
@@ -126,6 +145,10 @@ __device__ __forceinline__ uint32_t ldg_u16(const void* p) {
 }
 
 __device__ __forceinline__ void vm_drain() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// A work-group barrier over LDS only: the wave's LDS operations are complete, its global loads may still be in flight.
+// (__syncthreads() is a release fence too, so it would wait for every load in flight - the prefetch of the steps
+// ahead - before the barrier.)
+__device__ __forceinline__ void lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 template <int N>
 struct IntC {
@@ -332,16 +355,11 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
     }
     if (mt >= mt_bound) return;
     const int ng = *a.n_groups;
-    if (ng <= 0 || mt >= mtile[ng]) return;
-    int lo = 0, hi = ng - 1;   // the group whose tiles hold mt
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (mtile[mid] <= mt) lo = mid;
-        else hi = mid - 1;
-    }
-    const int g = lo;
-    const int r0 = a.bounds[g] + (mt - mtile[g]) * kBM;
-    const int nrows = min(kBM, a.bounds[g + 1] - r0);
+    const int nfull = mtile[kBM == 128 ? 0 : 2], npart = mtile[kBM == 128 ? 1 : 3];
+    if (ng <= 0 || mt >= nfull + npart) return;
+    const int64_t te = mt < nfull ? mt : mt_bound - 1 - (mt - nfull);   // the tile's entry (tile_list)
+    const int32_t* tl = tile_list(const_cast<int32_t*>(mtile), a.rows, a.cap_groups, kBM) + 2 * te;
+    const int g = tl[0] & 0xFFFF, nrows = tl[0] >> 16, r0 = tl[1];
     const int nrt = (nrows + 31) >> 5;   // live 32-row tiles
     const int H = (int)L.n_embd, F = (int)L.n_ff;
     const int K = DOWN ? F : H;
@@ -362,7 +380,7 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
         asrc[i] = (const uint8_t*)(DOWN ? a.h + (int64_t)(r0 + rr) * F : a.xb + (int64_t)a.src[r0 + rr] * H) + 16 * c;
     }
     // down: the routing entry of each row, staged in LDS for the epilogue (visible after the first step's barrier)
-    int32_t* const s_entry = (int32_t*)(lds + 2 * kBM * 128);
+    int32_t* const s_entry = (int32_t*)(lds + entry_offset(kBM));
     if (DOWN && tid < nrows) s_entry[tid] = a.entry[r0 + tid];
     // the A rows of step ks into buffer `buf`
     auto dma_a = [&](int ks, int buf) {
@@ -439,7 +457,7 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
 #pragma unroll
                 for (int p = 0; p < 4; ++p) {
                     const int ks = 4 * b + p;
-                    __syncthreads();   // A(ks) is in buffer ks & 1; step ks - 1 is done with the other
+                    lds_sync();   // A(ks) is in buffer ks & 1; step ks - 1 is done with the other
                     // the step's scales first: at p = 3 the header registers then take the next block's header
                     Q4Step sj[J];
 #pragma unroll
@@ -467,9 +485,9 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
             }
         } else if (T == kQ6_K) {
             // K is short here (n_ff: 12 steps at 768), so the loads of a step must be in flight two steps ahead.  The
-            // A tile goes through registers (loaded at step ks - 2, written to LDS at step ks - 1) rather than by LDS
-            // DMA: the wait for a register load is the compiler's own and exact, while a wait for "all but the newest
-            // n" on vmcnt cannot single out LDS DMA among ordinary loads.  The raw words of a half are loaded at the
+            // A tile goes through registers (loaded at the start of step ks - 2, written to LDS at the end of step
+            // ks - 1) rather than by LDS DMA: the wait for a register load is the compiler's own and exact, while a
+            // wait for "all but the newest n" on vmcnt cannot single out LDS DMA among ordinary loads.  The raw words of a half are loaded at the
             // first step of the half before.  With 3 blocks a row (n_ff 768) everything is straight-line code.
             uint4 areg[2][RT];   // A(ks) staging, slot ks & 1
             auto load_a = [&](int ks, int slot) {
@@ -497,9 +515,8 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
 #pragma unroll
                         for (int t = 0; t < 2; ++t) {
                             const int ks = 4 * b + 2 * n + t;
-                            __syncthreads();   // A(ks) is in buffer ks & 1; step ks - 1 is done with the other
-                            if (ks + 1 < nk) store_a((ks + 1) & 1, (ks + 1) & 1);
-                            if (ks + 2 < nk) load_a(ks + 2, ks & 1);
+                            lds_sync();   // A(ks) is in buffer ks & 1; step ks - 1 is done with the other
+                            if (ks + 2 < nk) load_a(ks + 2, ks & 1);   // (slot ks & 1 went to LDS last step)
                             if (t == 0 && 2 * b + n + 1 < 2 * nb) {   // the next half's words
                                 const int h1 = 2 * b + n + 1;
 #pragma unroll
@@ -514,6 +531,9 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
                                     fb[j] = q6k_frag(r[n][j], t, kk, q6k_scale(r[n][j], t, kk, hf), qc);
                                 mfma_step(ks, kk, fb);
                             }
+                            // A(ks + 1), loaded a step ago, into the buffer step ks - 1 read: at the step's end, so
+                            // that its loads have two steps to land
+                            if (ks + 1 < nk) store_a((ks + 1) & 1, (ks + 1) & 1);
                         }
                     }
                 }
@@ -548,7 +568,7 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
             };
             auto q8_step = [&](int ks, auto slot_c) {
                 constexpr int SL = decltype(slot_c)::value;
-                __syncthreads();   // A(ks) is in buffer ks & 1; step ks - 1 is done with the other
+                lds_sync();   // A(ks) is in buffer ks & 1; step ks - 1 is done with the other
                 const int kn = min(ks + 1, nk - 1);
                 load_a(kn);
                 load_w(kn, IntC<SL ^ 1>{});
@@ -589,36 +609,57 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
     else if (RT > 2 && nrt == 2) kloop(IntC<(RT > 2 ? 2 : 1)>{});
     else kloop(IntC<1>{});
 
-    // lane holds C[32 i + 8 (q / 4) + 4 (lane / 32) + q % 4][cb[j] + lane % 32]
+    // Epilogue.  Lane holds C[32 i + 8 (q / 4) + 4 (lane / 32) + q % 4][cb[j] + lane % 32].  The values go through a
+    // row-major staging tile in LDS, so that every global store is 16 contiguous bytes of an output row: down rows
+    // scatter by routing entry, h rows are the tile's own.  Staging column sc = 32 wave + lane % 32 of pass j is
+    // output column cb[j] + lane % 32 (down), or h column n0 + sc at its place in the step order (gate/up).
+    lds_sync();   // every wave is done with the A buffers
+    const bool f32out = DOWN && !a.parts_h;
+    const int esz = f32out ? 4 : 2, stride = f32out ? kStageF32 : kStageF16, rpp = f32out ? 64 : 128;
+    const int cpr = 128 * esz / 16;   // 16-byte chunks a staged row
+    const int sc = 32 * wave + (lane & 31);
+    const int spos = DOWN ? sc : (sc & ~63) + perm64(sc & 63);
 #pragma unroll
-    for (int i = 0; i < RT; ++i) {
-        if (i >= nrt) break;
+    for (int j = 0; j < (DOWN ? J : 1); ++j) {
+        for (int rb = 0; rb < 32 * nrt; rb += rpp) {
 #pragma unroll
-        for (int q = 0; q < 16; ++q) {
-            const int row = 32 * i + 8 * (q >> 2) + 4 * hf + (q & 3);
-            if (row >= nrows) continue;
-            if (DOWN) {
-                const int64_t o = (int64_t)s_entry[row] * H + n0;
-                if (a.parts_h) {
+            for (int i = 0; i < RT; ++i) {
+                if (i >= nrt || 32 * i < rb || 32 * i >= rb + rpp) continue;
 #pragma unroll
-                    for (int j = 0; j < J; ++j) {
-                        const float v = __builtin_fminf(__builtin_fmaxf(acc[i][j][q], -65504.0f), 65504.0f);
-                        a.parts_h[o + cb[j] + (lane & 31)] = f2h(v);
+                for (int q = 0; q < 16; ++q) {
+                    const int row = 32 * i + 8 * (q >> 2) + 4 * hf + (q & 3);
+                    uint8_t* dst = lds + (row - rb) * stride + spos * esz;
+                    if (DOWN) {
+                        const float v = acc[i][j][q];
+                        if (f32out) *(float*)dst = v;
+                        else *(uint16_t*)dst = f2h(__builtin_fminf(__builtin_fmaxf(v, -65504.0f), 65504.0f));
+                    } else {
+                        // SwiGLU on the hardware exp2 and reciprocal (the f16 path's tolerance, not canon's bits)
+                        const float gv = acc[i][0][q], uv = acc[i][J - 1][q];
+                        const float e = __builtin_amdgcn_exp2f(-gv * 1.4426950408889634f);
+                        float hv = gv * __builtin_amdgcn_rcpf(1.0f + e) * uv;
+                        hv = __builtin_fminf(__builtin_fmaxf(hv, -65504.0f), 65504.0f);
+                        *(uint16_t*)dst = f2h(hv);
                     }
-                } else {
-#pragma unroll
-                    for (int j = 0; j < J; ++j) a.parts[o + cb[j] + (lane & 31)] = acc[i][j][q];
                 }
-            } else {
-                // SwiGLU on the hardware exp2 and reciprocal (the f16 path's tolerance, not canon's bits), stored in
-                // the step order the down product reads
-                const float gv = acc[i][0][q], uv = acc[i][J - 1][q];
-                const float e = __builtin_amdgcn_exp2f(-gv * 1.4426950408889634f);
-                float hv = gv * __builtin_amdgcn_rcpf(1.0f + e) * uv;
-                hv = __builtin_fminf(__builtin_fmaxf(hv, -65504.0f), 65504.0f);
-                const int col = n0 + cb[0] + (lane & 31);
-                a.h[(int64_t)(r0 + row) * F + (col & ~63) + perm64(col & 63)] = f2h(hv);
             }
+            lds_sync();
+            const int nr = min(rpp, nrows - rb);
+            for (int idx = tid; idx < nr * cpr; idx += 256) {
+                const int r = idx / cpr, c = idx - r * cpr, row = rb + r;
+                const uint4 v = *(const uint4*)(lds + r * stride + 16 * c);
+                const int scol = c * (16 / esz);   // the chunk's first staged column
+                if (DOWN) {
+                    const int w = scol >> 5;
+                    const int col = (J == 1 ? 32 * w : 64 * w + 32 * j) + (scol & 31);
+                    const int64_t o = (int64_t)s_entry[row] * H + n0 + col;
+                    if (f32out) *(uint4*)(a.parts + o) = v;
+                    else *(uint4*)(a.parts_h + o) = v;
+                } else {
+                    *(uint4*)(a.h + (int64_t)(r0 + row) * F + n0 + scol) = v;
+                }
+            }
+            lds_sync();   // the next pass writes the staging tile again
         }
     }
 }
@@ -631,14 +672,13 @@ static hipError_t launch_gemm(const ExpertLayout& L, const PrefillArgs& a, hipSt
     const int bm = 32 * row_tiles(DOWN, q8_fast ? t : (t == kQ8_0 ? 0 : t));
     const int mt_bound = (int)((a.rows + bm - 1) / bm + a.cap_groups);
     const unsigned grid = (unsigned)(n_tiles % 8 == 0 ? mt_bound * n_tiles : 8 * ((mt_bound + 7) / 8) * n_tiles);
-    const size_t lds = (size_t)2 * bm * 128 + (DOWN ? (size_t)bm * 4 : 0);
-    const int32_t* mtile = a.mtile + (bm == 128 ? 0 : a.cap_groups + 1);
+    const size_t lds = (size_t)entry_offset(bm) + (DOWN ? (size_t)bm * 4 : 0);
     void (*k)(ExpertLayout, PrefillArgs, const int32_t*, int, int) =
         t == kQ4_K   ? grouped_mfma_kernel<DOWN, kQ4_K, row_tiles(DOWN, kQ4_K)>
         : t == kQ6_K ? grouped_mfma_kernel<DOWN, kQ6_K, row_tiles(DOWN, kQ6_K)>
         : t == kQ8_0 && q8_fast ? grouped_mfma_kernel<DOWN, kQ8_0, row_tiles(DOWN, kQ8_0)>
                      : grouped_mfma_kernel<DOWN, 0, row_tiles(DOWN, 0)>;
-    hipLaunchKernelGGL(k, dim3(grid), dim3(256), lds, s, L, a, mtile, mt_bound, n_tiles);
+    hipLaunchKernelGGL(k, dim3(grid), dim3(256), lds, s, L, a, a.mtile, mt_bound, n_tiles);
     return hipGetLastError();
 }
 
@@ -646,7 +686,7 @@ hipError_t launch_prefill_experts(const ExpertLayout& L, const PrefillArgs& a, h
     const int64_t nc = a.n_tok * L.n_embd / 8;
     hipLaunchKernelGGL(to_f16_kernel, dim3((unsigned)((nc + 255) / 256)), dim3(256), 0, s, a.x, a.xb, nc);
     if (!a.mtile_ready)
-        hipLaunchKernelGGL(tile_map_kernel, dim3(1), dim3(1024), 0, s, a.bounds, a.n_groups, a.mtile,
+        hipLaunchKernelGGL(tile_map_kernel, dim3(1), dim3(1024), 0, s, a.bounds, a.n_groups, a.mtile, a.rows,
                            (int)a.cap_groups);
     hipError_t e = launch_gemm<false>(L, a, s);
     if (e != hipSuccess) return e;

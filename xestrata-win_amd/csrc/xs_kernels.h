@@ -63,7 +63,7 @@ hipError_t launch_prefill_route(const int32_t* ids, int64_t n, int k, int n_expe
                                 const uint8_t* cache_base, long long blob, unsigned long long* grp_ptr, hipStream_t s);
 
 // the same permutation over ceil(n / 1024) work-groups (ghist: prefill_route_split_scratch bytes), and, when mtile
-// is given, the m-tile prefixes launch_prefill_experts would compute (PrefillArgs::mtile_ready)
+// is given, the m-tile table launch_prefill_experts would compute (PrefillArgs::mtile_ready)
 hipError_t launch_prefill_route_split(const int32_t* ids, int64_t n, int k, int n_expert, int32_t* src, int32_t* slot,
                                       int32_t* entry, int32_t* bounds, int32_t* experts, int32_t* n_groups,
                                       const uint8_t* cache_base, long long blob, unsigned long long* grp_ptr,
@@ -165,12 +165,41 @@ struct PrefillArgs {
     uint16_t* h;                    // scratch: [rows, n_ff] f16 SwiGLU output, in the GEMM's K order
     float* parts;                   // [n_tok * k, n_embd] routing-order outputs
     uint16_t* parts_h;              // the same in f16 (saturated), written in place of parts when set
-    int32_t* mtile;                 // scratch: [2, cap_groups + 1] m-tile prefixes of the groups (128-, 64-row tiles)
-    bool mtile_ready;               // mtile already holds them (launch_prefill_route_split wrote them)
+    int32_t* mtile;                 // scratch: the m-tile table (tile_table_words words, layout at tile_list)
+    bool mtile_ready;               // mtile already holds it (launch_prefill_route_split wrote it)
     int32_t* err;
     int64_t n_tok, rows, cap_groups;
 };
 hipError_t launch_prefill_experts(const ExpertLayout& L, const PrefillArgs& a, hipStream_t s);
+
+// The m-tile table of a prompt batch: words 0, 1 the counts of full and of partial tiles of the 128-row map, words
+// 2, 3 the same of the 64-row map, then each map's list of tile_cap entries {group | rows << 16, first row}: the full
+// tiles from the front (every group's, groups ascending), the partial ones from the back (entry cap - 1 - i for the
+// i-th), so that a work-group's m-tile index mt < full is entry mt and is dispatched before every partial tile.
+__host__ __device__ inline int64_t tile_cap(int64_t rows, int bm, int64_t cap_groups) {
+    return (rows + bm - 1) / bm + cap_groups;
+}
+__host__ __device__ inline int32_t* tile_list(int32_t* t, int64_t rows, int64_t cap_groups, int bm) {
+    return t + 4 + (bm == 128 ? 0 : 2 * tile_cap(rows, 128, cap_groups));
+}
+__host__ __device__ inline int64_t tile_table_words(int64_t rows, int64_t cap_groups) {
+    return 4 + 2 * (tile_cap(rows, 128, cap_groups) + tile_cap(rows, 64, cap_groups));
+}
+// the tiles of group g (rows [start, start + n)) in a map of bm-row tiles with `cap` entries, given the full and the
+// partial tiles of the groups before it
+__device__ inline void write_group_tiles(int32_t* list, int g, int start, int n, int bm, int full_before,
+                                         int part_before, int64_t cap) {
+    const int nf = n / bm;
+    for (int t = 0; t < nf; ++t) {
+        list[2 * (full_before + t)] = g | (bm << 16);
+        list[2 * (full_before + t) + 1] = start + t * bm;
+    }
+    if (n % bm) {
+        const int64_t e = cap - 1 - part_before;
+        list[2 * e] = g | ((n % bm) << 16);
+        list[2 * e + 1] = start + nf * bm;
+    }
+}
 
 // the decode layer over a workspace whose tagged hand-over words sit in fixed regions sized for the largest layout
 // (abi.cpp; the library's own scratch of noalloc.hip): hidden sizes up to kScratchMaxEmbd, expert widths up to
