@@ -168,26 +168,40 @@ def other_configs(torch, xm, dev, gen, steps):
     that every step reads its experts from HBM."""
     import numpy as np
     out = {}
-    # config 4: Qwen3-235B-A22B-shaped, IQ4_XS experts (hidden 4096, 128 experts, top-8, F 1536), batch 1 and 8
-    E, H, F, k, copies = 128, 4096, 1536, 8, 2
-    arena, L = xm.build_arena(E, H, F, xm.IQ4_XS, xm.IQ4_XS, seed=4, copies=copies)
+    # config 4: the Qwen3-235B-A22B-shaped stack, IQ4_XS experts (hidden 4096, 128 experts, top-8, F 1536): 94 layers
+    # resident in HBM (120.6 GB), one token (or 8) through all 94 in one graph - per-stack time.  Layer 0 is quantized
+    # from seeded random weights; layers 1..93 are device copies of it at their own addresses (each layer's experts
+    # are read from HBM, the caches hold none of them)
+    E, H, F, k, NL = 128, 4096, 1536, 8, 94
+    layer0, L = xm.build_arena(E, H, F, xm.IQ4_XS, xm.IQ4_XS, seed=4)
+    stack = torch.empty(NL * E, L.bytes, dtype=torch.uint8, device=dev)
+    for li in range(NL):
+        stack[li * E:(li + 1) * E].copy_(layer0)
+    del layer0
+    torch.cuda.synchronize()
+    log(f"config 4: {NL}-layer stack resident, {stack.numel() / 1e9:.1f} GB")
     for T in (1, 8):
-        n_sets = max(1, E // (T * k))
-        lg = set_logits(torch, n_sets, T, E, k, dev, gen)
+        lg = torch.randn(NL, T, E, device=dev, generator=gen)   # each layer its own routing
         x = torch.randn(T, H, device=dev, generator=gen).to(torch.bfloat16).float()
         res = torch.randn(T, H, device=dev, generator=gen)
         o = torch.empty(T, H, device=dev)
-        layer = xm.MoeLayer(L, arena, E, k, T)
-        calls = [(lambda c=c, s=s: layer(x, lg[s], res, o, arena=arena[c * E]))
-                 for s in range(n_sets) for c in range(copies)]
-        ms = time_steps(torch, calls, steps, len(calls))
-        b = distinct_experts(torch, lg, k) * L.bytes
-        out[f"config4_T{T}"] = dict(us_per_layer=round(ms * 1e3, 2), us_per_token=round(ms * 1e3 / T, 3),
+        layer = xm.MoeLayer(L, stack, E, k, T)
+
+        def one_token():
+            for li in range(NL):
+                layer(x, lg[li], res, o, arena=stack[li * E])
+        graph_time(torch, one_token, 1)
+        ms, _ = graph_time(torch, one_token, 3)
+        b = sum(len(torch.unique(torch.topk(lg[li], k, dim=1).indices)) for li in range(NL)) * L.bytes
+        out[f"config4_T{T}"] = dict(us_per_stack=round(ms * 1e3, 1), us_per_token=round(ms * 1e3 / T, 1),
+                                    us_per_layer=round(ms * 1e3 / NL, 2), tokens_per_s=round(T / (ms * 1e-3), 1),
                                     expert_gbs=round(b / (ms * 1e-3) / 1e9, 1),
                                     frac_hbm_peak=round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                                    expert_mb=round(b / 1e6, 1))
-        log(f"config 4 decode T={T}: {ms * 1e3:.2f} us/layer, {out[f'config4_T{T}']['expert_gbs']} GB/s")
-    del arena
+                                    expert_gb_per_step=round(b / 1e9, 2), layers=NL,
+                                    stack_gb=round(stack.numel() / 1e9, 1), status=layer.status())
+        log(f"config 4 decode T={T}, {NL}-layer stack: {ms * 1e3:.1f} us/stack ({ms * 1e3 / T:.1f} us/token, "
+            f"{ms * 1e3 / NL:.2f} us/layer), {out[f'config4_T{T}']['expert_gbs']} GB/s")
+    del stack
     torch.cuda.empty_cache()
     # config 5: DeepSeek-V3-shaped (hidden 7168, 256 routed Q4_K experts, top-8, F 2048, one shared Q8_0 expert),
     # routed by its own group-limited sigmoid router (bias, 8 groups, top-4, routed scale 2.5), the shared expert's
