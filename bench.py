@@ -140,6 +140,29 @@ def pmc_prefill(torch, xm):
     log("pmc prefill run: 4 config-3 prefill layers")
 
 
+def pmc_tput(torch, xm):
+    """The workload of a rocprofv3 --pmc pass on the throughput decode: one rotation of config-2 layers at T=16 (8 HBM
+    copies, disjoint expert sets) and of config-4 layers at T=8 (2 HBM copies of the IQ4_XS layer, disjoint sets)."""
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    for name, (E, H, F, gt, dt, T, copies, seed) in (("config 2 T=16", (128, 2048, 768, xm.Q4_K, xm.Q6_K, 16, 8, 0)),
+                                                     ("config 4 T=8", (128, 4096, 1536, xm.IQ4_XS, xm.IQ4_XS, 8, 2, 4))):
+        k = 8
+        arena, L = xm.build_arena(E, H, F, gt, dt, seed=seed, copies=copies)
+        n_sets = max(1, E // (T * k))
+        lg = set_logits(torch, n_sets, T, E, k, "cuda", gen)
+        x = torch.randn(T, H, device="cuda", generator=gen).to(torch.bfloat16).float()
+        res = torch.randn(T, H, device="cuda", generator=gen)
+        out = torch.empty(T, H, device="cuda")
+        layer = xm.MoeLayer(L, arena, E, k, T)
+        for c in range(copies):
+            for st in range(n_sets):
+                layer(x, lg[st], res, out, arena=arena[c * E])
+        torch.cuda.synchronize()
+        log(f"pmc tput run: {name}, {copies * n_sets} layers; status {layer.status()}")
+        del arena
+        torch.cuda.empty_cache()
+
+
 def set_logits(torch, n_sets, T, E, k, dev, gen):
     """n_sets logit sets [n_sets, T, E]: i.i.d. N(0,1) plus +8 on set s's T*k experts (s*T*k .. mod E), so that the
     steps of a rotation touch disjoint experts and no step finds its blobs still in the caches."""
@@ -353,6 +376,8 @@ def main():
     ap.add_argument("--no-others", action="store_true", help="skip configs 3 (verify), 4 and 5")
     ap.add_argument("--pmc-run", action="store_true", help="only the short workload of a rocprofv3 --pmc pass")
     ap.add_argument("--pmc-prefill", action="store_true", help="only 4 prefill layers, for a rocprofv3 --pmc pass")
+    ap.add_argument("--pmc-tput", action="store_true",
+                    help="only config-2 T=16 and config-4 T=8 decode rotations, for a rocprofv3 --pmc pass")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -371,6 +396,9 @@ def main():
         return
     if args.pmc_prefill:
         pmc_prefill(torch, xm)
+        return
+    if args.pmc_tput:
+        pmc_tput(torch, xm)
         return
     E, H, F, k = 128, 2048, 768, 8
     copies = args.copies

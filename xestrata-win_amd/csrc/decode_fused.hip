@@ -123,18 +123,7 @@ __device__ __forceinline__ int add_dev(int32_t* p, int v) {
 // fills the memory queues.  So the waves that load never store a hand-over word: waves 0..2 fetch (weights by DMA,
 // activations, polls), wave 3 writes h and parts from LDS.
 __device__ __forceinline__ void vm_drain() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-// wait until at most n of the wave's vector memory operations are outstanding (n wave-uniform; above 15, 15: a wait
-// for more than asked, never less)
-__device__ __forceinline__ void vm_wait_le(int n) {
-    switch (n < 15 ? n : 15) {
-#define XS_VMW(i) \
-    case i: asm volatile("s_waitcnt vmcnt(" #i ")" ::: "memory"); break;
-        XS_VMW(0) XS_VMW(1) XS_VMW(2) XS_VMW(3) XS_VMW(4) XS_VMW(5) XS_VMW(6) XS_VMW(7)
-        XS_VMW(8) XS_VMW(9) XS_VMW(10) XS_VMW(11) XS_VMW(12) XS_VMW(13) XS_VMW(14) XS_VMW(15)
-#undef XS_VMW
-        default: break;
-    }
-}
+// (vm_wait_le: xs_device.h)
 
 // A work-group barrier for LDS hand-overs.  __syncthreads() is also a work-group release, which makes every wave wait
 // for all of its LDS DMA in flight (vmcnt(0)) - the next unit's rows fetched ahead on purpose included.  Where a wave

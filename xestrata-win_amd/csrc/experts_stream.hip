@@ -32,35 +32,6 @@ constexpr int kStreamLds = 160 * 1024;
 constexpr int kStreamStepMax = 10 * 1024;
 constexpr int kStreamNiMax = 12;   // DMA instructions a step at most (12 KB)
 
-__device__ __forceinline__ void stream_vm_wait_le(int n) {
-    switch (n < 63 ? n : 63) {
-#define XS_SW(i) \
-    case i: asm volatile("s_waitcnt vmcnt(" #i ")" ::: "memory"); break;
-        XS_SW(0) XS_SW(1) XS_SW(2) XS_SW(3) XS_SW(4) XS_SW(5) XS_SW(6) XS_SW(7) XS_SW(8) XS_SW(9) XS_SW(10) XS_SW(11)
-        XS_SW(12) XS_SW(13) XS_SW(14) XS_SW(15) XS_SW(16) XS_SW(17) XS_SW(18) XS_SW(19) XS_SW(20) XS_SW(21) XS_SW(22)
-        XS_SW(23) XS_SW(24) XS_SW(25) XS_SW(26) XS_SW(27) XS_SW(28) XS_SW(29) XS_SW(30) XS_SW(31) XS_SW(32) XS_SW(33)
-        XS_SW(34) XS_SW(35) XS_SW(36) XS_SW(37) XS_SW(38) XS_SW(39) XS_SW(40) XS_SW(41) XS_SW(42) XS_SW(43) XS_SW(44)
-        XS_SW(45) XS_SW(46) XS_SW(47) XS_SW(48) XS_SW(49) XS_SW(50) XS_SW(51) XS_SW(52) XS_SW(53) XS_SW(54) XS_SW(55)
-        XS_SW(56) XS_SW(57) XS_SW(58) XS_SW(59) XS_SW(60) XS_SW(61) XS_SW(62) XS_SW(63)
-#undef XS_SW
-        default: break;
-    }
-}
-
-// One LDS DMA (global_load_lds_dwordx4: 16 bytes a lane to lds_off + 16 lane) issued from inline assembly: the
-// compiler does not count it, so it places no conservative vmcnt(0) before the slots' LDS reads (it would for the
-// builtin, whose LDS write may alias them); the kernel's own waits order the slots.  Waits the compiler places for
-// other loads can only grow by the uncounted DMAs (returns are in order), never shrink.
-__device__ __forceinline__ void stream_dma16(const void* src, uint32_t lds_off) {
-    // an SALU write of M0 needs one wait state before an LDS DMA reads it (the compiler adds it for its own code, not
-    // inside inline assembly)
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(src), "s"(lds_off)
-                 : "memory", "m0");
-}
-__device__ __forceinline__ uint32_t lds_offset(const void* p) {
-    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
-}
-
 struct StreamGeom {
     int64_t mat_off;   // the matrix's offset in a blob
     int rows_total;    // rows of the matrix
@@ -166,7 +137,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_kernel(GroupedArgs a
             const int so = so0 + rrb[j];
             const int a0 = so & ~15, a1 = (so + G.segb + 15) & ~15;
             const bool live = ok_b && rr[j] >= 0 && r0_ + rr[j] < G.rows_total && a0 + cc[j] < a1;
-            stream_dma16(live ? blob + a0 + cc[j] : dummy, __builtin_amdgcn_readfirstlane(slot_off + 1024 * j));
+            dma16_nt(live ? blob + a0 + cc[j] : dummy, __builtin_amdgcn_readfirstlane(slot_off + 1024 * j));
         }
     };
 
@@ -182,7 +153,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_kernel(GroupedArgs a
     bool ok = false;
     for (int q = 0; q < total; ++q) {
         if (q + G.slots - 1 < total) issue(q + G.slots - 1);
-        stream_vm_wait_le(min(G.slots - 1, total - 1 - q) * G.ni);
+        vm_wait_le(min(G.slots - 1, total - 1 - q) * G.ni);
         const int task = t_first + q / G.steps, s = q - (q / G.steps) * G.steps;
         const int g = task / G.rowgroups;
         if (s == 0) {
