@@ -97,6 +97,29 @@ def test_config3_prefill(xm, c2_arena, T):
     assert rel <= 2e-2, rel
 
 
+def test_prefill_outlier_activation(xm, c2_arena):
+    """The f16 prompt path saturates activations and h at +-65504 (the f16 range), never to inf or NaN: a token with a
+    1e6 activation gets a finite output row (computed from the saturated values), and every other token's row stays
+    within 2e-2 of the fp32 reference (the outlier touches only its own rows)."""
+    from test_gpu_experts import torch_reference_prefill
+    arena, L = c2_arena
+    E, k, T, bad = 128, 8, 64, 17
+    g = torch.Generator(device=DEV).manual_seed(91)
+    x = torch.randn(T, L.n_embd, device=DEV, generator=g).to(torch.bfloat16).float()
+    x[bad, 5] = 1e6
+    res = torch.randn(T, L.n_embd, device=DEV, generator=g)
+    logits = zipf_logits(T, E, 91)
+    out = torch.empty_like(res)
+    xm.MoeLayer(L, arena, E, k, T, prefill=True)(x, logits, res, out)
+    assert bool(torch.isfinite(out).all())
+    ids, w = xm.router_top10(logits, k)
+    keep = torch.arange(T, device=DEV) != bad
+    parts = torch_reference_prefill(xm, arena, L, x, ids, E)
+    moe = (parts.reshape(T, k, -1) * w[:, :, None]).sum(1)
+    rel = float(((out - res) - moe)[keep].abs().max() / moe[keep].abs().max())
+    assert rel <= 2e-2, rel
+
+
 def test_prefill_matches_decode_path(xm, xo, c2_arena):
     """The same 16 tokens through both paths: the f16 MFMA layer within 2e-2 of the fp32-accumulate one."""
     arena, L = c2_arena
