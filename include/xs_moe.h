@@ -115,6 +115,19 @@ int xs_iq_mmq_quantize(const float* x, const int32_t* ids, void* xq, int64_t col
  * iq_mmq_quantize_scatter (iq_mmq.hpp:42-47) and prefill::mmq::quantize_scatter (moe_mmq.hpp:50-55). */
 int xs_iq_mmq_quantize_scatter(const float* x, const int32_t* slot, void* xq, int64_t cols, int64_t ld,
                                int64_t tokens, int k_used, int sums, int dup, void* stream);
+/* n experts in one launch: expert e's weights ([w_rows, w_cols] in ggml `type`'s blocks) at w + e * expert_bytes (or
+ * at wtab[e] + woff when wtab, a device table, is given), times its activation rows bounds[e] .. bounds[e + 1] of xq
+ * (xs_iq_mmq_quantize's layout, total_rows rows; bounds on the device), into dst rows ids[row], ld_dst floats apart.
+ * Replaces iq_mmq_grouped (include/strata/kernels/iq_mmq.hpp:49-58) and prefill::mmq::Context::run
+ * (include/strata/prefill/moe_mmq.hpp:57-75).  The products run on the f16 MFMA path of xs_moe_prefill_experts: the
+ * int8 activations are taken as q * d rounded to f16, the weights dequantized to f16, fp32 accumulation (within 2e-2
+ * of the fp32 product, the reference's int8 path within its own int8 rounding).  Types: Q8_0 (8), Q4_K (12), Q6_K
+ * (14), IQ4_XS (23); w_cols a multiple of 256 (64 for Q8_0), w_rows of 256 (128 for Q6_K).  max_rows is not needed
+ * (the tiles come from bounds on the device); rows (0: total_rows) bounds the tiles.  The library keeps a scratch
+ * buffer a device (the f16 activations, the group table, the tile table), grown on demand outside graph capture. */
+int xs_iq_mmq_grouped(int type, const void* w, size_t expert_bytes, int64_t w_rows, int64_t w_cols, int n,
+                      const void* xq, int64_t total_rows, const int32_t* bounds, int64_t max_rows, const int32_t* ids,
+                      float* dst, int64_t ld_dst, const uint8_t* const* wtab, size_t woff, int64_t rows, void* stream);
 /* h[r, j] = g / (1 + exp(-g)) * u over rows of 2 n_ff floats (gate, up interleaved 2j / 2j+1, or split j / n_ff+j).
  * Replaces prefill::mmq::swiglu (moe_mmq.hpp:106-108; src/prefill/moe_mmq.cpp:128-136). */
 int xs_mmq_swiglu(const float* gu, float* h, int64_t rows, int64_t n_ff, int interleaved, void* stream);

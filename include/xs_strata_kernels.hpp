@@ -227,9 +227,84 @@ inline size_t moe_layer_prefill_workspace_bytes(const NativeExpertLayout& L, int
     return xs_moe_layer_prefill_workspace_bytes(&c, n_expert, k, n_tok);
 }
 
+/// include/strata/kernels/bf16_gemv.hpp:48-49 (one token).
+inline void bf16_gemv_fp32_mmvf(const float* x, const uint16_t* w, float* y, int64_t n_in, int64_t n_out,
+                                void* stream) {
+    detail::check(xs_bf16_gemv_fp32_mmvf_multi(x, n_in, w, y, n_out, n_in, n_out, 1, stream));
+}
+/// include/strata/kernels/bf16_gemv.hpp:52 (one token).
+inline void f32_gemv_fp32_mmvf(const float* x, const float* w, float* y, int64_t n_in, int64_t n_out, void* stream) {
+    detail::check(xs_f32_gemv_fp32_mmvf_multi(x, n_in, w, y, n_out, n_in, n_out, 1, stream));
+}
+/// include/strata/kernels/bf16_gemv.hpp:55-56
+inline void f32_gemv_fp32_mmvf_multi(const float* x, int64_t ldx, const float* w, float* y, int64_t ldy,
+                                     int64_t n_in, int64_t n_out, int n_tok, void* stream) {
+    detail::check(xs_f32_gemv_fp32_mmvf_multi(x, ldx, w, y, ldy, n_in, n_out, n_tok, stream));
+}
+/// include/strata/kernels/bf16_gemv.hpp:64-65
+inline void bf16_gemv_fp32_mmvf_multi(const float* x, int64_t ldx, const uint16_t* w, float* y, int64_t ldy,
+                                      int64_t n_in, int64_t n_out, int n_tok, void* stream) {
+    detail::check(xs_bf16_gemv_fp32_mmvf_multi(x, ldx, w, y, ldy, n_in, n_out, n_tok, stream));
+}
+/// include/strata/kernels/bf16_gemv.hpp:60-61
+inline void f32_gemm_rows(const float* x, int64_t ldx, const float* w, float* y, int64_t ldy, int64_t n_in,
+                          int64_t n_out, int64_t n_tok, void* stream) {
+    detail::check(xs_f32_gemm_rows(x, ldx, w, y, ldy, n_in, n_out, n_tok, stream));
+}
+/// include/strata/kernels/bf16_gemv.hpp:30
+inline void bf16_gemv(const uint16_t* x, const uint16_t* w, float* y, int64_t n_in, int64_t n_out, void* stream) {
+    detail::check(xs_bf16_gemv(x, w, y, n_in, n_out, stream));
+}
+/// include/strata/kernels/bf16_gemv.hpp:38-39
+inline void bf16_gemv_split(const uint16_t* x, const uint16_t* w, float* y, int64_t n_in, int64_t n_out,
+                            int threads_per_row, void* stream) {
+    detail::check(xs_bf16_gemv_split(x, w, y, n_in, n_out, threads_per_row, stream));
+}
+/// include/strata/kernels/elementwise.hpp:71
+inline void f32_to_bf16_bulk(const float* x, uint16_t* y, int64_t n, void* stream) {
+    detail::check(xs_f32_to_bf16_bulk(x, y, n, stream));
+}
+
+/// include/strata/kernels/iq_mmq.hpp:53-58 (the stream in place of the queue).
+inline void iq_mmq_grouped(void* stream, int ggml_type, const void* w, size_t expert_bytes, int64_t w_rows,
+                           int64_t w_cols, int n, const void* xq, int64_t total_rows, const int32_t* bounds,
+                           int64_t max_rows, const int32_t* ids, float* dst, int64_t ld_dst,
+                           const uint8_t* const* wtab = nullptr, size_t woff = 0, int64_t rows = 0) {
+    detail::check(xs_iq_mmq_grouped(ggml_type, w, expert_bytes, w_rows, w_cols, n, xq, total_rows, bounds, max_rows,
+                                    ids, dst, ld_dst, wtab, woff, rows, stream));
+}
+
 }  // namespace strata::kernels
 
 namespace strata::prefill::mmq {
+
+/// include/strata/prefill/moe_mmq.hpp:57-72: one grouped product over n experts.
+struct Product {
+    const void* w = nullptr;
+    int type = -1;
+    int64_t w_rows = 0, w_cols = 0;
+    size_t expert_bytes = 0;
+    int n = 0;
+    const void* xq = nullptr;
+    const int32_t* bounds = nullptr;
+    const int32_t* ids = nullptr;
+    int64_t total_rows = 0, max_rows = 0;
+    int64_t rows = 0;
+    float* dst = nullptr;
+    int64_t ld_dst = 0;
+    const uint8_t* const* wtab = nullptr;
+    size_t woff = 0;
+};
+
+/// include/strata/prefill/moe_mmq.hpp:74-84: the launch context (the library keeps its scratch itself).
+class Context {
+public:
+    void run(const Product& p, void* stream) {
+        kernels::detail::check(xs_iq_mmq_grouped(p.type, p.w, p.expert_bytes, p.w_rows, p.w_cols, p.n, p.xq,
+                                                 p.total_rows, p.bounds, p.max_rows, p.ids, p.dst, p.ld_dst, p.wtab,
+                                                 p.woff, p.rows, stream));
+    }
+};
 
 /// include/strata/prefill/moe_mmq.hpp:41-43
 inline size_t q8_bytes(int64_t rows, int64_t cols) { return xs_iq_mmq_act_bytes(rows, cols); }

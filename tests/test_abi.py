@@ -81,3 +81,26 @@ def test_argument_errors(xm):
     assert lib.xs_native_expert_grouped(ctypes.byref(L), 8, 8, 8, 8, 8, 1, 1, 8, 16, 8, None, 0) == xm.XS_EINVAL
     # resident_plan: more entries than a work-group
     assert lib.xs_resident_plan(8, 2000, 8, None, 128, None, None, 16, 8, 4000, 8, 1, 8) == xm.XS_EINVAL
+
+
+def test_mmq_grouped_refusals(xm):
+    """iq_mmq_grouped refuses, before any device call, the types its products do not decode, widths its tiles do not
+    cover, a dst row narrower than the weights' rows and missing spans; n = 0 or no rows is a no-op."""
+    lib = xm.lib()
+    E = xm.XS_EINVAL
+    args = dict(w=16, eb=4096, wr=512, wc=2048, n=4, xq=16, tot=64, b=16, mr=64, ids=16, dst=16, ld=512, wt=None,
+                wo=0, rows=0)
+
+    def call(t, **kw):
+        a = dict(args, **kw)
+        return lib.xs_iq_mmq_grouped(t, a["w"], a["eb"], a["wr"], a["wc"], a["n"], a["xq"], a["tot"], a["b"], a["mr"],
+                                     a["ids"], a["dst"], a["ld"], a["wt"], a["wo"], a["rows"], None)
+    assert call(10) == E                        # Q2_K: not among this build's products
+    assert "ggml type 10" in lib.xs_last_error().decode()
+    assert call(12, wc=2000) == E               # columns not a multiple of 256
+    assert call(12, wr=384) == E                # Q4_K rows: tiles of 256
+    assert call(12, ld=256) == E                # dst rows narrower than the weights' rows
+    assert call(12, ids=None) == E
+    assert call(12, w=None) == E                # neither w nor wtab
+    assert call(12, n=0) == xm.XS_OK
+    assert call(12, tot=0) == xm.XS_OK

@@ -31,6 +31,17 @@ void surface(void* stream) {
     m::quantize_scatter(nullptr, nullptr, nullptr, nullptr, 12, 256, 256, 1, 8, stream);
     m::swiglu(nullptr, nullptr, 1, 768, false, stream);
     m::iota(nullptr, 16, stream);
+    k::iq_mmq_grouped(stream, 12, nullptr, 0, 256, 256, 1, nullptr, 1, nullptr, 1, nullptr, nullptr, 256);
+    k::f32_gemv_fp32_mmvf(nullptr, nullptr, nullptr, 2048, 128, stream);
+    k::bf16_gemv_fp32_mmvf(nullptr, nullptr, nullptr, 2048, 128, stream);
+    k::f32_gemv_fp32_mmvf_multi(nullptr, 2048, nullptr, nullptr, 128, 2048, 128, 4, stream);
+    k::bf16_gemv_fp32_mmvf_multi(nullptr, 2048, nullptr, nullptr, 128, 2048, 128, 4, stream);
+    k::f32_gemm_rows(nullptr, 2048, nullptr, nullptr, 128, 2048, 128, 64, stream);
+    k::bf16_gemv(nullptr, nullptr, nullptr, 2048, 128, stream);
+    k::bf16_gemv_split(nullptr, nullptr, nullptr, 2048, 128, 32, stream);
+    k::f32_to_bf16_bulk(nullptr, nullptr, 2048, stream);
+    m::Product prod;
+    m::Context().run(prod, stream);
     k::native_moe_combine_multi_hits(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 2048, 8, 1, stream);
     const size_t ws = k::moe_layer_decode_workspace_bytes(L, 128, 8, 1);
     k::moe_layer_decode(L, nullptr, L.bytes, 128, 8, nullptr, nullptr, nullptr, nullptr, 1, nullptr, ws, stream);

@@ -197,3 +197,50 @@ def test_ids_from_own_logits(xm, xo, n_tok, n_expert, n_in, k):
     rids, rw = xo.router_top10(want_logits, k)
     assert np.array_equal(t2n(ids), rids)
     assert np.array_equal(t2n(wts).view(np.uint32), rw.view(np.uint32))
+
+
+@pytest.mark.parametrize("t,w_rows,w_cols,counts,use_wtab", [
+    (12, 512, 2048, [40, 0, 300, 7, 129, 64], False), (14, 2048, 768, [128, 1, 0, 257, 33], False),
+    (8, 512, 1024, [5, 200, 77, 0], True), (23, 256, 4096, [65, 3, 130], False),
+    (12, 768, 2048, [1, 2, 3, 150, 0, 0, 9, 31], True)])
+def test_iq_mmq_grouped(xm, t, w_rows, w_cols, counts, use_wtab):
+    """iq_mmq_grouped over xs_iq_mmq_quantize's int8 activations: expert e's rows bounds[e] .. bounds[e + 1] times its
+    weights (contiguous, or through a device table in another order) into dst rows ids[row] of a wider dst, against an
+    fp32 reference over the exactly dequantized weights and activations (q * d): within 2e-2 (the f16 MFMA path); the
+    columns past w_rows untouched."""
+    g = torch.Generator(device=DEV).manual_seed(t * 1000 + w_rows)
+    n = len(counts)
+    rb = xm.row_bytes(t, w_cols)
+    eb = (w_rows * rb + 255) // 256 * 256 + 256          # expert_bytes: padded past the matrix
+    wbuf = torch.zeros(n * eb, dtype=torch.uint8, device=DEV)
+    W = []
+    for e in range(n):
+        w = torch.randn(w_rows, w_cols, generator=g, device=DEV) * 0.02
+        xm.quantize_rows(t, w.reshape(-1), out=wbuf[e * eb:e * eb + w_rows * rb])
+        W.append(xm.iq_dequant_f32(t, wbuf[e * eb:e * eb + w_rows * rb], w_rows * w_cols).reshape(w_rows, w_cols))
+    total = sum(counts)
+    bounds = torch.tensor(np.concatenate([[0], np.cumsum(counts)]).astype(np.int32), device=DEV)
+    x = torch.randn(total, w_cols, generator=g, device=DEV)
+    xq = xm.iq_mmq_quantize(x, None, w_cols, w_cols, total, True)
+    q = xq[:total * w_cols].view(torch.int8).reshape(total, w_cols).float()
+    d = xq[total * w_cols:total * w_cols + total * (w_cols // 32) * 4].view(torch.float32).reshape(total, -1)
+    a = q * d.repeat_interleave(32, dim=1)
+    ids = torch.randperm(total, generator=torch.Generator().manual_seed(5)).to(torch.int32).to(DEV)
+    ld = w_rows + 64
+    dst = torch.full((total, ld), 7.0, device=DEV)
+    order = list(range(n))
+    table = None
+    if use_wtab:                                          # expert e's weights: blob order[e]
+        order = list(reversed(range(n)))
+        table = torch.tensor([wbuf.data_ptr() + o * eb for o in order], dtype=torch.int64, device=DEV)
+    xm.iq_mmq_grouped(t, None if use_wtab else wbuf, eb, w_rows, w_cols, n, xq, total, bounds, ids, dst, ld,
+                      wtab=table)
+    ref = torch.zeros(total, w_rows, device=DEV)
+    for e in range(n):
+        r0, r1 = int(bounds[e]), int(bounds[e + 1])
+        if r1 > r0:
+            ref[r0:r1] = a[r0:r1] @ W[order[e]].t().contiguous()
+    got = dst[ids.long()]
+    rel = float((got[:, :w_rows] - ref).abs().max() / ref.abs().max())
+    assert rel <= 2e-2, rel
+    assert bool((got[:, w_rows:] == 7.0).all())

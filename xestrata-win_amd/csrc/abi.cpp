@@ -8,6 +8,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 namespace {
@@ -508,9 +509,103 @@ int prefill_experts(const xs_expert_layout_t* L, const float* x, int64_t n_tok, 
     a.n_tok = n_tok;
     a.rows = rows;
     a.cap_groups = cap_groups;
+    a.ld_parts = L->n_embd;
     return finish(stream, xs::launch_prefill_experts(to_layout(L), a, S(stream)), "moe_prefill_experts");
 }
 }  // namespace
+
+namespace {
+// The library's own scratch for xs_iq_mmq_grouped (whose reference signature has no workspace): one buffer a device,
+// grown on demand outside graph capture and kept until the process ends.
+struct MmqScratch {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+};
+std::mutex g_mmq_mutex;
+MmqScratch g_mmq[64];
+}  // namespace
+
+int xs_iq_mmq_grouped(int type, const void* w, size_t expert_bytes, int64_t w_rows, int64_t w_cols, int n,
+                      const void* xq, int64_t total_rows, const int32_t* bounds, int64_t max_rows, const int32_t* ids,
+                      float* dst, int64_t ld_dst, const uint8_t* const* wtab, size_t woff, int64_t rows,
+                      void* stream) {
+    (void)max_rows;   // the grid comes from the tile table, built on the device from bounds
+    if (n <= 0 || total_rows <= 0) return ok();
+    if (type != 8 && type != 12 && type != 14 && type != 23)
+        return fail(XS_EINVAL, "iq_mmq_grouped: ggml type %d (this build's products: Q8_0, Q4_K, Q6_K, IQ4_XS)",
+                    type);
+    const int64_t out_tile = type == 14 ? 128 : 256;   // output columns a work-group: 128, or 256 (two rows a lane)
+    if (w_cols <= 0 || w_cols % (type == 8 ? 64 : 256) || w_rows <= 0 || w_rows % out_tile || n > 65535 ||
+        ld_dst < w_rows || ld_dst % 4)
+        return fail(XS_EINVAL,
+                    "iq_mmq_grouped: %lld x %lld weights (columns a multiple of %d, rows of %lld), %d experts, "
+                    "%lld floats a dst row",
+                    (long long)w_rows, (long long)w_cols, type == 8 ? 64 : 256, (long long)out_tile, n,
+                    (long long)ld_dst);
+    if (!(wtab ? aligned(wtab, 8) : (w && aligned(w, 16) && expert_bytes % 16 == 0)) || !aligned(xq, 16) ||
+        !aligned(bounds, 4) || !aligned(ids, 4) || !aligned(dst, 16))
+        return fail(XS_EINVAL, "iq_mmq_grouped: a span is missing or misaligned");
+    const int64_t nrows = rows > 0 ? rows : total_rows;
+    const size_t xb_bytes = up256((size_t)total_rows * (size_t)w_cols * 2);
+    const size_t ptr_bytes = up256((size_t)n * 8 + 256);   // the group pointers, then n_groups and the status word
+    const size_t need = xb_bytes + ptr_bytes + up256((size_t)xs::tile_table_words(nrows, n) * 4);
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return fail(XS_EDEVICE, "iq_mmq_grouped: no device");
+    void* scratch = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_mmq_mutex);
+        MmqScratch& m = g_mmq[dev];
+        if (m.bytes < need) {
+            hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+            if (hipStreamIsCapturing(S(stream), &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
+                return fail(XS_EINVAL, "iq_mmq_grouped: its scratch must grow (%zu bytes) outside graph capture", need);
+            if (m.ptr) {
+                (void)hipDeviceSynchronize();
+                (void)hipFree(m.ptr);
+                m.ptr = nullptr;
+                m.bytes = 0;
+            }
+            if (hipMalloc(&m.ptr, need) != hipSuccess) return fail(XS_EDEVICE, "iq_mmq_grouped: %zu bytes of scratch", need);
+            m.bytes = need;
+        }
+        scratch = m.ptr;
+    }
+    uint8_t* sp = (uint8_t*)scratch;
+    uint16_t* xb = (uint16_t*)sp;
+    unsigned long long* grp_ptr = (unsigned long long*)(sp + xb_bytes);
+    int32_t* n_groups = (int32_t*)(sp + xb_bytes + (size_t)n * 8);
+    int32_t* err = n_groups + 1;
+    int32_t* table = (int32_t*)(sp + xb_bytes + ptr_bytes);
+    xs::ExpertLayout L;
+    L.gu_type = L.d_type = type;
+    L.n_embd = w_rows;
+    L.n_ff = w_cols;
+    L.gu_row = L.d_row = (int64_t)xs_iq_row_bytes(type, w_cols);
+    L.up_off = L.down_off = 0;
+    L.bytes = (int64_t)expert_bytes;
+    xs::PrefillArgs a{};
+    a.bounds = bounds;
+    a.n_groups = n_groups;
+    a.wptr = grp_ptr;
+    a.entry = ids;
+    a.h = xb;
+    a.parts = dst;
+    a.parts_h = nullptr;
+    a.mtile = table;
+    a.mtile_ready = true;
+    a.err = err;
+    a.n_tok = total_rows;
+    a.rows = nrows;
+    a.cap_groups = n;
+    a.ld_parts = ld_dst;
+    if (int r = finish(stream, xs::launch_mmq_act_to_f16(xq, total_rows, w_cols, xb, S(stream)), "iq_mmq_grouped"))
+        return r;
+    if (int r = finish(stream, xs::launch_group_table((const uint8_t*)w, expert_bytes, wtab, woff, n, grp_ptr, n_groups,
+                                                      S(stream)),
+                       "iq_mmq_grouped"))
+        return r;
+    return finish(stream, xs::launch_grouped_product(L, a, S(stream)), "iq_mmq_grouped");
+}
 
 int xs_moe_prefill_experts(const xs_expert_layout_t* L, const float* x, int64_t n_tok, const int32_t* src,
                            const int32_t* entry_of, const int32_t* bounds, const int32_t* n_groups,

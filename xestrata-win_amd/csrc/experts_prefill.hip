@@ -652,7 +652,7 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
                 if (DOWN) {
                     const int w = scol >> 5;
                     const int col = (J == 1 ? 32 * w : 64 * w + 32 * j) + (scol & 31);
-                    const int64_t o = (int64_t)s_entry[row] * H + n0 + col;
+                    const int64_t o = (int64_t)s_entry[row] * a.ld_parts + n0 + col;
                     if (f32out) *(uint4*)(a.parts + o) = v;
                     else *(uint4*)(a.parts_h + o) = v;
                 } else {
@@ -680,6 +680,51 @@ static hipError_t launch_gemm(const ExpertLayout& L, const PrefillArgs& a, hipSt
                      : grouped_mfma_kernel<DOWN, 0, row_tiles(DOWN, 0)>;
     hipLaunchKernelGGL(k, dim3(grid), dim3(256), lds, s, L, a, a.mtile, mt_bound, n_tiles);
     return hipGetLastError();
+}
+
+// xq's int8 codes times their block scales, rounded to f16 (saturated) in the GEMM's K order: thread i writes chunk
+// i (8 values) of the [rows, cols] activations, as to_f16_kernel does for fp32 rows
+__global__ __launch_bounds__(256) void mmq_act_to_f16_kernel(const int8_t* __restrict__ q, const float* __restrict__ d,
+                                                             uint16_t* __restrict__ y, int64_t n_chunks, int64_t cols) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n_chunks) return;
+    const int64_t j = (i & ~(int64_t)7) * 8 + 8 * perm8((int)(i & 7));   // the chunk's first value (8 share a block)
+    const float dj = d[(j / cols) * (cols / 32) + (j % cols) / 32];
+    const uint2 w = *(const uint2*)(q + j);
+    float v[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) v[t] = (float)(int8_t)(((t < 4 ? w.x : w.y) >> (8 * (t & 3))) & 0xFFu) * dj;
+    *(uint4*)(y + 8 * i) = make_uint4(sat_f16x2(v[0], v[2]), sat_f16x2(v[1], v[3]), sat_f16x2(v[4], v[6]),
+                                      sat_f16x2(v[5], v[7]));
+}
+
+__global__ __launch_bounds__(256) void group_table_kernel(const uint8_t* w, size_t expert_bytes,
+                                                          const uint8_t* const* wtab, size_t woff, int n,
+                                                          unsigned long long* __restrict__ grp_ptr,
+                                                          int32_t* __restrict__ n_groups) {
+    for (int g = threadIdx.x; g < n; g += blockDim.x)
+        grp_ptr[g] = (unsigned long long)(uintptr_t)(wtab ? wtab[g] + woff : w + (size_t)g * expert_bytes);
+    if (threadIdx.x == 0) *n_groups = n;
+}
+
+hipError_t launch_mmq_act_to_f16(const void* xq, int64_t rows, int64_t cols, uint16_t* xb, hipStream_t s) {
+    const int64_t nc = rows * cols / 8;
+    hipLaunchKernelGGL(mmq_act_to_f16_kernel, dim3((unsigned)((nc + 255) / 256)), dim3(256), 0, s, (const int8_t*)xq,
+                       (const float*)((const int8_t*)xq + rows * cols), xb, nc, cols);
+    return hipGetLastError();
+}
+
+hipError_t launch_group_table(const uint8_t* w, size_t expert_bytes, const uint8_t* const* wtab, size_t woff, int n,
+                              unsigned long long* grp_ptr, int32_t* n_groups, hipStream_t s) {
+    hipLaunchKernelGGL(group_table_kernel, dim3(1), dim3(256), 0, s, w, expert_bytes, wtab, woff, n, grp_ptr,
+                       n_groups);
+    return hipGetLastError();
+}
+
+hipError_t launch_grouped_product(const ExpertLayout& L, const PrefillArgs& a, hipStream_t s) {
+    hipLaunchKernelGGL(tile_map_kernel, dim3(1), dim3(1024), 0, s, a.bounds, a.n_groups, a.mtile, a.rows,
+                       (int)a.cap_groups);
+    return launch_gemm<true>(L, a, s);
 }
 
 hipError_t launch_prefill_experts(const ExpertLayout& L, const PrefillArgs& a, hipStream_t s) {

@@ -110,6 +110,7 @@ _SIGS = {
     "xs_iq_mmq_quantize": (I, [P, P, P, I64, I64, I64, I, I, P]),
     "xs_iq_mmq_quantize_scatter": (I, [P, P, P, I64, I64, I64, I, I, I, P]),
     "xs_mmq_swiglu": (I, [P, P, I64, I64, I, P]),
+    "xs_iq_mmq_grouped": (I, [I, P, SZ, I64, I64, I, P, I64, P, I64, P, P, I64, P, SZ, I64, P]),
     "xs_mmq_iota": (I, [P, I64, P]),
     "xs_quantize_rows": (I, [I, P, I64, P, P]),
     "xs_router_top10": (I, [P, I, I, I, P, P, P]),
@@ -427,6 +428,17 @@ def iq_mmq_quantize(x, ids, cols, ld, rows, sums, dup=False, out=None, stream=No
         out = torch.zeros(iq_mmq_act_bytes(rows, 2 * cols if dup else cols), dtype=torch.uint8, device=x.device)
     _check(lib().xs_iq_mmq_quantize(_p(x), _p(ids), _p(out), cols, ld, rows, int(sums), int(dup), _stream(stream)))
     return out
+
+
+def iq_mmq_grouped(type_, w, expert_bytes, w_rows, w_cols, n, xq, total_rows, bounds, ids, dst, ld_dst, wtab=None,
+                   woff=0, rows=0, max_rows=0, stream=None):
+    """n experts' [w_rows, w_cols] products over the int8 MMQ activations xq into dst rows ids[row]
+    (xs_iq_mmq_grouped).  w: the first expert's weights (experts expert_bytes apart) or, with wtab (a device int64
+    tensor of n addresses), ignored."""
+    _check(lib().xs_iq_mmq_grouped(type_, _p(w), expert_bytes, w_rows, w_cols, n, _p(xq),
+                                   total_rows, _p(bounds), max_rows, _p(ids), _p(dst), ld_dst, _p(wtab), woff, rows,
+                                   _stream(stream)))
+    return dst
 
 
 def iq_mmq_quantize_scatter(x, slot, cols, ld, tokens, k_used, sums, dup=False, out=None, stream=None):
