@@ -27,7 +27,8 @@
 
 namespace xs {
 
-constexpr int kStreamWaves = 8;   // two waves a SIMD: one computes while the other waits
+constexpr int kStreamWaves = 8;   // waves a work-group: two a SIMD, one computes while the other waits
+constexpr int kStreamWavesWide = 12;   // three a SIMD, for gate/up kernels whose registers allow it (<= 168 VGPRs)
 constexpr int kStreamLds = 160 * 1024;
 constexpr int kStreamStepMax = 10 * 1024;
 constexpr int kStreamNiMax = 12;   // DMA instructions a step at most (12 KB)
@@ -55,10 +56,11 @@ struct StreamGeom {
     int ne;            // the kernel's entries a pass
     int F;             // n_ff (outputs of gate/up, h width)
     int H;             // n_embd
+    int waves;         // waves a work-group (kStreamWaves or kStreamWavesWide)
 };
 
-template <int T, bool DOWN, int LPR, int NE>
-__global__ __launch_bounds__(64 * kStreamWaves) void stream_kernel(GroupedArgs a, StreamGeom G, const int8_t* __restrict__ hact_q,
+template <int T, bool DOWN, int LPR, int NE, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void stream_kernel(GroupedArgs a, StreamGeom G, const int8_t* __restrict__ hact_q,
                                                      const float* __restrict__ hact_d, const int* __restrict__ hact_s) {
     using U = Unit<T, !DOWN>;
     extern __shared__ __align__(16) uint8_t lds[];
@@ -70,7 +72,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_kernel(GroupedArgs a
     int* m_start = (int*)(m_ptr + G.cap_groups);
     int* m_ent = m_start + G.cap_groups + 1;
     const int ng = min(*a.n_groups, G.cap_groups);
-    constexpr int NT = 64 * kStreamWaves;
+    constexpr int NT = 64 * WAVES;
     for (int i = tid; i < ng; i += NT) m_ptr[i] = a.grp_ptr[i];
     for (int i = tid; i <= ng; i += NT) m_start[i] = a.grp_start[i];
     const int e_end = a.grp_start[ng];
@@ -105,7 +107,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_kernel(GroupedArgs a
     int* ws16 = (int*)(wd8 + NE * nb32);
     uint8_t* ring = act + G.act_bytes + wave * G.ring;
     const int n_tasks = ng * G.rowgroups;
-    const int W = gridDim.x * kStreamWaves, w = blockIdx.x * kStreamWaves + wave;
+    const int W = gridDim.x * WAVES, w = blockIdx.x * WAVES + wave;
     const int per = (n_tasks + W - 1) / W;   // a contiguous range of tasks a wave: few group changes
     const int t_first = min(w * per, n_tasks), t_end = min(t_first + per, n_tasks);
     const int total = (t_end - t_first) * G.steps;
@@ -262,7 +264,7 @@ namespace {
 
 template <bool DOWN>
 bool stream_geom(const ExpertLayout& L, int unit, int block_values, int block_bytes, int n_tok, int64_t cap_groups,
-                 int64_t cap_entries, StreamGeom& G) {
+                 int64_t cap_entries, StreamGeom& G, bool wide = false) {
     G.n_in = DOWN ? (int)L.n_ff : (int)L.n_embd;
     G.rows_total = DOWN ? (int)L.n_embd : (int)(2 * L.n_ff);
     G.rb = (int)(DOWN ? L.d_row : L.gu_row);
@@ -303,11 +305,21 @@ bool stream_geom(const ExpertLayout& L, int unit, int block_values, int block_by
     G.ne = DOWN ? 4 : n_tok <= 4 ? 4 : 8;   // the kernel's NE: entries a pass
     if (G.steps != 1 && n_tok > G.ne) return false;   // passes re-read their one step's slot
     G.wact = DOWN ? ((G.ne * row_act + 15) & ~15) : 0;
-    G.act_bytes = DOWN ? kStreamWaves * G.wact : ((n_tok * row_act + 15) & ~15);
-    const int ring = (kStreamLds - G.meta_bytes - G.act_bytes) / kStreamWaves;
-    G.slots = ring / G.slot;
-    while (G.slots > 1 && (G.slots - 1) * G.ni > 63) --G.slots;
+    auto fit = [&](int waves) {
+        G.waves = waves;
+        G.act_bytes = DOWN ? waves * G.wact : ((n_tok * row_act + 15) & ~15);
+        const int ring = (kStreamLds - G.meta_bytes - G.act_bytes) / waves;
+        G.slots = ring / G.slot;
+        while (G.slots > 1 && (G.slots - 1) * G.ni > 63) --G.slots;
+    };
+    fit(kStreamWaves);
     if (G.slots < 1) return false;
+    // one slot a ring: every wave waits for each step it fetches, so more waves a SIMD hide more; three a SIMD where
+    // the rings still hold a slot and the kernel's registers allow it (gate/up of the formats but Q4_K)
+    if (G.slots == 1 && wide) {
+        fit(kStreamWavesWide);
+        if (G.slots < 1) fit(kStreamWaves);
+    }
     G.ring = G.slots * G.slot;
     return true;
 }
@@ -315,16 +327,20 @@ bool stream_geom(const ExpertLayout& L, int unit, int block_values, int block_by
 template <int T, bool DOWN, int LPR>
 hipError_t launch_lpr(const GroupedArgs& a, const StreamGeom& G, hipStream_t s, const int8_t* hq, const float* hd,
                       const int* hs) {
+    constexpr bool kWide = !DOWN && T != kQ4_K;   // the instances that fit three waves a SIMD
     void (*kern)(GroupedArgs, StreamGeom, const int8_t*, const float*, const int*) =
-        G.ne <= 4 ? stream_kernel<T, DOWN, LPR, 4> : stream_kernel<T, DOWN, LPR, 8>;
-    const size_t lds = (size_t)G.meta_bytes + (size_t)G.act_bytes + (size_t)kStreamWaves * G.ring;
+        kWide && G.waves == kStreamWavesWide
+            ? (G.ne <= 4 ? stream_kernel<T, DOWN, LPR, 4, kWide ? kStreamWavesWide : kStreamWaves>
+                         : stream_kernel<T, DOWN, LPR, 8, kWide ? kStreamWavesWide : kStreamWaves>)
+            : (G.ne <= 4 ? stream_kernel<T, DOWN, LPR, 4, kStreamWaves> : stream_kernel<T, DOWN, LPR, 8, kStreamWaves>);
+    const size_t lds = (size_t)G.meta_bytes + (size_t)G.act_bytes + (size_t)G.waves * G.ring;
     hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
     int dev = 0, cus = 256;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
         cus = 256;
-    hipLaunchKernelGGL(kern, dim3((unsigned)cus), dim3(64 * kStreamWaves), lds, s, a, G, hq, hd, hs);
+    hipLaunchKernelGGL(kern, dim3((unsigned)cus), dim3(64 * G.waves), lds, s, a, G, hq, hd, hs);
     return hipGetLastError();
 }
 
@@ -334,7 +350,7 @@ hipError_t launch_stream_t(const ExpertLayout& L, const GroupedArgs& a, hipStrea
     constexpr int bb = T == kQ8_0 ? 34 : T == kQ4_K ? 144 : T == kQ6_K ? 210 : 136;
     const int unit = DOWN || T == kQ8_0 ? 32 : 256;
     StreamGeom G;
-    if (!stream_geom<DOWN>(L, unit, bv, bb, a.max_entries, a.cap_groups, a.cap_entries_hint, G))
+    if (!stream_geom<DOWN>(L, unit, bv, bb, a.max_entries, a.cap_groups, a.cap_entries_hint, G, !DOWN && T != kQ4_K))
         return hipErrorNotSupported;
     const size_t f = (size_t)a.cap_entries_hint * (size_t)L.n_ff;   // the h region's int8 values
     int8_t* hq = (int8_t*)a.hact;
