@@ -657,6 +657,9 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
             const unsigned long long* pp = a.px + (int64_t)t * k * H + col;
             const float* ww = s_w + t * k;
             const float res = a.residual[(int64_t)t * H + col];   // in flight while the parts are polled
+            // the shared expert's row and gate logit, also in flight while the parts are polled
+            const float shv = a.shared ? a.shared[(int64_t)t * H + col] : 0.0f;
+            const float shg = a.shared && a.shared_gate ? a.shared_gate[t] : 0.0f;
             float sum = 0.0f;
             bool good = true;
             for (int e0 = 0; e0 < k; e0 += 16) {   // 16 parts in flight at once
@@ -692,8 +695,8 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
             }
             if (!good) atomicOr(a.err, 2);
             if (a.shared) {   // the shared expert's row, once, after the routed ones (times its gate's sigmoid)
-                float sv = a.shared[(int64_t)t * H + col];
-                if (a.shared_gate) sv = sv * (1.0f / (1.0f + expf(-a.shared_gate[t])));
+                float sv = shv;
+                if (a.shared_gate) sv = sv * (1.0f / (1.0f + expf(-shg)));
                 sum = sum + sv;
             }
             a.out[(int64_t)t * H + col] = res + sum;

@@ -267,6 +267,18 @@ __global__ __launch_bounds__(kT1) void moe_decode_t1_kernel(FusedArgs a) {
             }
     };
 
+    // the combine's operands that depend on no work of this call - the residual, the shared expert's row and its gate
+    // logit - loaded now by the threads that combine (loaded at the end, their latency was the kernel's last step)
+    static_assert(RD <= kT1, "a thread a combined row");
+    const bool combiner = has_dn && tid < rd;
+    float c_res = 0.0f, c_sh = 0.0f, c_gate = 0.0f;
+    if (combiner) {
+        const int64_t col = (int64_t)j_dn * rd + tid;
+        c_res = a.residual[col];
+        if (a.shared) c_sh = a.shared[col];
+        if (a.shared && a.shared_gate) c_gate = a.shared_gate[0];
+    }
+
     // ---- 1. routing (wave 0 exact; waves 1..3 speculate and fetch; waves 4..7 quantize x)
     if (wave == 0) {
         float lv[PER];
@@ -450,8 +462,10 @@ __global__ __launch_bounds__(kT1) void moe_decode_t1_kernel(FusedArgs a) {
         constexpr int kPollWaves = 3, kDecThreads = kT1 - 64 * (kPollWaves + 1);
         const bool poller = wave < kPollWaves;
         const int dtid = tid - 64 * kPollWaves;
-        // the k experts' q8_1 h: one block (9 words) a thread of the poller waves, polled until every word carries
-        // the tag, one read of the block in flight at a time
+        // the k experts' q8_1 h: one block (9 words) a thread of the poller waves, read whole first (h is mostly
+        // stored before the down rows land, so one round trip); then the block's scale word alone (9x fewer loads in
+        // flight across the grid) until it carries the tag, and the block again.  (A word a lane, so that a wave's
+        // load reads a few lines, measured slower.)
         if (poller)
             for (int q = tid; q < nblk; q += 64 * kPollWaves) {
                 const int e = q / nu, j = q - e * nu;
@@ -468,11 +482,10 @@ __global__ __launch_bounds__(kT1) void moe_decode_t1_kernel(FusedArgs a) {
                     for (int i = 0; i < kHWords; ++i) ok = ok && (unsigned int)(v[i] >> 32) == tag;
                     return ok;
                 };
-                // poll the block's scale word alone (9x fewer loads in flight across the grid), then read the block;
-                // a word not yet carrying the tag is read again
-                bool good = false;
+                poll(w);
+                bool good = tagged(w);
                 const long long t0 = wall_clock64();
-                for (int it = 1;; ++it) {
+                for (int it = 1; !good; ++it) {
                     const unsigned long long wd = t1_ld_tag(src + 8);
                     if ((unsigned int)(wd >> 32) == tag) {
                         poll(w);
@@ -570,7 +583,8 @@ __global__ __launch_bounds__(kT1) void moe_decode_t1_kernel(FusedArgs a) {
             if (c == 0) s_po[t] = sm;
         }
         t1_lds_barrier();
-        for (int r = tid; r < rd; r += kT1) {
+        if (combiner) {
+            const int r = tid;
             const int64_t col = (int64_t)j_dn * rd + r;
             float sum = 0.0f;
             for (int e = 0; e < k; ++e) {
@@ -578,11 +592,11 @@ __global__ __launch_bounds__(kT1) void moe_decode_t1_kernel(FusedArgs a) {
                 sum = e == 0 ? prod : sum + prod;
             }
             if (a.shared) {   // the shared expert's row, once, after the routed ones (times its gate's sigmoid)
-                float sv = a.shared[col];
-                if (a.shared_gate) sv = sv * (1.0f / (1.0f + expf(-a.shared_gate[0])));
+                float sv = c_sh;
+                if (a.shared_gate) sv = sv * (1.0f / (1.0f + expf(-c_gate)));
                 sum = sum + sv;
             }
-            a.out[col] = a.residual[col] + sum;
+            a.out[col] = c_res + sum;
         }
     } else if (spec_wave) {
         t1_vm_drain();
