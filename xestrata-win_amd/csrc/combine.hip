@@ -7,6 +7,8 @@
 #include "xs_device.h"
 #include "xs_kernels.h"
 
+#include <type_traits>
+
 namespace xs {
 
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ parts, const float* __restrict__ weights,
@@ -43,36 +45,49 @@ __global__ __launch_bounds__(256) void add_inplace_kernel(float* __restrict__ x,
 
 // The same sum over f16 parts (the prompt layer's, whose products are f16 MFMA results anyway), plus the residual:
 // 4 columns a thread (8-byte part reads, 16-byte residual and output accesses).
+// V columns a thread (8: 16-byte loads of the f16 parts, when n_embd allows; else 4); every column's sum in the same
+// order either way
+template <int V>
 __global__ __launch_bounds__(256) void combine_h_kernel(const uint16_t* __restrict__ parts,
                                                         const float* __restrict__ weights,
                                                         const float* __restrict__ shared,
                                                         const float* __restrict__ shared_gate,
                                                         const float* __restrict__ residual, float* __restrict__ out,
                                                         int64_t n_embd, int k) {
+    using PV = typename std::conditional<V == 8, uint4, uint2>::type;
     const int64_t t = blockIdx.y;
-    const int64_t c = 4 * ((int64_t)blockIdx.x * blockDim.x + threadIdx.x);
+    const int64_t c = V * ((int64_t)blockIdx.x * blockDim.x + threadIdx.x);
     if (c >= n_embd) return;
     const uint16_t* p = parts + t * k * n_embd + c;
     const float* w = weights + t * k;
-    float4 sum = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float sum[V];
     for (int e = 0; e < k; ++e) {
-        const uint2 v = *(const uint2*)(p + (int64_t)e * n_embd);
+        const PV v = *(const PV*)(p + (int64_t)e * n_embd);
+        const uint32_t* vw = (const uint32_t*)&v;
         const float we = w[e];
-        const float4 prod = make_float4(h2f((uint16_t)(v.x & 0xFFFFu)) * we, h2f((uint16_t)(v.x >> 16)) * we,
-                                        h2f((uint16_t)(v.y & 0xFFFFu)) * we, h2f((uint16_t)(v.y >> 16)) * we);
-        if (e == 0) sum = prod;
-        else sum = make_float4(sum.x + prod.x, sum.y + prod.y, sum.z + prod.z, sum.w + prod.w);
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+            const float prod = h2f((uint16_t)(vw[i / 2] >> (16 * (i & 1)))) * we;
+            sum[i] = e == 0 ? prod : sum[i] + prod;
+        }
     }
     if (shared) {   // the shared expert's row, once, after the routed ones (times its gate's sigmoid)
-        float4 sv = *(const float4*)(shared + t * n_embd + c);
-        if (shared_gate) {
-            const float gs = 1.0f / (1.0f + expf(-shared_gate[t]));
-            sv = make_float4(sv.x * gs, sv.y * gs, sv.z * gs, sv.w * gs);
+        const float gs = shared_gate ? 1.0f / (1.0f + expf(-shared_gate[t])) : 1.0f;
+#pragma unroll
+        for (int i = 0; i < V; i += 4) {
+            const float4 sv = *(const float4*)(shared + t * n_embd + c + i);
+            sum[i] = sum[i] + (shared_gate ? sv.x * gs : sv.x);
+            sum[i + 1] = sum[i + 1] + (shared_gate ? sv.y * gs : sv.y);
+            sum[i + 2] = sum[i + 2] + (shared_gate ? sv.z * gs : sv.z);
+            sum[i + 3] = sum[i + 3] + (shared_gate ? sv.w * gs : sv.w);
         }
-        sum = make_float4(sum.x + sv.x, sum.y + sv.y, sum.z + sv.z, sum.w + sv.w);
     }
-    const float4 r = *(const float4*)(residual + t * n_embd + c);
-    *(float4*)(out + t * n_embd + c) = make_float4(r.x + sum.x, r.y + sum.y, r.z + sum.z, r.w + sum.w);
+#pragma unroll
+    for (int i = 0; i < V; i += 4) {
+        const float4 r = *(const float4*)(residual + t * n_embd + c + i);
+        *(float4*)(out + t * n_embd + c + i) =
+            make_float4(r.x + sum[i], r.y + sum[i + 1], r.z + sum[i + 2], r.w + sum[i + 3]);
+    }
 }
 
 // native_moe_combine_multi with moe_hit_add folded in (the reference's native_moe_combine_multi_hits,
@@ -127,9 +142,15 @@ hipError_t launch_combine_hits(const float* parts, const float* hits, const int3
 hipError_t launch_combine_h(const uint16_t* parts, const float* weights, const float* shared,
                             const float* shared_gate, const float* residual, float* out, int64_t n_embd, int k,
                             int n_tok, hipStream_t s) {
-    const dim3 grid((unsigned)((n_embd / 4 + 255) / 256), (unsigned)n_tok);
-    hipLaunchKernelGGL(combine_h_kernel, grid, dim3(256), 0, s, parts, weights, shared, shared_gate, residual, out,
-                       n_embd, k);
+    if (n_embd % 8 == 0) {
+        const dim3 grid((unsigned)((n_embd / 8 + 255) / 256), (unsigned)n_tok);
+        hipLaunchKernelGGL(combine_h_kernel<8>, grid, dim3(256), 0, s, parts, weights, shared, shared_gate, residual,
+                           out, n_embd, k);
+    } else {
+        const dim3 grid((unsigned)((n_embd / 4 + 255) / 256), (unsigned)n_tok);
+        hipLaunchKernelGGL(combine_h_kernel<4>, grid, dim3(256), 0, s, parts, weights, shared, shared_gate, residual,
+                           out, n_embd, k);
+    }
     return hipGetLastError();
 }
 
