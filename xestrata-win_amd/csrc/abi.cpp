@@ -1018,9 +1018,56 @@ int layer_decode_shared(const xs_expert_layout_t* L, const uint8_t* arena, size_
     float* gate = (float*)(base + lw + up256((size_t)n_tok * (size_t)L->n_embd * 4));
     uint8_t* sws = base + lw + up256((size_t)n_tok * (size_t)L->n_embd * 4) + up256((size_t)n_tok * 4);
     const size_t sbytes = shared_ws(SL, n_tok, nullptr).bytes;
-    if (int r = xs_shared_expert_decode(SL, shared_blob, x, n_tok, w_gate, shared, w_gate ? gate : nullptr, sws, sbytes,
-                                        stream))
+    // up to 64 tokens: the shared expert as a one-expert layer in one persistent launch, in the layer's workspace
+    // (its head and tagged words, used again by the routed layer after it) - routing given (expert 0, weight 1.0) and
+    // no residual, so each row is the expert's own: fl(y x 1) = y, the canonical rows bit for bit.  That replaces
+    // four launches (q8_1, plan, gate/up, down).  Otherwise, or where the persistent plan does not take the shared
+    // layout or its h would not fit the layer's hand-over region, the shared expert's own chain.
+    xs::FusedPlan SP;
+    const xs::ExpertLayout SXL = to_layout(SL);
+    if (n_tok <= xs::kOneExpertMaxTok && SL->n_ff <= L->n_ff && fused_possible(L, n_expert, k) &&
+        xs::fused_decode_plan(SXL, 1, 1, n_tok, &SP) && aligned(shared_blob, 16)) {
+        const DecodeWs w = decode_ws(L, n_expert, k, n_tok, base);
+        const int32_t* one_ids = nullptr;
+        const float* one_w = nullptr;
+        if (hipError_t e = xs::one_expert_routing(&one_ids, &one_w)) return hip_status(e, who);
+        xs::FusedArgs a;
+        a.L = SXL;
+        a.arena = shared_blob;
+        a.blob = (long long)SL->bytes;
+        a.n_expert = 1;
+        a.k = 1;
+        a.n_tok = n_tok;
+        a.logits = nullptr;   // (routing given)
+        a.x = x;
+        a.residual = nullptr;
+        a.out = shared;
+        a.ids = w.ids;
+        a.weights = w.w;
+        a.hx = w.hx;
+        a.px = w.px;
+        a.sync = w.sync;
+        a.err = w.status;
+        a.rh = SP.rh;
+        a.rd = SP.rd;
+        a.nu = SP.nu;
+        a.nj = SP.nj;
+        a.slab_gu_bytes = SP.slab_gu;
+        a.slab_dn_bytes = SP.slab_dn;
+        a.ttab = SP.ttab;
+        a.direct = SP.direct;
+        a.spin_ticks = spin_ticks();
+        a.shared = nullptr;
+        a.shared_gate = nullptr;
+        a.pre_ids = one_ids;
+        a.pre_w = one_w;
+        if (int r = finish(stream, xs::launch_decode_fused(a, SP, S(stream)), who)) return r;
+        if (w_gate)
+            if (int r = xs_router_logits_f32(x, w_gate, gate, n_tok, SL->n_embd, 1, stream)) return r;
+    } else if (int r = xs_shared_expert_decode(SL, shared_blob, x, n_tok, w_gate, shared, w_gate ? gate : nullptr, sws,
+                                               sbytes, stream)) {
         return r;
+    }
     return layer_decode(L, arena, blob_bytes, n_expert, k, x, logits, residual, out, n_tok, workspace, lw, shared,
                         w_gate ? gate : nullptr, stream, nullptr, false, route);
 }

@@ -656,7 +656,8 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
             const int64_t col = (int64_t)j * rd + r;
             const unsigned long long* pp = a.px + (int64_t)t * k * H + col;
             const float* ww = s_w + t * k;
-            const float res = a.residual[(int64_t)t * H + col];   // in flight while the parts are polled
+            // (in flight while the parts are polled; no residual: the combined row alone)
+            const float res = a.residual ? a.residual[(int64_t)t * H + col] : 0.0f;
             // the shared expert's row and gate logit, also in flight while the parts are polled
             const float shv = a.shared ? a.shared[(int64_t)t * H + col] : 0.0f;
             const float shg = a.shared && a.shared_gate ? a.shared_gate[t] : 0.0f;
@@ -699,7 +700,7 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
                 if (a.shared_gate) sv = sv * (1.0f / (1.0f + expf(-shg)));
                 sum = sum + sv;
             }
-            a.out[(int64_t)t * H + col] = res + sum;
+            a.out[(int64_t)t * H + col] = a.residual ? res + sum : sum;
         }
     }
     done_call(a, tag);
@@ -831,6 +832,37 @@ static hipError_t resident_grid(const void* kern, int lds, int cap, int* grid_ma
     if (occ < 1) return hipErrorInvalidConfiguration;
     *grid_max = cus * (occ > cap ? cap : occ);
     g_shapes.push_back(LaunchShape{dev, kern, lds, cap, *grid_max});
+    return hipSuccess;
+}
+
+// the routing of a one-expert layer (a shared expert run through the persistent layer): every token's only entry is
+// expert 0 with weight 1.0
+#define XS_ONES8 1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.0f
+static __device__ int32_t g_one_ids[kOneExpertMaxTok];
+static __device__ float g_one_w[kOneExpertMaxTok] = {XS_ONES8, XS_ONES8, XS_ONES8, XS_ONES8,
+                                                     XS_ONES8, XS_ONES8, XS_ONES8, XS_ONES8};
+#undef XS_ONES8
+static_assert(kOneExpertMaxTok == 64, "the weights' initializer holds 64 ones");
+
+hipError_t one_expert_routing(const int32_t** ids, const float** w) {
+    static std::mutex mu;
+    static std::vector<std::pair<int, std::pair<const int32_t*, const float*>>> seen;   // per device
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    std::lock_guard<std::mutex> lock(mu);
+    for (const auto& d : seen)
+        if (d.first == dev) {
+            *ids = d.second.first;
+            *w = d.second.second;
+            return hipSuccess;
+        }
+    void *pi = nullptr, *pw = nullptr;
+    if ((e = hipGetSymbolAddress(&pi, HIP_SYMBOL(g_one_ids))) != hipSuccess) return e;
+    if ((e = hipGetSymbolAddress(&pw, HIP_SYMBOL(g_one_w))) != hipSuccess) return e;
+    seen.push_back({dev, {(const int32_t*)pi, (const float*)pw}});
+    *ids = (const int32_t*)pi;
+    *w = (const float*)pw;
     return hipSuccess;
 }
 

@@ -91,7 +91,7 @@ struct FusedArgs {
     int n_expert, k, n_tok;
     const float* logits;    // [n_tok, n_expert]
     const float* x;         // [n_tok, n_embd]
-    const float* residual;  // [n_tok, n_embd]
+    const float* residual;  // [n_tok, n_embd] (NULL: none, the combined rows alone; the persistent layer only)
     float* out;             // [n_tok, n_embd], may equal residual
     int32_t* ids;           // [n_tok * k]
     float* weights;         // [n_tok * k]
@@ -112,6 +112,10 @@ struct FusedArgs {
 };
 bool fused_decode_plan(const ExpertLayout& L, int n_expert, int k, int n_tok, FusedPlan* P);
 hipError_t launch_decode_fused(const FusedArgs& a, const FusedPlan& P, hipStream_t s);
+// a one-expert layer's routing for the persistent layer's pre_ids / pre_w (expert 0, weight 1.0 for each of up to
+// kOneExpertMaxTok tokens): device addresses of this device's arrays
+constexpr int kOneExpertMaxTok = 64;
+hipError_t one_expert_routing(const int32_t** ids, const float** w);
 // decode_t1.hip: the one-token layer (a.n_tok == 1) with the down units over every expert and the combine inside them;
 // *used = false (nothing launched) when the layout is not one it takes, and the caller launches launch_decode_fused.
 // Needs the same workspace (a.hx holds the q8_1 h words).
