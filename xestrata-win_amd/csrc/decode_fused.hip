@@ -752,14 +752,15 @@ bool fused_decode_plan(const ExpertLayout& L, int n_expert, int k, int n_tok, Fu
     if (rd > 64) rd = 64;
     while (rd > 8 && H % rd) rd -= 8;
     if (H % rd) return false;
-    // one token with more gate/up units than two work-groups a CU (large experts): the direct form - a unit's rows
+    // one token with at least as many gate/up units as two work-groups a CU (large experts; a shared expert of
+    // hidden 7168 as a one-expert layer is one exactly: 111.3 -> 108.5 us at config 5): the direct form - a unit's rows
     // fill the work-group's lanes (each row's canonical lanes, 256 in all), every lane reads its blocks from HBM
     // itself, and without slabs the LDS holds up to four work-groups a CU, whose loads hide each other's latency
     // (only with at least 4 gate/up units a lane: fewer, and each lane's few dependent loads leave it idle - measured
     // slower at hidden 4096, 2 a lane)
     P->direct = 0;
     const int ug = H / (L.gu_type == kQ8_0 ? 32 : 256);
-    if (n_tok == 1 && (int64_t)k * (F / rh) > 2 * device_cus() && ug / canon_lanes(ug) >= 4) {
+    if (n_tok == 1 && (int64_t)k * (F / rh) >= 2 * device_cus() && ug / canon_lanes(ug) >= 4) {
         const int lg = canon_lanes(ug), ld = canon_lanes(F / 32);
         const int rh2 = 128 / lg, rd2 = 256 / ld;
         if (F % rh2 == 0 && H % rd2 == 0 && rd2 <= 64) {
