@@ -330,13 +330,8 @@ __device__ __forceinline__ void dma_rows(const uint8_t* const* src, size_t off, 
                                          0);
 }
 
-// Q4_K with RT = 2 (64-row tiles, for groups of ~64 rows or fewer) holds half the accumulators and is built for four
-// work-groups a CU; every other instance for two
-template <int T, int RT>
-constexpr int gemm_min_blocks() { return T == kQ4_K && RT == 2 ? 3 : 2; }
-
 template <bool DOWN, int T, int RT>
-__global__ __launch_bounds__(256, (gemm_min_blocks<T, RT>())) void grouped_mfma_kernel(ExpertLayout L, PrefillArgs a,
+__global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, PrefillArgs a,
                                                               const int32_t* __restrict__ mtile, int mt_bound,
                                                               int n_tiles) {
     constexpr int kBM = 32 * RT;
@@ -674,15 +669,12 @@ static hipError_t launch_gemm(const ExpertLayout& L, const PrefillArgs& a, hipSt
     const int t = DOWN ? L.d_type : L.gu_type;
     const int n_tiles = DOWN ? (int)(L.n_embd / (128 * lane_rows(DOWN, t))) : (int)(L.n_ff / (kBN / 2));
     const bool q8_fast = (DOWN ? L.n_ff : L.n_embd) % 128 == 0;   // Q8_0's own path takes its K steps in pairs
-    // Q4_K groups of 64 rows or fewer on average (uniform routing over many experts: config 5's ~32 rows an expert)
-    // take 64-row tiles: a 128-row tile would run mostly empty at half the waves a SIMD
-    const bool small = t == kQ4_K && a.rows <= 64 * a.cap_groups;
-    const int bm = small ? 64 : 32 * row_tiles(DOWN, q8_fast ? t : (t == kQ8_0 ? 0 : t));
+    const int bm = 32 * row_tiles(DOWN, q8_fast ? t : (t == kQ8_0 ? 0 : t));
     const int mt_bound = (int)((a.rows + bm - 1) / bm + a.cap_groups);
     const unsigned grid = (unsigned)(n_tiles % 8 == 0 ? mt_bound * n_tiles : 8 * ((mt_bound + 7) / 8) * n_tiles);
     const size_t lds = (size_t)entry_offset(bm) + (DOWN ? (size_t)bm * 4 : 0);
     void (*k)(ExpertLayout, PrefillArgs, const int32_t*, int, int) =
-        t == kQ4_K   ? (small ? grouped_mfma_kernel<DOWN, kQ4_K, 2> : grouped_mfma_kernel<DOWN, kQ4_K, row_tiles(DOWN, kQ4_K)>)
+        t == kQ4_K   ? grouped_mfma_kernel<DOWN, kQ4_K, row_tiles(DOWN, kQ4_K)>
         : t == kQ6_K ? grouped_mfma_kernel<DOWN, kQ6_K, row_tiles(DOWN, kQ6_K)>
         : t == kQ8_0 && q8_fast ? grouped_mfma_kernel<DOWN, kQ8_0, row_tiles(DOWN, kQ8_0)>
                      : grouped_mfma_kernel<DOWN, 0, row_tiles(DOWN, 0)>;
