@@ -867,6 +867,15 @@ int route_of(const xs_router_cfg_t* cfg, int n_expert, int k, Route* r, const ch
 }
 
 // status: where the persistent layer's error bits go (NULL: the workspace's status word); fixed_tagged: decode_ws's
+// the grouped sigmoid router's wave form (xs_route.h route_grouped_sigmoid_wave): the groups on whole lanes, lanes a
+// group a power of two (launch_router_grouped_sigmoid's condition)
+bool sigmoid_wave_form(int n_expert, int n_group) {
+    const int PER = n_expert <= 64 ? 1 : n_expert <= 128 ? 2 : n_expert <= 256 ? 4 : n_expert <= 512 ? 8 : 16;
+    const int per = n_group > 0 ? n_expert / n_group : 0;
+    const int lpg = per % PER == 0 ? per / PER : 0;
+    return n_expert <= 1024 && n_group > 0 && per * n_group == n_expert && lpg > 0 && (lpg & (lpg - 1)) == 0;
+}
+
 int layer_decode(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_bytes, int n_expert, int k,
                  const float* x, const float* logits, const float* residual, float* out, int n_tok, void* workspace,
                  size_t workspace_bytes, const float* shared, const float* shared_gate, void* stream,
@@ -889,16 +898,22 @@ int layer_decode(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_
         return fail(XS_EINVAL, "moe_layer_decode: a span is missing or misaligned");
     const xs::ExpertLayout XL = to_layout(L);
     const bool pre = route.kind == XS_ROUTER_GROUPED_SIGMOID;
-    if (pre)   // the other router first, into the workspace's ids and weights
-        if (int r = xs_router_grouped_sigmoid(logits, route.bias, n_tok, n_expert, route.n_group, route.topk_group, k,
-                                              route.scale, w.ids, w.w, stream))
-            return r;
     xs::FusedPlan P;
     // 2..16 tokens of a wide layer (hidden >= 4096): the chained path on the weight-stream kernels, measured faster
     // there than the persistent layer (config 4 at 8 tokens: 565 -> ~250 us); narrower layers keep the persistent one
     const bool streamed = n_tok >= 2 && L->n_embd >= 4096 &&
                           xs::stream_usable(XL, n_tok, capx < n_expert ? capx : n_expert, capx);
-    if (!streamed && xs::fused_decode_plan(XL, n_expert, k, n_tok, &P)) {
+    const bool fused = !streamed && xs::fused_decode_plan(XL, n_expert, k, n_tok, &P);
+    // the grouped sigmoid router inside the persistent layer's routing stage where its groups fall on whole lanes
+    // (the wave form) and the layout's instances carry it (the Q4_K pair): one launch less (config 5 T=1: 109.5 ->
+    // 105.6 us); otherwise its own launch first, into the workspace's ids and weights
+    const bool sig_in = pre && fused && sigmoid_wave_form(n_expert, route.n_group) &&
+                        xs::fused_sigmoid_layout(L->gu_type, L->d_type);
+    if (pre && !sig_in)
+        if (int r = xs_router_grouped_sigmoid(logits, route.bias, n_tok, n_expert, route.n_group, route.topk_group, k,
+                                              route.scale, w.ids, w.w, stream))
+            return r;
+    if (fused) {
         // the whole layer in one persistent launch
         xs::FusedArgs a;
         a.L = XL;
@@ -928,8 +943,14 @@ int layer_decode(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_
         a.spin_ticks = spin_ticks();
         a.shared = shared;
         a.shared_gate = shared_gate;
-        a.pre_ids = pre ? w.ids : nullptr;
-        a.pre_w = pre ? w.w : nullptr;
+        a.pre_ids = pre && !sig_in ? w.ids : nullptr;
+        a.pre_w = pre && !sig_in ? w.w : nullptr;
+        if (sig_in) {
+            a.sig_bias = route.bias;
+            a.sig_group = route.n_group;
+            a.sig_topk_group = route.topk_group;
+            a.sig_scale = route.scale;
+        }
         if (n_tok == 1) {   // the one-token kernel where the layout fits it
             bool used = false;
             const hipError_t e1 = xs::launch_decode_t1(a, S(stream), &used);

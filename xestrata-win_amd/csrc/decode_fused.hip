@@ -217,7 +217,13 @@ __device__ __forceinline__ int epoch_of(unsigned long long c) {   // lanes 0..15
     return (int)((((unsigned long long)hi << 32) | lo) >> 20);
 }
 
-template <int PER>
+template <int TG, int TD>
+constexpr bool kFusedSigmoid = TG == kQ4_K && TD == kQ4_K;
+bool fused_sigmoid_layout(int gu_type, int d_type) { return gu_type == kQ4_K && d_type == kQ4_K; }
+
+// SIG: the instance carries the group-limited sigmoid router's stage (only the Q4_K pair's instances: code an instance
+// never runs still takes instruction-cache room - config 4's one-token layer 40.5 -> 41.3 us with it)
+template <int PER, bool SIG>
 __device__ __forceinline__ void route_tokens_wave(const FusedArgs& a, int T, int* s_ids, float* s_w,
                                                   unsigned long long& ctr) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, E = a.n_expert, k = a.k;
@@ -228,6 +234,20 @@ __device__ __forceinline__ void route_tokens_wave(const FusedArgs& a, int T, int
                 s_ids[t * k + lane] = a.pre_ids[t * k + lane];
                 s_w[t * k + lane] = a.pre_w[t * k + lane];
             }
+        return;
+    }
+    if (SIG && a.sig_group > 0) {   // the group-limited sigmoid router, a wave a token
+        ctr = load_counter(a);
+        for (int t = wave; t < T; t += kFT / 64) {
+            int id;
+            float w;
+            route_grouped_sigmoid_wave<PER>(a.logits + (int64_t)t * E, a.sig_bias, E, a.sig_group, a.sig_topk_group, k,
+                                            a.sig_scale, id, w);
+            if (lane < k) {
+                s_ids[t * k + lane] = id;
+                s_w[t * k + lane] = w;
+            }
+        }
         return;
     }
     float lv[PER];
@@ -293,7 +313,7 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
         for (int j8 = tid - 64; j8 < H / 8; j8 += kFT - 64)
             q8_1_256_to_act(a.x, j8, q, (float*)(q + H), (int*)(q + H + H / 8));
     }
-    route_tokens_wave<PER>(a, T, s_ids, s_w, ctr);   // PER = the experts a lane (64 PER >= E, chosen by the host)
+    route_tokens_wave<PER, kFusedSigmoid<TG, TD>>(a, T, s_ids, s_w, ctr);   // PER = the experts a lane (64 PER >= E, chosen by the host)
     if (wave == 0) {
         const int epoch = epoch_of(ctr);
         if (lane == 0) s_misc[3] = epoch;

@@ -91,72 +91,13 @@ __global__ __launch_bounds__(256) void router_grouped_sigmoid_wave_kernel(
     int topk_group, int k, float routed_scale, int32_t* __restrict__ ids, float* __restrict__ weights) {
     const int lane = threadIdx.x & 63, t = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
     if (t >= n_tokens) return;
-    const float* l = logits + (int64_t)t * n_expert;
-    const int per = n_expert / n_group, lpg = per / PER, my_g = lane / lpg;
-    float s[PER], c[PER];
-#pragma unroll
-    for (int j = 0; j < PER; ++j) {
-        const int e = lane * PER + j;
-        const bool in = e < n_expert;
-        s[j] = in ? canon_rcp(1.0f + canon_exp(-l[e])) : 0.0f;
-        c[j] = in ? s[j] + (bias ? bias[e] : 0.0f) : -INFINITY;
-    }
-    float b1 = -INFINITY, b2 = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < PER; ++j) {
-        const float v = c[j];
-        if (v > b1) { b2 = b1; b1 = v; }
-        else if (v > b2) b2 = v;
-    }
-    for (int o = 1; o < lpg; o <<= 1) {
-        const float o1 = __shfl_xor(b1, o, 64), o2 = __shfl_xor(b2, o, 64);
-        const float n1 = fmaxf(b1, o1), n2 = fmaxf(fminf(b1, o1), fmaxf(b2, o2));
-        b1 = n1;
-        b2 = n2;
-    }
-    const float gs = b1 + b2;
-    int rank = 0;
-    for (int g = 0; g < n_group; ++g) {
-        const float og = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gs), g * lpg));
-        rank += og > gs || (og == gs && g < my_g) ? 1 : 0;
-    }
-    const bool chosen = my_g < n_group && rank < topk_group;
-    if (!chosen) {
-#pragma unroll
-        for (int j = 0; j < PER; ++j) c[j] = -INFINITY;
-    }
-    // a pass: each lane's best candidate as an unsigned key of c (the float order; NaN and "none" 0, so never picked),
-    // the wave's largest key by DPP, its lowest lane by ballot (the lower lane holds the lower experts, and a lane's
-    // own ties keep its lower one): better()'s order
-    float my_w = 0.0f;
-    int my_id = 0;
-    for (int i = 0; i < k; ++i) {
-        uint32_t lk = 0u;
-        int lj = 0;
-        float ls = 0.0f;
-#pragma unroll
-        for (int j = 0; j < PER; ++j) {
-            const float v = c[j] + 0.0f;   // -0 as +0: equal floats, equal keys
-            const uint32_t b = __float_as_uint(v);
-            const uint32_t key = !chosen || lane * PER + j >= n_expert || v != v ? 0u
-                                 : (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-            if (key > lk) { lk = key; lj = j; ls = s[j]; }
-        }
-        const uint32_t m = wave_max_u32(lk);
-        if (m == 0u) break;
-        const int owner = (int)__builtin_ctzll(__ballot(lk == m));
-        const int bi = owner * PER + __builtin_amdgcn_readlane(lj, owner);
-        const float sv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ls), owner));
-#pragma unroll
-        for (int j = 0; j < PER; ++j)
-            if (lane == owner && j == lj) c[j] = -INFINITY;   // taken
-        if (lane == i) { my_w = sv; my_id = bi; }
-    }
-    float sum = 0.0f;
-    for (int i = 0; i < k; ++i) sum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_w), i));
+    int my_id;
+    float my_w;
+    route_grouped_sigmoid_wave<PER>(logits + (int64_t)t * n_expert, bias, n_expert, n_group, topk_group, k,
+                                    routed_scale, my_id, my_w);
     if (lane < k) {
         ids[(int64_t)t * k + lane] = my_id;
-        weights[(int64_t)t * k + lane] = my_w / sum * routed_scale;
+        weights[(int64_t)t * k + lane] = my_w;
     }
 }
 

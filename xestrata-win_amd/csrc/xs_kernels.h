@@ -109,9 +109,17 @@ struct FusedArgs {
     // order, read instead of routing the logits (NULL: the softmax top-k of the logits)
     const int32_t* pre_ids = nullptr;
     const float* pre_w = nullptr;
+    // the group-limited sigmoid router in the routing stage itself (sig_group > 0: n_group; the groups on whole lanes,
+    // route_grouped_sigmoid_wave in xs_route.h), instead of softmax top-k, when pre_ids is NULL
+    const float* sig_bias = nullptr;
+    int sig_group = 0, sig_topk_group = 0;
+    float sig_scale = 1.0f;
 };
 bool fused_decode_plan(const ExpertLayout& L, int n_expert, int k, int n_tok, FusedPlan* P);
 hipError_t launch_decode_fused(const FusedArgs& a, const FusedPlan& P, hipStream_t s);
+// whether the persistent layer's instances for this layout can run the grouped sigmoid router in their routing stage
+// (FusedArgs sig_group): the Q4_K pair's (DeepSeek-V3's layout here); other layouts take the router's own launch
+bool fused_sigmoid_layout(int gu_type, int d_type);
 // a one-expert layer's routing for the persistent layer's pre_ids / pre_w (expert 0, weight 1.0 for each of up to
 // kOneExpertMaxTok tokens): device addresses of this device's arrays
 constexpr int kOneExpertMaxTok = 64;
