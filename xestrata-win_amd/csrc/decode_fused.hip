@@ -765,9 +765,10 @@ bool fused_decode_plan(const ExpertLayout& L, int n_expert, int k, int n_tok, Fu
             }
     }
     // down-slab rows: about 20 KB of down rows; 40 KB for one token (config 4's IQ4_XS rows: 32 rows, two down units
-    // a work-group of the grid: 46.6 -> 40.3 us a layer; 64 rows, one a work-group: 55.3 us; at 4 tokens, 40 KB slabs
-    // left Zipf-routed windows with too few down units: config 3's verify 59.7 -> 63.0 us)
-    int rd = (int)(((n_tok == 1 ? 40960 : 20480) / L.d_row) & ~7ll);
+    // a work-group of the grid: 46.6 -> 40.3 us a layer; 64 rows, one a work-group: 55.3 us) and from 8 tokens on
+    // (config 2 at 16 tokens: 198.2 -> 195.3 us); at 4 tokens, 40 KB slabs left Zipf-routed windows with too few down
+    // units: config 3's verify 59.7 -> 63.0 us
+    int rd = (int)(((n_tok == 1 || n_tok >= 8 ? 40960 : 20480) / L.d_row) & ~7ll);
     if (rd < 8) rd = 8;
     if (rd > 64) rd = 64;
     while (rd > 8 && H % rd) rd -= 8;
