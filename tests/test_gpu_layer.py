@@ -270,6 +270,41 @@ def c2_shared(xm):
     return sh_arena, SL, w_gate
 
 
+def test_prefill_shared_graph_replays(xm, c2_arena, c2_shared):
+    """The prompt layer with a (gated) shared expert captured in a HIP graph: the shared expert's work runs on a side
+    stream forked from the caller's and joined before the combine, so the graph holds two branches.  Every replay
+    (with eager work and waits between them) gives the eager call's bits."""
+    arena, L = c2_arena
+    sh_arena, SL, w_gate = c2_shared
+    T = 64
+    g = torch.Generator(device=DEV).manual_seed(78)
+    logits = torch.randn(T, 128, device=DEV, generator=g)
+    x = torch.randn(T, L.n_embd, device=DEV, generator=g).to(torch.bfloat16).float()
+    res = torch.randn(T, L.n_embd, device=DEV, generator=g)
+    layer = xm.MoeLayer(L, arena, 128, 8, T, prefill=True, shared=(SL, sh_arena, w_gate))
+    eager = torch.empty_like(res)
+    print("[case] prefill + shared expert, graph replays", flush=True)
+    layer(x, logits, res, eager)
+    torch.cuda.synchronize()
+    out = torch.zeros_like(res)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        layer(x, logits, res, out, stream=s)   # warm-up on the capture stream
+        s.synchronize()
+        with torch.cuda.graph(graph, stream=s):
+            layer(x, logits, res, out, stream=s)
+    torch.cuda.synchronize()
+    for r in range(4):
+        out.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int32), eager.view(torch.int32)), r
+    assert not torch.equal(eager, res)   # the layer added something
+
+
 def test_shared_expert_decode(xm, xo, c2_shared):
     """xs_shared_expert_decode: every token through the one expert, rows bit for bit the oracle's (the same canonical
     rows as the routed experts); the gate logit within 1e-5 of a float64 dot (the router-logit GEMV's bound)."""

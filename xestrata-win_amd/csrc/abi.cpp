@@ -9,6 +9,7 @@
 #include <cstdio>
 #include <cstring>
 #include <mutex>
+#include <vector>
 #include <string>
 
 namespace {
@@ -1153,6 +1154,38 @@ SharedPrefillWs shared_prefill_ws(const xs_expert_layout_t* SL, int n_tok, uint8
     return d;
 }
 
+// A side stream forked from the caller's: per host thread and device (so that calls from several threads, or a
+// graph captured on one of them, never share one), made on first use at the default priority and kept until the
+// process ends, with the two events of the fork and the join.  side_stream_fork records the fork on the caller's
+// stream and makes the side stream wait for it; work is then issued on side->stream, side->join recorded after it,
+// and the caller's stream waits for side->join (under graph capture these become the graph's branch and join).
+struct SideStream {
+    int dev;
+    hipStream_t stream;
+    hipEvent_t fork, join;
+};
+hipError_t side_stream_fork(hipStream_t caller, SideStream** out) {
+    thread_local std::vector<SideStream> sides;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    SideStream* sd = nullptr;
+    for (SideStream& x : sides)
+        if (x.dev == dev) sd = &x;
+    if (!sd) {
+        SideStream x{dev, nullptr, nullptr, nullptr};
+        if ((e = hipStreamCreateWithFlags(&x.stream, hipStreamNonBlocking)) != hipSuccess) return e;
+        if ((e = hipEventCreateWithFlags(&x.fork, hipEventDisableTiming)) != hipSuccess) return e;
+        if ((e = hipEventCreateWithFlags(&x.join, hipEventDisableTiming)) != hipSuccess) return e;
+        sides.push_back(x);
+        sd = &sides.back();
+    }
+    if ((e = hipEventRecord(sd->fork, caller)) != hipSuccess) return e;
+    if ((e = hipStreamWaitEvent(sd->stream, sd->fork, 0)) != hipSuccess) return e;
+    *out = sd;
+    return hipSuccess;
+}
+
 int layer_prefill(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_bytes, int n_expert, int k,
                   const float* x, const float* logits, const float* residual, float* out, int n_tok, const Route& route,
                   const xs_expert_layout_t* SL, const uint8_t* shared_blob, const float* w_gate, void* workspace,
@@ -1171,6 +1204,31 @@ int layer_prefill(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob
         return fail(XS_EINVAL, "%s: workspace missing, misaligned or short", who);
     const PrefillWs w = prefill_ws(L, n_expert, k, n_tok, (uint8_t*)workspace);
     const int64_t n = (int64_t)n_tok * k;
+    // the shared expert first, on a side stream forked from the caller's (its own plan, f16 activations, GEMMs and
+    // gate, in its own workspace): its one group of the prompt's rows leaves most of the GPU idle in its GEMMs, which
+    // now run beside the routed experts' work; joined before the combine
+    const float* shared = nullptr;
+    const float* gate = nullptr;
+    SideStream* side = nullptr;
+    if (SL) {   // every token through the shared expert (one group), its rows in fp32; its gate's logits
+        if (hipError_t e = side_stream_fork(S(stream), &side)) return hip_status(e, who);
+        void* ss = (void*)side->stream;
+        const SharedPrefillWs sw = shared_prefill_ws(SL, n_tok, (uint8_t*)workspace + w.bytes);
+        if (int r = finish(ss, xs::launch_single_group_plan(sw.grp_ptr, sw.start, sw.n_groups, sw.idx, n_tok,
+                                                            shared_blob, side->stream),
+                           who))
+            return r;
+        if (int r = prefill_experts(SL, x, n_tok, sw.idx, sw.idx, sw.start, sw.n_groups, sw.grp_ptr, 1, n_tok,
+                                    sw.scratch, sw.rows, nullptr, false, ss))
+            return r;
+        if (w_gate) {
+            // the prompt path's gate GEMM order (f32_gemm_rows) at every token count
+            if (int r = xs_f32_gemm_rows(x, SL->n_embd, w_gate, sw.gate, 1, SL->n_embd, 1, n_tok, ss)) return r;
+            gate = sw.gate;
+        }
+        shared = sw.rows;
+        if (hipError_t e = hipEventRecord(side->join, side->stream)) return hip_status(e, who);
+    }
     if (route.kind == XS_ROUTER_GROUPED_SIGMOID) {
         if (int r = xs_router_grouped_sigmoid(logits, route.bias, n_tok, n_expert, route.n_group, route.topk_group, k,
                                               route.scale, w.ids, w.w, stream))
@@ -1189,24 +1247,8 @@ int layer_prefill(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob
     if (int r = prefill_experts(L, x, n_tok, w.src, w.entry, w.bounds, w.n_groups, w.grp_ptr, cap_groups, n, w.scratch,
                                 nullptr, w.parts, true, stream))
         return r;
-    const float* shared = nullptr;
-    const float* gate = nullptr;
-    if (SL) {   // every token through the shared expert (one group), its rows in fp32; its gate's logits
-        const SharedPrefillWs sw = shared_prefill_ws(SL, n_tok, (uint8_t*)workspace + w.bytes);
-        if (int r = finish(stream, xs::launch_single_group_plan(sw.grp_ptr, sw.start, sw.n_groups, sw.idx, n_tok,
-                                                                shared_blob, S(stream)),
-                           who))
-            return r;
-        if (int r = prefill_experts(SL, x, n_tok, sw.idx, sw.idx, sw.start, sw.n_groups, sw.grp_ptr, 1, n_tok,
-                                    sw.scratch, sw.rows, nullptr, false, stream))
-            return r;
-        if (w_gate) {
-            // the prompt path's gate GEMM order (f32_gemm_rows) at every token count
-            if (int r = xs_f32_gemm_rows(x, SL->n_embd, w_gate, sw.gate, 1, SL->n_embd, 1, n_tok, stream)) return r;
-            gate = sw.gate;
-        }
-        shared = sw.rows;
-    }
+    if (side)   // the combine waits for the shared expert's rows
+        if (hipError_t e = hipStreamWaitEvent(S(stream), side->join, 0)) return hip_status(e, who);
     return finish(stream,
                   xs::launch_combine_h(w.parts, w.w, shared, gate, residual, out, L->n_embd, k, n_tok, S(stream)), who);
 }
