@@ -941,6 +941,7 @@ int layer_decode(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_
         a.slab_dn_bytes = P.slab_dn;
         a.ttab = P.ttab;
         a.direct = P.direct;
+        a.slab_alias = P.alias;
         a.spin_ticks = spin_ticks();
         a.shared = shared;
         a.shared_gate = shared_gate;
@@ -1078,6 +1079,7 @@ int layer_decode_shared(const xs_expert_layout_t* L, const uint8_t* arena, size_
         a.slab_dn_bytes = SP.slab_dn;
         a.ttab = SP.ttab;
         a.direct = SP.direct;
+        a.slab_alias = SP.alias;
         a.spin_ticks = spin_ticks();
         a.shared = nullptr;
         a.shared_gate = nullptr;

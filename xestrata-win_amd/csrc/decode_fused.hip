@@ -42,9 +42,12 @@ __host__ __device__ inline int up16(int v) { return (v + 15) & ~15; }
 // one entry's LDS activation of n values: int8 values | n / 32 fp32 scales | n / 16 int sums of 16
 __host__ __device__ inline int act_stride(int n) { return up16(n + n / 8 + n / 4); }
 
-// ttab: tokens of the LDS activation table of the pipelined gate/up path (0: none; it then also has no second slab)
+// ttab: tokens of the LDS activation table of the pipelined gate/up path (0: none; it then also has no second slab);
+// alias: the down slab over the gate/up slab(s) - a work-group's down units follow all of its gate/up units, so the two
+// are never live at once unless the first down rows are fetched early (which alias turns off)
 template <int NE>
-__host__ __device__ inline FusedLds fused_lds(int n_expert, int H, int F, int rh, int slab_gu, int slab_dn, int ttab) {
+__host__ __device__ inline FusedLds fused_lds(int n_expert, int H, int F, int rh, int slab_gu, int slab_dn, int ttab,
+                                              int alias) {
     FusedLds o;
     int at = 0;
     o.ids = at; at += up16(kFMaxN * 4);
@@ -61,7 +64,12 @@ __host__ __device__ inline FusedLds fused_lds(int n_expert, int H, int F, int rh
     o.po = at; at += up16(NE * 64 * 4);
     o.slab_gu = at; at += up16(slab_gu);
     if (ttab > 0) at += up16(slab_gu);   // a second gate/up slab: a unit is fetched while one computes
-    o.slab_dn = at; at += up16(slab_dn);
+    if (alias) {
+        o.slab_dn = o.slab_gu;
+        if (at < o.slab_gu + up16(slab_dn)) at = o.slab_gu + up16(slab_dn);
+    } else {
+        o.slab_dn = at; at += up16(slab_dn);
+    }
     o.act_g = at; at += (ttab > NE ? ttab : NE) * act_stride(H);   // the passes' activations, or the token table
     o.act_d = at; at += NE * act_stride(F);
     o.total = at;
@@ -277,7 +285,7 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
     const ExpertLayout& L = a.L;
     const int H = (int)L.n_embd, F = (int)L.n_ff, k = a.k, T = NE == 1 ? 1 : a.n_tok, n = T * k, E = a.n_expert;
     const int rh = a.rh, rd = a.rd, nu = a.nu, nj = a.nj;
-    const FusedLds o = fused_lds<NE>(E, H, F, rh, a.slab_gu_bytes, a.slab_dn_bytes, a.ttab);
+    const FusedLds o = fused_lds<NE>(E, H, F, rh, a.slab_gu_bytes, a.slab_dn_bytes, a.ttab, a.slab_alias);
     int* s_ids = (int*)(lds + o.ids);
     float* s_w = (float*)(lds + o.w);
     int* s_excl = (int*)(lds + o.excl);
@@ -443,7 +451,8 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
     const int d_begin = runs ? wg * dq + min(wg, dr) : wg;
     const int d_end = runs ? d_begin + dq + (wg < dr ? 1 : 0) : n_dn;
     const int d_step = runs ? 1 : G;
-    const bool dn_early = !piped && !DIRECT && n_gu <= G && wg < n_gu && d_begin < d_end;   // (round robin: d_begin = wg)
+    const bool dn_early = !piped && !DIRECT && !a.slab_alias && n_gu <= G && wg < n_gu && d_begin < d_end;
+    // (round robin: d_begin = wg)
     if (piped) {
         // 4..16 tokens, several units a work-group: every token's q8_1 activation once, into an LDS table, then the
         // units' slabs double-buffered - unit i + 1's DMA flies while unit i computes.  The load waves issue nothing
@@ -803,12 +812,16 @@ bool fused_decode_plan(const ExpertLayout& L, int n_expert, int k, int n_tok, Fu
     P->slab_dn = P->direct ? 0 : rd * (int)L.d_row;
     P->ne = n_tok >= 4 ? 4 : n_tok >= 2 ? 2 : 1;
     auto lds_of = [&](int ttab) {
-        return (P->ne == 1 ? fused_lds<1>(n_expert, H, F, rh, P->slab_gu, P->slab_dn, ttab)
-                : P->ne == 2 ? fused_lds<2>(n_expert, H, F, rh, P->slab_gu, P->slab_dn, ttab)
-                             : fused_lds<4>(n_expert, H, F, rh, P->slab_gu, P->slab_dn, ttab)).total;
+        return (P->ne == 1 ? fused_lds<1>(n_expert, H, F, rh, P->slab_gu, P->slab_dn, ttab, P->alias)
+                : P->ne == 2 ? fused_lds<2>(n_expert, H, F, rh, P->slab_gu, P->slab_dn, ttab, P->alias)
+                             : fused_lds<4>(n_expert, H, F, rh, P->slab_gu, P->slab_dn, ttab, P->alias)).total;
     };
     // 4..16 tokens: the pipelined gate/up path, if its token table and second slab fit
     P->ttab = 0;
+    // from two tokens the down slab lies over the gate/up slabs (the early down fetch serves one token), so that the
+    // pipelined path's table and second slab fit beside 40 KB down slabs (config 2 at 8 and 16 tokens: 115.7 -> 107.1
+    // and 196.2 -> 177.3 us); without the table, two work-groups a CU measured no faster than one
+    P->alias = n_tok >= 2;
     if (P->ne == 4 && n_tok <= 16 && lds_of(16) <= 160 * 1024) P->ttab = 16;
     P->lds = lds_of(P->ttab);
     return P->lds <= 160 * 1024;

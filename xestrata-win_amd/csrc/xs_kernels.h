@@ -83,6 +83,7 @@ struct FusedPlan {     // the fused decode layer's unit sizes (a function of the
     int ne, lds;       // entries a pass, dynamic LDS bytes
     int ttab;          // tokens of the pipelined gate/up path's activation table (0: that path is off)
     int direct;        // 1: one token, units read their rows from HBM straight into registers (no LDS slabs)
+    int alias;         // 1: the down slab lies over the gate/up slabs (no down rows fetched during gate/up units)
 };
 struct FusedArgs {
     ExpertLayout L;
@@ -102,6 +103,7 @@ struct FusedArgs {
                             // call's tag - 1 = their sum >> 20), zero before the first call
     int32_t* err;
     int rh, rd, nu, nj, slab_gu_bytes, slab_dn_bytes, ttab, direct;
+    int slab_alias = 0;     // FusedPlan::alias
     long long spin_ticks;   // bound of a wait, in wall-clock ticks
     const float* shared;       // [n_tok, n_embd] the shared expert's rows, added once by the combine (NULL: none)
     const float* shared_gate;  // [n_tok] its gate logits (NULL: ungated)
