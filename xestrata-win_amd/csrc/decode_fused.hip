@@ -30,6 +30,11 @@
 namespace xs {
 
 constexpr int kFT = 256;          // threads a work-group
+// threads a work-group of the pipelined 4..16-token instance: its LDS (token table, two slabs) holds one work-group a
+// CU, and with 256 threads that is one wave a SIMD, whose LDS and ALU latencies nothing hides; 512 give a down slab's
+// rows a thread each (64 rows x 8 canonical lanes) and route two tokens a wave instead of four
+constexpr int kFTPiped = 512;
+__host__ __device__ constexpr int fused_threads(int ne, int mode) { return ne == 4 && mode == 1 ? kFTPiped : kFT; }
 constexpr int kFMaxN = 256;       // routed entries (tokens x k) a call
 constexpr int kLoadWaves = 3;     // waves 0..2 issue every global load; wave 3 every tagged store
 constexpr int kLT = 64 * kLoadWaves;
@@ -81,13 +86,18 @@ typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 // q8_1 of values 8j .. 8j + 7 of one row (one scale a 256: 32 neighbouring lanes) straight into an LDS activation
 // (int8 values, fp32 scale, sums of 16): the values quantize_q8_1_rows writes (q8_1_256_lane), as the grouped
 // kernels read them back
+__device__ __forceinline__ void q8_1_256_store(const float (&v)[8], int j, int8_t* q, float* d8, int* us16);
 __device__ __forceinline__ void q8_1_256_to_act(const float* __restrict__ x, int j, int8_t* q, float* d8, int* us16) {
-    float v[8], a = 0.0f;
+    float v[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        v[i] = x[8 * j + i];
-        a = fmaxf(a, fabsf(v[i]));
-    }
+    for (int i = 0; i < 8; ++i) v[i] = x[8 * j + i];
+    q8_1_256_store(v, j, q, d8, us16);
+}
+// the same from values already loaded (values 8j .. 8j + 7; 32 neighbouring lanes hold a 256-value block)
+__device__ __forceinline__ void q8_1_256_store(const float (&v)[8], int j, int8_t* q, float* d8, int* us16) {
+    float a = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) a = fmaxf(a, fabsf(v[i]));
     const float amax = group_max32(a);
     const float d = q8_scale(amax), id = q8_inv(d);
     uint32_t w0 = 0, w1 = 0;
@@ -190,6 +200,24 @@ __device__ __forceinline__ bool gather_tagged(const unsigned long long* p, int n
 }
 
 // the row-dot lane sum for a run-time lane count (lane 0 of each group gets it)
+// f(EntriesC<M>()) with M = m, 1 <= m <= NE: a pass's entry count as a compile-time constant, so that the units' per-
+// entry branches fold away and their LDS reads go out together (with the count at run time every entry's reads waited
+// behind the branch before them)
+template <int N>
+struct EntriesC {
+    static constexpr int value = N;
+};
+template <int NE, typename Fn>
+__device__ __forceinline__ void with_entries(int m, Fn&& f) {
+    if constexpr (NE >= 4) {
+        if (m >= 4) return f(EntriesC<4>());
+        if (m == 3) return f(EntriesC<3>());
+    }
+    if constexpr (NE >= 2)
+        if (m == 2) return f(EntriesC<2>());
+    f(EntriesC<1>());
+}
+
 __device__ __forceinline__ float lanes_sum(float v, int l) {
     return l == 8 ? lane0_sum<8>(v) : l == 4 ? lane0_sum<4>(v) : l == 2 ? lane0_sum<2>(v) : v;
 }
@@ -231,13 +259,13 @@ bool fused_sigmoid_layout(int gu_type, int d_type) { return gu_type == kQ4_K && 
 
 // SIG: the instance carries the group-limited sigmoid router's stage (only the Q4_K pair's instances: code an instance
 // never runs still takes instruction-cache room - config 4's one-token layer 40.5 -> 41.3 us with it)
-template <int PER, bool SIG>
+template <int PER, bool SIG, int NT>
 __device__ __forceinline__ void route_tokens_wave(const FusedArgs& a, int T, int* s_ids, float* s_w,
                                                   unsigned long long& ctr) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, E = a.n_expert, k = a.k;
     if (a.pre_ids) {   // routed already (another router): the tokens' ids and weights as given
         ctr = load_counter(a);
-        for (int t = wave; t < T; t += kFT / 64)
+        for (int t = wave; t < T; t += NT / 64)
             if (lane < k) {
                 s_ids[t * k + lane] = a.pre_ids[t * k + lane];
                 s_w[t * k + lane] = a.pre_w[t * k + lane];
@@ -246,7 +274,7 @@ __device__ __forceinline__ void route_tokens_wave(const FusedArgs& a, int T, int
     }
     if (SIG && a.sig_group > 0) {   // the group-limited sigmoid router, a wave a token
         ctr = load_counter(a);
-        for (int t = wave; t < T; t += kFT / 64) {
+        for (int t = wave; t < T; t += NT / 64) {
             int id;
             float w;
             route_grouped_sigmoid_wave<PER>(a.logits + (int64_t)t * E, a.sig_bias, E, a.sig_group, a.sig_topk_group, k,
@@ -258,16 +286,21 @@ __device__ __forceinline__ void route_tokens_wave(const FusedArgs& a, int T, int
         }
         return;
     }
-    float lv[PER];
+    float lv[PER], ln[PER];
     if (wave < T) load_logits_wave<PER>(a.logits + (int64_t)wave * E, E, lv);
     ctr = load_counter(a);
-    for (int t = wave; t < T; t += kFT / 64) {
+    for (int t = wave; t < T; t += NT / 64) {
+        // the wave's next token's logits are in flight while this one routes
+        const int tn = t + NT / 64;
+        if (tn < T) load_logits_wave<PER>(a.logits + (int64_t)tn * E, E, ln);
         if (lane < k) {   // ranks a NaN row leaves unwritten stay invalid
             s_ids[t * k + lane] = -1;
             s_w[t * k + lane] = 0.0f;
         }
-        if (t != wave) load_logits_wave<PER>(a.logits + (int64_t)t * E, E, lv);
         route_topk_wave_lv<PER>(lv, E, k, s_ids + t * k, s_w + t * k);
+        if (tn < T)
+#pragma unroll
+            for (int i = 0; i < PER; ++i) lv[i] = ln[i];
     }
 }
 
@@ -277,8 +310,9 @@ __device__ __forceinline__ void route_tokens_wave(const FusedArgs& a, int T, int
 // path's code; MODE 0 otherwise.  Each instance carries only its own paths: the kernel's code is large, and what an
 // instance does not run still costs instruction-cache room.
 template <int TG, int TD, int NE, int MODE, int PER>
-__global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
+__global__ __launch_bounds__(fused_threads(NE, MODE)) void moe_decode_fused_kernel(FusedArgs a) {
     constexpr bool DIRECT = NE == 1 && MODE == 1;
+    constexpr int NT = fused_threads(NE, MODE);
     extern __shared__ __align__(16) uint8_t lds[];
     using UG = Unit<TG, true>;
     using UD = Unit<TD, false>;
@@ -318,10 +352,10 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
     const bool x_early = T == 1 && a.ttab == 0;
     if (x_early && wave > 0) {
         int8_t* q = (int8_t*)(lds + o.act_g);
-        for (int j8 = tid - 64; j8 < H / 8; j8 += kFT - 64)
+        for (int j8 = tid - 64; j8 < H / 8; j8 += NT - 64)
             q8_1_256_to_act(a.x, j8, q, (float*)(q + H), (int*)(q + H + H / 8));
     }
-    route_tokens_wave<PER, kFusedSigmoid<TG, TD>>(a, T, s_ids, s_w, ctr);   // PER = the experts a lane (64 PER >= E, chosen by the host)
+    route_tokens_wave<PER, kFusedSigmoid<TG, TD>, NT>(a, T, s_ids, s_w, ctr);   // PER = the experts a lane (64 PER >= E, chosen by the host)
     if (wave == 0) {
         const int epoch = epoch_of(ctr);
         if (lane == 0) s_misc[3] = epoch;
@@ -382,7 +416,7 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
             }
         }
     } else {   // the work-group: leaders by LDS atomicMin, group numbers and starts by one exclusive scan
-        for (int e = tid; e < E; e += kFT) s_first[e] = n;
+        for (int e = tid; e < E; e += NT) s_first[e] = n;
         __syncthreads();
         const int ex = tid < n ? s_ids[tid] : -1;
         if (__syncthreads_or(tid < n && (ex < 0 || ex >= E))) {
@@ -400,7 +434,7 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
                 }
             int total;
             const int excl = block_exclusive_scan(leader ? ((cnt << 16) | 1) : 0, s_wave, &total);
-            s_excl[tid] = excl;
+            if (tid < kFMaxN) s_excl[tid] = excl;   // (entries index it: tid < n <= kFMaxN)
             __syncthreads();
             if (tid < n) {
                 const int le = s_excl[s_first[ex]];
@@ -438,6 +472,7 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
     const int n16a = rh * (int)L.gu_row / 16, n16d = rd * (int)L.d_row / 16;
     float* s_po = (float*)(lds + o.po);
     const bool loader = wave < kLoadWaves;
+    const bool storer = wave == kLoadWaves;   // the one wave that writes tagged words (the others past it only compute)
     // with at most one gate/up unit a work-group, the store wave fetches the work-group's first down rows once the
     // gate/up slab is in: they then land while the gate/up products run and h travels
     const bool piped = NE == 4 && MODE == 1;   // the pipelined gate/up path below (4..16 tokens, the table in use)
@@ -458,13 +493,6 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
         // units' slabs double-buffered - unit i + 1's DMA flies while unit i computes.  The load waves issue nothing
         // but those DMAs meanwhile, so waiting for unit i is vmcnt <= (unit i + 1's DMA instructions of the wave).
         int8_t* ttab = (int8_t*)(lds + o.act_g);
-        for (int t = 0; t < T; ++t) {
-            const float* xr = a.x + (int64_t)t * H;
-            int8_t* q = ttab + t * act_stride(H);
-            for (int j8 = tid; j8 < H / 8; j8 += kFT)
-                q8_1_256_to_act(xr, j8, q, (float*)(q + H), (int*)(q + H + H / 8));
-        }
-        vm_drain();
         uint8_t* slab2[2] = {slab_gu, slab_gu + up16(a.slab_gu_bytes)};
         const int per_wave = loader && 2 * n16a > 64 * wave ? (2 * n16a - 64 * wave + kLT - 1) / kLT : 0;
         auto dma_unit = [&](int u, uint8_t* dst) {
@@ -476,7 +504,37 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
                 return (const void*)(i < n16a ? srcg + 16 * (size_t)i : srcu + 16 * (size_t)(i - n16a));
             });
         };
+        // the first unit's DMA goes out before the table, so that its rows land while the table is built
         if (loader && wg < n_gu) dma_unit(wg, slab2[0]);
+        // the table: chunk i = (token, 8 values) of every token, four chunks a thread with their loads in flight at
+        // once (a token at a time, every token's loads waited out a round trip of their own: ~1 us a token).  Chunks
+        // come 32 to a 256-value block, and the token rows are multiples of 32 chunks, so each 32-lane group is whole.
+        {
+            const int nch = H / 8, total = T * nch;
+            for (int i0 = 0; i0 < total; i0 += 4 * NT) {
+                float v[4][8];
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    const int i = i0 + b * NT + tid;
+                    if (i < total) {
+                        const int t = i / nch, j8 = i - t * nch;
+                        const float4* xr = (const float4*)(a.x + (int64_t)t * H + 8 * j8);
+                        const float4 u0 = xr[0], u1 = xr[1];
+                        v[b][0] = u0.x; v[b][1] = u0.y; v[b][2] = u0.z; v[b][3] = u0.w;
+                        v[b][4] = u1.x; v[b][5] = u1.y; v[b][6] = u1.z; v[b][7] = u1.w;
+                    }
+                }
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    const int i = i0 + b * NT + tid;
+                    if (i < total) {
+                        const int t = i / nch, j8 = i - t * nch;
+                        int8_t* q = ttab + t * act_stride(H);
+                        q8_1_256_store(v[b], j8, q, (float*)(q + H), (int*)(q + H + H / 8));
+                    }
+                }
+            }
+        }
         int it = 0;
         for (int u1 = wg; u1 < n_gu; u1 += gridDim.x, ++it) {
             const int g = u1 / nu, j = u1 - g * nu, next = u1 + (int)gridDim.x;
@@ -502,22 +560,27 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
                     at[e] = Act{q, (const float*)(q + H), (const int*)(q + H + H / 8)};
                 }
                 const int c = lane & (lpr_g - 1);
-                for (int rr = tid / lpr_g; rr < 2 * rh; rr += kFT / lpr_g) {
-                    float acc[NE];
+                with_entries<NE>(m, [&](auto mc) {
+                    constexpr int M = decltype(mc)::value;
+                    Act am[M];
 #pragma unroll
-                    for (int e = 0; e < NE; ++e) acc[e] = 0.0f;
-                    for (int u = c; u < H / UG::kUnit; u += lpr_g)
-                        UG::template apply<NE>(slab, rr * (int)L.gu_row, u, at, m, acc);
+                    for (int e = 0; e < M; ++e) am[e] = at[e];
+                    for (int rr = tid / lpr_g; rr < 2 * rh; rr += NT / lpr_g) {
+                        float acc[M];
 #pragma unroll
-                    for (int e = 0; e < NE; ++e) acc[e] = lanes_sum(acc[e], lpr_g);
-                    if (c == 0) {
+                        for (int e = 0; e < M; ++e) acc[e] = 0.0f;
+                        for (int u = c; u < H / UG::kUnit; u += lpr_g)
+                            UG::template apply<M>(slab, rr * (int)L.gu_row, u, am, M, acc);
 #pragma unroll
-                        for (int e = 0; e < NE; ++e)
-                            if (e < m) s_gu[e * 2 * rh + rr] = acc[e];
+                        for (int e = 0; e < M; ++e) acc[e] = lanes_sum(acc[e], lpr_g);
+                        if (c == 0) {
+#pragma unroll
+                            for (int e = 0; e < M; ++e) s_gu[e * 2 * rh + rr] = acc[e];
+                        }
                     }
-                }
+                });
                 lds_barrier();
-                if (!loader)
+                if (storer)
                     for (int i = lane; i < m * rh; i += 64) {
                         const int e = i / rh, r = i - e * rh;
                         st_tag(a.hx + (int64_t)(p + e) * F + j * rh + r,
@@ -550,7 +613,7 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
                 vm_drain();   // the slab and the activations have landed
             }
             __syncthreads();
-            if (dn_early && !loader && u1 == wg && p == e0) {
+            if (dn_early && storer && u1 == wg && p == e0) {
                 const int gd = d_begin / nj, jd = d_begin - gd * nj;
                 const uint8_t* srcd =
                     a.arena + (size_t)s_gexp[gd] * (size_t)a.blob + L.down_off + (size_t)jd * rd * L.d_row;
@@ -560,7 +623,7 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
             // the rows from the slab (LDS reads), or in the direct form from the blob (global reads): two loops, so
             // that each one's loads have a known address space
             auto gu_rows = [&](auto row_base) {
-                for (int rr = tid / lpr_g; rr < 2 * rh; rr += kFT / lpr_g) {
+                for (int rr = tid / lpr_g; rr < 2 * rh; rr += NT / lpr_g) {
                     float acc[NE];
 #pragma unroll
                     for (int e = 0; e < NE; ++e) acc[e] = 0.0f;
@@ -581,7 +644,7 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
             else
                 gu_rows([&](int) { return (const uint8_t*)slab_gu; });
             lds_barrier();
-            if (!loader)
+            if (storer)
                 for (int i = lane; i < m * rh; i += 64) {
                     const int e = i / rh, r = i - e * rh;
                     st_tag(a.hx + (int64_t)(p + e) * F + j * rh + r,
@@ -651,25 +714,30 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
             __syncthreads();
             const int c = lane & (lpr_d - 1);
             auto dn_rows = [&](const uint8_t* rb) {   // (the slab or, direct, the blob: as above, two instances)
-                for (int rr = tid / lpr_d; rr < rd; rr += kFT / lpr_d) {
-                    float acc[NE];
+                with_entries<NE>(m, [&](auto mc) {
+                    constexpr int M = decltype(mc)::value;
+                    Act am[M];
 #pragma unroll
-                    for (int e = 0; e < NE; ++e) acc[e] = 0.0f;
-                    for (int u = c; u < F / UD::kUnit; u += lpr_d)
-                        UD::template apply<NE>(rb, rr * (int)L.d_row, u, actd, m, acc);
+                    for (int e = 0; e < M; ++e) am[e] = actd[e];
+                    for (int rr = tid / lpr_d; rr < rd; rr += NT / lpr_d) {
+                        float acc[M];
 #pragma unroll
-                    for (int e = 0; e < NE; ++e) acc[e] = lanes_sum(acc[e], lpr_d);
-                    if (c == 0) {
+                        for (int e = 0; e < M; ++e) acc[e] = 0.0f;
+                        for (int u = c; u < F / UD::kUnit; u += lpr_d)
+                            UD::template apply<M>(rb, rr * (int)L.d_row, u, am, M, acc);
 #pragma unroll
-                        for (int e = 0; e < NE; ++e)
-                            if (e < m) s_po[e * rd + rr] = acc[e];
+                        for (int e = 0; e < M; ++e) acc[e] = lanes_sum(acc[e], lpr_d);
+                        if (c == 0) {
+#pragma unroll
+                            for (int e = 0; e < M; ++e) s_po[e * rd + rr] = acc[e];
+                        }
                     }
-                }
+                });
             };
             if (DIRECT) dn_rows(srcd);
             else dn_rows(slab_dn);
             __syncthreads();
-            if (!loader)
+            if (storer)
                 for (int i = lane; i < m * rd; i += 64) {
                     const int e = i / rd, r = i - e * rd;
                     st_tag(a.px + (int64_t)s_dst[p + e] * H + j * rd + r, s_po[e * rd + r], tag);
@@ -679,9 +747,11 @@ __global__ __launch_bounds__(kFT) void moe_decode_fused_kernel(FusedArgs a) {
     }
 
     // ---- 4. combines: (token t, down slab j), the slab's columns of the token's k parts in rank order + residual
-    for (int c = wg; c < T * nj; c += gridDim.x) {
+    // rd <= 64 threads a task (a column each), NT / rd tasks of a work-group at once (their polls overlap)
+    const int tg = NT / rd;
+    for (int c = wg + (tid / rd) * (int)gridDim.x; tid < tg * rd && c < T * nj; c += tg * (int)gridDim.x) {
         const int t = c / nj, j = c - t * nj;
-        for (int r = tid; r < rd; r += kFT) {
+        for (int r = tid % rd; r < rd; r += NT) {
             const int64_t col = (int64_t)j * rd + r;
             const unsigned long long* pp = a.px + (int64_t)t * k * H + col;
             const float* ww = s_w + t * k;
@@ -854,7 +924,7 @@ std::mutex g_shape_mu;
 std::vector<LaunchShape> g_shapes;
 }  // namespace
 
-static hipError_t resident_grid(const void* kern, int lds, int cap, int* grid_max) {
+static hipError_t resident_grid(const void* kern, int threads, int lds, int cap, int* grid_max) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
@@ -868,7 +938,7 @@ static hipError_t resident_grid(const void* kern, int lds, int cap, int* grid_ma
         return e;
     int cus = 0, occ = 0;
     if ((e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return e;
-    if ((e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, kFT, lds)) != hipSuccess) return e;
+    if ((e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, threads, lds)) != hipSuccess) return e;
     if (occ < 1) return hipErrorInvalidConfiguration;
     *grid_max = cus * (occ > cap ? cap : occ);
     g_shapes.push_back(LaunchShape{dev, kern, lds, cap, *grid_max});
@@ -917,13 +987,14 @@ hipError_t launch_decode_fused(const FusedArgs& a, const FusedPlan& P, hipStream
     else kern = pick<kQ4_K, kQ4_K>(P.ne, mode, E);
     // every work-group resident at once: the down units wait on the gate/up units of others
     int grid = 0;
-    hipError_t e = resident_grid(kern, P.lds, P.direct ? 4 : 2, &grid);
+    const int threads = fused_threads(P.ne, mode);
+    hipError_t e = resident_grid(kern, threads, P.lds, P.direct ? 4 : 2, &grid);
     if (e != hipSuccess) return e;
     const int cap = a.n_tok * a.k < a.n_expert ? a.n_tok * a.k : a.n_expert;
     const int need = cap * (P.nu > P.nj ? P.nu : P.nj);
     if (grid > need) grid = need;
     void* args[] = {(void*)&a};
-    return hipLaunchKernel(kern, dim3(grid), dim3(kFT), args, P.lds, s);
+    return hipLaunchKernel(kern, dim3(grid), dim3(threads), args, P.lds, s);
 }
 
 }  // namespace xs
