@@ -259,12 +259,15 @@ bool fused_sigmoid_layout(int gu_type, int d_type) { return gu_type == kQ4_K && 
 
 // SIG: the instance carries the group-limited sigmoid router's stage (only the Q4_K pair's instances: code an instance
 // never runs still takes instruction-cache room - config 4's one-token layer 40.5 -> 41.3 us with it)
-template <int PER, bool SIG, int NT>
+// after_loads() runs once the wave's first logits loads are out (loads issued there queue behind them, so the routing
+// waits for its own loads only)
+template <int PER, bool SIG, int NT, typename Fn>
 __device__ __forceinline__ void route_tokens_wave(const FusedArgs& a, int T, int* s_ids, float* s_w,
-                                                  unsigned long long& ctr) {
+                                                  unsigned long long& ctr, Fn&& after_loads) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, E = a.n_expert, k = a.k;
     if (a.pre_ids) {   // routed already (another router): the tokens' ids and weights as given
         ctr = load_counter(a);
+        after_loads();
         for (int t = wave; t < T; t += NT / 64)
             if (lane < k) {
                 s_ids[t * k + lane] = a.pre_ids[t * k + lane];
@@ -274,6 +277,7 @@ __device__ __forceinline__ void route_tokens_wave(const FusedArgs& a, int T, int
     }
     if (SIG && a.sig_group > 0) {   // the group-limited sigmoid router, a wave a token
         ctr = load_counter(a);
+        after_loads();
         for (int t = wave; t < T; t += NT / 64) {
             int id;
             float w;
@@ -289,6 +293,7 @@ __device__ __forceinline__ void route_tokens_wave(const FusedArgs& a, int T, int
     float lv[PER], ln[PER];
     if (wave < T) load_logits_wave<PER>(a.logits + (int64_t)wave * E, E, lv);
     ctr = load_counter(a);
+    after_loads();
     for (int t = wave; t < T; t += NT / 64) {
         // the wave's next token's logits are in flight while this one routes
         const int tn = t + NT / 64;
@@ -313,6 +318,7 @@ template <int TG, int TD, int NE, int MODE, int PER>
 __global__ __launch_bounds__(fused_threads(NE, MODE)) void moe_decode_fused_kernel(FusedArgs a) {
     constexpr bool DIRECT = NE == 1 && MODE == 1;
     constexpr int NT = fused_threads(NE, MODE);
+    constexpr bool PIPED = NE == 4 && MODE == 1;   // the pipelined 4..16-token path (token table, two slabs)
     extern __shared__ __align__(16) uint8_t lds[];
     using UG = Unit<TG, true>;
     using UD = Unit<TD, false>;
@@ -355,7 +361,27 @@ __global__ __launch_bounds__(fused_threads(NE, MODE)) void moe_decode_fused_kern
         for (int j8 = tid - 64; j8 < H / 8; j8 += NT - 64)
             q8_1_256_to_act(a.x, j8, q, (float*)(q + H), (int*)(q + H + H / 8));
     }
-    route_tokens_wave<PER, kFusedSigmoid<TG, TD>, NT>(a, T, s_ids, s_w, ctr);   // PER = the experts a lane (64 PER >= E, chosen by the host)
+    // the pipelined path's token table: its first 8 chunks a thread (chunk i = 8 values of token i / (H / 8)) are
+    // loaded beside the routing's logits (x does not depend on it); quantized into the table after the plan
+    constexpr int kXPre = PIPED ? 8 : 1;
+    float xv[kXPre][8];
+    auto load_x = [&]() {
+        if constexpr (PIPED) {
+            const int nch = H / 8, total = T * nch;
+#pragma unroll
+            for (int b = 0; b < kXPre; ++b) {
+                const int i = b * NT + tid;
+                if (i < total) {
+                    const int t = i / nch, j8 = i - t * nch;
+                    const float4* xr = (const float4*)(a.x + (int64_t)t * H + 8 * j8);
+                    const float4 u0 = xr[0], u1 = xr[1];
+                    xv[b][0] = u0.x; xv[b][1] = u0.y; xv[b][2] = u0.z; xv[b][3] = u0.w;
+                    xv[b][4] = u1.x; xv[b][5] = u1.y; xv[b][6] = u1.z; xv[b][7] = u1.w;
+                }
+            }
+        }
+    };
+    route_tokens_wave<PER, kFusedSigmoid<TG, TD>, NT>(a, T, s_ids, s_w, ctr, load_x);   // PER = the experts a lane (64 PER >= E, chosen by the host)
     if (wave == 0) {
         const int epoch = epoch_of(ctr);
         if (lane == 0) s_misc[3] = epoch;
@@ -381,6 +407,52 @@ __global__ __launch_bounds__(fused_threads(NE, MODE)) void moe_decode_fused_kern
     // the plan: groups = distinct experts in order of first occurrence, a group's entries ascending
     if (T == 1) {
         // planned above
+    } else if (PIPED) {
+        // a bit an entry in its expert's mask (LDS past o.slab_gu: slabs and table are filled after the plan, and
+        // the region holds 2 slabs + the table, well over the E x W words); an entry's position in its group is the
+        // count of the mask's bits below its own, a group's size the mask's count, its leader the entry at position 0
+        const int W = (n + 31) >> 5;
+        uint32_t* s_mask = (uint32_t*)(lds + o.slab_gu);
+        for (int i = tid; i < E * W; i += NT) s_mask[i] = 0u;
+        __syncthreads();
+        const int ex = tid < n ? s_ids[tid] : -1;
+        if (__syncthreads_or(tid < n && (ex < 0 || ex >= E))) {
+            if (tid == 0) s_misc[0] = -1;
+        } else {
+            if (tid < n) atomicOr(&s_mask[ex * W + (tid >> 5)], 1u << (tid & 31));
+            __syncthreads();
+            int cnt = 0, pos = 0;
+            if (tid < n) {
+                const uint32_t* mk = s_mask + ex * W;
+                for (int w = 0; w < W; ++w) {
+                    const uint32_t b = mk[w];
+                    cnt += __popc(b);
+                    pos += w < (tid >> 5) ? __popc(b) : w == (tid >> 5) ? __popc(b & ((1u << (tid & 31)) - 1u)) : 0;
+                }
+            }
+            const bool leader = tid < n && pos == 0;
+            int total;
+            const int excl = block_exclusive_scan(leader ? ((cnt << 16) | 1) : 0, s_wave, &total);
+            if (tid < kFMaxN) s_excl[tid] = excl;
+            __syncthreads();
+            // the leader's scan value reaches the group's entries through s_first (the leader's entry, per expert)
+            if (leader) s_first[ex] = tid;
+            __syncthreads();
+            if (tid < n) {
+                const int le = s_excl[s_first[ex]];
+                const int g = le & 0xffff, gs = le >> 16;
+                s_dst[gs + pos] = tid;
+                s_tok[gs + pos] = tid / k;
+                if (leader) {
+                    s_gexp[g] = ex;
+                    s_start[g] = gs;
+                }
+            }
+            if (tid == 0) {
+                s_start[total & 0xffff] = n;
+                s_misc[0] = total & 0xffff;
+            }
+        }
     } else if (n <= 64) {   // one wave: uniform v_readlane loops, no work-group scan
         if (wave == 0) {
             const int ex = lane < n ? s_ids[lane] : -1;
@@ -472,7 +544,9 @@ __global__ __launch_bounds__(fused_threads(NE, MODE)) void moe_decode_fused_kern
     const int n16a = rh * (int)L.gu_row / 16, n16d = rd * (int)L.d_row / 16;
     float* s_po = (float*)(lds + o.po);
     const bool loader = wave < kLoadWaves;
-    const bool storer = wave == kLoadWaves;   // the one wave that writes tagged words (the others past it only compute)
+    // the one wave that writes tagged words (the others past the load waves only compute); with 512 threads, wave 4,
+    // which has no rows of a gate/up slab (32 rows x 8 lanes fill waves 0..3), so its SwiGLU and stores overlap them
+    const bool storer = wave == (NT > 256 ? 4 : kLoadWaves);
     // with at most one gate/up unit a work-group, the store wave fetches the work-group's first down rows once the
     // gate/up slab is in: they then land while the gate/up products run and h travels
     const bool piped = NE == 4 && MODE == 1;   // the pipelined gate/up path below (4..16 tokens, the table in use)
@@ -511,7 +585,16 @@ __global__ __launch_bounds__(fused_threads(NE, MODE)) void moe_decode_fused_kern
         // come 32 to a 256-value block, and the token rows are multiples of 32 chunks, so each 32-lane group is whole.
         {
             const int nch = H / 8, total = T * nch;
-            for (int i0 = 0; i0 < total; i0 += 4 * NT) {
+#pragma unroll
+            for (int b = 0; b < kXPre; ++b) {   // the chunks loaded at the kernel's start
+                const int i = b * NT + tid;
+                if (i < total) {
+                    const int t = i / nch, j8 = i - t * nch;
+                    int8_t* q = ttab + t * act_stride(H);
+                    q8_1_256_store(xv[b], j8, q, (float*)(q + H), (int*)(q + H + H / 8));
+                }
+            }
+            for (int i0 = kXPre * NT; i0 < total; i0 += 4 * NT) {
                 float v[4][8];
 #pragma unroll
                 for (int b = 0; b < 4; ++b) {
@@ -535,6 +618,14 @@ __global__ __launch_bounds__(fused_threads(NE, MODE)) void moe_decode_fused_kern
                 }
             }
         }
+        // the store wave's last h value of a pass (one a lane), written once the next unit's slab is in: its SwiGLU
+        // and store then run beside the next unit's products instead of before the next unit's first barrier
+        float pg = 0.0f, pu = 0.0f;
+        unsigned long long* pdst = nullptr;
+        auto flush_h = [&]() {
+            if (pdst) st_tag(pdst, canon_silu_mul(pg, pu), tag);
+            pdst = nullptr;
+        };
         int it = 0;
         for (int u1 = wg; u1 < n_gu; u1 += gridDim.x, ++it) {
             const int g = u1 / nu, j = u1 - g * nu, next = u1 + (int)gridDim.x;
@@ -549,6 +640,7 @@ __global__ __launch_bounds__(fused_threads(NE, MODE)) void moe_decode_fused_kern
                 }
             }
             lds_barrier();   // this unit's slab is in
+            if (storer) flush_h();
             const int e0 = s_start[g], e1 = s_start[g + 1];
             for (int p = e0; p < e1; p += NE) {
                 const int m = min(NE, e1 - p);
@@ -580,14 +672,23 @@ __global__ __launch_bounds__(fused_threads(NE, MODE)) void moe_decode_fused_kern
                     }
                 });
                 lds_barrier();
-                if (storer)
+                if (storer) {
+                    flush_h();   // (a group of more than NE entries: the previous pass's)
                     for (int i = lane; i < m * rh; i += 64) {
                         const int e = i / rh, r = i - e * rh;
-                        st_tag(a.hx + (int64_t)(p + e) * F + j * rh + r,
-                               canon_silu_mul(s_gu[e * 2 * rh + r], s_gu[e * 2 * rh + rh + r]), tag);
+                        unsigned long long* dst = a.hx + (int64_t)(p + e) * F + j * rh + r;
+                        if (i + 64 < m * rh) {
+                            st_tag(dst, canon_silu_mul(s_gu[e * 2 * rh + r], s_gu[e * 2 * rh + rh + r]), tag);
+                        } else {
+                            pg = s_gu[e * 2 * rh + r];
+                            pu = s_gu[e * 2 * rh + rh + r];
+                            pdst = dst;
+                        }
                     }
+                }
             }
         }
+        if (storer) flush_h();
     } else
     for (int u1 = wg; u1 < n_gu; u1 += gridDim.x) {
         const int g = u1 / nu, j = u1 - g * nu;
@@ -892,7 +993,11 @@ bool fused_decode_plan(const ExpertLayout& L, int n_expert, int k, int n_tok, Fu
     // pipelined path's table and second slab fit beside 40 KB down slabs (config 2 at 8 and 16 tokens: 115.7 -> 107.1
     // and 196.2 -> 177.3 us); without the table, two work-groups a CU measured no faster than one
     P->alias = n_tok >= 2;
-    if (P->ne == 4 && n_tok <= 16 && lds_of(16) <= 160 * 1024) P->ttab = 16;
+    if (P->ne == 4 && n_tok <= 16 && lds_of(16) <= 160 * 1024) {
+        const FusedLds o4 = fused_lds<4>(n_expert, H, F, rh, P->slab_gu, P->slab_dn, 16, P->alias);
+        // the pipelined path plans in the LDS past its slab offset: E words for each 32 entries
+        if ((int64_t)n_expert * ((kFMaxN + 31) / 32) * 4 <= o4.total - o4.slab_gu) P->ttab = 16;
+    }
     P->lds = lds_of(P->ttab);
     return P->lds <= 160 * 1024;
 }
