@@ -551,11 +551,13 @@ __global__ __launch_bounds__(fused_threads(NE, MODE)) void moe_decode_fused_kern
     // gate/up slab is in: they then land while the gate/up products run and h travels
     const bool piped = NE == 4 && MODE == 1;   // the pipelined gate/up path below (4..16 tokens, the table in use)
     // down units: with one token and more units than work-groups, a work-group takes a run of consecutive ones
-    // (mostly one expert's), so its entry's h is gathered and quantized once for the run rather than once a unit.
-    // (With more tokens a unit's cost is its group's entry count, and runs would load the work-groups unevenly: there
-    // the units go round the work-groups.)
+    // (mostly one expert's), so its entry's h is gathered and quantized once for the run rather than once a unit; so
+    // too on the pipelined path below 8 tokens when most groups hold one entry (config 2 at 4 tokens, uniform
+    // routing: 62.4 -> 60.3 us a layer).  Otherwise a unit's cost is its group's entry count and runs load the
+    // work-groups unevenly (16 tokens: 170 -> 178 us a call; config 3's Zipf-routed verify: 55.9 -> 58.8 us a layer),
+    // so the units go round the work-groups.
     const int G = (int)gridDim.x;
-    const bool runs = T == 1 && n_dn > G;
+    const bool runs = (T == 1 || (PIPED && T < 8 && 4 * ng >= 3 * n)) && n_dn > G;
     const int dq = n_dn / G, dr = n_dn - dq * G;
     const int d_begin = runs ? wg * dq + min(wg, dr) : wg;
     const int d_end = runs ? d_begin + dq + (wg < dr ? 1 : 0) : n_dn;
