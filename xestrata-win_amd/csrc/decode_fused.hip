@@ -46,6 +46,10 @@ struct FusedLds {                 // byte offsets in the dynamic LDS
 __host__ __device__ inline int up16(int v) { return (v + 15) & ~15; }
 // one entry's LDS activation of n values: int8 values | n / 32 fp32 scales | n / 16 int sums of 16
 __host__ __device__ inline int act_stride(int n) { return up16(n + n / 8 + n / 4); }
+// a gate/up activation (n a multiple of 256): the same with kGuPad bytes after each 256 int8 values (Unit's PAD)
+constexpr int kGuPad = 16;
+__host__ __device__ inline int act_q_bytes_g(int n) { return n + n / 256 * kGuPad; }
+__host__ __device__ inline int act_stride_g(int n) { return up16(act_q_bytes_g(n) + n / 8 + n / 4); }
 
 // ttab: tokens of the LDS activation table of the pipelined gate/up path (0: none; it then also has no second slab);
 // alias: the down slab over the gate/up slab(s) - a work-group's down units follow all of its gate/up units, so the two
@@ -75,7 +79,7 @@ __host__ __device__ inline FusedLds fused_lds(int n_expert, int H, int F, int rh
     } else {
         o.slab_dn = at; at += up16(slab_dn);
     }
-    o.act_g = at; at += (ttab > NE ? ttab : NE) * act_stride(H);   // the passes' activations, or the token table
+    o.act_g = at; at += (ttab > NE ? ttab : NE) * act_stride_g(H);   // the passes' activations, or the token table
     o.act_d = at; at += NE * act_stride(F);
     o.total = at;
     return o;
@@ -109,7 +113,7 @@ __device__ __forceinline__ void q8_1_256_store(const float (&v)[8], int j, int8_
         w1 |= (uint32_t)(uint8_t)q1 << (8 * i);
         s += q0 + q1;
     }
-    *(uint2*)(q + 8 * j) = make_uint2(w0, w1);
+    *(uint2*)(q + 8 * j + kGuPad * (j >> 5)) = make_uint2(w0, w1);   // (a gate/up activation: padded blocks)
     const int s16 = s + dpp_i<kDppXor1>(s);
     if ((j & 1) == 0) us16[j >> 1] = s16;
     if ((j & 3) == 0) d8[j >> 2] = h2f(f2h(d));
@@ -320,7 +324,7 @@ __global__ __launch_bounds__(fused_threads(NE, MODE)) void moe_decode_fused_kern
     constexpr int NT = fused_threads(NE, MODE);
     constexpr bool PIPED = NE == 4 && MODE == 1;   // the pipelined 4..16-token path (token table, two slabs)
     extern __shared__ __align__(16) uint8_t lds[];
-    using UG = Unit<TG, true>;
+    using UG = Unit<TG, true, kGuPad>;
     using UD = Unit<TD, false>;
     const ExpertLayout& L = a.L;
     const int H = (int)L.n_embd, F = (int)L.n_ff, k = a.k, T = NE == 1 ? 1 : a.n_tok, n = T * k, E = a.n_expert;
@@ -344,8 +348,8 @@ __global__ __launch_bounds__(fused_threads(NE, MODE)) void moe_decode_fused_kern
     Act actg[NE], actd[NE];
 #pragma unroll
     for (int e = 0; e < NE; ++e) {
-        int8_t* qg = (int8_t*)(lds + o.act_g) + e * act_stride(H);
-        actg[e] = Act{qg, (const float*)(qg + H), (const int*)(qg + H + H / 8)};
+        int8_t* qg = (int8_t*)(lds + o.act_g) + e * act_stride_g(H);
+        actg[e] = Act{qg, (const float*)(qg + act_q_bytes_g(H)), (const int*)(qg + act_q_bytes_g(H) + H / 8)};
         int8_t* qd = (int8_t*)(lds + o.act_d) + e * act_stride(F);
         actd[e] = Act{qd, (const float*)(qd + F), (const int*)(qd + F + F / 8)};
     }
@@ -359,7 +363,7 @@ __global__ __launch_bounds__(fused_threads(NE, MODE)) void moe_decode_fused_kern
     if (x_early && wave > 0) {
         int8_t* q = (int8_t*)(lds + o.act_g);
         for (int j8 = tid - 64; j8 < H / 8; j8 += NT - 64)
-            q8_1_256_to_act(a.x, j8, q, (float*)(q + H), (int*)(q + H + H / 8));
+            q8_1_256_to_act(a.x, j8, q, (float*)(q + act_q_bytes_g(H)), (int*)(q + act_q_bytes_g(H) + H / 8));
     }
     // the pipelined path's token table: its first 8 chunks a thread (chunk i = 8 values of token i / (H / 8)) are
     // loaded beside the routing's logits (x does not depend on it); quantized into the table after the plan
@@ -592,8 +596,8 @@ __global__ __launch_bounds__(fused_threads(NE, MODE)) void moe_decode_fused_kern
                 const int i = b * NT + tid;
                 if (i < total) {
                     const int t = i / nch, j8 = i - t * nch;
-                    int8_t* q = ttab + t * act_stride(H);
-                    q8_1_256_store(xv[b], j8, q, (float*)(q + H), (int*)(q + H + H / 8));
+                    int8_t* q = ttab + t * act_stride_g(H);
+                    q8_1_256_store(xv[b], j8, q, (float*)(q + act_q_bytes_g(H)), (int*)(q + act_q_bytes_g(H) + H / 8));
                 }
             }
             for (int i0 = kXPre * NT; i0 < total; i0 += 4 * NT) {
@@ -614,8 +618,8 @@ __global__ __launch_bounds__(fused_threads(NE, MODE)) void moe_decode_fused_kern
                     const int i = i0 + b * NT + tid;
                     if (i < total) {
                         const int t = i / nch, j8 = i - t * nch;
-                        int8_t* q = ttab + t * act_stride(H);
-                        q8_1_256_store(v[b], j8, q, (float*)(q + H), (int*)(q + H + H / 8));
+                        int8_t* q = ttab + t * act_stride_g(H);
+                        q8_1_256_store(v[b], j8, q, (float*)(q + act_q_bytes_g(H)), (int*)(q + act_q_bytes_g(H) + H / 8));
                     }
                 }
             }
@@ -650,8 +654,8 @@ __global__ __launch_bounds__(fused_threads(NE, MODE)) void moe_decode_fused_kern
                 Act at[NE];
 #pragma unroll
                 for (int e = 0; e < NE; ++e) {
-                    int8_t* q = ttab + (e < m ? s_tok[p + e] : 0) * act_stride(H);
-                    at[e] = Act{q, (const float*)(q + H), (const int*)(q + H + H / 8)};
+                    int8_t* q = ttab + (e < m ? s_tok[p + e] : 0) * act_stride_g(H);
+                    at[e] = Act{q, (const float*)(q + act_q_bytes_g(H)), (const int*)(q + act_q_bytes_g(H) + H / 8)};
                 }
                 const int c = lane & (lpr_g - 1);
                 with_entries<NE>(m, [&](auto mc) {
@@ -709,9 +713,9 @@ __global__ __launch_bounds__(fused_threads(NE, MODE)) void moe_decode_fused_kern
             if (loader) {
                 for (int e = 0; e < (x_early ? 0 : m); ++e) {    // the entries' tokens to q8_1, one scale a 256
                     const float* xr = a.x + (int64_t)s_tok[p + e] * H;
-                    int8_t* q = (int8_t*)(lds + o.act_g) + e * act_stride(H);
+                    int8_t* q = (int8_t*)(lds + o.act_g) + e * act_stride_g(H);
                     for (int j8 = tid; j8 < H / 8; j8 += kLT)
-                        q8_1_256_to_act(xr, j8, q, (float*)(q + H), (int*)(q + H + H / 8));
+                        q8_1_256_to_act(xr, j8, q, (float*)(q + act_q_bytes_g(H)), (int*)(q + act_q_bytes_g(H) + H / 8));
                 }
                 vm_drain();   // the slab and the activations have landed
             }

@@ -53,12 +53,15 @@ __device__ __forceinline__ void lds_words_a2(const uint8_t* base, int off, uint3
 
 __device__ __forceinline__ int us32(const Act& a, int g) { return a.us16[2 * g] + a.us16[2 * g + 1]; }
 
-template <int T, bool S256>
+// PAD: bytes between the int8 values of consecutive 256-value blocks of the activation (0: packed).  Lanes of a row
+// read the same piece of 8 neighbouring blocks at once; 256 bytes apart those reads all hit the same LDS banks, 272
+// apart they spread over all of them.
+template <int T, bool S256, int PAD = 0>
 struct Unit;
 
 // ---- Q4_K
-template <bool S256>
-struct Unit<kQ4_K, S256> {
+template <bool S256, int PAD>
+struct Unit<kQ4_K, S256, PAD> {
     static constexpr int kUnit = S256 ? 256 : 32;
     template <int NE>
     __device__ static __forceinline__ void apply(const uint8_t* base, int roff, int u, const Act (&a)[NE], int n,
@@ -81,7 +84,7 @@ struct Unit<kQ4_K, S256> {
 #pragma unroll
                 for (int e = 0; e < NE; ++e) {
                     if (e >= n) break;
-                    const int8_t* q = a[e].q + 256 * b + 64 * p;
+                    const int8_t* q = a[e].q + (256 + PAD) * b + 64 * p;
                     const uint4 l0 = *(const uint4*)q, l1 = *(const uint4*)(q + 16);
                     const uint4 h0 = *(const uint4*)(q + 32), h1 = *(const uint4*)(q + 48);
                     const uint32_t al[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
@@ -113,7 +116,7 @@ struct Unit<kQ4_K, S256> {
 #pragma unroll
             for (int e = 0; e < NE; ++e) {
                 if (e >= n) break;
-                const int8_t* q = a[e].q + 32 * u;
+                const int8_t* q = a[e].q + 32 * u + PAD * (u >> 3);
                 const uint4 l0 = *(const uint4*)q, l1 = *(const uint4*)(q + 16);
                 const uint32_t al[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
                 int is = 0;
@@ -129,8 +132,8 @@ struct Unit<kQ4_K, S256> {
 
 // ---- Q6_K: 32-value group gg of a block: half n = gg / 4, s = gg % 4; codes (ql >> 4(s >> 1)) & 15 | ((qh >> 2s) & 3) << 4
 // from ql[64n + 32(s & 1) + l] and qh[32n + l]; scales sc[2gg] (values 0..15), sc[2gg + 1] (16..31)
-template <bool S256>
-struct Unit<kQ6_K, S256> {
+template <bool S256, int PAD>
+struct Unit<kQ6_K, S256, PAD> {
     static constexpr int kUnit = S256 ? 256 : 32;
     template <int NE>
     __device__ static __forceinline__ void group(const uint8_t* base, int boff, int gg, int v0, const Act (&a)[NE],
@@ -148,7 +151,7 @@ struct Unit<kQ6_K, S256> {
 #pragma unroll
         for (int e = 0; e < NE; ++e) {
             if (e >= n) break;
-            const int8_t* x = a[e].q + v0;
+            const int8_t* x = a[e].q + v0 + PAD * (v0 >> 8);
             const uint4 l0 = *(const uint4*)x, l1 = *(const uint4*)(x + 16);
             int i0 = 0, i1 = 0;
             i0 = sdot4((int)q[0], (int)l0.x, i0);
@@ -188,8 +191,8 @@ struct Unit<kQ6_K, S256> {
 };
 
 // ---- Q8_0: unit = block u (34 bytes)
-template <bool S256>
-struct Unit<kQ8_0, S256> {
+template <bool S256, int PAD>
+struct Unit<kQ8_0, S256, PAD> {
     static constexpr int kUnit = 32;
     template <int NE>
     __device__ static __forceinline__ void apply(const uint8_t* base, int roff, int u, const Act (&a)[NE], int n,
@@ -201,7 +204,7 @@ struct Unit<kQ8_0, S256> {
 #pragma unroll
         for (int e = 0; e < NE; ++e) {
             if (e >= n) break;
-            const int8_t* x = a[e].q + 32 * u;
+            const int8_t* x = a[e].q + 32 * u + PAD * (u >> 3);
             const uint4 l0 = *(const uint4*)x, l1 = *(const uint4*)(x + 16);
             const uint32_t al[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
             int is = 0;
@@ -213,8 +216,8 @@ struct Unit<kQ8_0, S256> {
 };
 
 // ---- IQ4_XS: sub-block s: 16 qs bytes, low nibbles values 0..15, high 16..31, codebook kvalues_iq4nl, scale ls - 32
-template <bool S256>
-struct Unit<kIQ4_XS, S256> {
+template <bool S256, int PAD>
+struct Unit<kIQ4_XS, S256, PAD> {
     static constexpr int kUnit = S256 ? 256 : 32;
     template <int NE>
     __device__ static __forceinline__ void sub(const uint8_t* blk, uint2 hdr, int s, int v0, const Act (&a)[NE], int n,
@@ -234,7 +237,7 @@ struct Unit<kIQ4_XS, S256> {
 #pragma unroll
         for (int e = 0; e < NE; ++e) {
             if (e >= n) break;
-            const int8_t* x = a[e].q + v0;
+            const int8_t* x = a[e].q + v0 + PAD * (v0 >> 8);
             const uint4 l0 = *(const uint4*)x, l1 = *(const uint4*)(x + 16);
             int is = 0;
             is = sdot4(lo[0], (int)l0.x, is);
