@@ -30,6 +30,10 @@ namespace xs {
 constexpr int kStreamWaves = 8;   // waves a work-group: two a SIMD, one computes while the other waits
 constexpr int kStreamWavesWide = 12;   // three a SIMD, for gate/up kernels whose registers allow it (<= 168 VGPRs)
 constexpr int kStreamLds = 160 * 1024;
+// bytes after each 256 int8 values of a staged gate/up activation row (Unit's PAD): a row's lanes read neighbouring
+// 256-value blocks at once, which unpadded all fall in the same LDS banks
+constexpr int kStreamPad = 16;
+__host__ __device__ inline int stream_rowq(int n_in) { return n_in + ((n_in + 255) >> 8) * kStreamPad; }
 constexpr int kStreamStepMax = 10 * 1024;
 constexpr int kStreamNiMax = 12;   // DMA instructions a step at most (12 KB)
 
@@ -62,7 +66,7 @@ struct StreamGeom {
 template <int T, bool DOWN, int LPR, int NE, int WAVES>
 __global__ __launch_bounds__(64 * WAVES) void stream_kernel(GroupedArgs a, StreamGeom G, const int8_t* __restrict__ hact_q,
                                                      const float* __restrict__ hact_d, const int* __restrict__ hact_s) {
-    using U = Unit<T, !DOWN>;
+    using U = Unit<T, !DOWN, DOWN ? 0 : kStreamPad>;
     extern __shared__ __align__(16) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n_in = G.n_in, nb32 = n_in >> 5, nb16 = n_in >> 4;
@@ -79,7 +83,8 @@ __global__ __launch_bounds__(64 * WAVES) void stream_kernel(GroupedArgs a, Strea
     for (int i = tid; i < e_end && i < G.cap_entries; i += NT) m_ent[i] = DOWN ? a.ent_dst[i] : a.ent_tok[i];
     uint8_t* act = lds + G.meta_bytes;
     int8_t* aq = (int8_t*)act;
-    float* ad = (float*)(aq + G.n_tok * n_in);
+    const int rowq = stream_rowq(n_in);   // a staged token row's int8 bytes (gate/up)
+    float* ad = (float*)(aq + G.n_tok * rowq);
     int* as16 = (int*)(ad + G.n_tok * nb32);
     if (!DOWN) {   // every token's q8_1 row: int8 values, the fp16 scale as a float, the sums of 16
         for (int i = tid; i < G.n_tok * nb32; i += NT) {
@@ -87,7 +92,8 @@ __global__ __launch_bounds__(64 * WAVES) void stream_kernel(GroupedArgs a, Strea
             uint32_t wd[9];
 #pragma unroll
             for (int j = 0; j < 9; ++j) wd[j] = blk[j];
-            uint4* dst = (uint4*)(aq + 32 * (int64_t)i);
+            const int t = i / nb32, b = i - t * nb32;
+            uint4* dst = (uint4*)(aq + (int64_t)t * rowq + 32 * b + kStreamPad * (b >> 3));
             dst[0] = make_uint4(wd[1], wd[2], wd[3], wd[4]);
             dst[1] = make_uint4(wd[5], wd[6], wd[7], wd[8]);
             ad[i] = h2f((uint16_t)(wd[0] & 0xFFFFu));
@@ -208,7 +214,7 @@ __global__ __launch_bounds__(64 * WAVES) void stream_kernel(GroupedArgs a, Strea
                         for (int e = 0; e < NP; ++e) {
                             const int j = src[pp + e];
                             av[e] = DOWN ? Act{wq + j * n_in, wd8 + j * nb32, ws16 + j * nb16}
-                                         : Act{aq + j * n_in, ad + j * nb32, as16 + j * nb16};
+                                         : Act{aq + j * rowq, ad + j * nb32, as16 + j * nb16};
                         }
                         U::template apply<NP>(slot, roff, u, av, min(n - pp, NP), *(float(*)[NP])(acc + pp));
                     }
@@ -307,7 +313,7 @@ bool stream_geom(const ExpertLayout& L, int unit, int block_values, int block_by
     G.wact = DOWN ? ((G.ne * row_act + 15) & ~15) : 0;
     auto fit = [&](int waves) {
         G.waves = waves;
-        G.act_bytes = DOWN ? waves * G.wact : ((n_tok * row_act + 15) & ~15);
+        G.act_bytes = DOWN ? waves * G.wact : ((n_tok * (row_act + stream_rowq(G.n_in) - G.n_in) + 15) & ~15);
         const int ring = (kStreamLds - G.meta_bytes - G.act_bytes) / waves;
         G.slots = ring / G.slot;
         while (G.slots > 1 && (G.slots - 1) * G.ni > 63) --G.slots;
