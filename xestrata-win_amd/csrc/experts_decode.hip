@@ -36,14 +36,18 @@ typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 template <int T, int LPR, bool DOWN, int NE>
 __global__ __launch_bounds__(kThreads) void grouped_kernel(ExpertLayout L, GroupedArgs a, int rows_total, int slab_rows,
                                                            int64_t mat_off, int64_t rb) {
-    using U = Unit<T, !DOWN>;
+    // gate/up: the staged rows carry kActPad bytes after every 256 int8 values (Unit's PAD), so that a row's lanes,
+    // which read neighbouring 256-value blocks at once, hit distinct LDS banks
+    constexpr int kPad = DOWN ? 0 : kActPad;
+    using U = Unit<T, !DOWN, kPad>;
     extern __shared__ __align__(16) uint8_t lds[];
     const int n_in = DOWN ? (int)L.n_ff : (int)L.n_embd;
+    const int rowq = act_rowq(n_in, kPad);   // a staged row's int8 bytes
     const int units = n_in / U::kUnit;
     const int64_t slab_bytes = (int64_t)slab_rows * rb;
     uint8_t* slab = lds;
     int8_t* actq = (int8_t*)(lds + slab_bytes);
-    float* actd = (float*)(actq + NE * n_in);
+    float* actd = (float*)(actq + NE * rowq);
     int* acts = (int*)(actd + NE * (n_in >> 5));
     const int tid = threadIdx.x, lane = tid & 63;
     const int r0 = blockIdx.x * slab_rows;
@@ -54,7 +58,7 @@ __global__ __launch_bounds__(kThreads) void grouped_kernel(ExpertLayout L, Group
     const int nb = n_in >> 5;
     Act act[NE];
 #pragma unroll
-    for (int e = 0; e < NE; ++e) act[e] = Act{actq + e * n_in, actd + e * nb, acts + e * (n_in >> 4)};
+    for (int e = 0; e < NE; ++e) act[e] = Act{actq + e * rowq, actd + e * nb, acts + e * (n_in >> 4)};
 
     for (int g = blockIdx.y; g < ngroups; g += gridDim.y) {
         const uint8_t* blob = (const uint8_t*)a.grp_ptr[g];
@@ -86,7 +90,7 @@ __global__ __launch_bounds__(kThreads) void grouped_kernel(ExpertLayout L, Group
                     uint32_t w[9];
 #pragma unroll
                     for (int k = 0; k < 9; ++k) w[k] = blk[k];
-                    uint4* dst = (uint4*)(actq + e * n_in + 32 * bi);
+                    uint4* dst = (uint4*)(actq + e * rowq + 32 * bi + kPad * (bi >> 3));
                     dst[0] = make_uint4(w[1], w[2], w[3], w[4]);
                     dst[1] = make_uint4(w[5], w[6], w[7], w[8]);
                     actd[e * nb + bi] = h2f((uint16_t)(w[0] & 0xFFFFu));
@@ -181,7 +185,7 @@ static hipError_t launch_t(const ExpertLayout& L, const GroupedArgs& a, hipStrea
     if (slab_rows > rows_total) slab_rows = rows_total;
     // entries a pass: the most a group can hold (one per token), up to kNE
     const int ne = a.max_entries > 0 && a.max_entries < 4 ? (a.max_entries == 1 ? 1 : 2) : kNE;
-    const size_t lds = (size_t)slab_rows * rb + (size_t)ne * (n_in + (n_in / 32) * 4 + (n_in / 16) * 4);
+    const size_t lds = (size_t)slab_rows * rb + (size_t)ne * (act_rowq(n_in, DOWN ? 0 : kActPad) + (n_in / 32) * 4 + (n_in / 16) * 4);
     const int64_t gy = a.grid_groups > 0 && a.grid_groups < a.cap_groups ? a.grid_groups : a.cap_groups;
     const dim3 grid((unsigned)((rows_total + slab_rows - 1) / slab_rows), (unsigned)gy);
     void (*kern)(ExpertLayout, GroupedArgs, int, int, int64_t, int64_t) = nullptr;

@@ -58,6 +58,9 @@ __device__ __forceinline__ int us32(const Act& a, int g) { return a.us16[2 * g] 
 // apart they spread over all of them.
 template <int T, bool S256, int PAD = 0>
 struct Unit;
+// the padding the modular kernels give their staged gate/up rows, and a staged row's int8 bytes with a padding
+constexpr int kActPad = 16;
+__host__ __device__ inline int act_rowq(int n, int pad) { return n + ((n + 255) >> 8) * pad; }
 
 // ---- Q4_K
 template <bool S256, int PAD>
