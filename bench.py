@@ -80,6 +80,79 @@ def run_graph(torch, calls):
     return ms
 
 
+def best_of_means(torch, fn, reps, trials=5):
+    """The reference's prompt timing rule (src/kernels/iq_mmq_parity.cpp:150-163: the best of 5 means of 10): fn()
+    captured once in a HIP graph; `trials` times, `reps` replays between two events; the smallest mean, ms."""
+    _, g = graph_time(torch, fn, 1)
+    best = float("inf")
+    for _ in range(trials):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        best = min(best, e0.elapsed_time(e1) / reps)
+    return best
+
+
+def measured_peaks(torch, xm, arena, span):
+    """This box's achieved peaks, measured with the library's probes (xs_bench_hbm_read, xs_bench_mfma_f16):
+    - hbm_stream_gbs: a read-only stream over 2 GiB, nontemporal 16-byte loads, the best of four grid sizes (means of
+      5 launches after one untimed);
+    - hbm_one_launch: `span` bytes (one decode layer's experts) read by one launch, the launches rotated over the
+      headline's arena in `span`-byte regions (the caches hold none of them) and replayed from one graph, as the
+      headline is; the best of four grid sizes;
+    - mfma_f16_tflops: v_mfma_f32_32x32x16_f16 back to back, 8 accumulators a wave, 2 waves a SIMD on every CU."""
+    dev = "cuda"
+    st = torch.cuda.current_stream().cuda_stream
+    sink = torch.zeros(1 << 16, dtype=torch.int32, device=dev)
+    buf = torch.empty(2 << 30, dtype=torch.uint8, device=dev).fill_(7)
+    stream = {}
+    for grid in (1024, 2048, 4096, 8192):
+        xm.lib().xs_bench_hbm_read(buf.data_ptr(), buf.numel(), sink.data_ptr(), grid, st)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(5):
+            xm._check(xm.lib().xs_bench_hbm_read(buf.data_ptr(), buf.numel(), sink.data_ptr(), grid, st))
+        e1.record()
+        torch.cuda.synchronize()
+        stream[grid] = buf.numel() / (e0.elapsed_time(e1) / 5 * 1e-3) / 1e9
+    del buf
+    torch.cuda.empty_cache()
+    flat = arena.view(-1)
+    n_reg = flat.numel() // span
+    one = {}
+    for grid in (256, 512, 1024, 2048):
+        def fn(grid=grid):
+            cs = torch.cuda.current_stream().cuda_stream
+            for r in range(n_reg):
+                xm._check(xm.lib().xs_bench_hbm_read(flat.data_ptr() + r * span, span, sink.data_ptr(), grid, cs))
+        ms = run_graph(torch, [fn])
+        one[grid] = ms * 1e3 / n_reg
+    g1 = min(one, key=one.get)
+    grid_m, iters = 1024, 2000
+    fsink = torch.zeros(grid_m * 128, device=dev)
+    xm._check(xm.lib().xs_bench_mfma_f16(iters, grid_m, fsink.data_ptr(), st))
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(5):
+        xm._check(xm.lib().xs_bench_mfma_f16(iters, grid_m, fsink.data_ptr(), st))
+    e1.record()
+    torch.cuda.synchronize()
+    tf = grid_m * 2 * iters * 8 * 32768.0 / (e0.elapsed_time(e1) / 5 * 1e-3) / 1e12
+    gs = max(stream, key=stream.get)
+    out = dict(hbm_stream_gbs=round(stream[gs], 1), hbm_stream_grid=gs, hbm_stream_bytes=2 << 30,
+               hbm_one_launch_bytes=span, hbm_one_launch_us=round(one[g1], 3),
+               hbm_one_launch_gbs=round(span / (one[g1] * 1e-6) / 1e9, 1), hbm_one_launch_grid=g1,
+               mfma_f16_tflops=round(tf, 1),
+               method="xs_bench_hbm_read / xs_bench_mfma_f16 (xestrata-win_amd/csrc/peaks.hip)")
+    log(f"measured peaks: HBM stream {out['hbm_stream_gbs']} GB/s (grid {gs}); one launch of {span / 1e6:.2f} MB "
+        f"{out['hbm_one_launch_us']} us = {out['hbm_one_launch_gbs']} GB/s (grid {g1}); f16 MFMA {tf:.0f} TFLOP/s")
+    return out
+
+
 TRAFFIC_FILE = ROOT / "profiles" / "moe_decode_t1_config2_traffic.md"
 
 
@@ -192,17 +265,18 @@ def other_configs(torch, xm, dev, gen, steps):
     import numpy as np
     out = {}
     # config 4: the Qwen3-235B-A22B-shaped stack, IQ4_XS experts (hidden 4096, 128 experts, top-8, F 1536): 94 layers
-    # resident in HBM (120.6 GB), one token (or 8) through all 94 in one graph - per-stack time.  Layer 0 is quantized
-    # from seeded random weights; layers 1..93 are device copies of it at their own addresses (each layer's experts
-    # are read from HBM, the caches hold none of them)
+    # resident in HBM (120.6 GB), one token (or 8) through all 94 in one graph - per-stack time.  Each layer is
+    # quantized from its own seeded random weights (seeds 4000 + layer), so every layer's experts are distinct bytes
+    # read from HBM
     E, H, F, k, NL = 128, 4096, 1536, 8, 94
-    layer0, L = xm.build_arena(E, H, F, xm.IQ4_XS, xm.IQ4_XS, seed=4)
+    L = xm.native_expert_layout(xm.IQ4_XS, xm.IQ4_XS, H, F)
+    t0 = time.time()
     stack = torch.empty(NL * E, L.bytes, dtype=torch.uint8, device=dev)
-    for li in range(NL):
-        stack[li * E:(li + 1) * E].copy_(layer0)
-    del layer0
+    for li in range(NL):   # every layer its own seeded random weights, quantized to IQ4_XS
+        xm.fill_layer(stack[li * E:(li + 1) * E], L, seed=4000 + li)
     torch.cuda.synchronize()
-    log(f"config 4: {NL}-layer stack resident, {stack.numel() / 1e9:.1f} GB")
+    log(f"config 4: {NL}-layer stack resident, {stack.numel() / 1e9:.1f} GB, {NL} distinct seeds, built in "
+        f"{time.time() - t0:.1f} s")
     for T in (1, 8):
         lg = torch.randn(NL, T, E, device=dev, generator=gen)   # each layer its own routing
         x = torch.randn(T, H, device=dev, generator=gen).to(torch.bfloat16).float()
@@ -231,25 +305,37 @@ def other_configs(torch, xm, dev, gen, steps):
     # row added by the combine: one call a layer (xs_moe_layer_decode_ex / xs_moe_layer_prefill_ex)
     E, H, F, k = 256, 7168, 2048, 8
     arena, L = xm.build_arena(E, H, F, xm.Q4_K, xm.Q4_K, seed=5)
-    sarena, SL = xm.build_arena(1, H, 2048, xm.Q8_0, xm.Q8_0, seed=55)
+    s_copies = 8
+    sarena, SL = xm.build_arena(1, H, 2048, xm.Q8_0, xm.Q8_0, seed=55, copies=s_copies)
     bias = torch.randn(E, device=dev, generator=gen) * 0.1
     router = xm.grouped_sigmoid_router(bias, 8, 4, 2.5)
     n_sets = E // k
-    # logits whose group-limited top-8 are disjoint from set to set: +8 on set s's 8 experts, one in each of its 4
-    # groups' top pairs (experts s*8 .. s*8+7 lie in groups (s*8 .. s*8+7) // 32, two a group at most)
-    lg = torch.randn(n_sets, 1, E, device=dev, generator=gen)
+    # logits whose group-limited top-8 are disjoint from set to set and cover all 256 experts once: set s lifts two
+    # experts in each of four groups (groups 0-3 for even s, 4-7 for odd; pair s // 2 of the group's 16), the rest
+    # sit 4 below N(0,1), so the four lifted groups win and their lifted pairs are the top-8 (checked below)
+    lg = torch.randn(n_sets, 1, E, device=dev, generator=gen) - 4.0
+    boosted = []
     for st in range(n_sets):
-        lg[st, :, torch.arange(8, device=dev) * 32 + st] += 8.0
+        idx = [gi * 32 + 2 * (st // 2) + j for gi in ((0, 1, 2, 3) if st % 2 == 0 else (4, 5, 6, 7)) for j in (0, 1)]
+        lg[st, :, idx] += 12.0
+        boosted.append(sorted(idx))
+    for st in range(n_sets):
+        got = sorted(xm.router_grouped_sigmoid(lg[st], bias, 8, 4, k, 2.5)[0].view(-1).tolist())
+        assert got == boosted[st], (st, got, boosted[st])
     x = torch.randn(1, H, device=dev, generator=gen).to(torch.bfloat16).float()
     res = torch.randn(1, H, device=dev, generator=gen)
     o = torch.empty(1, H, device=dev)
     layer = xm.MoeLayer(L, arena, E, k, 1, shared=(SL, sarena[0], None), router=router)
-    ms = time_steps(torch, [(lambda st=st: layer(x, lg[st], res, o)) for st in range(n_sets)], steps, n_sets)
+    # step st: routed set st, shared copy st % 8 (a routed expert comes back after 32 steps, 6.3 GB later; a shared
+    # copy after 8, 1.96 GB later: both past the 256 MB Infinity Cache)
+    ms = time_steps(torch, [(lambda st=st: layer(x, lg[st], res, o, shared_blob=sarena[st % s_copies]))
+                            for st in range(n_sets)], steps, n_sets)
     ms_r = time_steps(torch, [lambda: xm.router_grouped_sigmoid(lg[0], bias, 8, 4, k, 2.5)] * 32, steps, 32)
     distinct = float(np.mean([len(torch.unique(xm.router_grouped_sigmoid(lg[st], bias, 8, 4, k, 2.5)[0]))
                               for st in range(n_sets)]))
     b = distinct * L.bytes + SL.bytes
     out["config5_T1"] = dict(us_per_layer=round(ms * 1e3, 2), expert_gbs=round(b / (ms * 1e-3) / 1e9, 1),
+                             shared_copies=s_copies, sets=n_sets,
                              frac_hbm_peak=round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), expert_mb=round(b / 1e6, 1),
                              routing="the group-limited sigmoid router (bias, 8 groups, top-4, k 8, scale 2.5) inside "
                                      "the one-call layer (its own launch, included); the shared expert's row added",
@@ -284,14 +370,31 @@ def other_configs(torch, xm, dev, gen, steps):
     return out
 
 
-def cpu_model():
+def cpu_info():
+    """The host's CPU as /proc/cpuinfo names it: the full model string, logical CPUs, physical cores (distinct
+    (physical id, core id) pairs), sockets, and the CPUs this process may run on."""
+    model, logical, cores, sockets, phys = "unknown", 0, set(), set(), None
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            key, _, val = line.partition(":")
+            key, val = key.strip(), val.strip()
+            if key == "processor":
+                logical += 1
+            elif key == "model name" and model == "unknown":
+                model = val
+            elif key == "physical id":
+                phys = val
+                sockets.add(val)
+            elif key == "core id":
+                cores.add((phys, val))
     except OSError:
         pass
-    return "unknown"
+    try:
+        allowed = len(os.sched_getaffinity(0))
+    except OSError:
+        allowed = None
+    return dict(model=model, logical_cpus=logical, physical_cores=len(cores) or None, sockets=len(sockets) or None,
+                cpus_allowed=allowed)
 
 
 def cpu_baseline(torch, xm, np, arena, L, E, H, F, k, dev, gen, max_threads=16):
@@ -357,7 +460,7 @@ def cpu_baseline(torch, xm, np, arena, L, E, H, F, k, dev, gen, max_threads=16):
                        "over the 16 disjoint 8-expert sets of one 392 MB host copy (every 16 calls read all 128 "
                        "experts from DRAM); config 1 likewise over 32 host copies of its 13 MB layer",
                 us_per_token=round(us2, 1), expert_gbs=round(gbs2, 2), rel_to_gpu=float(f"{r2:.3e}"),
-                cpu_model=cpu_model(), threads="one a physical core, pinned, at most 16 (the box's CPU share)",
+                cpu=cpu_info(), threads="one a physical core, pinned, at most 16 (the box's CPU share)",
                 path="oracle/cpu_path.cpp: Q8_K activations, AVX2 multi-token Q4_K/Q6_K rows, SwiGLU "
                      "g/(1+exp(-g))*u, h re-quantized to Q8_K, rank-order combine (src/kernels/cpu/"
                      "native_expert.cpp, iq_avx2_rows.inl); the float accumulation order is this file's",
@@ -460,6 +563,9 @@ def main():
         + (f", HBM traffic {traffic / 1e6:.2f} MB/launch (rocprofv3 --pmc, from {TRAFFIC_FILE.name})"
            if traffic else ""))
 
+    # ---------------------------------------------------------------- this box's achieved peaks
+    peaks = measured_peaks(torch, xm, arena, int(round(roof_bytes)) // 16 * 16)
+
     # ---------------------------------------------------------------- decode batches 4 and 16, verify 4
     extra = {}
     for T in (4, 16):
@@ -500,15 +606,17 @@ def main():
         for c in range(pc):
             player(xp, zl, rp, op[c], arena=arena[c * E])
 
-    ms_p, _ = graph_time(torch, prefill_round, max(1, args.prefill_steps // pc))
-    ms_p /= pc
+    ms_p = best_of_means(torch, prefill_round, max(1, args.prefill_steps // pc)) / pc
     flops = 6.0 * Tp * k * H * F
     tf = flops / (ms_p * 1e-3) / 1e12
     log(f"prefill T={Tp}: {ms_p * 1e3:.1f} us/layer, {tf:.1f} TFLOP/s")
     prefill = dict(tokens=Tp, us_per_layer=round(ms_p * 1e3, 1), tflops=round(tf, 2),
-                   frac_mfma_peak=round(tf / BF16_PEAK_TFLOPS, 4), mfma="f16 operands, fp32 accumulate (dense peak "
+                   frac_mfma_peak=round(tf / BF16_PEAK_TFLOPS, 4),
+                   frac_measured_mfma=round(tf / peaks["mfma_f16_tflops"], 4), mfma="f16 operands, fp32 accumulate (dense peak "
                    "2.5 PFLOP/s, as bf16)", tokens_per_s=round(Tp / (ms_p * 1e-3), 0),
-                   flops_per_layer=flops, routing="Zipf alpha=1.2 (Gumbel-top-k)")
+                   flops_per_layer=flops, routing="Zipf alpha=1.2 (Gumbel-top-k)",
+                   timing=f"best of 5 means of {max(1, args.prefill_steps // pc)} graph replays of {pc} layers "
+                          "(two HBM copies of the weights)")
 
     others = {} if args.no_others else other_configs(torch, xm, dev, gen, max(64, args.steps // 4))
 
@@ -538,12 +646,15 @@ def main():
         "frac_hbm_peak": round(gbs1 / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm", "achieved": round(roof_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(roof_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "frac_measured_stream": round(roof_gbs / peaks["hbm_stream_gbs"], 4),
+                     "frac_measured_one_launch": round(roof_gbs / peaks["hbm_one_launch_gbs"], 4),
                      "traffic_source": f"{TRAFFIC_FILE.relative_to(ROOT)}: rocprofv3 --pmc FETCH_SIZE + WRITE_SIZE of "
                                        "the same rotation (bench.py --pmc-run), scaled by a copy kernel of known size; "
                                        "read from the committed summary, not measured in this run",
                      "kernel": "moe_decode_t1_kernel<Q4_K, Q6_K, 2, 2048, 768, 8> (xs_moe_layer_decode at one token, "
                                "one launch a layer)",
                      "algorithmic_bytes_per_launch": round(roof_bytes), "avg_launch_us": round(roof_us, 3)},
+        "measured_peaks": peaks,
         "decode_batches": extra,
         "prefill": prefill,
         "other_configs": others,

@@ -122,9 +122,11 @@ int xs_iq_mmq_quantize_scatter(const float* x, const int32_t* slot, void* xq, in
  * (include/strata/prefill/moe_mmq.hpp:57-75).  The products run on the f16 MFMA path of xs_moe_prefill_experts: the
  * int8 activations are taken as q * d rounded to f16, the weights dequantized to f16, fp32 accumulation (within 2e-2
  * of the fp32 product, the reference's int8 path within its own int8 rounding).  Types: Q8_0 (8), Q4_K (12), Q6_K
- * (14), IQ4_XS (23); w_cols a multiple of 256 (64 for Q8_0), w_rows of 256 (128 for Q6_K).  max_rows is not needed
- * (the tiles come from bounds on the device); rows (0: total_rows) bounds the tiles.  The library keeps a scratch
- * buffer a device (the f16 activations, the group table, the tile table), grown on demand outside graph capture. */
+ * (14), IQ4_XS (23); w_cols a multiple of 256 (64 for Q8_0), w_rows of 256 (128 for Q6_K).  max_rows and rows are
+ * not needed (every work-group finds its tile from bounds on the device; the grid covers all total_rows rows).  One
+ * launch; no allocation, no scratch and no synchronisation (the reference's contract, native_moe.hpp:18): the GEMM
+ * turns the int8 rows to f16 as it stages them, and reads each expert's weights through w or wtab itself.  Calls on
+ * different streams share nothing. */
 int xs_iq_mmq_grouped(int type, const void* w, size_t expert_bytes, int64_t w_rows, int64_t w_cols, int n,
                       const void* xq, int64_t total_rows, const int32_t* bounds, int64_t max_rows, const int32_t* ids,
                       float* dst, int64_t ld_dst, const uint8_t* const* wtab, size_t woff, int64_t rows, void* stream);
@@ -259,6 +261,12 @@ int32_t* xs_moe_layer_decode_status(void* workspace);
  * work-groups needed, and that call's output is not to be used).  Call it at the next synchronisation point after
  * a layer call (or a run of them).  Not to be called inside a graph capture.  No counterpart in the reference. */
 int xs_moe_status_check(int32_t* status, void* stream);
+/* The bound of the persistent layer's waits, in ticks of the device's wall clock (hipDeviceAttributeWallClockRate
+ * kHz), for calls made after it, process-wide; 0 restores the default (50 ms); a negative value makes every wait
+ * expire at once (no hand-over word is taken: the error path forced from the host - every work-group still ends
+ * normally, the status word reports bit 1 and the output is not to be used).  A test and diagnosis hook; no
+ * counterpart in the reference. */
+void xs_moe_set_wait_bound(long long ticks);
 
 /* xs_moe_layer_decode without a caller workspace, for callers that cannot allocate device memory (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc).  No counterpart in the reference.  The layer
@@ -273,6 +281,11 @@ int xs_moe_status_check(int32_t* status, void* stream);
 int xs_moe_layer_decode_noalloc(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_bytes, int n_expert,
                                 int k, const float* x, const float* logits, const float* residual, float* out,
                                 int n_tok, int32_t* status, void* stream);
+/* The current device's status word of that fixed scratch: where xs_moe_layer_decode_noalloc ORs its error bits when
+ * its status argument is NULL.  Read and clear it with xs_moe_status_check.  NULL (and the message set) when the
+ * device's array cannot be looked up.  The first call on a device must not be inside a graph capture.  No counterpart
+ * in the reference. */
+int32_t* xs_moe_layer_decode_noalloc_status(void);
 
 /* A shared expert over a decode / verify window: every token through one dense expert in the native format (blob:
  * [gate rows | up rows | down rows] of layout SL, 16-byte aligned), shared[t] = down(SwiGLU(gate x_t, up x_t)) on q8_1
@@ -338,6 +351,14 @@ int xs_moe_layer_prefill_ex(const xs_expert_layout_t* L, const uint8_t* arena, s
                             const float* w_gate, void* workspace, size_t workspace_bytes, void* stream);
 size_t xs_moe_layer_prefill_ex_workspace_bytes(const xs_expert_layout_t* L, int n_expert, int k, int n_tok,
                                                const xs_expert_layout_t* SL);
+
+/* Measuring kernels for the achieved peaks of the box (no counterpart in the reference; bench.py's roofline lines).
+ * xs_bench_hbm_read: reads `bytes` (16-byte aligned, a multiple of 16) at src once with `grid` work-groups of 256
+ * threads, nontemporal 16-byte loads; writes grid words to sink.  xs_bench_mfma_f16: `grid` work-groups of two waves,
+ * each wave `iters` x 8 back-to-back v_mfma_f32_32x32x16_f16 (32,768 flops each); writes nothing but keeps sink
+ * (grid x 128 floats) as its output.  Enqueued on `stream`. */
+int xs_bench_hbm_read(const void* src, size_t bytes, unsigned int* sink, int grid, void* stream);
+int xs_bench_mfma_f16(int iters, int grid, float* sink, void* stream);
 
 #ifdef __cplusplus
 }

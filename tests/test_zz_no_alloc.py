@@ -38,16 +38,37 @@ def test_noalloc_matches_workspace_entry(xm):
 
 def test_noalloc_refuses_past_its_scratch(xm):
     """Sizes past the fixed scratch fail with XS_EINVAL before any launch: too many entries for the array at config
-    5's expert shape, and a hidden size past the scratch's largest layout."""
+    5's expert shape, and a hidden size past the scratch's largest layout.  The arena is NULL, so a regression of the
+    size checks is still refused on the host (the layer's own arena check) and launches nothing."""
     L5 = xm.native_expert_layout(12, 12, 7168, 2048)
     x = torch.zeros(128, 7168, device=DEV)
     lg = torch.zeros(128, 256, device=DEV)
     out = torch.zeros_like(x)
     with pytest.raises(xm.XsError, match="past the fixed"):
-        xm.moe_layer_decode_noalloc(L5, torch.zeros(16, dtype=torch.uint8, device=DEV), 256, 8, x, lg, x, out,
-                                    blob_bytes=L5.bytes)
+        xm.moe_layer_decode_noalloc(L5, None, 256, 8, x, lg, x, out, blob_bytes=L5.bytes)
     L9 = xm.native_expert_layout(12, 12, 9216, 512)
     x9 = torch.zeros(1, 9216, device=DEV)
     with pytest.raises(xm.XsError, match="past the fixed scratch"):
-        xm.moe_layer_decode_noalloc(L9, torch.zeros(16, dtype=torch.uint8, device=DEV), 8, 2, x9, lg[:1, :8], x9,
-                                    x9.clone(), blob_bytes=L9.bytes)
+        xm.moe_layer_decode_noalloc(L9, None, 8, 2, x9, lg[:1, :8], x9, x9.clone(), blob_bytes=L9.bytes)
+
+
+def test_noalloc_status_word_without_caller_status(xm):
+    """With status=None the call ORs its bits into the fixed scratch's own status word, which
+    xs_moe_layer_decode_noalloc_status exposes: a token whose logits are all NaN (its router finds fewer than k
+    experts: bit 2, no output) is reported by noalloc_status_check, which then clears the word; a good call after it
+    leaves the word clear."""
+    arena, L = xm.build_arena(8, 1024, 512, 8, 8, seed=0)
+    xm.noalloc_status_check()   # clear whatever earlier calls left
+    x = torch.randn(1, 1024, device=DEV)
+    res = torch.randn(1, 1024, device=DEV)
+    out = torch.zeros_like(res)
+    bad = torch.full((1, 8), float("nan"), device=DEV)
+    print("[case] noalloc NaN logits, status=None", flush=True)
+    xm.moe_layer_decode_noalloc(L, arena, 8, 2, x, bad, res, out)
+    with pytest.raises(xm.XsError):
+        xm.noalloc_status_check()
+    xm.noalloc_status_check()   # cleared by the check above
+    good = torch.randn(1, 8, device=DEV)
+    xm.moe_layer_decode_noalloc(L, arena, 8, 2, x, good, res, out)
+    xm.noalloc_status_check()
+    assert torch.isfinite(out).all()

@@ -26,7 +26,7 @@ FLAGS = [
     "-Wall", "-Wno-unused-function", "-Wno-unused-variable", "-Wno-unused-but-set-variable",
 ]
 SOURCES = ["formats.hip", "quant_act.hip", "experts_decode.hip", "experts_stream.hip", "experts_prefill.hip", "router.hip", "dispatch.hip",
-           "combine.hip", "decode_layer.hip", "decode_fused.hip", "decode_t1.hip", "tiers.hip", "noalloc.hip", "mmq.hip", "gemv.hip",
+           "combine.hip", "decode_layer.hip", "decode_fused.hip", "decode_t1.hip", "tiers.hip", "noalloc.hip", "mmq.hip", "gemv.hip", "peaks.hip",
            "abi.cpp", "pack.cpp"]
 
 

@@ -2,12 +2,14 @@
 // thread's error message, and the launches.  Nothing here allocates device memory.
 #include "../../include/xs_moe.h"
 #include "xs_kernels.h"
+#include "xs_plan.h"
 
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <atomic>
 #include <mutex>
 #include <vector>
 #include <string>
@@ -44,8 +46,14 @@ bool overlap(const void* a, size_t an, const void* b, size_t bn) {
 }
 size_t up256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-// 50 ms of the device's wall clock: the bound of the fused decode layer's waits (each normally a few microseconds)
+// the bound of the persistent decode layers' waits (each normally a few microseconds): 50 ms of the device's wall
+// clock, or the ticks xs_moe_set_wait_bound set; 0 when it asked every wait to expire at once (the kernels then take
+// no hand-over word: a test of the expired-wait path forced from the host)
+std::atomic<long long> g_wait_bound{0};
 long long spin_ticks() {
+    const long long set = g_wait_bound.load(std::memory_order_relaxed);
+    if (set > 0) return set;
+    if (set < 0) return 0;
     int dev = 0, khz = 0;
     if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess ||
         khz <= 0)
@@ -82,9 +90,8 @@ int check_layout(const xs_expert_layout_t* L, const char* what) {
     return ok();
 }
 
-// plan layout for capx entries (reference src/kernels/xe/verify_kernels.cpp:860-866)
-long long plan_ptr_off(long long capx) { return ((4 + (capx + 1) + 2 * capx) + 1) & ~1ll; }
-size_t plan_words(long long capx) { return (size_t)(plan_ptr_off(capx) + 4 * capx + capx + 1 + 1); }
+// the plan's words for capx entries (xs_plan.h)
+size_t plan_words(long long capx) { return (size_t)xs::PlanWords{capx}.words(); }
 
 }  // namespace
 
@@ -429,11 +436,12 @@ int xs_project_bf16(const float* x, uint16_t* x_bf16, const uint16_t* w, float* 
 
 void xs_plan_offsets(long long capx, long long* start, long long* dst, long long* tok, long long* ptr,
                      long long* start2) {
-    if (start) *start = 4;
-    if (dst) *dst = 4 + capx + 1;
-    if (tok) *tok = 4 + capx + 1 + capx;
-    if (ptr) *ptr = plan_ptr_off(capx);
-    if (start2) *start2 = plan_ptr_off(capx) + 4 * capx;
+    const xs::PlanWords w{capx};
+    if (start) *start = w.start();
+    if (dst) *dst = w.dst();
+    if (tok) *tok = w.tok();
+    if (ptr) *ptr = w.ptr();
+    if (start2) *start2 = w.start2();
 }
 
 int xs_resident_plan(const int32_t* ids, int n_entries, int k, const int32_t* res_layer, int n_expert,
@@ -515,29 +523,19 @@ int prefill_experts(const xs_expert_layout_t* L, const float* x, int64_t n_tok, 
 }
 }  // namespace
 
-namespace {
-// The library's own scratch for xs_iq_mmq_grouped (whose reference signature has no workspace): one buffer a device,
-// grown on demand outside graph capture and kept until the process ends.
-struct MmqScratch {
-    void* ptr = nullptr;
-    size_t bytes = 0;
-};
-std::mutex g_mmq_mutex;
-MmqScratch g_mmq[64];
-}  // namespace
-
 int xs_iq_mmq_grouped(int type, const void* w, size_t expert_bytes, int64_t w_rows, int64_t w_cols, int n,
                       const void* xq, int64_t total_rows, const int32_t* bounds, int64_t max_rows, const int32_t* ids,
                       float* dst, int64_t ld_dst, const uint8_t* const* wtab, size_t woff, int64_t rows,
                       void* stream) {
-    (void)max_rows;   // the grid comes from the tile table, built on the device from bounds
+    (void)max_rows;   // the grid covers every row of xq; each work-group finds its tile from bounds on the device
+    (void)rows;
     if (n <= 0 || total_rows <= 0) return ok();
     if (type != 8 && type != 12 && type != 14 && type != 23)
         return fail(XS_EINVAL, "iq_mmq_grouped: ggml type %d (this build's products: Q8_0, Q4_K, Q6_K, IQ4_XS)",
                     type);
     const int64_t out_tile = type == 14 ? 128 : 256;   // output columns a work-group: 128, or 256 (two rows a lane)
     if (w_cols <= 0 || w_cols % (type == 8 ? 64 : 256) || w_rows <= 0 || w_rows % out_tile || n > 65535 ||
-        ld_dst < w_rows || ld_dst % 4)
+        ld_dst < w_rows || ld_dst % 4 || total_rows > INT32_MAX / 2)
         return fail(XS_EINVAL,
                     "iq_mmq_grouped: %lld x %lld weights (columns a multiple of %d, rows of %lld), %d experts, "
                     "%lld floats a dst row",
@@ -546,37 +544,8 @@ int xs_iq_mmq_grouped(int type, const void* w, size_t expert_bytes, int64_t w_ro
     if (!(wtab ? aligned(wtab, 8) : (w && aligned(w, 16) && expert_bytes % 16 == 0)) || !aligned(xq, 16) ||
         !aligned(bounds, 4) || !aligned(ids, 4) || !aligned(dst, 16))
         return fail(XS_EINVAL, "iq_mmq_grouped: a span is missing or misaligned");
-    const int64_t nrows = rows > 0 ? rows : total_rows;
-    const size_t xb_bytes = up256((size_t)total_rows * (size_t)w_cols * 2);
-    const size_t ptr_bytes = up256((size_t)n * 8 + 256);   // the group pointers, then n_groups and the status word
-    const size_t need = xb_bytes + ptr_bytes + up256((size_t)xs::tile_table_words(nrows, n) * 4);
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return fail(XS_EDEVICE, "iq_mmq_grouped: no device");
-    void* scratch = nullptr;
-    {
-        std::lock_guard<std::mutex> lock(g_mmq_mutex);
-        MmqScratch& m = g_mmq[dev];
-        if (m.bytes < need) {
-            hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-            if (hipStreamIsCapturing(S(stream), &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
-                return fail(XS_EINVAL, "iq_mmq_grouped: its scratch must grow (%zu bytes) outside graph capture", need);
-            if (m.ptr) {
-                (void)hipDeviceSynchronize();
-                (void)hipFree(m.ptr);
-                m.ptr = nullptr;
-                m.bytes = 0;
-            }
-            if (hipMalloc(&m.ptr, need) != hipSuccess) return fail(XS_EDEVICE, "iq_mmq_grouped: %zu bytes of scratch", need);
-            m.bytes = need;
-        }
-        scratch = m.ptr;
-    }
-    uint8_t* sp = (uint8_t*)scratch;
-    uint16_t* xb = (uint16_t*)sp;
-    unsigned long long* grp_ptr = (unsigned long long*)(sp + xb_bytes);
-    int32_t* n_groups = (int32_t*)(sp + xb_bytes + (size_t)n * 8);
-    int32_t* err = n_groups + 1;
-    int32_t* table = (int32_t*)(sp + xb_bytes + ptr_bytes);
+    // one launch and no scratch (the reference's contract: no allocation or sync): the GEMM reads the int8 rows and
+    // their scales itself, and takes each group's weights and tile from w / wtab and bounds
     xs::ExpertLayout L;
     L.gu_type = L.d_type = type;
     L.n_embd = w_rows;
@@ -586,26 +555,19 @@ int xs_iq_mmq_grouped(int type, const void* w, size_t expert_bytes, int64_t w_ro
     L.bytes = (int64_t)expert_bytes;
     xs::PrefillArgs a{};
     a.bounds = bounds;
-    a.n_groups = n_groups;
-    a.wptr = grp_ptr;
     a.entry = ids;
-    a.h = xb;
     a.parts = dst;
     a.parts_h = nullptr;
-    a.mtile = table;
-    a.mtile_ready = true;
-    a.err = err;
     a.n_tok = total_rows;
-    a.rows = nrows;
+    a.rows = total_rows;
     a.cap_groups = n;
     a.ld_parts = ld_dst;
-    if (int r = finish(stream, xs::launch_mmq_act_to_f16(xq, total_rows, w_cols, xb, S(stream)), "iq_mmq_grouped"))
-        return r;
-    if (int r = finish(stream, xs::launch_group_table((const uint8_t*)w, expert_bytes, wtab, woff, n, grp_ptr, n_groups,
-                                                      S(stream)),
-                       "iq_mmq_grouped"))
-        return r;
-    return finish(stream, xs::launch_grouped_product(L, a, S(stream)), "iq_mmq_grouped");
+    a.xq = (const int8_t*)xq;
+    a.wbase = (const uint8_t*)w;
+    a.wstride = expert_bytes;
+    a.wtab = wtab;
+    a.woff = woff;
+    return finish(stream, xs::launch_mmq_product(L, a, S(stream)), "iq_mmq_grouped");
 }
 
 int xs_moe_prefill_experts(const xs_expert_layout_t* L, const float* x, int64_t n_tok, const int32_t* src,
@@ -816,6 +778,8 @@ PrefillWs prefill_ws(const xs_expert_layout_t* L, int n_expert, int k, int n_tok
 int32_t* xs_moe_layer_decode_status(void* workspace) {
     return workspace ? (int32_t*)workspace : nullptr;
 }
+
+void xs_moe_set_wait_bound(long long ticks) { g_wait_bound.store(ticks, std::memory_order_relaxed); }
 
 int xs_moe_status_check(int32_t* status, void* stream) {
     if (!aligned(status, 4)) return fail(XS_EINVAL, "moe status check: the status word is missing or misaligned");

@@ -183,6 +183,7 @@ __device__ __forceinline__ void dma_to_lds(uint8_t* dst, int n16, Src src) {
 template <int N>
 __device__ __forceinline__ bool gather_tagged(const unsigned long long* p, int n, unsigned int tag, long long ticks,
                                               float (&v)[N]) {
+    if (ticks <= 0) return false;   // the host forces every wait to expire at once (a test of the error path)
     long long t0 = 0;
     for (int it = 0;; ++it) {
         unsigned long long w[N];
@@ -247,14 +248,18 @@ __device__ __forceinline__ unsigned long long load_counter(const FusedArgs& a) {
                                                 __HIP_MEMORY_SCOPE_AGENT)
                             : 0ull;
 }
-__device__ __forceinline__ int epoch_of(unsigned long long c) {   // lanes 0..15 (row 0) by DPP, read from lane 0
+// The call's tag from its counters (lanes 0..15, row 0, summed by DPP, read from lane 0): the epoch (the sum >> 20, the
+// calls before this one) mod 2^32 - 1, plus one.  Consecutive calls get different tags and no tag is 0, the value of a
+// word that was never written (a zeroed workspace), so a poller never takes an unwritten word for a stored one.
+__device__ __forceinline__ unsigned int call_tag(unsigned long long c) {
     static_assert(kCounters == 16, "one 16-lane row of counters");
     c += dpp_u64<kDppXor1, 0xF>(c);
     c += dpp_u64<kDppXor2, 0xF>(c);
     c += dpp_u64<kDppRor4, 0xF>(c);
     c += dpp_u64<kDppRor8, 0xF>(c);
     const unsigned int lo = __builtin_amdgcn_readlane((int)c, 0), hi = __builtin_amdgcn_readlane((int)(c >> 32), 0);
-    return (int)((((unsigned long long)hi << 32) | lo) >> 20);
+    const unsigned long long epoch = (((unsigned long long)hi << 32) | lo) >> 20;
+    return (unsigned int)(epoch % 0xFFFFFFFFull) + 1u;
 }
 
 template <int TG, int TD>
@@ -333,7 +338,6 @@ __global__ __launch_bounds__(fused_threads(NE, MODE)) void moe_decode_fused_kern
     int* s_ids = (int*)(lds + o.ids);
     float* s_w = (float*)(lds + o.w);
     int* s_excl = (int*)(lds + o.excl);
-    int* s_wave = (int*)(lds + o.wave);
     int* s_first = (int*)(lds + o.first);
     int* s_gexp = (int*)(lds + o.gexp);
     int* s_start = (int*)(lds + o.start);
@@ -387,8 +391,8 @@ __global__ __launch_bounds__(fused_threads(NE, MODE)) void moe_decode_fused_kern
     };
     route_tokens_wave<PER, kFusedSigmoid<TG, TD>, NT>(a, T, s_ids, s_w, ctr, load_x);   // PER = the experts a lane (64 PER >= E, chosen by the host)
     if (wave == 0) {
-        const int epoch = epoch_of(ctr);
-        if (lane == 0) s_misc[3] = epoch;
+        const unsigned int ctag = call_tag(ctr);
+        if (lane == 0) s_misc[3] = (int)ctag;
         if (T == 1) {   // one token: its k experts are distinct, each a group of one entry, in rank order
             const int ex = lane < k ? s_ids[lane] : 0;   // this lane's own rank (route_topk_wave_lv writes lane < k)
             if (__ballot(lane < k && (ex < 0 || ex >= E))) {
@@ -408,128 +412,31 @@ __global__ __launch_bounds__(fused_threads(NE, MODE)) void moe_decode_fused_kern
         }
     }
     __syncthreads();
-    // the plan: groups = distinct experts in order of first occurrence, a group's entries ascending
-    if (T == 1) {
-        // planned above
-    } else if (PIPED) {
-        // a bit an entry in its expert's mask (LDS past o.slab_gu: slabs and table are filled after the plan, and
-        // the region holds 2 slabs + the table, well over the E x W words); an entry's position in its group is the
-        // count of the mask's bits below its own, a group's size the mask's count, its leader the entry at position 0
-        const int W = (n + 31) >> 5;
-        uint32_t* s_mask = (uint32_t*)(lds + o.slab_gu);
-        for (int i = tid; i < E * W; i += NT) s_mask[i] = 0u;
-        __syncthreads();
+    // the plan: groups = distinct experts in order of first occurrence, a group's entries ascending (one token: planned
+    // above).  Wave 0 numbers the groups (plan_groups_wave, xs_route.h: the expert ids' LDS group numbers, 16 bits,
+    // over s_first; the entries' group | place over s_excl; the group sizes, then starts, in s_start); then every
+    // thread places its entry.
+    if (T > 1) {
         const int ex = tid < n ? s_ids[tid] : -1;
         if (__syncthreads_or(tid < n && (ex < 0 || ex >= E))) {
             if (tid == 0) s_misc[0] = -1;
         } else {
-            if (tid < n) atomicOr(&s_mask[ex * W + (tid >> 5)], 1u << (tid & 31));
-            __syncthreads();
-            int cnt = 0, pos = 0;
-            if (tid < n) {
-                const uint32_t* mk = s_mask + ex * W;
-                for (int w = 0; w < W; ++w) {
-                    const uint32_t b = mk[w];
-                    cnt += __popc(b);
-                    pos += w < (tid >> 5) ? __popc(b) : w == (tid >> 5) ? __popc(b & ((1u << (tid & 31)) - 1u)) : 0;
-                }
+            const PlanLds pl{(int16_t*)s_first, s_excl, s_start, s_gexp};
+            if (wave == 0) {
+                const int groups = plan_groups_wave(s_ids, n, E, pl);
+                if (lane == 0) s_misc[0] = groups;
             }
-            const bool leader = tid < n && pos == 0;
-            int total;
-            const int excl = block_exclusive_scan(leader ? ((cnt << 16) | 1) : 0, s_wave, &total);
-            if (tid < kFMaxN) s_excl[tid] = excl;
-            __syncthreads();
-            // the leader's scan value reaches the group's entries through s_first (the leader's entry, per expert)
-            if (leader) s_first[ex] = tid;
             __syncthreads();
             if (tid < n) {
-                const int le = s_excl[s_first[ex]];
-                const int g = le & 0xffff, gs = le >> 16;
-                s_dst[gs + pos] = tid;
-                s_tok[gs + pos] = tid / k;
-                if (leader) {
-                    s_gexp[g] = ex;
-                    s_start[g] = gs;
-                }
-            }
-            if (tid == 0) {
-                s_start[total & 0xffff] = n;
-                s_misc[0] = total & 0xffff;
-            }
-        }
-    } else if (n <= 64) {   // one wave: uniform v_readlane loops, no work-group scan
-        if (wave == 0) {
-            const int ex = lane < n ? s_ids[lane] : -1;
-            if (__ballot(lane < n && (ex < 0 || ex >= E)) == 0) {
-                // first = the lane of the expert's first entry, pos = earlier entries with the expert
-                int first = lane, pos = 0;
-                for (int j = 0; j < n; ++j) {
-                    const bool same = __builtin_amdgcn_readlane(ex, j) == ex;
-                    first = same && j < first ? j : first;
-                    pos += same && j < lane ? 1 : 0;
-                }
-                const bool leader = lane < n && pos == 0;
-                // group = leaders before mine; start = entries whose expert's first entry is before mine
-                const unsigned long long lead = __ballot(leader);
-                const int g = __popcll(lead & ((1ull << first) - 1ull));
-                int gs = 0;
-                for (int j = 0; j < n; ++j) gs += __builtin_amdgcn_readlane(first, j) < first ? 1 : 0;
-                const int ngr = __popcll(lead);
-                if (lane < n) {
-                    s_dst[gs + pos] = lane;
-                    s_tok[gs + pos] = lane / k;
-                    if (leader) {
-                        s_gexp[g] = ex;
-                        s_start[g] = gs;
-                    }
-                }
-                if (lane == 0) {
-                    s_start[ngr] = n;
-                    s_misc[0] = ngr;
-                }
-            } else if (lane == 0) {
-                s_misc[0] = -1;
-            }
-        }
-    } else {   // the work-group: leaders by LDS atomicMin, group numbers and starts by one exclusive scan
-        for (int e = tid; e < E; e += NT) s_first[e] = n;
-        __syncthreads();
-        const int ex = tid < n ? s_ids[tid] : -1;
-        if (__syncthreads_or(tid < n && (ex < 0 || ex >= E))) {
-            if (tid == 0) s_misc[0] = -1;
-        } else {
-            if (tid < n) atomicMin(&s_first[ex], tid);
-            __syncthreads();
-            int cnt = 0, pos = 0;
-            const bool leader = tid < n && s_first[ex] == tid;
-            if (tid < n)
-                for (int j = 0; j < n; ++j) {
-                    if (s_ids[j] != ex) continue;
-                    if (leader) ++cnt;
-                    if (j < tid) ++pos;
-                }
-            int total;
-            const int excl = block_exclusive_scan(leader ? ((cnt << 16) | 1) : 0, s_wave, &total);
-            if (tid < kFMaxN) s_excl[tid] = excl;   // (entries index it: tid < n <= kFMaxN)
-            __syncthreads();
-            if (tid < n) {
-                const int le = s_excl[s_first[ex]];
-                const int g = le & 0xffff, gs = le >> 16;
-                s_dst[gs + pos] = tid;
-                s_tok[gs + pos] = tid / k;
-                if (leader) {
-                    s_gexp[g] = ex;
-                    s_start[g] = gs;
-                }
-            }
-            if (tid == 0) {
-                s_start[total & 0xffff] = n;
-                s_misc[0] = total & 0xffff;
+                const int e = s_excl[tid];
+                const int slot = s_start[e & 0xffff] + (e >> 16);
+                s_dst[slot] = tid;
+                s_tok[slot] = tid / k;
             }
         }
     }
     if (T > 1) __syncthreads();
-    const unsigned int tag = (unsigned int)s_misc[3] + 1u;
+    const unsigned int tag = (unsigned int)s_misc[3];
     if (s_misc[0] < 0) {   // a rank left unwritten (NaN logits): no output this call
         if (tid == 0) atomicOr(a.err, 4);
         done_call(a, tag);
@@ -885,6 +792,10 @@ __global__ __launch_bounds__(fused_threads(NE, MODE)) void moe_decode_fused_kern
                             ok = ok && tag_ok(w[q], tag);
                             pv[q] = tag_val(w[q]);
                         }
+                    if (a.spin_ticks <= 0) {   // every wait forced to expire at once (the host's test of the path)
+                        good = false;
+                        break;
+                    }
                     if (ok) break;
                     if (it == 0) t0 = wall_clock64();
                     else if (wall_clock64() - t0 > a.spin_ticks) {

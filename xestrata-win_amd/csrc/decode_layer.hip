@@ -22,10 +22,8 @@ __global__ __launch_bounds__(kRouteThreads) void decode_route_kernel(const float
                                                                      int32_t* __restrict__ plan, long long capx,
                                                                      uint32_t* skip, const uint8_t* arena, long long blob,
                                                                      uint8_t* __restrict__ xq) {
-    extern __shared__ int s_first[];   // n_expert
-    __shared__ int s_ids[kRouteThreads];
-    __shared__ int s_excl[kRouteThreads];
-    __shared__ int s_wave[64];
+    extern __shared__ int16_t s_gid[];   // n_expert
+    __shared__ int s_ids[kRouteThreads], s_ent[kRouteThreads], s_gsz[kRouteThreads + 1], s_gexp[kRouteThreads];
     const int tid = threadIdx.x, wave = tid >> 6;
     if (blockIdx.x > 0) {
         // the activations: 8 values a lane, one scale a 256 (whole 1024-lane rounds, so every wave's groups are whole)
@@ -54,13 +52,14 @@ __global__ __launch_bounds__(kRouteThreads) void decode_route_kernel(const float
         }
         return;
     }
-    build_plan(s_ids, s_first, s_excl, s_wave, n, k, nullptr, n_expert, arena, nullptr, blob, plan, capx, skip, 1u);
+    write_decode_plan(s_ids, PlanLds{s_gid, s_ent, s_gsz, s_gexp}, n, k, n_expert, nullptr, arena, nullptr, blob, plan,
+                      capx, skip, 1u);
 }
 
 hipError_t launch_decode_route(const float* logits, const float* x, int n_tok, int n_expert, int k, int64_t n_embd,
                                int32_t* ids, float* weights, int32_t* plan, long long capx, uint32_t* skip,
                                const uint8_t* arena, long long blob, void* xq, hipStream_t s) {
-    const size_t lds = (size_t)n_expert * sizeof(int);
+    const size_t lds = ((size_t)n_expert * sizeof(int16_t) + 3) & ~(size_t)3;
     const int64_t rounds = ((int64_t)n_tok * n_embd / 8 + kRouteThreads - 1) / kRouteThreads;
     const dim3 g((unsigned)(1 + (rounds < 64 ? rounds : 64))), b(kRouteThreads);
 #define XS_ROUTE(PER)                                                                                                  \

@@ -178,13 +178,15 @@ __device__ __forceinline__ unsigned long long t1_load_counter(const FusedArgs& a
                                          __HIP_MEMORY_SCOPE_AGENT)
                      : 0ull;
 }
-__device__ __forceinline__ int t1_epoch(unsigned long long c) {
+// the call's tag, 1 .. 2^32 - 1 (decode_fused.hip's call_tag: the epoch mod 2^32 - 1, plus one; never 0)
+__device__ __forceinline__ unsigned int t1_tag(unsigned long long c) {
     c += dpp_u64<kDppXor1, 0xF>(c);
     c += dpp_u64<kDppXor2, 0xF>(c);
     c += dpp_u64<kDppRor4, 0xF>(c);
     c += dpp_u64<kDppRor8, 0xF>(c);
     const unsigned int lo = __builtin_amdgcn_readlane((int)c, 0), hi = __builtin_amdgcn_readlane((int)(c >> 32), 0);
-    return (int)((((unsigned long long)hi << 32) | lo) >> 20);
+    const unsigned long long epoch = (((unsigned long long)hi << 32) | lo) >> 20;
+    return (unsigned int)(epoch % 0xFFFFFFFFull) + 1u;
 }
 __device__ __forceinline__ void t1_done(const FusedArgs& a) {   // this work-group's share of the call's 2^20
     if (threadIdx.x != 0) return;
@@ -214,7 +216,7 @@ __global__ __launch_bounds__(kT1) void moe_decode_t1_kernel(FusedArgs a) {
     int* s_ids = (int*)(lds + o.ids);
     float* s_w = (float*)(lds + o.w);
     int* s_spec = (int*)(lds + o.spec);
-    int* s_misc = (int*)(lds + o.misc);   // [0] 0 good / -1 bad routing, [1] the epoch
+    int* s_misc = (int*)(lds + o.misc);   // [0] 0 good / -1 bad routing, [1] the call's tag
     float* s_gu = (float*)(lds + o.gu);   // gate outputs 0..31, then up outputs 0..31
     float* s_po = (float*)(lds + o.po);
     uint8_t* s_hq = lds + o.hq;
@@ -289,12 +291,12 @@ __global__ __launch_bounds__(kT1) void moe_decode_t1_kernel(FusedArgs a) {
             s_w[lane] = 0.0f;
         }
         route_topk_wave_lv<PER>(lv, E, k, s_ids, s_w);
-        const int ep = t1_epoch(ctr);
+        const unsigned int ep = t1_tag(ctr);
         const int ex = lane < k ? s_ids[lane] : 0;
         const bool bad = __ballot(lane < k && (ex < 0 || ex >= E)) != 0;
         if (lane == 0) {
             s_misc[0] = bad ? -1 : 0;
-            s_misc[1] = ep;
+            s_misc[1] = (int)ep;
         }
     } else if (spec_wave) {
         float lv[PER];
@@ -338,7 +340,7 @@ __global__ __launch_bounds__(kT1) void moe_decode_t1_kernel(FusedArgs a) {
         t1_done(a);
         return;
     }
-    const unsigned int tag = (unsigned int)s_misc[1] + 1u;
+    const unsigned int tag = (unsigned int)s_misc[1];
     bool same = true;
     for (int i = 0; i < k; ++i) same = same && s_spec[i] == s_ids[i];
     if (!same && spec_wave) {   // the speculation missed: drain what it fetched, fetch the exact experts' rows
@@ -482,10 +484,11 @@ __global__ __launch_bounds__(kT1) void moe_decode_t1_kernel(FusedArgs a) {
                     for (int i = 0; i < kHWords; ++i) ok = ok && (unsigned int)(v[i] >> 32) == tag;
                     return ok;
                 };
+                // (spin_ticks <= 0: the host forces every wait to expire at once - a test of the error path)
                 poll(w);
-                bool good = tagged(w);
+                bool good = a.spin_ticks > 0 && tagged(w);
                 const long long t0 = wall_clock64();
-                for (int it = 1; !good; ++it) {
+                for (int it = 1; !good && a.spin_ticks > 0; ++it) {
                     const unsigned long long wd = t1_ld_tag(src + 8);
                     if ((unsigned int)(wd >> 32) == tag) {
                         poll(w);

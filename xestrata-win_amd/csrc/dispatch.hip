@@ -1,10 +1,9 @@
 // xestrata-win_amd/csrc/dispatch.hip - token-to-expert dispatch on the device.
 //
-//  * resident_plan: the decode / verify-window plan in the reference's host-pool layout (reference
-//    src/kernels/xe/verify_kernels.cpp:819-890; layout include/strata/core/expert_source.hpp:219-243): groups are the
-//    distinct experts in order of first occurrence, a group's entries ascending.  A leader (an expert's first entry)
-//    is found with an LDS atomicMin, groups are numbered by one work-group exclusive scan of (entries << 16 | 1) over
-//    the leaders, and an entry's place in its group is the count of earlier entries with its expert.
+//  * resident_plan: the decode / verify-window plan in the engine's plan words (xs_plan.h; reference
+//    src/kernels/xe/verify_kernels.cpp:819-890): groups are the distinct experts in order of first occurrence, a
+//    group's entries ascending.  One wave walks the entries in order and numbers the groups as their experts first
+//    appear (plan_groups_wave, xs_route.h); then every thread places its entry.
 //  * prefill_route: the prompt path's permutation (reference src/prefill/plain_prompt.cpp:576-637, there on the
 //    host after a blocking copy): histogram, experts ascending, exclusive prefix, and a STABLE fill.  Here one
 //    work-group of 16 waves: each wave counts its own contiguous segment of entries into its own LDS histogram, the
@@ -25,10 +24,8 @@ __global__ __launch_bounds__(kPlanThreads) void resident_plan_kernel(const int32
                                                                      const unsigned long long* __restrict__ slot_off,
                                                                      long long blob, int32_t* __restrict__ pl,
                                                                      long long capx, uint32_t* skip, uint32_t ring) {
-    extern __shared__ int s_first[];   // n_expert
-    __shared__ int s_ids[kPlanThreads];
-    __shared__ int s_excl[kPlanThreads];
-    __shared__ int s_wave[64];
+    extern __shared__ int16_t s_gid[];   // n_expert
+    __shared__ int s_ids[kPlanThreads], s_ent[kPlanThreads], s_gsz[kPlanThreads + 1], s_gexp[kPlanThreads];
     const int t = threadIdx.x;
     bool bad = false;
     if (t < n) {
@@ -40,7 +37,8 @@ __global__ __launch_bounds__(kPlanThreads) void resident_plan_kernel(const int32
         if (t == 0) *skip = 0u;
         return;
     }
-    build_plan(s_ids, s_first, s_excl, s_wave, n, k, res, n_expert, cache_base, slot_off, blob, pl, capx, skip, ring);
+    write_decode_plan(s_ids, PlanLds{s_gid, s_ent, s_gsz, s_gexp}, n, k, n_expert, res, cache_base, slot_off, blob, pl,
+                      capx, skip, ring);
 }
 
 constexpr int kRouteWaves = 16;
@@ -302,7 +300,7 @@ size_t prefill_route_split_scratch(int64_t n, int n_expert) {
 hipError_t launch_resident_plan(const int32_t* ids, int n, int k, const int32_t* res, int n_expert,
                                 const uint8_t* cache_base, const unsigned long long* slot_off, long long blob,
                                 int32_t* plan, long long capx, uint32_t* skip, uint32_t ring, hipStream_t s) {
-    const size_t lds = (size_t)n_expert * sizeof(int);
+    const size_t lds = ((size_t)n_expert * sizeof(int16_t) + 3) & ~(size_t)3;
     hipLaunchKernelGGL(resident_plan_kernel, dim3(1), dim3(kPlanThreads), lds, s, ids, n, k, res, n_expert, cache_base,
                        slot_off, blob, plan, capx, skip, ring);
     return hipGetLastError();

@@ -143,6 +143,50 @@ __device__ __forceinline__ uint2 ldg8(const void* p) {
 __device__ __forceinline__ uint32_t ldg_u16(const void* p) {
     return *(const __attribute__((address_space(1))) uint16_t*)p;
 }
+__device__ __forceinline__ uint32_t ldg_u32(const void* p) {
+    return *(const __attribute__((address_space(1))) uint32_t*)p;
+}
+
+// The standalone product's m-tile mt: the groups' tiles one after another, ceil(rows / bm) a group, groups ascending,
+// found from the bounds alone (no table, no scratch).  Every wave walks the groups 256 at a time - each lane's bounds
+// loads for four chunks of 64 in flight together - and scans each chunk's tile counts; the chunk that holds tile mt
+// names its group by a ballot.  Rows past total_rows are cut off.  False when mt is past the last tile.
+__device__ bool walk_tiles(const int32_t* __restrict__ bounds, int n, int64_t total_rows, int bm, int mt, int& g,
+                           int& nrows, int& r0) {
+    const int lane = threadIdx.x & 63;
+    int carry = 0;
+    for (int g0 = 0; g0 < n; g0 += 256) {
+        int lo[4], hi[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int gg = g0 + 64 * u + lane;
+            lo[u] = gg < n ? bounds[gg] : 0;
+            hi[u] = gg < n ? bounds[gg + 1] : 0;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int top = (int)min((int64_t)hi[u], total_rows);
+            const int cnt = top > lo[u] ? (top - lo[u] + bm - 1) / bm : 0;
+            int inc = cnt;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const int y = __shfl_up(inc, o, 64);
+                if (lane >= o) inc += y;
+            }
+            const int total = __shfl(inc, 63, 64);
+            if (mt < carry + total) {
+                const int l = __ffsll((long long)__ballot(carry + inc > mt)) - 1;
+                const int first = __shfl(carry + inc - cnt, l, 64);
+                g = g0 + 64 * u + l;
+                r0 = __shfl(lo[u], l, 64) + (mt - first) * bm;
+                nrows = min(bm, __shfl(top, l, 64) - r0);
+                return true;
+            }
+            carry += total;
+        }
+    }
+    return false;
+}
 
 __device__ __forceinline__ void vm_drain() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 // A work-group barrier over LDS only: the wave's LDS operations are complete, its global loads may still be in flight.
@@ -330,7 +374,7 @@ __device__ __forceinline__ void dma_rows(const uint8_t* const* src, size_t off, 
                                          0);
 }
 
-template <bool DOWN, int T, int RT>
+template <bool DOWN, int T, int RT, bool MMQ = false>
 __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, PrefillArgs a,
                                                               const int32_t* __restrict__ mtile, int mt_bound,
                                                               int n_tiles) {
@@ -354,12 +398,19 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
         nt = c8 % n_tiles;
     }
     if (mt >= mt_bound) return;
-    const int ng = *a.n_groups;
-    const int nfull = mtile[kBM == 128 ? 0 : 2], npart = mtile[kBM == 128 ? 1 : 3];
-    if (ng <= 0 || mt >= nfull + npart) return;
-    const int64_t te = mt < nfull ? mt : mt_bound - 1 - (mt - nfull);   // the tile's entry (tile_list)
-    const int32_t* tl = tile_list(const_cast<int32_t*>(mtile), a.rows, a.cap_groups, kBM) + 2 * te;
-    const int g = tl[0] & 0xFFFF, nrows = tl[0] >> 16, r0 = tl[1];
+    int g, nrows, r0;
+    if constexpr (MMQ) {
+        if (!walk_tiles(a.bounds, (int)a.cap_groups, a.n_tok, kBM, mt, g, nrows, r0)) return;
+    } else {
+        const int ng = *a.n_groups;
+        const int nfull = mtile[kBM == 128 ? 0 : 2], npart = mtile[kBM == 128 ? 1 : 3];
+        if (ng <= 0 || mt >= nfull + npart) return;
+        const int64_t te = mt < nfull ? mt : mt_bound - 1 - (mt - nfull);   // the tile's entry (tile_list)
+        const int32_t* tl = tile_list(const_cast<int32_t*>(mtile), a.rows, a.cap_groups, kBM) + 2 * te;
+        g = tl[0] & 0xFFFF;
+        nrows = tl[0] >> 16;
+        r0 = tl[1];
+    }
     const int nrt = (nrows + 31) >> 5;   // live 32-row tiles
     const int H = (int)L.n_embd, F = (int)L.n_ff;
     const int K = DOWN ? F : H;
@@ -371,14 +422,45 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
     // A by DMA: wave w fills rows [8 RT w, 8 RT (w + 1)) of the tile, 8 rows an instruction; lane l of instruction i
     // holds LDS slot swz(R, l & 7) of row R = 8 RT w + 8 i + l / 8, i.e. chunk (l & 7) ^ (R & 7) of that row (rows
     // past the group's end read its first row)
+    // (MMQ: the chunk's 8 int8 codes - values 8 perm8(c) .. + 8 of the step - and their block's scale instead)
     const uint8_t* asrc[RT];
+    const uint8_t* adsc[RT];
 #pragma unroll
     for (int i = 0; i < RT; ++i) {
         const int R = 8 * RT * wave + 8 * i + (lane >> 3);
         const int rr = R < nrows ? R : 0;
         const int c = (lane & 7) ^ (R & 7);
-        asrc[i] = (const uint8_t*)(DOWN ? a.h + (int64_t)(r0 + rr) * F : a.xb + (int64_t)a.src[r0 + rr] * H) + 16 * c;
+        if constexpr (MMQ) {
+            asrc[i] = (const uint8_t*)(a.xq + (int64_t)(r0 + rr) * K) + 8 * perm8(c);
+            adsc[i] = (const uint8_t*)((const float*)(a.xq + a.n_tok * K) + (int64_t)(r0 + rr) * (K / 32) + perm8(c) / 4);
+        } else {
+            asrc[i] = (const uint8_t*)(DOWN ? a.h + (int64_t)(r0 + rr) * F : a.xb + (int64_t)a.src[r0 + rr] * H) +
+                      16 * c;
+            adsc[i] = nullptr;
+        }
     }
+    // a chunk of A step ks as loaded (f16, or MMQ's codes and scale), and as written to LDS (f16: the codes times the
+    // scale rounded to f16, saturated, in the slot order - the bits of a saturated f16 copy of xq)
+    auto a_load = [&](int i, int ks) -> uint4 {
+        if constexpr (MMQ) {
+            const uint2 q = ldg8(asrc[i] + (size_t)ks * 64);
+            return make_uint4(q.x, q.y, ldg_u32(adsc[i] + (size_t)ks * 8), 0u);
+        } else {
+            return ldg16(asrc[i] + (size_t)ks * 128);
+        }
+    };
+    auto a_f16 = [&](const uint4& r) -> uint4 {
+        if constexpr (MMQ) {
+            const float d = __uint_as_float(r.z);
+            float v[8];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) v[t] = (float)(int8_t)(((t < 4 ? r.x : r.y) >> (8 * (t & 3))) & 0xFFu) * d;
+            return make_uint4(sat_f16x2(v[0], v[2]), sat_f16x2(v[1], v[3]), sat_f16x2(v[4], v[6]),
+                              sat_f16x2(v[5], v[7]));
+        } else {
+            return r;
+        }
+    };
     // down: the routing entry of each row, staged in LDS for the epilogue (visible after the first step's barrier)
     int32_t* const s_entry = (int32_t*)(lds + entry_offset(kBM));
     if (DOWN && tid < nrows) s_entry[tid] = a.entry[r0 + tid];
@@ -395,7 +477,10 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
     for (int j = 0; j < J; ++j) {
         const int col = cb[j] + (lane & 31);
         const int wrow = DOWN ? n0 + col : (col < kBN / 2 ? n0 + col : F + n0 + (col - kBN / 2));
-        brow[j] = (const uint8_t*)a.wptr[g] + (DOWN ? L.down_off : 0) + (int64_t)wrow * wrb;
+        const uint8_t* wb;
+        if constexpr (MMQ) wb = a.wtab ? a.wtab[g] + a.woff : a.wbase + (size_t)g * a.wstride;
+        else wb = (const uint8_t*)a.wptr[g];
+        brow[j] = wb + (DOWN ? L.down_off : 0) + (int64_t)wrow * wrb;
     }
 
     f32x16_t acc[RT][J];
@@ -437,12 +522,12 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
             uint4 areg[RT];
             auto load_a = [&](int ks) {
 #pragma unroll
-                for (int i = 0; i < RT; ++i) areg[i] = ldg16(asrc[i] + (size_t)ks * 128);
+                for (int i = 0; i < RT; ++i) areg[i] = a_load(i, ks);
             };
             auto store_a = [&](int buf) {
                 uint8_t* dst = lds + buf * (kBM * 128) + wave * 8 * RT * 128 + 16 * lane;
 #pragma unroll
-                for (int i = 0; i < RT; ++i) *(uint4*)(dst + i * 1024) = areg[i];
+                for (int i = 0; i < RT; ++i) *(uint4*)(dst + i * 1024) = a_f16(areg[i]);
             };
             const int nb = K / 256;
             uint4 hdr[J], q[2][J];   // header of the block; the qs run of steps (even, odd)
@@ -492,12 +577,12 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
             uint4 areg[2][RT];   // A(ks) staging, slot ks & 1
             auto load_a = [&](int ks, int slot) {
 #pragma unroll
-                for (int i = 0; i < RT; ++i) areg[slot][i] = ldg16(asrc[i] + (size_t)ks * 128);
+                for (int i = 0; i < RT; ++i) areg[slot][i] = a_load(i, ks);
             };
             auto store_a = [&](int slot, int buf) {
                 uint8_t* dst = lds + buf * (kBM * 128) + wave * 8 * RT * 128 + 16 * lane;
 #pragma unroll
-                for (int i = 0; i < RT; ++i) *(uint4*)(dst + i * 1024) = areg[slot][i];
+                for (int i = 0; i < RT; ++i) *(uint4*)(dst + i * 1024) = a_f16(areg[slot][i]);
             };
             auto q6loop = [&](auto nbc) {
                 constexpr int NBC = decltype(nbc)::value;
@@ -546,12 +631,12 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
             uint4 areg[RT];
             auto load_a = [&](int ks) {
 #pragma unroll
-                for (int i = 0; i < RT; ++i) areg[i] = ldg16(asrc[i] + (size_t)ks * 128);
+                for (int i = 0; i < RT; ++i) areg[i] = a_load(i, ks);
             };
             auto store_a = [&](int buf) {
                 uint8_t* dst = lds + buf * (kBM * 128) + wave * 8 * RT * 128 + 16 * lane;
 #pragma unroll
-                for (int i = 0; i < RT; ++i) *(uint4*)(dst + i * 1024) = areg[i];
+                for (int i = 0; i < RT; ++i) *(uint4*)(dst + i * 1024) = a_f16(areg[i]);
             };
             uint4 qv[2][2][J];       // codes of (step parity, block of the step, row)
             uint32_t dv[2][2][J];    // their blocks' scales (f16 bits)
@@ -588,6 +673,24 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
             for (int ks = 0; ks < nk; ks += 2) {   // nk is even (K % 128 == 0 for this instance)
                 q8_step(ks, IntC<0>{});
                 q8_step(ks + 1, IntC<1>{});
+            }
+        } else if constexpr (MMQ) {
+            // other formats over MMQ rows: each step's A chunks loaded, converted and written to LDS, then its products
+            for (int ks = 0; ks < nk; ++ks) {
+                uint4 r[RT];
+#pragma unroll
+                for (int i = 0; i < RT; ++i) r[i] = a_load(i, ks);
+                uint8_t* dst = lds + (ks & 1) * (kBM * 128) + wave * 8 * RT * 128 + 16 * lane;
+#pragma unroll
+                for (int i = 0; i < RT; ++i) *(uint4*)(dst + i * 1024) = a_f16(r[i]);
+                lds_sync();
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk) {
+                    f16x8_t fb[J];
+#pragma unroll
+                    for (int j = 0; j < J; ++j) fb[j] = generic_frag(brow[j], wtype, ks * kBK, kk, hf);
+                    mfma_step(ks, kk, fb);
+                }
             }
         } else {
             dma_a(0, 0);
@@ -664,67 +767,28 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
     }
 }
 
-template <bool DOWN>
+template <bool DOWN, bool MMQ = false>
 static hipError_t launch_gemm(const ExpertLayout& L, const PrefillArgs& a, hipStream_t s) {
     const int t = DOWN ? L.d_type : L.gu_type;
     const int n_tiles = DOWN ? (int)(L.n_embd / (128 * lane_rows(DOWN, t))) : (int)(L.n_ff / (kBN / 2));
     const bool q8_fast = (DOWN ? L.n_ff : L.n_embd) % 128 == 0;   // Q8_0's own path takes its K steps in pairs
     const int bm = 32 * row_tiles(DOWN, q8_fast ? t : (t == kQ8_0 ? 0 : t));
-    const int mt_bound = (int)((a.rows + bm - 1) / bm + a.cap_groups);
+    // tiles: at most ceil(rows / bm) + one partial tile a group (the standalone product counts every row of xq)
+    const int64_t rows = MMQ ? a.n_tok : a.rows;
+    const int mt_bound = (int)((rows + bm - 1) / bm + a.cap_groups);
     const unsigned grid = (unsigned)(n_tiles % 8 == 0 ? mt_bound * n_tiles : 8 * ((mt_bound + 7) / 8) * n_tiles);
     const size_t lds = (size_t)entry_offset(bm) + (DOWN ? (size_t)bm * 4 : 0);
     void (*k)(ExpertLayout, PrefillArgs, const int32_t*, int, int) =
-        t == kQ4_K   ? grouped_mfma_kernel<DOWN, kQ4_K, row_tiles(DOWN, kQ4_K)>
-        : t == kQ6_K ? grouped_mfma_kernel<DOWN, kQ6_K, row_tiles(DOWN, kQ6_K)>
-        : t == kQ8_0 && q8_fast ? grouped_mfma_kernel<DOWN, kQ8_0, row_tiles(DOWN, kQ8_0)>
-                     : grouped_mfma_kernel<DOWN, 0, row_tiles(DOWN, 0)>;
+        t == kQ4_K   ? grouped_mfma_kernel<DOWN, kQ4_K, row_tiles(DOWN, kQ4_K), MMQ>
+        : t == kQ6_K ? grouped_mfma_kernel<DOWN, kQ6_K, row_tiles(DOWN, kQ6_K), MMQ>
+        : t == kQ8_0 && q8_fast ? grouped_mfma_kernel<DOWN, kQ8_0, row_tiles(DOWN, kQ8_0), MMQ>
+                     : grouped_mfma_kernel<DOWN, 0, row_tiles(DOWN, 0), MMQ>;
     hipLaunchKernelGGL(k, dim3(grid), dim3(256), lds, s, L, a, a.mtile, mt_bound, n_tiles);
     return hipGetLastError();
 }
 
-// xq's int8 codes times their block scales, rounded to f16 (saturated) in the GEMM's K order: thread i writes chunk
-// i (8 values) of the [rows, cols] activations, as to_f16_kernel does for fp32 rows
-__global__ __launch_bounds__(256) void mmq_act_to_f16_kernel(const int8_t* __restrict__ q, const float* __restrict__ d,
-                                                             uint16_t* __restrict__ y, int64_t n_chunks, int64_t cols) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n_chunks) return;
-    const int64_t j = (i & ~(int64_t)7) * 8 + 8 * perm8((int)(i & 7));   // the chunk's first value (8 share a block)
-    const float dj = d[(j / cols) * (cols / 32) + (j % cols) / 32];
-    const uint2 w = *(const uint2*)(q + j);
-    float v[8];
-#pragma unroll
-    for (int t = 0; t < 8; ++t) v[t] = (float)(int8_t)(((t < 4 ? w.x : w.y) >> (8 * (t & 3))) & 0xFFu) * dj;
-    *(uint4*)(y + 8 * i) = make_uint4(sat_f16x2(v[0], v[2]), sat_f16x2(v[1], v[3]), sat_f16x2(v[4], v[6]),
-                                      sat_f16x2(v[5], v[7]));
-}
-
-__global__ __launch_bounds__(256) void group_table_kernel(const uint8_t* w, size_t expert_bytes,
-                                                          const uint8_t* const* wtab, size_t woff, int n,
-                                                          unsigned long long* __restrict__ grp_ptr,
-                                                          int32_t* __restrict__ n_groups) {
-    for (int g = threadIdx.x; g < n; g += blockDim.x)
-        grp_ptr[g] = (unsigned long long)(uintptr_t)(wtab ? wtab[g] + woff : w + (size_t)g * expert_bytes);
-    if (threadIdx.x == 0) *n_groups = n;
-}
-
-hipError_t launch_mmq_act_to_f16(const void* xq, int64_t rows, int64_t cols, uint16_t* xb, hipStream_t s) {
-    const int64_t nc = rows * cols / 8;
-    hipLaunchKernelGGL(mmq_act_to_f16_kernel, dim3((unsigned)((nc + 255) / 256)), dim3(256), 0, s, (const int8_t*)xq,
-                       (const float*)((const int8_t*)xq + rows * cols), xb, nc, cols);
-    return hipGetLastError();
-}
-
-hipError_t launch_group_table(const uint8_t* w, size_t expert_bytes, const uint8_t* const* wtab, size_t woff, int n,
-                              unsigned long long* grp_ptr, int32_t* n_groups, hipStream_t s) {
-    hipLaunchKernelGGL(group_table_kernel, dim3(1), dim3(256), 0, s, w, expert_bytes, wtab, woff, n, grp_ptr,
-                       n_groups);
-    return hipGetLastError();
-}
-
-hipError_t launch_grouped_product(const ExpertLayout& L, const PrefillArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL(tile_map_kernel, dim3(1), dim3(1024), 0, s, a.bounds, a.n_groups, a.mtile, a.rows,
-                       (int)a.cap_groups);
-    return launch_gemm<true>(L, a, s);
+hipError_t launch_mmq_product(const ExpertLayout& L, const PrefillArgs& a, hipStream_t s) {
+    return launch_gemm<true, true>(L, a, s);
 }
 
 hipError_t launch_prefill_experts(const ExpertLayout& L, const PrefillArgs& a, hipStream_t s) {

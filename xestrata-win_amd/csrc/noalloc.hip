@@ -86,4 +86,11 @@ int xs_moe_layer_decode_noalloc(const xs_expert_layout_t* L, const uint8_t* aren
                                   kScratchBytes, status, stream);
 }
 
+// the fixed scratch's own status word (its first int32, where calls with status == NULL OR their bits): this device's
+int32_t* xs_moe_layer_decode_noalloc_status(void) {
+    void* ptr = nullptr;
+    if (scratch_address(&ptr)) return nullptr;
+    return (int32_t*)ptr;
+}
+
 }  // extern "C"

@@ -184,16 +184,20 @@ struct PrefillArgs {
     int32_t* err;
     int64_t n_tok, rows, cap_groups;
     int64_t ld_parts;               // values between the rows of parts / parts_h (n_embd for the layer's own)
+    // the standalone product (launch_mmq_product): no scratch.  A rows are the int8 MMQ activations ([rows][K] codes,
+    // then a float scale a 32), turned to f16 as they are staged; group g's weights at wtab[g] + woff, or at wbase +
+    // g * wstride; each work-group finds its m-tile from bounds (cap_groups groups)
+    const int8_t* xq;
+    const uint8_t* wbase;
+    size_t wstride;
+    const uint8_t* const* wtab;
+    size_t woff;
 };
 hipError_t launch_prefill_experts(const ExpertLayout& L, const PrefillArgs& a, hipStream_t s);
-// The grouped product alone (the reference's iq_mmq_grouped): the int8 MMQ activations xq ([rows][cols] codes, then a
-// float scale a 32) to f16 in the GEMM's K order; each group's weights at w + g * expert_bytes or wtab[g] + woff into
-// grp_ptr (and n into *n_groups); then a.h ([rows, n_ff] f16) times every group's [n_embd, n_ff] matrix into
-// a.parts[a.entry[row] * a.ld_parts + ...] (the down product's tiles: L.d_type, L.d_row).
-hipError_t launch_mmq_act_to_f16(const void* xq, int64_t rows, int64_t cols, uint16_t* xb, hipStream_t s);
-hipError_t launch_group_table(const uint8_t* w, size_t expert_bytes, const uint8_t* const* wtab, size_t woff, int n,
-                              unsigned long long* grp_ptr, int32_t* n_groups, hipStream_t s);
-hipError_t launch_grouped_product(const ExpertLayout& L, const PrefillArgs& a, hipStream_t s);
+// The grouped product alone (the reference's iq_mmq_grouped), one launch and no scratch: the int8 MMQ activations
+// a.xq times every group's [n_embd, n_ff] matrix (the down product's tiles: L.d_type, L.d_row) into
+// a.parts[a.entry[row] * a.ld_parts + ...] in fp32.
+hipError_t launch_mmq_product(const ExpertLayout& L, const PrefillArgs& a, hipStream_t s);
 
 // The m-tile table of a prompt batch: words 0, 1 the counts of full and of partial tiles of the 128-row map, words
 // 2, 3 the same of the 64-row map, then each map's list of tile_cap entries {group | rows << 16, first row}: the full

@@ -3,6 +3,7 @@
 #pragma once
 
 #include "xs_device.h"
+#include "xs_plan.h"
 
 namespace xs {
 
@@ -230,65 +231,125 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* s_wave, int* tot
     return r;
 }
 
-// The decode plan in the reference's host-pool layout (src/kernels/xe/verify_kernels.cpp:819-890; layout
-// include/strata/core/expert_source.hpp:219-243): groups are the distinct experts in order of first occurrence, a
-// group's entries ascending.  A leader (an expert's first entry) is found with an LDS atomicMin, groups are numbered
-// by one work-group exclusive scan of (entries << 16 | 1) over the leaders, and an entry's place in its group is the
-// count of earlier entries with its expert.  s_ids[0..n) hold the ids (validated by the caller); s_first has n_expert
-// ints; every thread of the work-group calls this (n <= blockDim.x).  Returns nothing; *skip = ring at the end.
-__device__ __forceinline__ void build_plan(const int* s_ids, int* s_first, int* s_excl, int* s_wave, int n, int k,
-                                           const int32_t* __restrict__ res, int n_expert, const uint8_t* cache_base,
-                                           const unsigned long long* __restrict__ slot_off, long long blob,
-                                           int32_t* __restrict__ pl, long long capx, uint32_t* skip, uint32_t ring) {
+// ---------------------------------------------------------------- the decode plan
+// Groups are the distinct experts in order of first occurrence and a group's entries ascend: the order the engine's
+// plan consumers expect (reference src/kernels/xe/verify_kernels.cpp:819-890, the host pool's plan
+// src/core/expert_source.cpp:2193-2344).  Built by ONE wave that walks the entries in order, 64 at a time, with each
+// expert's group number kept in LDS (-1 until its first entry):
+//  * the lanes holding one expert inside a step find each other by a ballot match over the expert's bits; the lowest
+//    of them (the step's head for that expert) acts for all;
+//  * a head whose expert has no group yet opens one, numbered after the groups already open and the heads below it
+//    that open one too (a popcount of the opening ballot): groups come out in first-occurrence order;
+//  * an entry's place in its group is the group's size before the step plus its rank among its expert's lanes; the
+//    head then adds the step's count to the size.
+// The wave then turns the sizes into starts (a 64-group inclusive sum, carried from chunk to chunk).  No atomics and
+// no work-group scan: 1024 entries are 16 steps of a few ballots.  The caller places the entries afterwards:
+// slot = start[group] + place.
+struct PlanLds {
+    int16_t* gid;    // [n_expert]: the expert's group, -1 before its first entry
+    int32_t* ent;    // [n]: the entry's group | its place in the group << 16
+    int32_t* gsz;    // [n + 1]: a group's size, then its first slot; [groups] = n
+    int32_t* gexp;   // [n]: the group's expert
+};
+
+// Every lane of one wave calls it, with s_ids[0..n) valid ids below n_expert (n <= 32768).  Returns the group count.
+__device__ int plan_groups_wave(const int* s_ids, int n, int n_expert, const PlanLds& p) {
+    const int lane = threadIdx.x & 63;
+    for (int e = lane; e < n_expert; e += 64) p.gid[e] = -1;
+    int nbits = 1;
+    while ((1 << nbits) < n_expert) ++nbits;
+    const uint64_t below = lane ? ~0ull >> (64 - lane) : 0ull;
+    int groups = 0;
+    for (int s = 0; s < n; s += 64) {
+        const int i = s + lane;
+        const bool in = i < n;
+        const int ex = in ? s_ids[i] : 0;
+        uint64_t same = __ballot(in);
+        for (int b = 0; b < nbits; ++b) {
+            const bool bit = (ex >> b) & 1;
+            const uint64_t m = __ballot(bit);
+            same &= bit ? m : ~m;
+        }
+        const int rank = __popcll(same & below);
+        const bool head = in && rank == 0;
+        const int prev = head ? (int)p.gid[ex] : -1;
+        const bool opens = head && prev < 0;
+        const uint64_t opening = __ballot(opens);
+        const int g = opens ? groups + __popcll(opening & below) : prev;
+        const int size0 = head && !opens ? p.gsz[g] : 0;
+        const int hl = in ? __ffsll((long long)same) - 1 : lane;
+        const int eg = __shfl(g, hl, 64), es = __shfl(size0, hl, 64);
+        if (in) p.ent[i] = eg | (es + rank) << 16;
+        if (head) {
+            p.gsz[g] = size0 + __popcll(same);
+            if (opens) {
+                p.gid[ex] = (int16_t)g;
+                p.gexp[g] = ex;
+            }
+        }
+        groups += __popcll(opening);
+        __builtin_amdgcn_wave_barrier();
+    }
+    int carry = 0;
+    for (int g0 = 0; g0 < groups; g0 += 64) {
+        const int g = g0 + lane;
+        const int v = g < groups ? p.gsz[g] : 0;
+        int inc = v;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(inc, o, 64);
+            if (lane >= o) inc += y;
+        }
+        if (g < groups) p.gsz[g] = carry + inc - v;
+        carry += __shfl(inc, 63, 64);
+    }
+    if (lane == 0) p.gsz[groups] = n;
+    return groups;
+}
+
+// The plan of n entries into the engine's words (PlanWords): wave 0 groups them (plan_groups_wave), then every thread
+// of the work-group places its entry and the group it heads.  A group's blob is slot_off[slot] past cache_base when
+// the caller maps slots, else slot * blob, with slot = res[expert] (the resident layer's slot) or the expert itself.
+// Every thread calls it (n <= blockDim.x).  The last store, after a fence, is *skip = ring.
+__device__ __forceinline__ void write_decode_plan(const int* s_ids, const PlanLds& p, int n, int k, int n_expert,
+                                                  const int32_t* __restrict__ res, const uint8_t* cache_base,
+                                                  const unsigned long long* __restrict__ slot_off, long long blob,
+                                                  int32_t* __restrict__ pl, long long cap, uint32_t* skip,
+                                                  uint32_t ring) {
     const int t = threadIdx.x;
-    for (int e = t; e < n_expert; e += blockDim.x) s_first[e] = n;
-    __syncthreads();
-    const int ex = t < n ? s_ids[t] : -1;
-    if (t < n) atomicMin(&s_first[ex], t);
-    __syncthreads();
-    int cnt = 0, pos = 0;
-    const bool leader = t < n && s_first[ex] == t;
-    if (t < n) {
-        for (int j = 0; j < n; ++j) {
-            if (s_ids[j] != ex) continue;
-            if (leader) ++cnt;
-            if (j < t) ++pos;
-        }
-    }
-    int total;
-    const int pack = leader ? ((cnt << 16) | 1) : 0;
-    const int excl = block_exclusive_scan(pack, s_wave, &total);
-    s_excl[t] = excl;
-    __syncthreads();
-    int32_t* counts = pl;
-    int32_t* start = pl + 4;
-    int32_t* dst = start + capx + 1;
-    int32_t* tok = dst + capx;
-    const long long ptr_off = ((4 + (capx + 1) + 2 * capx) + 1) & ~1ll;
-    unsigned long long* ptr = (unsigned long long*)(pl + ptr_off);
-    int32_t* start2 = pl + ptr_off + 4 * capx;
-    if (t < n) {
-        const int le = s_excl[s_first[ex]];
-        const int g = le & 0xffff, gstart = le >> 16;
-        dst[gstart + pos] = t;
-        tok[gstart + pos] = t / k;
-        if (leader) {
-            const int32_t slot = res ? res[ex] : ex;
-            ptr[g] = (unsigned long long)(uintptr_t)(cache_base +
-                                                     (slot_off ? (size_t)slot_off[slot] : (size_t)slot * (size_t)blob));
-            start[g] = gstart;
-        }
+    __shared__ int s_groups;
+    if (t < 64) {
+        const int groups = plan_groups_wave(s_ids, n, n_expert, p);
+        if (t == 0) s_groups = groups;
     }
     __syncthreads();
-    if (t != 0) return;
-    const int groups = total & 0xffff;
-    start[groups] = n;
-    start2[0] = n;
-    counts[0] = groups;
-    counts[1] = n;
-    counts[2] = 0;
-    __threadfence();
-    *skip = ring;
+    const int groups = s_groups;
+    const PlanWords w{cap};
+    if (t < n) {
+        const int e = p.ent[t];
+        const int slot = p.gsz[e & 0xffff] + (e >> 16);
+        pl[w.dst() + slot] = t;
+        pl[w.tok() + slot] = t / k;
+    }
+    for (int g = t; g <= groups; g += blockDim.x) {
+        pl[w.start() + g] = p.gsz[g];
+        if (g == groups) continue;
+        const int ex = p.gexp[g];
+        const size_t at = res ? (size_t)res[ex] : (size_t)ex;
+        const size_t off = slot_off ? (size_t)slot_off[at] : at * (size_t)blob;
+        ((unsigned long long*)(pl + w.ptr()))[g] = (unsigned long long)(uintptr_t)(cache_base + off);
+    }
+    if (t == 0) {
+        pl[w.counts() + 0] = groups;
+        pl[w.counts() + 1] = n;
+        pl[w.counts() + 2] = 0;   // no PCIe groups
+        pl[w.start2()] = n;
+    }
+    __syncthreads();
+    if (t == 0) {
+        __threadfence();
+        *skip = ring;
+    }
 }
 
 // q8_1 of values 8j .. 8j + 7 of rows whose width is a whole number of 256s (reference iq_kernels.cpp:1850-1879):

@@ -97,6 +97,9 @@ _SIGS = {
     "xs_iq_dequant_bf16": (I, [I, P, I64, P, P]),
     "xs_iq_dequant_f16": (I, [I, P, I64, P, P]),
     "xs_moe_status_check": (I, [P, P]),
+    "xs_moe_set_wait_bound": (None, [LL]),
+    "xs_bench_hbm_read": (I, [P, SZ, P, I, P]),
+    "xs_bench_mfma_f16": (I, [I, I, P, P]),
     "xs_f32_gemv_fp32_mmvf_multi": (I, [P, I64, P, P, I64, I64, I64, I, P]),
     "xs_bf16_gemv_fp32_mmvf_multi": (I, [P, I64, P, P, I64, I64, I64, I, P]),
     "xs_f32_gemm_rows": (I, [P, I64, P, P, I64, I64, I64, I64, P]),
@@ -130,6 +133,7 @@ _SIGS = {
     "xs_moe_layer_decode_workspace_bytes": (SZ, [LP, I, I, I]),
     "xs_moe_layer_decode_status": (P, [P]),
     "xs_moe_layer_decode_noalloc": (I, [LP, P, SZ, I, I, P, P, P, P, I, P, P]),
+    "xs_moe_layer_decode_noalloc_status": (P, []),
     "xs_moe_layer_prefill": (I, [LP, P, SZ, I, I, P, P, P, P, I, P, SZ, P]),
     "xs_shared_expert_decode": (I, [LP, P, P, I, P, P, P, P, SZ, P]),
     "xs_shared_expert_decode_workspace_bytes": (SZ, [LP, I]),
@@ -495,6 +499,15 @@ def moe_layer_decode_noalloc(L, arena, n_expert, k, x, logits, residual, out, st
     return out
 
 
+def noalloc_status_check(stream=None):
+    """Synchronize and raise XsError when the fixed scratch's own status word (where xs_moe_layer_decode_noalloc ORs
+    its bits when called with status=None) is set; the word is then cleared."""
+    st = lib().xs_moe_layer_decode_noalloc_status()
+    if not st:
+        raise XsError(XS_EDEVICE, lib().xs_last_error().decode())
+    _check(lib().xs_moe_status_check(st, _stream(stream)))
+
+
 def shared_expert_decode(SL, blob, x, w_gate=None, stream=None):
     """One shared expert over the tokens of x [T, n_embd] (blob: the expert's native bytes on the device) -> (shared
     rows [T, n_embd], gate logits [T] or None)."""
@@ -549,11 +562,13 @@ class MoeLayer:
         if not self.prefill:
             _check(lib().xs_moe_status_check(self.ws_ptr, None))
 
-    def __call__(self, x, logits, residual, out, n_tok=None, arena=None, stream=None):
+    def __call__(self, x, logits, residual, out, n_tok=None, arena=None, stream=None, shared_blob=None):
+        """shared_blob: this call's shared-expert blob in place of the one given at construction (same layout)."""
         n_tok = x.shape[0] if n_tok is None else n_tok
         arena = self.arena if arena is None else arena
         if self.ex:
             SL, sblob, w_gate = self.shared if self.shared is not None else (None, None, None)
+            sblob = sblob if shared_blob is None else shared_blob
             fn = lib().xs_moe_layer_prefill_ex if self.prefill else lib().xs_moe_layer_decode_ex
             _check(fn(ctypes.byref(self.L), _p(arena), self.blob, self.n_expert, self.k, _p(x), _p(logits),
                       _p(residual), _p(out), n_tok, None if self.router is None else ctypes.addressof(self.router),
@@ -562,6 +577,7 @@ class MoeLayer:
             return out
         if self.shared is not None:
             SL, sblob, w_gate = self.shared
+            sblob = sblob if shared_blob is None else shared_blob
             _check(lib().xs_moe_layer_decode_shared(
                 ctypes.byref(self.L), _p(arena), self.blob, self.n_expert, self.k, _p(x), _p(logits), _p(residual),
                 _p(out), n_tok, ctypes.byref(SL), _p(sblob), _p(w_gate), self.ws_ptr, self.ws_bytes, _stream(stream)))
@@ -668,6 +684,25 @@ class Pack:
 
 
 # ------------------------------------------------------------------------------------------------ synthetic experts
+
+def fill_layer(out, L, seed, std=0.02, chunk=16):
+    """One layer's experts (out: uint8 [n_expert, blob], blob >= L.bytes) from random fp32 N(0, std) weights drawn on
+    out's device with a generator seeded by `seed`, quantized with this library's quantizer: each matrix of `chunk`
+    experts at once (one draw, one quantization, one strided copy into the blobs).  Same format as build_arena, other
+    draws (the weights of `chunk` experts come out of one stream); for building many distinct layers fast."""
+    n_expert = out.shape[0]
+    g = torch.Generator(device=out.device)
+    g.manual_seed(seed)
+    for e0 in range(0, n_expert, chunk):
+        c = min(chunk, n_expert - e0)
+        for off, rows, cols, t in ((0, L.n_ff, L.n_embd, L.gu_type), (L.up_off, L.n_ff, L.n_embd, L.gu_type),
+                                   (L.down_off, L.n_embd, L.n_ff, L.d_type)):
+            w = torch.randn(c * rows, cols, generator=g, device=out.device, dtype=torch.float32) * std
+            nbytes = rows * row_bytes(t, cols)
+            q = quantize_rows(t, w.reshape(-1))
+            out[e0:e0 + c, off:off + nbytes].copy_(q.view(c, nbytes))
+            del w, q
+
 
 def build_arena(n_expert, n_embd, n_ff, gu_type, d_type, seed=0, std=0.02, device="cuda", gen_device="cuda",
                 copies=1):
