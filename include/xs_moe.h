@@ -262,10 +262,11 @@ int32_t* xs_moe_layer_decode_status(void* workspace);
  * a layer call (or a run of them).  Not to be called inside a graph capture.  No counterpart in the reference. */
 int xs_moe_status_check(int32_t* status, void* stream);
 /* The bound of the persistent layer's waits, in ticks of the device's wall clock (hipDeviceAttributeWallClockRate
- * kHz), for calls made after it, process-wide; 0 restores the default (50 ms); a negative value makes every wait
- * expire at once (no hand-over word is taken: the error path forced from the host - every work-group still ends
- * normally, the status word reports bit 1 and the output is not to be used).  A test and diagnosis hook; no
- * counterpart in the reference. */
+ * kHz), for calls made after it, process-wide; 0 restores the default (50 ms); -1 makes every wait expire at once
+ * (no hand-over word is taken: the error path forced from the host - every work-group still ends normally, the
+ * status word reports bit 1 and the output is not to be used); -2 makes every waiter of the one-token layer compute
+ * each unit it would wait on itself (the path taken for units whose owners have not started: the output is the same,
+ * bit for bit).  A test and diagnosis hook; no counterpart in the reference. */
 void xs_moe_set_wait_bound(long long ticks);
 
 /* xs_moe_layer_decode without a caller workspace, for callers that cannot allocate device memory (code under HIP
@@ -359,6 +360,10 @@ size_t xs_moe_layer_prefill_ex_workspace_bytes(const xs_expert_layout_t* L, int 
  * (grid x 128 floats) as its output.  Enqueued on `stream`. */
 int xs_bench_hbm_read(const void* src, size_t bytes, unsigned int* sink, int grid, void* stream);
 int xs_bench_mfma_f16(int iters, int grid, float* sink, void* stream);
+/* n_wg work-groups of 64 threads, each holding lds_bytes of LDS (<= 160 KB: one a compute unit at the most) for `ticks`
+ * of the device's wall clock (<= 20 s), then ending: other work owning part of the GPU, for tests of the persistent
+ * layers beside it.  sink: n_wg words (written only in a case that never happens). */
+int xs_bench_occupy(int n_wg, int lds_bytes, long long ticks, unsigned int* sink, void* stream);
 
 #ifdef __cplusplus
 }

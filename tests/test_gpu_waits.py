@@ -81,3 +81,59 @@ def test_call_tag_wrap(xm, c2, T):
         layer(x, logits, res, out)
         layer.check()
         assert torch.equal(out.view(torch.int32), want.view(torch.int32)), i
+
+
+@pytest.mark.parametrize("cfg", ["config2", "config1"])
+def test_help_path_bit_exact(xm, c2, cfg):
+    """The path a waiter takes for a unit whose owner has not started (it computes the unit itself from the rows in
+    HBM), forced for every unit from the host (xs_moe_set_wait_bound(-2)): the output equals the normal path's bit for
+    bit, and the status stays clean."""
+    if cfg == "config2":
+        arena, L = c2
+        E, k = 128, 8
+    else:
+        arena, L = xm.build_arena(8, 1024, 512, xm.Q8_0, xm.Q8_0, seed=0)
+        E, k = 8, 2
+    x, res, logits = inputs(1, L.n_embd, E, 800)
+    want = reference_out(xm, arena, L, E, k, 1, x, logits, res)
+    layer = xm.MoeLayer(L, arena, E, k, 1)
+    out = torch.full_like(res, float("nan"))
+    print(f"[case] help path forced, {cfg}", flush=True)
+    xm.lib().xs_moe_set_wait_bound(-2)
+    try:
+        layer(x, logits, res, out)
+        torch.cuda.synchronize()
+    finally:
+        xm.lib().xs_moe_set_wait_bound(0)
+    layer.check()
+    assert torch.equal(out.view(torch.int32), want.view(torch.int32)), float((out - want).abs().max())
+
+
+@pytest.mark.parametrize("T", [1])
+def test_layer_beside_other_work(xm, c2, T):
+    """Half the compute units held by other work on another stream (xs_bench_occupy: one work-group a CU with all of
+    its LDS, for 100 ms of the wall clock, then it ends) while the layer runs: the layer's grid cannot be resident at
+    once, so its units must be taken in dependency order (gate/up before down before combine) for its waits to end.
+    It must finish with a clean status (no wait ran into its 50 ms bound) and the reference's output bit for bit."""
+    import time
+    arena, L = c2
+    E, k = 128, 8
+    x, res, logits = inputs(T, L.n_embd, E, 700 + T)
+    want = reference_out(xm, arena, L, E, k, T, x, logits, res)
+    layer = xm.MoeLayer(L, arena, E, k, T)
+    out = torch.full_like(res, float("nan"))
+    n_cu = torch.cuda.get_device_properties(0).multi_processor_count
+    sink = torch.zeros(n_cu, dtype=torch.int32, device=DEV)
+    side = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    print(f"[case] layer T={T} beside {n_cu // 2} occupied CUs", flush=True)
+    xm._check(xm.lib().xs_bench_occupy(n_cu // 2, 160 * 1024, 10_000_000, sink.data_ptr(), side.cuda_stream))
+    time.sleep(0.005)   # the occupier's work-groups are placed
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    layer(x, logits, res, out)
+    e1.record()
+    torch.cuda.synchronize()
+    print(f"[case] layer beside the occupier: {e0.elapsed_time(e1):.3f} ms", flush=True)
+    layer.check()
+    assert torch.equal(out.view(torch.int32), want.view(torch.int32))

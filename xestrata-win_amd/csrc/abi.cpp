@@ -50,10 +50,11 @@ size_t up256(size_t v) { return (v + 255) & ~(size_t)255; }
 // clock, or the ticks xs_moe_set_wait_bound set; 0 when it asked every wait to expire at once (the kernels then take
 // no hand-over word: a test of the expired-wait path forced from the host)
 std::atomic<long long> g_wait_bound{0};
+int help_all() { return g_wait_bound.load(std::memory_order_relaxed) == -2 ? 1 : 0; }
 long long spin_ticks() {
     const long long set = g_wait_bound.load(std::memory_order_relaxed);
     if (set > 0) return set;
-    if (set < 0) return 0;
+    if (set == -1) return 0;
     int dev = 0, khz = 0;
     if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess ||
         khz <= 0)
@@ -700,6 +701,7 @@ namespace {
 struct DecodeWs {
     int32_t* status;   // the error word, first in the workspace
     int32_t* sync;     // the persistent layer's call counters (same 4 KB head, from byte 128)
+    uint32_t* marks;   // the persistent layer's unit marks (kMarkWords words after the tagged hand-over words)
     unsigned long long *hx, *px;   // the persistent layer's tagged hand-over words (256 entries)
     int32_t* ids;
     float* w;
@@ -733,6 +735,8 @@ DecodeWs decode_ws(const xs_expert_layout_t* L, int n_expert, int k, int n_tok, 
     const int64_t px_embd = fixed_tagged ? xs::kScratchMaxEmbd : L->n_embd;
     d.hx = (unsigned long long*)take(fused ? (size_t)256 * (size_t)hx_ff * 8 : 0);
     d.px = (unsigned long long*)take(fused ? (size_t)256 * (size_t)px_embd * 8 : 0);
+    // (after the tagged words, not in the head: the h words' offsets decide which memory channels the polls meet)
+    d.marks = (uint32_t*)take(fused ? (size_t)xs::kMarkWords * 4 : 0);
     d.ids = (int32_t*)take((size_t)capx * 4);
     d.w = (float*)take((size_t)capx * 4);
     d.plan = (int32_t*)take(plan_words(capx) * 4);
@@ -896,6 +900,7 @@ int layer_decode(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_
         a.hx = w.hx;
         a.px = w.px;
         a.sync = w.sync;
+        a.marks = w.marks;
         a.err = status ? status : w.status;
         a.rh = P.rh;
         a.rd = P.rd;
@@ -907,6 +912,7 @@ int layer_decode(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_
         a.direct = P.direct;
         a.slab_alias = P.alias;
         a.spin_ticks = spin_ticks();
+        a.help_ticks = help_all() ? -1 : a.spin_ticks / 10000;   // 5 us of the 50 ms bound
         a.shared = shared;
         a.shared_gate = shared_gate;
         a.pre_ids = pre && !sig_in ? w.ids : nullptr;
@@ -1034,6 +1040,7 @@ int layer_decode_shared(const xs_expert_layout_t* L, const uint8_t* arena, size_
         a.hx = w.hx;
         a.px = w.px;
         a.sync = w.sync;
+        a.marks = w.marks;
         a.err = w.status;
         a.rh = SP.rh;
         a.rd = SP.rd;
@@ -1045,6 +1052,7 @@ int layer_decode_shared(const xs_expert_layout_t* L, const uint8_t* arena, size_
         a.direct = SP.direct;
         a.slab_alias = SP.alias;
         a.spin_ticks = spin_ticks();
+        a.help_ticks = help_all() ? -1 : a.spin_ticks / 10000;   // 5 us of the 50 ms bound
         a.shared = nullptr;
         a.shared_gate = nullptr;
         a.pre_ids = one_ids;

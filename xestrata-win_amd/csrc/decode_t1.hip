@@ -81,7 +81,9 @@ __host__ __device__ inline T1Lds t1_lds(int k, int H, int F, int gu_row, int d_r
     o.gu = at; at += t1_up16(64 * 4);
     o.po = at; at += t1_up16(k * rd * 4);
     o.hq = at; at += t1_up16(64);
-    o.part = at; at += t1_up16(32 * (H / 256) * 8);
+    // gate/up's integer parts; in the down phase, the list of units to compute here (t1_help_unit)
+    const int part = 32 * (H / 256) * 8, help = 4 * (1 + k * (F / 32));
+    o.part = at; at += t1_up16(part > help ? part : help);
     o.act_x = at; at += t1_act_bytes(H, qs);
     o.slab_gu = at;   // the gate/up rows; then, decoded, the down rows
     const int gu = 64 * gu_row, dec = decode ? k * rd * t1_dec_stride(F) : 0;
@@ -197,6 +199,64 @@ __device__ __forceinline__ void t1_done(const FusedArgs& a) {   // this work-gro
 }
 
 }  // namespace
+
+// A gate/up unit that a waiter found unmarked - its owner had not started 5 us into the wait (other work held the
+// compute units its work-group needed) - computed by the waiting work-group itself from the rows in HBM: the 64
+// canonical row dots (Unit::apply: the same sums the owner's own form gives, bit for bit), SwiGLU, the q8_1 block;
+// into this work-group's down activation for expert rank e (block j) and, tagged, into every replica for the other
+// waiters.  An owner that starts later computes and stores the same bits again.  Every thread calls it.  (Inlined: a
+// call would give the kernel a stack - scratch memory every launch sets up - and twice the registers.)
+template <int TG, int H, int F>
+__device__ __forceinline__ void t1_help_unit(const uint8_t* arena, long long blob_bytes, long long up_off,
+                                          unsigned long long* hx, int q, int k, unsigned int tag, const int* s_ids,
+                                          Act ax, Act ad, float* s_gu) {
+    using UG = Unit<TG, true, t1_act_qs<TG>() - 256>;   // (x's blocks lie t1_act_qs apart in LDS)
+    constexpr int nu = F / 32, gu_row = (int)row_bytes(TG, H);
+    constexpr int lprc = canon_lanes(H / UG::kUnit);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int e = q / nu, j = q - e * nu;
+    const uint8_t* blob = arena + (size_t)s_ids[e] * (size_t)blob_bytes;
+    const int c = lane & (lprc - 1);
+    for (int rr = tid / lprc; rr < 64; rr += kT1 / lprc) {   // gate rows 0..31, then up rows 0..31 of unit j
+        const uint8_t* row = rr < 32 ? blob + (size_t)(32 * j + rr) * gu_row
+                                     : blob + up_off + (size_t)(32 * j + rr - 32) * gu_row;
+        float acc[1] = {0.0f};
+        const Act at[1] = {ax};
+        for (int u = c; u < H / UG::kUnit; u += lprc) UG::template apply<1>(row, 0, u, at, 1, acc);
+        const float sm = lane0_sum<lprc>(acc[0]);
+        if (c == 0) s_gu[rr] = sm;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        const float h = lane < 32 ? canon_silu_mul(s_gu[lane], s_gu[32 + lane]) : 0.0f;
+        const float amax = group_max32(fabsf(h));   // lanes 0..31 hold the block
+        const float d = q8_scale(amax), id = q8_inv(d);
+        const uint32_t code = lane < 32 ? (uint32_t)(uint8_t)(int8_t)q8_value(h, id) : 0u;
+        uint32_t word = 0;   // lane i < 8: codes 4 i .. 4 i + 3
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const uint32_t cb = (uint32_t)__shfl((int)code, (4 * lane + b) & 63, 64);
+            word |= cb << (8 * b);
+        }
+        const uint32_t dbits = (uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(h2f(f2h(d))), 0);
+        const uint32_t val = lane < 8 ? word : dbits;   // lane i < 9: word i of the block
+        const int s4 = lane < 8 ? sdot4((int)word, 0x01010101, 0) : 0;
+        const int s8 = s4 + __shfl_xor(s4, 1, 64);
+        const int s16 = s8 + __shfl_xor(s8, 2, 64);   // lane 0: codes 0..15, lane 4: 16..31
+        if (lane < 8) ((uint32_t*)(ad.q + 32 * j))[lane] = word;
+        if (lane == 0) ((int*)ad.us16)[2 * j] = s16;
+        if (lane == 4) ((int*)ad.us16)[2 * j + 1] = s16;
+        if (lane == 8) ((float*)ad.d8)[j] = __uint_as_float(dbits);
+        static_assert(kHRep * kHWords <= 128, "two stores a lane");
+        const uint32_t v0 = (uint32_t)__shfl((int)val, lane % kHWords, 64);          // (every lane active)
+        const uint32_t v1 = (uint32_t)__shfl((int)val, (lane + 64) % kHWords, 64);
+        for (int li = lane; li < kHRep * kHWords; li += 64) {
+            const int r = li / kHWords, i = li - r * kHWords;
+            t1_st_tag(hx + (size_t)r * t1_h_replica(k, F) + (size_t)q * t1_h_stride(k) + i, li < 64 ? v0 : v1, tag);
+        }
+    }
+    __syncthreads();
+}
 
 // One token, at a hidden size H, expert width F and RD down rows a unit known at compile time (every index below is
 // then shifts and constants).  a.nu: gate/up units an expert (F / 32); a.nj: down units (H / RD).
@@ -341,6 +401,10 @@ __global__ __launch_bounds__(kT1) void moe_decode_t1_kernel(FusedArgs a) {
         return;
     }
     const unsigned int tag = (unsigned int)s_misc[1];
+    // this work-group runs its gate/up unit: the mark a waiter checks before it waits on the unit (the store wave
+    // writes it; it loads nothing after x)
+    if (has_gu && wave == kStoreWave && lane == 0)
+        __hip_atomic_store(a.marks + 32 * (b & 31) + (b >> 5), tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     bool same = true;
     for (int i = 0; i < k; ++i) same = same && s_spec[i] == s_ids[i];
     if (!same && spec_wave) {   // the speculation missed: drain what it fetched, fetch the exact experts' rows
@@ -454,6 +518,8 @@ __global__ __launch_bounds__(kT1) void moe_decode_t1_kernel(FusedArgs a) {
 
     // ---- 3. the down unit: rows j_dn * rd .. + rd of all k experts, combined in rank order, + residual
     if (has_dn) {
+        int* s_help = (int*)s_part;   // [0] count, then the units to compute here (s_part is free after gate/up)
+        if (tid == 0) s_help[0] = 0;
         if (dn_wave) t1_vm_drain();   // the down rows have landed (every wave reads them after this barrier; polling
                                       // h while they land measured slower: the polls slow the rows and the h stores)
         t1_lds_barrier();
@@ -484,10 +550,15 @@ __global__ __launch_bounds__(kT1) void moe_decode_t1_kernel(FusedArgs a) {
                     for (int i = 0; i < kHWords; ++i) ok = ok && (unsigned int)(v[i] >> 32) == tag;
                     return ok;
                 };
-                // (spin_ticks <= 0: the host forces every wait to expire at once - a test of the error path)
+                // (spin_ticks <= 0: the host forces every wait to expire at once - a test of the error path;
+                // help_ticks < 0: every unit is computed here - a test of that path.)  Polled for help_ticks (5 us)
+                // first; a block still not stored then is rare: its owner's mark is read - no mark, the owner has not
+                // started (other work holds the compute units it needs), so the unit goes on this work-group's list
+                // to be computed here after the polls; else the wait goes on for the rest of the bound.  So no wait
+                // depends on a work-group that is not resident.
                 poll(w);
-                bool good = a.spin_ticks > 0 && tagged(w);
-                const long long t0 = wall_clock64();
+                bool good = a.spin_ticks > 0 && a.help_ticks >= 0 && tagged(w);
+                long long t0 = wall_clock64();
                 for (int it = 1; !good && a.spin_ticks > 0; ++it) {
                     const unsigned long long wd = t1_ld_tag(src + 8);
                     if ((unsigned int)(wd >> 32) == tag) {
@@ -497,8 +568,24 @@ __global__ __launch_bounds__(kT1) void moe_decode_t1_kernel(FusedArgs a) {
                             break;
                         }
                     }
-                    if ((it & 15) == 0 && wall_clock64() - t0 > a.spin_ticks) break;
+                    if ((it & 15) == 0 && wall_clock64() - t0 > a.help_ticks) break;
                     __builtin_amdgcn_s_sleep(8);
+                }
+                if (!good && a.spin_ticks > 0) {
+                    if (a.help_ticks < 0 || __hip_atomic_load(a.marks + 32 * (q & 31) + (q >> 5), __ATOMIC_RELAXED,
+                                                              __HIP_MEMORY_SCOPE_AGENT) != tag) {
+                        s_help[1 + atomicAdd(&s_help[0], 1)] = q;
+                        continue;
+                    }
+                    for (int it = 1; !good; ++it) {
+                        const unsigned long long wd = t1_ld_tag(src + 8);
+                        if ((unsigned int)(wd >> 32) == tag) {
+                            poll(w);
+                            good = tagged(w);
+                        }
+                        if (!good && (it & 15) == 0 && wall_clock64() - t0 > a.spin_ticks) break;
+                        __builtin_amdgcn_s_sleep(8);
+                    }
                 }
                 if (!good) {
                     atomicOr(a.err, 2);
@@ -548,6 +635,13 @@ __global__ __launch_bounds__(kT1) void moe_decode_t1_kernel(FusedArgs a) {
             }
         }
         t1_lds_barrier();
+        // the units no owner ran (none when the grid was resident): computed here, one at a time
+        const int nh = s_help[0];
+        if (__builtin_expect(nh > 0, 0))
+        for (int i = 0; i < nh; ++i) {
+            const int q = s_help[1 + i];
+            t1_help_unit<TG, H, F>(a.arena, a.blob, L.up_off, a.hx, q, k, tag, s_ids, ax, act_d(q / nu), s_gu);
+        }
         constexpr int lpd = canon_lanes(F / UD::kUnit);
         const int c = lane & (lpd - 1);
         for (int t = tid / lpd; t < k * rd; t += kT1 / lpd) {
@@ -679,7 +773,9 @@ hipError_t launch_decode_t1(const FusedArgs& a0, hipStream_t s, bool* used) {
     hipError_t e = t1_resident(kern, lds, &grid);
     if (e != hipSuccess) return e;
     const int nu = F / 32, nj = H / inst->rd;
-    if (nj > grid || k * nu > grid) return hipSuccess;   // every unit's work-group resident at once
+    // a work-group a unit, the grid resident at once when nothing else runs (the kernel stays correct when it is not:
+    // waiters compute units whose owners have not started), and a mark word a gate/up unit
+    if (nj > grid || k * nu > grid || k * nu > kMarkWords) return hipSuccess;
     FusedArgs a = a0;
     a.rd = inst->rd;
     a.nu = nu;

@@ -7,7 +7,8 @@
 //  * mfma_loop_kernel: v_mfma_f32_32x32x16_f16 back to back on eight independent accumulators a wave (enough to keep
 //    the matrix pipe full: 32 cycles an instruction, a chain's next issue waits for its result), 2 waves a SIMD -
 //    the dense rate the prompt GEMMs' instruction uses.
-// No counterpart in the reference; used by bench.py's roofline lines.
+// No counterpart in the reference; used by bench.py's roofline lines.  occupy_kernel holds compute units for a bounded
+// time (tests of the decode layer beside other work).
 #include "../../include/xs_moe.h"
 #include "xs_error.h"
 
@@ -68,6 +69,21 @@ __global__ __launch_bounds__(128) void mfma_loop_kernel(int iters, float* __rest
     if (s == 12345.678f) sink[blockIdx.x * blockDim.x + threadIdx.x] = s;   // keeps the products live
 }
 
+// holds its compute unit (its dynamic LDS) for `ticks` of the wall clock, then ends: a bounded stand-in for other
+// work that owns part of the GPU while a layer runs
+__global__ __launch_bounds__(64) void occupy_kernel(long long ticks, unsigned int* __restrict__ sink) {
+    extern __shared__ unsigned int s_hold[];
+    const long long t0 = wall_clock64();
+    unsigned int n = 0;
+    while (wall_clock64() - t0 < ticks) {
+        __builtin_amdgcn_s_sleep(127);
+        ++n;
+    }
+    s_hold[threadIdx.x] = n;
+    __syncthreads();
+    if (threadIdx.x == 0 && s_hold[1] == 0xFFFFFFFFu) sink[blockIdx.x] = n;   // (keeps the LDS allocation live)
+}
+
 }  // namespace
 
 extern "C" {
@@ -86,6 +102,19 @@ int xs_bench_mfma_f16(int iters, int grid, float* sink, void* stream) {
     hipLaunchKernelGGL(mfma_loop_kernel, dim3((unsigned)grid), dim3(128), 0, (hipStream_t)stream, iters, sink);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? XS_OK : xs::set_error(XS_EDEVICE, std::string("bench_mfma_f16: ") + hipGetErrorString(e));
+}
+
+int xs_bench_occupy(int n_wg, int lds_bytes, long long ticks, unsigned int* sink, void* stream) {
+    if (n_wg <= 0 || lds_bytes < 256 || lds_bytes > 160 * 1024 || ticks <= 0 || ticks > 2000000000ll || !sink)
+        return xs::set_error(XS_EINVAL, "bench_occupy: work-groups, LDS (256 B .. 160 KB) or ticks (<= 20 s)");
+    hipError_t e = hipFuncSetAttribute((const void*)occupy_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       lds_bytes);
+    if (e == hipSuccess) {
+        hipLaunchKernelGGL(occupy_kernel, dim3((unsigned)n_wg), dim3(64), (size_t)lds_bytes, (hipStream_t)stream,
+                           ticks, sink);
+        e = hipGetLastError();
+    }
+    return e == hipSuccess ? XS_OK : xs::set_error(XS_EDEVICE, std::string("bench_occupy: ") + hipGetErrorString(e));
 }
 
 }  // extern "C"

@@ -85,6 +85,7 @@ struct FusedPlan {     // the fused decode layer's unit sizes (a function of the
     int direct;        // 1: one token, units read their rows from HBM straight into registers (no LDS slabs)
     int alias;         // 1: the down slab lies over the gate/up slabs (no down rows fetched during gate/up units)
 };
+constexpr int kMarkWords = 1024;
 struct FusedArgs {
     ExpertLayout L;
     const uint8_t* arena;
@@ -99,12 +100,17 @@ struct FusedArgs {
     // hand-over words: a float's bits | the call's tag << 32 (tags never repeat, so no reset is needed)
     unsigned long long* hx; // [256, n_ff] SwiGLU outputs, plan order
     unsigned long long* px; // [256, n_embd] expert outputs, routing order
-    int32_t* sync;          // 16 64-bit call counters at sync + 32 i (2 KB, 8-byte aligned; 2^20 a call in all, this
-                            // call's tag - 1 = their sum >> 20), zero before the first call
+    int32_t* sync;          // 16 64-bit call counters at sync + 32 i (2 KB, 8-byte aligned; 2^20 a call in all, the
+                            // call's tag from their sum >> 20), zero before the first call
+    uint32_t* marks;        // [kMarkWords] a word a unit or virtual work-group: the call's tag once its owner runs it
+                            // (the waiters' test of whether an owner has started, decode_t1.hip / decode_fused.hip)
     int32_t* err;
     int rh, rd, nu, nj, slab_gu_bytes, slab_dn_bytes, ttab, direct;
     int slab_alias = 0;     // FusedPlan::alias
     long long spin_ticks;   // bound of a wait, in wall-clock ticks
+    long long help_ticks = 0;   // how long a waiter waits before it reads the owner's mark (the one-token layer: an
+                                // unmarked unit is computed by the waiter); < 0: every waiter computes every unit
+                                // (the host's test of that path)
     const float* shared;       // [n_tok, n_embd] the shared expert's rows, added once by the combine (NULL: none)
     const float* shared_gate;  // [n_tok] its gate logits (NULL: ungated)
     // routing already done by another router (DeepSeek's group-limited sigmoid): ids / weights [n_tok, k] in rank
