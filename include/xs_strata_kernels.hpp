@@ -296,7 +296,8 @@ struct Product {
     size_t woff = 0;
 };
 
-/// include/strata/prefill/moe_mmq.hpp:74-84: the launch context (the library keeps its scratch itself).
+/// include/strata/prefill/moe_mmq.hpp:74-84: the launch context.  It holds nothing: the product allocates nothing and
+/// keeps no state (one launch), so one Context per prompt path, as the reference has it, costs nothing.
 class Context {
 public:
     void run(const Product& p, void* stream) {
