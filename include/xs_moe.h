@@ -268,6 +268,13 @@ int xs_moe_status_check(int32_t* status, void* stream);
  * each unit it would wait on itself (the path taken for units whose owners have not started: the output is the same,
  * bit for bit).  A test and diagnosis hook; no counterpart in the reference. */
 void xs_moe_set_wait_bound(long long ticks);
+/* The prompt layer's product split, process-wide, for calls made after it: on (the default), a layer without a
+ * shared expert whose weights are Q4_K or Q6_K runs every whole 256-row tile of an expert's rows on the tall-tile
+ * GEMMs (256 x 256 tiles, weights dequantized once a step into LDS) and the other rows beside them on a side stream;
+ * off (0), every row takes the 128/64-row GEMMs; 2 runs the split's two chains one after the other on the caller's
+ * stream (each chain's kernels then time alone).  All give the f16 path's results bit for bit (the tiles differ, not
+ * the arithmetic of a value).  A test and measurement switch; no counterpart in the reference. */
+void xs_moe_set_prefill_tall(int on);
 
 /* xs_moe_layer_decode without a caller workspace, for callers that cannot allocate device memory (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc).  No counterpart in the reference.  The layer
@@ -360,6 +367,9 @@ size_t xs_moe_layer_prefill_ex_workspace_bytes(const xs_expert_layout_t* L, int 
  * (grid x 128 floats) as its output.  Enqueued on `stream`. */
 int xs_bench_hbm_read(const void* src, size_t bytes, unsigned int* sink, int grid, void* stream);
 int xs_bench_mfma_f16(int iters, int grid, float* sink, void* stream);
+/* grid work-groups of 1024 threads, each thread iters x 8 conflict-free 16-byte LDS reads (ds_read_b128): the LDS
+ * read rate, iters x 8 x 16 x 1024 bytes a work-group.  sink: grid words (written only in a case that never happens). */
+int xs_bench_lds_read(int iters, int grid, unsigned int* sink, void* stream);
 /* n_wg work-groups of 64 threads, each holding lds_bytes of LDS (<= 160 KB: one a compute unit at the most) for `ticks`
  * of the device's wall clock (<= 20 s), then ending: other work owning part of the GPU, for tests of the persistent
  * layers beside it.  sink: n_wg words (written only in a case that never happens). */

@@ -50,6 +50,8 @@ size_t up256(size_t v) { return (v + 255) & ~(size_t)255; }
 // clock, or the ticks xs_moe_set_wait_bound set; 0 when it asked every wait to expire at once (the kernels then take
 // no hand-over word: a test of the expired-wait path forced from the host)
 std::atomic<long long> g_wait_bound{0};
+// the prompt layer's tall-tile split (xs_moe_set_prefill_tall): on unless switched off
+std::atomic<int> g_tall{1};
 int help_all() { return g_wait_bound.load(std::memory_order_relaxed) == -2 ? 1 : 0; }
 long long spin_ticks() {
     const long long set = g_wait_bound.load(std::memory_order_relaxed);
@@ -486,11 +488,52 @@ int32_t* prefill_mtile(void* scratch, int64_t n_tok, int64_t rows, const xs_expe
     return (int32_t*)((uint8_t*)scratch + up256((size_t)n_tok * (size_t)L->n_embd * 2) +
                       up256((size_t)rows * (size_t)L->n_ff * 2));
 }
-// the grouped experts writing fp32 parts, or f16 parts when parts_h is set (the whole-layer path)
+// A side stream beside the caller's: per host thread and device (so that calls from several threads, or a graph
+// captured on one of them, never share one), made on first use at the default priority and kept until the process
+// ends, with two events for a fork (recorded on the caller's stream, waited for by the side stream) and a join
+// (recorded on the side stream, waited for by the caller's; under graph capture these become the graph's branch and
+// join).
+struct SideStream {
+    int dev;
+    hipStream_t stream;
+    hipEvent_t fork, join;
+};
+hipError_t side_stream_get(SideStream** out) {
+    thread_local std::vector<SideStream> sides;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    for (SideStream& x : sides)
+        if (x.dev == dev) {
+            *out = &x;
+            return hipSuccess;
+        }
+    SideStream x{dev, nullptr, nullptr, nullptr};
+    if ((e = hipStreamCreateWithFlags(&x.stream, hipStreamNonBlocking)) != hipSuccess) return e;
+    if ((e = hipEventCreateWithFlags(&x.fork, hipEventDisableTiming)) != hipSuccess) return e;
+    if ((e = hipEventCreateWithFlags(&x.join, hipEventDisableTiming)) != hipSuccess) return e;
+    sides.push_back(x);
+    *out = &sides.back();
+    return hipSuccess;
+}
+// the side stream, forked from the caller's now
+hipError_t side_stream_fork(hipStream_t caller, SideStream** out) {
+    SideStream* sd = nullptr;
+    hipError_t e = side_stream_get(&sd);
+    if (e != hipSuccess) return e;
+    if ((e = hipEventRecord(sd->fork, caller)) != hipSuccess) return e;
+    if ((e = hipStreamWaitEvent(sd->stream, sd->fork, 0)) != hipSuccess) return e;
+    *out = sd;
+    return hipSuccess;
+}
+
+// the grouped experts writing fp32 parts, or f16 parts when parts_h is set (the whole-layer path); with `split` (a
+// side stream of the caller's, and mtile written in the split form) the whole 256-row tiles run on the tall-tile
+// GEMMs and the other rows beside them on the side stream
 int prefill_experts(const xs_expert_layout_t* L, const float* x, int64_t n_tok, const int32_t* src,
                     const int32_t* entry_of, const int32_t* bounds, const int32_t* n_groups,
                     const unsigned long long* grp_ptr, int64_t cap_groups, int64_t rows, void* scratch, float* parts,
-                    uint16_t* parts_h, bool mtile_ready, void* stream) {
+                    uint16_t* parts_h, bool mtile_ready, void* stream, const SideStream* split = nullptr) {
     if (rows <= 0 || cap_groups <= 0) return ok();
     if (int r = check_layout(L, "moe_prefill_experts")) return r;
     if (cap_groups > rows) return fail(XS_EINVAL, "moe_prefill_experts: cap_groups %lld > rows %lld", (long long)cap_groups,
@@ -520,6 +563,11 @@ int prefill_experts(const xs_expert_layout_t* L, const float* x, int64_t n_tok, 
     a.rows = rows;
     a.cap_groups = cap_groups;
     a.ld_parts = L->n_embd;
+    if (split)
+        return finish(stream,
+                      xs::launch_prefill_experts_split(to_layout(L), a, S(stream), split->stream, split->fork,
+                                                       split->join),
+                      "moe_prefill_experts");
     return finish(stream, xs::launch_prefill_experts(to_layout(L), a, S(stream)), "moe_prefill_experts");
 }
 }  // namespace
@@ -784,6 +832,8 @@ int32_t* xs_moe_layer_decode_status(void* workspace) {
 }
 
 void xs_moe_set_wait_bound(long long ticks) { g_wait_bound.store(ticks, std::memory_order_relaxed); }
+
+void xs_moe_set_prefill_tall(int on) { g_tall.store(on == 2 ? 2 : on ? 1 : 0, std::memory_order_relaxed); }
 
 int xs_moe_status_check(int32_t* status, void* stream) {
     if (!aligned(status, 4)) return fail(XS_EINVAL, "moe status check: the status word is missing or misaligned");
@@ -1128,38 +1178,6 @@ SharedPrefillWs shared_prefill_ws(const xs_expert_layout_t* SL, int n_tok, uint8
     return d;
 }
 
-// A side stream forked from the caller's: per host thread and device (so that calls from several threads, or a
-// graph captured on one of them, never share one), made on first use at the default priority and kept until the
-// process ends, with the two events of the fork and the join.  side_stream_fork records the fork on the caller's
-// stream and makes the side stream wait for it; work is then issued on side->stream, side->join recorded after it,
-// and the caller's stream waits for side->join (under graph capture these become the graph's branch and join).
-struct SideStream {
-    int dev;
-    hipStream_t stream;
-    hipEvent_t fork, join;
-};
-hipError_t side_stream_fork(hipStream_t caller, SideStream** out) {
-    thread_local std::vector<SideStream> sides;
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) return e;
-    SideStream* sd = nullptr;
-    for (SideStream& x : sides)
-        if (x.dev == dev) sd = &x;
-    if (!sd) {
-        SideStream x{dev, nullptr, nullptr, nullptr};
-        if ((e = hipStreamCreateWithFlags(&x.stream, hipStreamNonBlocking)) != hipSuccess) return e;
-        if ((e = hipEventCreateWithFlags(&x.fork, hipEventDisableTiming)) != hipSuccess) return e;
-        if ((e = hipEventCreateWithFlags(&x.join, hipEventDisableTiming)) != hipSuccess) return e;
-        sides.push_back(x);
-        sd = &sides.back();
-    }
-    if ((e = hipEventRecord(sd->fork, caller)) != hipSuccess) return e;
-    if ((e = hipStreamWaitEvent(sd->stream, sd->fork, 0)) != hipSuccess) return e;
-    *out = sd;
-    return hipSuccess;
-}
-
 int layer_prefill(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob_bytes, int n_expert, int k,
                   const float* x, const float* logits, const float* residual, float* out, int n_tok, const Route& route,
                   const xs_expert_layout_t* SL, const uint8_t* shared_blob, const float* w_gate, void* workspace,
@@ -1211,15 +1229,24 @@ int layer_prefill(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob
         return r;
     }
     const int64_t cap_groups = n < n_expert ? n : n_expert;
+    // without a shared expert on the side stream, the whole 256-row tiles of the routed experts take the tall-tile
+    // GEMMs and the other rows run beside them there
+    SideStream* split = nullptr;
+    SideStream serial{0, S(stream), nullptr, nullptr};   // both chains on the caller's stream
+    const int tall = g_tall.load(std::memory_order_relaxed);
+    if (!SL && tall && xs::tall_usable(to_layout(L)) && n >= 256) {
+        if (tall == 2) split = &serial;
+        else if (hipError_t e = side_stream_get(&split)) return hip_status(e, who);
+    }
     if (int r = finish(stream,
                        xs::launch_prefill_route_split(w.ids, n, k, n_expert, w.src, w.slot, w.entry, w.bounds,
                                                       w.experts, w.n_groups, arena, (long long)blob_bytes, w.grp_ptr,
                                                       w.ghist, prefill_mtile(w.scratch, n_tok, n, L), (int)cap_groups,
-                                                      S(stream)),
+                                                      S(stream), split != nullptr),
                        who))
         return r;
     if (int r = prefill_experts(L, x, n_tok, w.src, w.entry, w.bounds, w.n_groups, w.grp_ptr, cap_groups, n, w.scratch,
-                                nullptr, w.parts, true, stream))
+                                nullptr, w.parts, true, stream, split))
         return r;
     if (side)   // the combine waits for the shared expert's rows
         if (hipError_t e = hipStreamWaitEvent(S(stream), side->join, 0)) return hip_status(e, who);

@@ -180,7 +180,7 @@ __global__ __launch_bounds__(1024) void route_fill_kernel(
     const int32_t* __restrict__ ids, int n, int k, int n_expert, int nbits, const int32_t* __restrict__ ghist, int nblk,
     int32_t* __restrict__ src, int32_t* __restrict__ slot, int32_t* __restrict__ entry, int32_t* __restrict__ bounds,
     int32_t* __restrict__ experts, int32_t* __restrict__ n_groups, const uint8_t* cache_base, long long blob,
-    unsigned long long* __restrict__ grp_ptr, int32_t* __restrict__ mtile, int cap_groups) {
+    unsigned long long* __restrict__ grp_ptr, int32_t* __restrict__ mtile, int cap_groups, int split) {
     extern __shared__ int s_w[];   // [16][n_expert]: each wave's counts, then its bases
     __shared__ int s_wave[64];
     __shared__ int s_bad;
@@ -209,7 +209,7 @@ __global__ __launch_bounds__(1024) void route_fill_kernel(
     const int rank = __popcll(peers & below);
     if (in && rank == 0) s_w[wave * E + e] = __popcll(peers);
     __syncthreads();
-    int carry = 0, gcarry = 0, f128 = 0, p128 = 0, f64 = 0, p64 = 0;
+    int carry = 0, gcarry = 0, f128 = 0, p128 = 0, f64 = 0, p64 = 0, ftall = 0;
     const int64_t cap128 = tile_cap(n, 128, cap_groups), cap64 = tile_cap(n, 64, cap_groups);
     for (int e0 = 0; e0 < E; e0 += 1024) {
         const int ee = e0 + tid;
@@ -228,19 +228,28 @@ __global__ __launch_bounds__(1024) void route_fill_kernel(
         int sum_all;
         const int st = block_exclusive_scan(tot, s_wave, &sum_all) + carry;
         if (blk == 0) {   // the groups (experts ascending), and the m-tile table of 128- and 64-row tiles
-            int g_all, a0, a1, a2, a3;
+            // (split: the group's whole 256-row tiles in the tall list, the maps over the rows past them)
+            const int ntall = split ? tot / 256 : 0, rest = tot - 256 * ntall;
+            int g_all, a0, a1, a2, a3, a4;
             const int gi = block_exclusive_scan(tot > 0 ? 1 : 0, s_wave, &g_all) + gcarry;
-            const int b128 = block_exclusive_scan(tot / 128, s_wave, &a0) + f128;
-            const int q128 = block_exclusive_scan(tot % 128 ? 1 : 0, s_wave, &a1) + p128;
-            const int b64 = block_exclusive_scan(tot / 64, s_wave, &a2) + f64;
-            const int q64 = block_exclusive_scan(tot % 64 ? 1 : 0, s_wave, &a3) + p64;
+            const int b128 = block_exclusive_scan(rest / 128, s_wave, &a0) + f128;
+            const int q128 = block_exclusive_scan(rest % 128 ? 1 : 0, s_wave, &a1) + p128;
+            const int b64 = block_exclusive_scan(rest / 64, s_wave, &a2) + f64;
+            const int q64 = block_exclusive_scan(rest % 64 ? 1 : 0, s_wave, &a3) + p64;
+            const int bt = split ? block_exclusive_scan(ntall, s_wave, &a4) + ftall : 0;
             if (ee < E && tot > 0) {
                 experts[gi] = ee;
                 bounds[gi] = st;
                 if (grp_ptr) grp_ptr[gi] = (unsigned long long)(uintptr_t)(cache_base + (size_t)ee * (size_t)blob);
                 if (mtile && gi < cap_groups) {
-                    write_group_tiles(tile_list(mtile, n, cap_groups, 128), gi, st, tot, 128, b128, q128, cap128);
-                    write_group_tiles(tile_list(mtile, n, cap_groups, 64), gi, st, tot, 64, b64, q64, cap64);
+                    const int rs = st + 256 * ntall;
+                    write_group_tiles(tile_list(mtile, n, cap_groups, 128), gi, rs, rest, 128, b128, q128, cap128);
+                    write_group_tiles(tile_list(mtile, n, cap_groups, 64), gi, rs, rest, 64, b64, q64, cap64);
+                    int32_t* lt = tall_list(mtile, n, cap_groups);
+                    for (int t = 0; t < ntall; ++t) {
+                        lt[1 + 2 * (bt + t)] = gi;
+                        lt[2 + 2 * (bt + t)] = st + 256 * t;
+                    }
                 }
             }
             gcarry += g_all;
@@ -248,6 +257,7 @@ __global__ __launch_bounds__(1024) void route_fill_kernel(
             p128 += a1;
             f64 += a2;
             p64 += a3;
+            if (split) ftall += a4;
         }
         if (ee < E) {
             int b = st + pre;
@@ -267,6 +277,7 @@ __global__ __launch_bounds__(1024) void route_fill_kernel(
             mtile[1] = p128;
             mtile[2] = f64;
             mtile[3] = p64;
+            if (split) *tall_list(mtile, n, cap_groups) = ftall;
         }
     }
     __syncthreads();
@@ -281,7 +292,7 @@ __global__ __launch_bounds__(1024) void route_fill_kernel(
 hipError_t launch_prefill_route_split(const int32_t* ids, int64_t n, int k, int n_expert, int32_t* src, int32_t* slot,
                                       int32_t* entry, int32_t* bounds, int32_t* experts, int32_t* n_groups,
                                       const uint8_t* cache_base, long long blob, unsigned long long* grp_ptr,
-                                      int32_t* ghist, int32_t* mtile, int cap_groups, hipStream_t s) {
+                                      int32_t* ghist, int32_t* mtile, int cap_groups, hipStream_t s, bool split) {
     int nbits = 1;
     while ((1 << nbits) < n_expert) ++nbits;
     const int nblk = (int)((n + kSeg - 1) / kSeg);
@@ -289,7 +300,7 @@ hipError_t launch_prefill_route_split(const int32_t* ids, int64_t n, int k, int 
                        n_expert, ghist);
     hipLaunchKernelGGL(route_fill_kernel, dim3(nblk), dim3(1024), (size_t)16 * n_expert * sizeof(int), s, ids, (int)n,
                        k, n_expert, nbits, ghist, nblk, src, slot, entry, bounds, experts, n_groups, cache_base, blob,
-                       grp_ptr, mtile, cap_groups);
+                       grp_ptr, mtile, cap_groups, split ? 1 : 0);
     return hipGetLastError();
 }
 

@@ -25,7 +25,7 @@
 // down weights take a 128-row x 128-weight-row tile, one weight row a lane: a dequantized fragment then feeds four
 // MFMAs (against 64-row tiles' two), which halves the dequantization and the weight loads a product.  The
 // tile's activation rows reach LDS by DMA (global_load_lds_dwordx4, gathered through src for gate/up) into a double
-// buffer, chunk c of row r at slot c ^ (r & 7) (fragment reads of 8 neighbouring rows hit 8 bank groups).  Row tiles
+// buffer, chunk c of row r at slot c ^ swk(r) (a fragment read is free of bank conflicts).  Row tiles
 // of 32 past the group's rows are skipped.  A work-group's m-tile comes from a flat index over every group's
 // ceil(rows / 128) tiles (a prefix computed on the device).  Work-group b runs on XCD b % 8; an XCD takes every
 // eighth m-tile and runs its n-tiles one after the other, so the m-tile's activations and its expert's weights are
@@ -80,25 +80,28 @@ __global__ __launch_bounds__(256) void to_f16_kernel(const float* __restrict__ x
 }
 
 // the m-tile table (tile_list) of the groups in bounds: one work-group, the groups 1024 at a time; each thread
-// writes its group's tiles of both maps
+// writes its group's tiles of both maps.  split: a group's whole 256-row tiles go to the tall list (tall_list) and the
+// maps cover only its rows past them.
 __global__ __launch_bounds__(1024) void tile_map_kernel(const int32_t* __restrict__ bounds,
                                                         const int32_t* __restrict__ n_groups, int32_t* __restrict__ mt,
-                                                        int64_t rows, int cap_groups) {
-    __shared__ int s_wave[16][4];
-    __shared__ int s_carry[4];
+                                                        int64_t rows, int cap_groups, int split) {
+    __shared__ int s_wave[16][5];
+    __shared__ int s_carry[5];
     const int ng = min(*n_groups, cap_groups);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t cap128 = tile_cap(rows, 128, cap_groups), cap64 = tile_cap(rows, 64, cap_groups);
     int32_t* l128 = tile_list(mt, rows, cap_groups, 128);
     int32_t* l64 = tile_list(mt, rows, cap_groups, 64);
-    if (tid < 4) s_carry[tid] = 0;
+    int32_t* lt = tall_list(mt, rows, cap_groups);
+    if (tid < 5) s_carry[tid] = 0;
     __syncthreads();
     for (int g0 = 0; g0 < max(ng, 0); g0 += 1024) {
         const int g = g0 + tid;
         const int start = g < ng ? bounds[g] : 0, n = g < ng ? bounds[g + 1] - start : 0;
-        int c[4] = {n / 128, n % 128 ? 1 : 0, n / 64, n % 64 ? 1 : 0}, inc[4];
+        const int nt = split ? n / 256 : 0, rs = start + 256 * nt, rn = n - 256 * nt;   // tall tiles; the rest
+        int c[5] = {rn / 128, rn % 128 ? 1 : 0, rn / 64, rn % 64 ? 1 : 0, nt}, inc[5];
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {   // inclusive wave scans of the four counts
+        for (int m = 0; m < 5; ++m) {   // inclusive wave scans of the five counts
             inc[m] = c[m];
             for (int o = 1; o < 64; o <<= 1) {
                 const int y = __shfl_up(inc[m], o, 64);
@@ -107,23 +110,28 @@ __global__ __launch_bounds__(1024) void tile_map_kernel(const int32_t* __restric
             if (lane == 63) s_wave[wave][m] = inc[m];
         }
         __syncthreads();
-        int before[4];
+        int before[5];
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
+        for (int m = 0; m < 5; ++m) {
             before[m] = s_carry[m] + inc[m] - c[m];
             for (int w = 0; w < wave; ++w) before[m] += s_wave[w][m];
         }
         if (g < ng) {
-            write_group_tiles(l128, g, start, n, 128, before[0], before[1], cap128);
-            write_group_tiles(l64, g, start, n, 64, before[2], before[3], cap64);
+            write_group_tiles(l128, g, rs, rn, 128, before[0], before[1], cap128);
+            write_group_tiles(l64, g, rs, rn, 64, before[2], before[3], cap64);
+            for (int t = 0; t < nt; ++t) {
+                lt[1 + 2 * (before[4] + t)] = g;
+                lt[2 + 2 * (before[4] + t)] = start + 256 * t;
+            }
         }
         __syncthreads();
         if (tid == 1023)
 #pragma unroll
-            for (int m = 0; m < 4; ++m) s_carry[m] = before[m] + c[m];
+            for (int m = 0; m < 5; ++m) s_carry[m] = before[m] + c[m];
         __syncthreads();
     }
     if (tid < 4) mt[tid] = s_carry[tid];
+    if (tid == 4) lt[0] = s_carry[4];
 }
 
 // Loads through a global-address-space pointer.  Blob addresses come from memory (the group table), so the compiler
@@ -199,7 +207,13 @@ struct IntC {
     static constexpr int value = N;
 };
 
-__device__ __forceinline__ int swz(int r, int c) { return r * 8 + (c ^ (r & 7)); }   // in 16-byte units
+// The 16-byte slot of chunk c of row r in a row-major LDS slab of 128-byte rows: c ^ swk(r).  A fragment read takes
+// one chunk of 32 consecutive rows, served 16 lanes at a time from 64 banks: rows of one parity share a half of the
+// banks, so the 8 even (odd) rows among 16 consecutive ones need 8 different keys - swk is a bijection of bits 1..3
+// of r.  Its low bit is bit 3 of r, so the 4 even rows among 8 consecutive ones have keys of distinct high bits: a
+// lane pair writing chunks (c, c ^ 1) of each of those rows (the tall tile's weight stores) is also conflict-free.
+__device__ __forceinline__ int swk(int r) { return (((r >> 1) & 3) << 1) | ((r >> 3) & 1); }
+__device__ __forceinline__ int swz(int r, int c) { return r * 8 + (c ^ swk(r)); }   // in 16-byte units
 
 __device__ __forceinline__ h2_t h2(uint32_t w) { return __builtin_bit_cast(h2_t, w); }
 __device__ __forceinline__ uint32_t u32(h2_t h) { return __builtin_bit_cast(uint32_t, h); }
@@ -420,7 +434,7 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
     const int64_t wrb = DOWN ? L.d_row : L.gu_row;
 
     // A by DMA: wave w fills rows [8 RT w, 8 RT (w + 1)) of the tile, 8 rows an instruction; lane l of instruction i
-    // holds LDS slot swz(R, l & 7) of row R = 8 RT w + 8 i + l / 8, i.e. chunk (l & 7) ^ (R & 7) of that row (rows
+    // holds LDS slot swz(R, l & 7) of row R = 8 RT w + 8 i + l / 8, i.e. chunk (l & 7) ^ swk(R) of that row (rows
     // past the group's end read its first row)
     // (MMQ: the chunk's 8 int8 codes - values 8 perm8(c) .. + 8 of the step - and their block's scale instead)
     const uint8_t* asrc[RT];
@@ -429,7 +443,7 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
     for (int i = 0; i < RT; ++i) {
         const int R = 8 * RT * wave + 8 * i + (lane >> 3);
         const int rr = R < nrows ? R : 0;
-        const int c = (lane & 7) ^ (R & 7);
+        const int c = (lane & 7) ^ swk(R);
         if constexpr (MMQ) {
             asrc[i] = (const uint8_t*)(a.xq + (int64_t)(r0 + rr) * K) + 8 * perm8(c);
             adsc[i] = (const uint8_t*)((const float*)(a.xq + a.n_tok * K) + (int64_t)(r0 + rr) * (K / 32) + perm8(c) / 4);
@@ -767,6 +781,332 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
     }
 }
 
+// ---------------------------------------------------------------- tall tiles
+// A whole 256-row tile of one group against BN weight rows (gate/up: BN / 2 gate rows and their up rows, so BN / 2 h
+// columns; down: BN output columns), by 8 waves, two a SIMD.  Each K step (64 values) the
+// work-group dequantizes the step's BN x 64 weight slab once into LDS (512 / BN threads a weight row, each a share of
+// the row's 8 fragments) and stages the 256 x 64 activation slab, both double-buffered; wave w then multiplies rows
+// [64 (w % 4), + 64) by BN / 2 weight rows of the tile (gate/up: BN / 4 gate rows and their up rows), so a dequantized
+// fragment feeds 8 products (a 64-row tile's lane-held fragments feed 2 to 4).  The raw words of step ks + 2 and
+// the activation rows of step ks + 1 are loaded at the start of step ks; step ks + 1 is dequantized and staged while
+// step ks's products run (the A rows stored halfway, which frees their registers for the second half's products),
+// one barrier a step.  Work-group b runs on XCD b % 8; XCD x takes tall tiles x, x + 8, ...
+// and runs each one's n-tiles side by side, so the tile's activations reach its L2 once.
+constexpr int kTallSlab = 256 * 128;   // one activation buffer: 256 rows x 64 f16 values
+__host__ __device__ constexpr int tall_lds(int bn) { return 2 * kTallSlab + 2 * bn * 128; }
+
+template <bool DOWN, int T, int BN>
+__global__ __launch_bounds__(512) void tall_mfma_kernel(ExpertLayout L, PrefillArgs a, const int32_t* __restrict__ tall,
+                                                        int n_tiles) {
+    static_assert(T == kQ4_K || T == kQ6_K, "tall tiles take Q4_K and Q6_K weights");
+    static_assert(BN == 128 || BN == 256, "a tile is 128 or 256 weight rows");
+    constexpr int TPC = 512 / BN;     // threads a weight row
+    constexpr int NF = 8 / TPC;       // fragments a thread dequantizes a step
+    constexpr int JW = BN / 64;       // 32-column MFMA tiles a wave
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, hf = lane >> 5;
+    const int c8 = (int)(blockIdx.x >> 3), xcd = (int)(blockIdx.x & 7);
+    const int mt = (c8 / n_tiles) * 8 + xcd, nt = c8 % n_tiles;
+    if (*a.n_groups <= 0 || mt >= tall[0]) return;   // (no groups: the route refused the ids and wrote no table)
+    const int g = tall[1 + 2 * mt], r0 = tall[2 + 2 * mt];
+    if (g >= *a.n_groups || r0 < 0 || r0 + 256 > a.rows) return;
+    const int H = (int)L.n_embd, F = (int)L.n_ff;
+    const int K = DOWN ? F : H, nk = K / kBK;   // nk % 4 == 0 (K is whole 256-value blocks)
+    const int n0 = nt * (DOWN ? BN : BN / 2);
+    uint8_t* const sA = lds;
+    uint8_t* const sB = lds + 2 * kTallSlab;
+    int32_t* const s_entry = (int32_t*)(lds + tall_lds(BN));
+    if (DOWN && tid < 256) s_entry[tid] = a.entry[r0 + tid];
+
+    // A: thread t stages rows 64 i + t / 8 (i < 4), slot t % 8 of each: chunk (t % 8) ^ swk(row) of the row (byte
+    // offsets from abase: the f16 activations are far below 4 GB)
+    const uint8_t* const abase = (const uint8_t*)(DOWN ? a.h : a.xb);
+    uint32_t aoff[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int R = 64 * i + (tid >> 3);
+        const int c = (tid & 7) ^ swk(R);
+        aoff[i] = (uint32_t)(DOWN ? (r0 + R) * F : a.src[r0 + R] * H) * 2u + 16u * c;
+    }
+    // B: thread t dequantizes weight row cw = t / TPC of the tile, lane half hb = t % 2 of the raw words, and of the
+    // row's fragments 2 kk + hb those with kk = 2 kp + f (f < NF; kp = t / 2 % 2 when TPC = 4, else kk = f)
+    const int cw = tid / TPC, hb = tid & 1, kp = TPC == 4 ? (tid >> 1) & 1 : 0;
+    const int wrow = DOWN ? n0 + cw : (cw < BN / 2 ? n0 + cw : F + n0 + (cw - BN / 2));
+    const uint8_t* const brow = (const uint8_t*)a.wptr[g] + (DOWN ? L.down_off : 0) +
+                                (int64_t)wrow * (DOWN ? L.d_row : L.gu_row);
+    uint8_t* const bdst = sB + cw * 128;
+    const int bsw = swk(cw);
+
+    // wave tile: rows 64 wm + 32 i (i < 2), weight columns cb[j] (j < JW)
+    const int wm = wave & 3, wn = wave >> 2;
+    int cb[JW];
+#pragma unroll
+    for (int j = 0; j < JW; ++j)
+        cb[j] = DOWN ? (BN / 2) * wn + 32 * j
+                     : (j < JW / 2 ? (BN / 4) * wn + 32 * j : BN / 2 + (BN / 4) * wn + 32 * (j - JW / 2));
+    f32x16_t acc[2][JW];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < JW; ++j)
+#pragma unroll
+            for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.0f;
+    // the code-unpacking constants: masks uniform (SGPRs: one scalar operand a v_and_or_b32), magic words in VGPRs
+    QConst qc;
+    qc.nib[0] = __builtin_amdgcn_readfirstlane(0x000F000Fu);
+    qc.nib[1] = __builtin_amdgcn_readfirstlane(0x00F000F0u);
+    qc.two[0] = __builtin_amdgcn_readfirstlane(0x00300030u);
+    qc.two[1] = __builtin_amdgcn_readfirstlane(0x03000300u);
+    qc.byte = __builtin_amdgcn_readfirstlane(0x00FF00FFu);
+    qc.mag[0] = vreg<0x64006400u>();
+    qc.mag[1] = vreg<0x4C004C00u>();
+
+    uint4 areg[4];   // A rows of the next step
+    auto load_a = [&](int s) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) areg[i] = ldg16(abase + aoff[i] + (size_t)s * 128);
+    };
+    auto store_a = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) *(uint4*)(sA + buf * kTallSlab + i * 8192 + tid * 16) = areg[i];
+    };
+    // raw weights.  Q4_K: the step's 16 qs bytes (slot step & 1) and the block header (hnext, moved to hcur when the
+    // block's first step is dequantized).  Q6_K: a half block's words (slot half & 1), loaded at odd steps for the
+    // half three steps on; with TPC = 4 only the ql run of the thread's kp (in l0).
+    uint4 qraw[2], hcur, hnext;
+    Q6Raw r6[2];
+    auto load_b = [&](int s, auto slot_c, auto p_c) {   // Q4_K: step s (its position p in the block)
+        constexpr int SL = decltype(slot_c)::value, P = decltype(p_c)::value;
+        const uint8_t* blk = brow + 144 * (s >> 2);
+        qraw[SL] = ldg16(blk + 16 + 32 * P + 16 * hb);
+        if (P == 0) hnext = ldg16(blk);
+    };
+    auto load_q6 = [&](int hh, Q6Raw& r) {   // half hh of the row
+        const uint8_t* blk = brow + 210 * (hh >> 1);
+        const int n = hh & 1;
+        if constexpr (TPC == 2) {
+            q6k_load(blk, n, hb, r);
+        } else {
+            r.l0 = ldg16(blk + 64 * n + 32 * kp + 16 * hb);
+            r.hq = ldg16(blk + 128 + 32 * n + 16 * hb);
+            r.sc = ldg8(blk + 192 + 8 * n);
+            r.d = ldg_u16(blk + 208);
+        }
+    };
+    // fragment f of step s (position p in its block; Q4_K: the block's header hdr) into B buffer buf
+    auto dequant = [&](int f, int buf, auto slot_c, auto p_c, const uint4& hdr) {
+        constexpr int SL = decltype(slot_c)::value, P = decltype(p_c)::value;
+        const int kk = TPC == 2 ? f : 2 * kp + f;
+        f16x8_t v;
+        if constexpr (T == kQ4_K) {
+            if constexpr (TPC == 2) {
+                v = q4k_frag(qraw[SL], f, q4k_step(hdr, P), qc);
+            } else {   // sub-block 2 p + kp: low nibbles (kp 0) or high (kp 1) of words (0, 1) / (2, 3)
+                const float d = h2f((uint16_t)(hdr.x & 0xFFFFu)), dmin = h2f((uint16_t)(hdr.x >> 16));
+                int sv, mv;
+                q4k_sm(hdr.y, hdr.z, hdr.w, 2 * P + kp, sv, mv);
+                const h2_t d1 = h2b(d * (float)sv);
+                const h2_t sc = kp ? d1 * (h2_t){4.0f16, 4.0f16} : d1;
+                const h2_t c = kp ? d1 * (h2_t){-64.0f16, -64.0f16} : d1 * (h2_t){-1024.0f16, -1024.0f16};
+                const h2_t mn = -h2b(dmin * (float)mv);
+                const uint32_t m = kp ? qc.nib[1] : qc.nib[0], o = kp ? qc.mag[1] : qc.mag[0];
+                const uint4& D = qraw[SL];
+                const uint32_t w0 = (f & 1) ? D.z : D.x, w1 = (f & 1) ? D.w : D.y;
+                const uint32_t u[4] = {and_or(w0, m, o), and_or(w0 >> 8, m, o), and_or(w1, m, o),
+                                       and_or(w1 >> 8, m, o)};
+                uint32_t r[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) r[i] = u32(__builtin_elementwise_fma(h2(u[i]), sc, c) + mn);
+                v = __builtin_bit_cast(f16x8_t, make_uint4(r[0], r[1], r[2], r[3]));
+            }
+        } else {
+            const int t = P & 1;
+            if constexpr (TPC == 2) {
+                v = q6k_frag(r6[SL], t, f, q6k_scale(r6[SL], t, f, hb), qc);
+            } else {   // ql words of the kp run (in l0), qh bits 2 (2 t + kp) of each byte
+                const Q6Raw& r = r6[SL];
+                const uint32_t l0 = (f & 1) ? r.l0.z : r.l0.x, l1 = (f & 1) ? r.l0.w : r.l0.y;
+                const uint32_t q0 = (f & 1) ? r.hq.z : r.hq.x, q1 = (f & 1) ? r.hq.w : r.hq.y;
+                const int sl = kp ? 2 : 4, sr = kp ? 6 : 4;
+                const uint32_t ml = qc.nib[t], mh = qc.two[t], o = qc.mag[t];
+                const uint32_t u[4] = {and_or(l0, ml, and_or(q0 << sl, mh, o)),
+                                       and_or(l0 >> 8, ml, and_or(q0 >> sr, mh, o)),
+                                       and_or(l1, ml, and_or(q1 << sl, mh, o)),
+                                       and_or(l1 >> 8, ml, and_or(q1 >> sr, mh, o))};
+                const int si = 2 * kp + hb;   // scale 4 t + si of the half
+                const uint32_t sw = t ? r.sc.y : r.sc.x;
+                const h2_t s1 = h2b(h2f((uint16_t)r.d) * (float)(int8_t)((sw >> (8 * si)) & 0xFFu));
+                const h2_t sc = t ? s1 * (h2_t){4.0f16, 4.0f16} : s1;
+                const h2_t off = t ? (h2_t){-24.0f16, -24.0f16} : (h2_t){-1056.0f16, -1056.0f16};
+                uint32_t w[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) w[i] = u32((h2(u[i]) + off) * sc);
+                v = __builtin_bit_cast(f16x8_t, make_uint4(w[0], w[1], w[2], w[3]));
+            }
+        }
+        *(f16x8_t*)(bdst + buf * (BN * 128) + 16 * ((2 * kk + hb) ^ bsw)) = v;
+    };
+    // prologue: step 0 staged, the raw weights of step 1 loaded
+    load_a(0);
+    if constexpr (T == kQ4_K) {
+        hcur = ldg16(brow);
+        load_b(0, IntC<0>{}, IntC<0>{});
+        load_b(1, IntC<1>{}, IntC<1>{});
+    } else {
+        load_q6(0, r6[0]);
+        load_q6(1, r6[1]);
+    }
+    store_a(0);
+#pragma unroll
+    for (int f = 0; f < NF; ++f) dequant(f, 0, IntC<0>{}, IntC<0>{}, hcur);
+    lds_sync();
+
+    // iteration ks = ks0 + U: products of step ks (buffer U & 1), step ks + 1 staged into the other buffer (its
+    // weights dequantized between the products, its A rows - loaded at the iteration's start - stored halfway).  The
+    // last iteration (LAST) stages nothing; no other branch is taken in the loop, so the compiler's waits for the raw
+    // words count exactly the loads issued after them.
+    auto iter = [&](int ks0, auto u_c) {
+        constexpr int U = decltype(u_c)::value;
+        const int ks = ks0 + U;
+        const bool more = U < 3 || ks0 + 4 < nk;   // a step ks + 1
+        // step ks + 1 opens a block at U = 3: its header, loaded an iteration ago, is current from here on
+        if (T == kQ4_K && U == 3) hcur = hnext;
+        {   // A of step ks + 1, raw weights of step ks + 2 (the last steps reload the last one: no branch around them)
+            load_a(min(ks + 1, nk - 1));
+            const int s2 = min(ks + 2, nk - 1);
+            if constexpr (T == kQ4_K) {
+                load_b(s2, IntC<U & 1>{}, IntC<(U + 2) & 3>{});
+            } else if constexpr (U & 1) {   // half (ks + 3) / 2 into slot ((ks + 3) / 2) & 1 (= U / 2)
+                load_q6(min((ks + 3) >> 1, 2 * (K / 256) - 1), r6[U >> 1]);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);   // the loads stay ahead of the step's products
+        const uint8_t* A = sA + (U & 1) * kTallSlab;
+        const uint8_t* B = sB + (U & 1) * (BN * 128);
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            const int ch = 2 * kk + hf;
+            f16x8_t fa[2], fb[JW];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                fa[i] = *(const f16x8_t*)(A + 16 * swz(64 * wm + 32 * i + (lane & 31), ch));
+#pragma unroll
+            for (int j = 0; j < JW; ++j) fb[j] = *(const f16x8_t*)(B + 16 * swz(cb[j] + (lane & 31), ch));
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < JW; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+            if (more && kk < NF) {
+                if constexpr (T == kQ4_K) dequant(kk, (U + 1) & 1, IntC<(U + 1) & 1>{}, IntC<(U + 1) & 3>{}, hcur);
+                else dequant(kk, (U + 1) & 1, IntC<((U + 1) >> 1) & 1>{}, IntC<(U + 1) & 1>{}, hcur);
+            }
+            if (more && kk == 1) store_a((U + 1) & 1);
+        }
+        lds_sync();
+    };
+    for (int ks0 = 0; ks0 < nk; ks0 += 4) {
+        iter(ks0, IntC<0>{});
+        iter(ks0, IntC<1>{});
+        iter(ks0, IntC<2>{});
+        iter(ks0, IntC<3>{});
+    }
+
+    // Epilogue.  Lane holds C[64 wm + 32 i + 8 (q / 4) + 4 hf + q % 4][cb[j] + lane % 32]; the values go through a
+    // row-major staging tile in LDS (the A and B buffers are free), so that each global store is 16 contiguous bytes
+    if constexpr (!DOWN) {
+        // h column hc = (BN / 4) wn + 32 j + lane % 32 (j < JW / 2) = SwiGLU(gate acc[i][j], up acc[i][j + JW / 2]),
+        // at its place in the step order of the h row
+        constexpr int stride = BN + 16;   // BN / 2 f16 values a staged row
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < JW / 2; ++j) {
+                const int hc = (BN / 4) * wn + 32 * j + (lane & 31);
+                const int spos = (hc & ~63) + perm64(hc & 63);
+#pragma unroll
+                for (int q = 0; q < 16; ++q) {
+                    const int row = 64 * wm + 32 * i + 8 * (q >> 2) + 4 * hf + (q & 3);
+                    const float gv = acc[i][j][q], uv = acc[i][j + JW / 2][q];
+                    const float e = __builtin_amdgcn_exp2f(-gv * 1.4426950408889634f);
+                    float hv = gv * __builtin_amdgcn_rcpf(1.0f + e) * uv;
+                    hv = __builtin_fminf(__builtin_fmaxf(hv, -65504.0f), 65504.0f);
+                    *(uint16_t*)(lds + row * stride + 2 * spos) = f2h(hv);
+                }
+            }
+        lds_sync();
+        constexpr int cpr = BN / 16;   // 16-byte chunks a row
+#pragma unroll
+        for (int u = 0; u < 256 * cpr / 512; ++u) {
+            const int idx = tid + 512 * u, row = idx / cpr, c = idx % cpr;
+            *(uint4*)(a.h + (int64_t)(r0 + row) * F + n0 + 8 * c) = *(const uint4*)(lds + row * stride + 16 * c);
+        }
+    } else {
+        auto epilogue = [&](auto esz_c) {
+            constexpr int ESZ = decltype(esz_c)::value;
+            constexpr int stride = BN * ESZ + 16, rpp = BN * ESZ <= 256 ? 256 : BN * ESZ <= 512 ? 128 : 64;
+            constexpr int cpr = BN * ESZ / 16;   // 16-byte chunks a staged row
+#pragma unroll
+            for (int rb = 0; rb < 256; rb += rpp) {
+                lds_sync();   // every wave is done with the buffers (or with the last pass's staging)
+                if (64 * wm >= rb && 64 * wm < rb + rpp) {
+#pragma unroll
+                    for (int i = 0; i < 2; ++i)
+#pragma unroll
+                        for (int j = 0; j < JW; ++j) {
+                            const int col = cb[j] + (lane & 31);
+#pragma unroll
+                            for (int q = 0; q < 16; ++q) {
+                                const int row = 64 * wm + 32 * i + 8 * (q >> 2) + 4 * hf + (q & 3) - rb;
+                                const float v = acc[i][j][q];
+                                if constexpr (ESZ == 4) *(float*)(lds + row * stride + 4 * col) = v;
+                                else *(uint16_t*)(lds + row * stride + 2 * col) =
+                                         f2h(__builtin_fminf(__builtin_fmaxf(v, -65504.0f), 65504.0f));
+                            }
+                        }
+                }
+                lds_sync();
+#pragma unroll
+                for (int u = 0; u < rpp * cpr / 512; ++u) {
+                    const int idx = tid + 512 * u, r = idx / cpr, c = idx - r * cpr;
+                    const uint4 v = *(const uint4*)(lds + r * stride + 16 * c);
+                    const int64_t o = (int64_t)s_entry[rb + r] * a.ld_parts + n0 + c * (16 / ESZ);
+                    if constexpr (ESZ == 4) *(uint4*)(a.parts + o) = v;
+                    else *(uint4*)(a.parts_h + o) = v;
+                }
+            }
+        };
+        if (a.parts_h) epilogue(IntC<2>{});
+        else epilogue(IntC<4>{});
+    }
+}
+
+// weight rows a tall tile: Q4_K gate/up 256 (128 h columns); 128 for down (output columns) and for Q6_K gate/up,
+// whose raw words take the registers a 256-row tile's accumulators need
+__host__ __device__ constexpr int tall_bn(bool down, int t) { return down || t == kQ6_K ? 128 : 256; }
+
+template <bool DOWN>
+static hipError_t launch_tall(const ExpertLayout& L, const PrefillArgs& a, hipStream_t s) {
+    const int t = DOWN ? L.d_type : L.gu_type;
+    const int BN = tall_bn(DOWN, t);
+    const int n_tiles = DOWN ? (int)(L.n_embd / BN) : (int)(L.n_ff / (BN / 2));
+    const int mt_cap = (int)(a.rows / 256);
+    if (mt_cap == 0) return hipSuccess;
+    const unsigned grid = (unsigned)(8 * ((mt_cap + 7) / 8) * n_tiles);
+    const size_t lds = (size_t)tall_lds(BN) + (DOWN ? 256 * 4 : 0);
+    void (*k)(ExpertLayout, PrefillArgs, const int32_t*, int) =
+        t == kQ4_K ? tall_mfma_kernel<DOWN, kQ4_K, tall_bn(DOWN, kQ4_K)> : tall_mfma_kernel<DOWN, kQ6_K, 128>;
+    hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k, dim3(grid), dim3(512), lds, s, L, a, tall_list(a.mtile, a.rows, a.cap_groups), n_tiles);
+    return hipGetLastError();
+}
+
+bool tall_usable(const ExpertLayout& L) {
+    auto q = [](int t) { return t == kQ4_K || t == kQ6_K; };
+    return q(L.gu_type) && q(L.d_type) && L.n_ff % 256 == 0 && L.n_embd % 256 == 0;
+}
+
 template <bool DOWN, bool MMQ = false>
 static hipError_t launch_gemm(const ExpertLayout& L, const PrefillArgs& a, hipStream_t s) {
     const int t = DOWN ? L.d_type : L.gu_type;
@@ -796,10 +1136,31 @@ hipError_t launch_prefill_experts(const ExpertLayout& L, const PrefillArgs& a, h
     hipLaunchKernelGGL(to_f16_kernel, dim3((unsigned)((nc + 255) / 256)), dim3(256), 0, s, a.x, a.xb, nc);
     if (!a.mtile_ready)
         hipLaunchKernelGGL(tile_map_kernel, dim3(1), dim3(1024), 0, s, a.bounds, a.n_groups, a.mtile, a.rows,
-                           (int)a.cap_groups);
+                           (int)a.cap_groups, 0);
     hipError_t e = launch_gemm<false>(L, a, s);
     if (e != hipSuccess) return e;
     return launch_gemm<true>(L, a, s);
+}
+
+hipError_t launch_prefill_experts_split(const ExpertLayout& L, const PrefillArgs& a, hipStream_t s, hipStream_t side,
+                                        hipEvent_t fork, hipEvent_t join) {
+    const int64_t nc = a.n_tok * L.n_embd / 8;
+    hipLaunchKernelGGL(to_f16_kernel, dim3((unsigned)((nc + 255) / 256)), dim3(256), 0, s, a.x, a.xb, nc);
+    if (!a.mtile_ready)
+        hipLaunchKernelGGL(tile_map_kernel, dim3(1), dim3(1024), 0, s, a.bounds, a.n_groups, a.mtile, a.rows,
+                           (int)a.cap_groups, 1);
+    hipError_t e;
+    const bool two = side != s;   // (side == s: the two chains one after the other)
+    if (two && ((e = hipEventRecord(fork, s)) != hipSuccess || (e = hipStreamWaitEvent(side, fork, 0)) != hipSuccess))
+        return e;
+    // the tall tiles on s, first (a tall work-group takes a whole compute unit: issued first, they are placed before
+    // the other chain's work-groups fill the units), the remainder rows on the side stream
+    if ((e = launch_tall<false>(L, a, s)) != hipSuccess || (e = launch_tall<true>(L, a, s)) != hipSuccess) return e;
+    if ((e = launch_gemm<false>(L, a, side)) != hipSuccess || (e = launch_gemm<true>(L, a, side)) != hipSuccess)
+        return e;
+    if (!two) return hipSuccess;
+    if ((e = hipEventRecord(join, side)) != hipSuccess) return e;
+    return hipStreamWaitEvent(s, join, 0);
 }
 
 }  // namespace xs

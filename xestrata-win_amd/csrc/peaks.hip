@@ -7,8 +7,9 @@
 //  * mfma_loop_kernel: v_mfma_f32_32x32x16_f16 back to back on eight independent accumulators a wave (enough to keep
 //    the matrix pipe full: 32 cycles an instruction, a chain's next issue waits for its result), 2 waves a SIMD -
 //    the dense rate the prompt GEMMs' instruction uses.
-// No counterpart in the reference; used by bench.py's roofline lines.  occupy_kernel holds compute units for a bounded
-// time (tests of the decode layer beside other work).
+// No counterpart in the reference; used by bench.py's roofline lines.  lds_read_kernel measures the LDS read rate
+// (the operand supply of LDS-fed MFMA tiles); occupy_kernel holds compute units for a bounded time (tests of the
+// decode layer beside other work).
 #include "../../include/xs_moe.h"
 #include "xs_error.h"
 
@@ -69,6 +70,30 @@ __global__ __launch_bounds__(128) void mfma_loop_kernel(int iters, float* __rest
     if (s == 12345.678f) sink[blockIdx.x * blockDim.x + threadIdx.x] = s;   // keeps the products live
 }
 
+// ds_read_b128 back to back from LDS, conflict-free (lane l reads 16 bytes at 16 l of its wave's 1 KB row, 8 rows a
+// wave in turn), eight reads in flight a lane; folded into one word a work-group
+__global__ __launch_bounds__(1024) void lds_read_kernel(int iters, unsigned int* __restrict__ sink) {
+    __shared__ uint4 s_buf[64 * 128];   // 128 KB
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int i = tid; i < 64 * 128; i += 1024) s_buf[i] = make_uint4(i, i + 1, i + 2, i + 3);
+    __syncthreads();
+    uint4 acc = make_uint4(0, 0, 0, 0);
+    const int base = (wave * 8) * 64 + lane;
+    for (int it = 0; it < iters; ++it) {
+        uint4 v[8];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) v[r] = s_buf[(base + 64 * ((r + it) & 7)) & (64 * 128 - 1)];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            acc.x ^= v[r].x;
+            acc.y ^= v[r].y;
+            acc.z ^= v[r].z;
+            acc.w ^= v[r].w;
+        }
+    }
+    if ((acc.x ^ acc.y ^ acc.z ^ acc.w) == 0x12345678u) sink[blockIdx.x] = acc.x;
+}
+
 // holds its compute unit (its dynamic LDS) for `ticks` of the wall clock, then ends: a bounded stand-in for other
 // work that owns part of the GPU while a layer runs
 __global__ __launch_bounds__(64) void occupy_kernel(long long ticks, unsigned int* __restrict__ sink) {
@@ -102,6 +127,13 @@ int xs_bench_mfma_f16(int iters, int grid, float* sink, void* stream) {
     hipLaunchKernelGGL(mfma_loop_kernel, dim3((unsigned)grid), dim3(128), 0, (hipStream_t)stream, iters, sink);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? XS_OK : xs::set_error(XS_EDEVICE, std::string("bench_mfma_f16: ") + hipGetErrorString(e));
+}
+
+int xs_bench_lds_read(int iters, int grid, unsigned int* sink, void* stream) {
+    if (iters <= 0 || grid <= 0 || !sink) return xs::set_error(XS_EINVAL, "bench_lds_read: iters, grid or sink");
+    hipLaunchKernelGGL(lds_read_kernel, dim3((unsigned)grid), dim3(1024), 0, (hipStream_t)stream, iters, sink);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? XS_OK : xs::set_error(XS_EDEVICE, std::string("bench_lds_read: ") + hipGetErrorString(e));
 }
 
 int xs_bench_occupy(int n_wg, int lds_bytes, long long ticks, unsigned int* sink, void* stream) {

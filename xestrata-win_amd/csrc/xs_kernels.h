@@ -63,11 +63,13 @@ hipError_t launch_prefill_route(const int32_t* ids, int64_t n, int k, int n_expe
                                 const uint8_t* cache_base, long long blob, unsigned long long* grp_ptr, hipStream_t s);
 
 // the same permutation over ceil(n / 1024) work-groups (ghist: prefill_route_split_scratch bytes), and, when mtile
-// is given, the m-tile table launch_prefill_experts would compute (PrefillArgs::mtile_ready)
+// is given, the m-tile table launch_prefill_experts would compute (PrefillArgs::mtile_ready), or with split the one
+// launch_prefill_experts_split takes (the tall list, and the maps over the rows past each group's tall tiles)
 hipError_t launch_prefill_route_split(const int32_t* ids, int64_t n, int k, int n_expert, int32_t* src, int32_t* slot,
                                       int32_t* entry, int32_t* bounds, int32_t* experts, int32_t* n_groups,
                                       const uint8_t* cache_base, long long blob, unsigned long long* grp_ptr,
-                                      int32_t* ghist, int32_t* mtile, int cap_groups, hipStream_t s);
+                                      int32_t* ghist, int32_t* mtile, int cap_groups, hipStream_t s,
+                                      bool split = false);
 size_t prefill_route_split_scratch(int64_t n, int n_expert);
 
 // decode_layer.hip
@@ -200,6 +202,13 @@ struct PrefillArgs {
     size_t woff;
 };
 hipError_t launch_prefill_experts(const ExpertLayout& L, const PrefillArgs& a, hipStream_t s);
+// The same products split in two chains: every whole 256-row tile of a group on the tall-tile GEMMs (8 waves over 256 x
+// 256 tiles, weights dequantized once a step into LDS) on `s`, the remaining rows on the existing GEMMs on `side`
+// (which waits for `s` to have built the f16 activations and the tables: `fork` is recorded on s, `join` on side).
+// Only for the layouts tall_usable accepts.
+bool tall_usable(const ExpertLayout& L);
+hipError_t launch_prefill_experts_split(const ExpertLayout& L, const PrefillArgs& a, hipStream_t s, hipStream_t side,
+                                        hipEvent_t fork, hipEvent_t join);
 // The grouped product alone (the reference's iq_mmq_grouped), one launch and no scratch: the int8 MMQ activations
 // a.xq times every group's [n_embd, n_ff] matrix (the down product's tiles: L.d_type, L.d_row) into
 // a.parts[a.entry[row] * a.ld_parts + ...] in fp32.
@@ -215,8 +224,13 @@ __host__ __device__ inline int64_t tile_cap(int64_t rows, int bm, int64_t cap_gr
 __host__ __device__ inline int32_t* tile_list(int32_t* t, int64_t rows, int64_t cap_groups, int bm) {
     return t + 4 + (bm == 128 ? 0 : 2 * tile_cap(rows, 128, cap_groups));
 }
+// the tall-tile list (experts_prefill.hip, tall_mfma_kernel): after both maps, its count, then {group, first row} of
+// every whole 256-row tile of a group (when the maps were written for the rows past those tiles only)
+__host__ __device__ inline int32_t* tall_list(int32_t* t, int64_t rows, int64_t cap_groups) {
+    return t + 4 + 2 * (tile_cap(rows, 128, cap_groups) + tile_cap(rows, 64, cap_groups));
+}
 __host__ __device__ inline int64_t tile_table_words(int64_t rows, int64_t cap_groups) {
-    return 4 + 2 * (tile_cap(rows, 128, cap_groups) + tile_cap(rows, 64, cap_groups));
+    return 4 + 2 * (tile_cap(rows, 128, cap_groups) + tile_cap(rows, 64, cap_groups)) + 1 + 2 * (rows / 256 + 1);
 }
 // the tiles of group g (rows [start, start + n)) in a map of bm-row tiles with `cap` entries, given the full and the
 // partial tiles of the groups before it

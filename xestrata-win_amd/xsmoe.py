@@ -98,9 +98,11 @@ _SIGS = {
     "xs_iq_dequant_f16": (I, [I, P, I64, P, P]),
     "xs_moe_status_check": (I, [P, P]),
     "xs_moe_set_wait_bound": (None, [LL]),
+    "xs_moe_set_prefill_tall": (None, [I]),
     "xs_bench_hbm_read": (I, [P, SZ, P, I, P]),
     "xs_bench_mfma_f16": (I, [I, I, P, P]),
     "xs_bench_occupy": (I, [I, I, LL, P, P]),
+    "xs_bench_lds_read": (I, [I, I, P, P]),
     "xs_f32_gemv_fp32_mmvf_multi": (I, [P, I64, P, P, I64, I64, I64, I, P]),
     "xs_bf16_gemv_fp32_mmvf_multi": (I, [P, I64, P, P, I64, I64, I64, I, P]),
     "xs_f32_gemm_rows": (I, [P, I64, P, P, I64, I64, I64, I64, P]),
