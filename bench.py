@@ -34,18 +34,21 @@ _FLUSH = []
 
 
 def flush_caches(torch):
-    """Read and write 1 GiB of unrelated memory (4x the 256 MB Infinity Cache): nothing a timed step reads is left
-    in the caches by the untimed runs before it."""
+    """Read 1 GiB of unrelated memory (4x the 256 MB Infinity Cache) with the library's read-only stream kernel
+    (xs_bench_hbm_read): nothing a timed step reads is left in the caches by the untimed runs before it, and - unlike
+    a copy - the flush leaves no dirty lines whose write-back would compete with the timed steps' reads (a 1 GiB copy
+    here cost the T=1 decode layer 0.5 us a step even at 400 steps)."""
+    import xsmoe as xm
     if not _FLUSH:
-        _FLUSH.append(torch.empty(1 << 29, dtype=torch.uint8, device="cuda").fill_(1))
-        _FLUSH.append(torch.empty(1 << 29, dtype=torch.uint8, device="cuda"))
-    _FLUSH[1].copy_(_FLUSH[0])
-    _FLUSH[0].copy_(_FLUSH[1])
+        _FLUSH.append(torch.ones(1 << 30, dtype=torch.uint8, device="cuda"))
+        _FLUSH.append(torch.zeros(4096, dtype=torch.int32, device="cuda"))
+    xm._check(xm.lib().xs_bench_hbm_read(_FLUSH[0].data_ptr(), _FLUSH[0].numel(), _FLUSH[1].data_ptr(), 4096,
+                                         torch.cuda.current_stream().cuda_stream))
 
 
 def graph_time(torch, fn, replays, flush=False):
     """Capture fn() once in a HIP graph; replay `replays` times between two events; return ms per replay.  The cache
-    flush (1 GiB read and written, when asked) is enqueued right before the first event with no synchronisation in
+    flush (1 GiB read, when asked) is enqueued right before the first event with no synchronisation in
     between, so the host prepares the replays while it runs and the events hold the replays' GPU time only, not the
     graph launch's host latency (at 20 steps that latency alone was ~1.5 us a step)."""
     s = torch.cuda.Stream()
@@ -210,8 +213,12 @@ def pmc_prefill(torch, xm):
     layer = xm.MoeLayer(L, arena, E, k, Tp, prefill=True)
     for _ in range(4):
         layer(xp, zl, rp, op)
+    src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(2):   # calibration of FETCH_SIZE / WRITE_SIZE: copies of a known size
+        dst.copy_(src)
     torch.cuda.synchronize()
-    log("pmc prefill run: 4 config-3 prefill layers")
+    log("pmc prefill run: 4 config-3 prefill layers, 2 copies of 256 MiB")
 
 
 def pmc_tput(torch, xm):
@@ -480,6 +487,9 @@ def main():
     ap.add_argument("--no-others", action="store_true", help="skip configs 3 (verify), 4 and 5")
     ap.add_argument("--pmc-run", action="store_true", help="only the short workload of a rocprofv3 --pmc pass")
     ap.add_argument("--pmc-prefill", action="store_true", help="only 4 prefill layers, for a rocprofv3 --pmc pass")
+    ap.add_argument("--prefill-split", type=int, default=1, choices=(0, 1, 2),
+                    help="the prompt layer's tall-tile split (xs_moe_set_prefill_tall): 1 on (the default), 0 off, 2 "
+                         "its two chains one after the other (each kernel then times alone)")
     ap.add_argument("--pmc-tput", action="store_true",
                     help="only config-2 T=16 and config-4 T=8 decode rotations, for a rocprofv3 --pmc pass")
     args = ap.parse_args()
@@ -495,6 +505,7 @@ def main():
 
     dev = "cuda:0"
     torch.cuda.set_device(0)
+    xm.lib().xs_moe_set_prefill_tall(args.prefill_split)
     if args.pmc_run:
         pmc_run(torch, xm, args.copies)
         return
@@ -616,6 +627,9 @@ def main():
                    frac_measured_mfma=round(tf / peaks["mfma_f16_tflops"], 4), mfma="f16 operands, fp32 accumulate (dense peak "
                    "2.5 PFLOP/s, as bf16)", tokens_per_s=round(Tp / (ms_p * 1e-3), 0),
                    flops_per_layer=flops, routing="Zipf alpha=1.2 (Gumbel-top-k)",
+                   split={0: "off: every row on the 128/64-row GEMMs",
+                          1: "whole 256-row tiles on the tall-tile GEMMs, the rest beside them on a side stream",
+                          2: "tall-tile and remainder chains one after the other"}[args.prefill_split],
                    timing=f"best of 5 means of {max(1, args.prefill_steps // pc)} graph replays of {pc} layers "
                           "(two HBM copies of the weights)")
 
