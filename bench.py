@@ -221,6 +221,31 @@ def pmc_prefill(torch, xm):
     log("pmc prefill run: 4 config-3 prefill layers, 2 copies of 256 MiB")
 
 
+def pmc_verify(torch, xm):
+    """The workload of a rocprofv3 pass on config 3's spec-verify decode: 4 tokens, Zipf(1.2) popularity (the bench's
+    own logits: default_rng(3)), one rotation over 8 HBM copies of the config-2-shaped layer (8 launches of the fused
+    kernel, ~21.5 distinct experts each)."""
+    import numpy as np
+    E, H, F, k, copies = 128, 2048, 768, 8, 8
+    arena, L = xm.build_arena(E, H, F, xm.Q4_K, xm.Q6_K, seed=0, copies=copies)
+    rng = np.random.default_rng(3)
+    pop = -1.2 * np.log(np.arange(1, E + 1))[rng.permutation(E)]
+    zv = torch.from_numpy((pop[None, None, :] + rng.gumbel(size=(copies, 4, E))).astype(np.float32)).cuda()
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    xv = torch.randn(4, H, device="cuda", generator=gen).to(torch.bfloat16).float()
+    rv = torch.randn(4, H, device="cuda", generator=gen)
+    ov = torch.empty(4, H, device="cuda")
+    layer = xm.MoeLayer(L, arena, E, k, 4)
+    for c in range(copies):
+        layer(xv, zv[c], rv, ov, arena=arena[c * E])
+    src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(2):   # calibration of FETCH_SIZE / WRITE_SIZE: copies of a known size
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"pmc verify run: {copies} config-3 verify layers (T=4, Zipf); status {layer.status()}")
+
+
 def pmc_tput(torch, xm):
     """The workload of a rocprofv3 --pmc pass on the throughput decode: one rotation of config-2 layers at T=16 (8 HBM
     copies, disjoint expert sets) and of config-4 layers at T=8 (2 HBM copies of the IQ4_XS layer, disjoint sets)."""
@@ -487,6 +512,8 @@ def main():
     ap.add_argument("--no-others", action="store_true", help="skip configs 3 (verify), 4 and 5")
     ap.add_argument("--pmc-run", action="store_true", help="only the short workload of a rocprofv3 --pmc pass")
     ap.add_argument("--pmc-prefill", action="store_true", help="only 4 prefill layers, for a rocprofv3 --pmc pass")
+    ap.add_argument("--pmc-verify", action="store_true",
+                    help="only a rotation of config 3's verify layers (T=4, Zipf), for a rocprofv3 --pmc pass")
     ap.add_argument("--prefill-split", type=int, default=1, choices=(0, 1, 2),
                     help="the prompt layer's tall-tile split (xs_moe_set_prefill_tall): 1 on (the default), 0 off, 2 "
                          "its two chains one after the other (each kernel then times alone)")
@@ -514,6 +541,9 @@ def main():
         return
     if args.pmc_tput:
         pmc_tput(torch, xm)
+        return
+    if args.pmc_verify:
+        pmc_verify(torch, xm)
         return
     E, H, F, k = 128, 2048, 768, 8
     copies = args.copies
