@@ -219,6 +219,11 @@ int xs_moe_prefill_experts(const xs_expert_layout_t* L, const float* x, int64_t 
                            const unsigned long long* grp_ptr, int64_t cap_groups, int64_t rows, void* scratch,
                            float* parts, void* stream);
 size_t xs_moe_prefill_scratch_bytes(int64_t n_tok, int64_t rows, int64_t n_embd, int64_t n_ff);
+/* Device address of the status word inside xs_moe_prefill_experts' scratch (the same sizes as the call): bit 8 set
+ * when an activation, an h value or a part passed the f16 range (|v| > 65504) and was saturated - those rows are not
+ * the fp32 result.  The bit stays set until the caller clears the word (xs_moe_status_check reads and clears it); a
+ * zero-filled scratch starts clear.  No counterpart in the reference (whose FP16 path overflows to inf). */
+int32_t* xs_moe_prefill_status(void* scratch, int64_t n_tok, int64_t rows, int64_t n_embd, int64_t n_ff);
 
 /* The weighted combine: output = fl(p0 w0) + fl(p1 w1) + ... in rank order, + shared (the shared row once; times
  * the sigmoid of shared_gate[t] when given).  k in 1..15.  Replaces native_moe_combine and
@@ -349,6 +354,11 @@ int xs_moe_layer_prefill(const xs_expert_layout_t* L, const uint8_t* arena, size
                          int k, const float* x, const float* logits, const float* residual, float* out, int n_tok,
                          void* workspace, size_t workspace_bytes, void* stream);
 size_t xs_moe_layer_prefill_workspace_bytes(const xs_expert_layout_t* L, int n_expert, int k, int n_tok);
+/* Device address of the prompt layer workspace's status word (its first word; _ex's too): 0 after good calls; bit 8 a
+ * value of the f16 path (an activation, h or a part, routed or shared) passed the f16 range and was saturated at
+ * +-65504 - the affected rows are not the fp32 result.  A zero-filled workspace starts clear; the bits stay until the
+ * caller clears the word (xs_moe_status_check).  No counterpart in the reference. */
+int32_t* xs_moe_layer_prefill_status(void* workspace);
 /* The prompt layer with either router and an optional shared expert: every token through the shared expert (one group
  * of the f16 MFMA GEMMs, rows in fp32) and the combine adding its row once after the routed ones, times the sigmoid of
  * its gate logit w_gate . x when w_gate is given - the reference's prompt layer (src/prefill/plain_prompt.cpp:

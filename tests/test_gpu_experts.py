@@ -154,3 +154,31 @@ def test_prefill_experts(xm, gu, dt, H, F, T, E):
     want = torch_reference_prefill(xm, arena, L, x, ids, E)
     rel = float((parts - want).abs().max() / want.abs().max())
     assert rel <= 2e-2, rel
+
+
+def test_prefill_experts_saturation_status(xm):
+    """xs_moe_prefill_experts flags a value saturated to the f16 range in its scratch's status word
+    (xs_moe_prefill_status): clear after a normal call on a zero-filled scratch, bit 8 after a 1e6 activation, and
+    xs_moe_status_check raises and clears it."""
+    H, F, E, k, T = 1024, 512, 8, 2, 32
+    arena, L = xm.build_arena(E, H, F, xm.Q4_K, xm.Q6_K, seed=9)
+    g = torch.Generator(device=DEV).manual_seed(9)
+    x = torch.randn(T, H, device=DEV, generator=g)
+    logits = torch.randn(T, E, device=DEV, generator=g)
+    ids, _ = xm.router_top10(logits, k)
+    r = xm.prefill_route(ids.reshape(-1), k, E, cache_base=arena.data_ptr(), blob=L.bytes, with_ptr=True)
+    n = T * k
+    scratch = torch.zeros(xm.moe_prefill_scratch_bytes(T, n, H, F), dtype=torch.uint8, device=DEV)
+    status = xm.lib().xs_moe_prefill_status(scratch.data_ptr(), T, n, H, F)
+    parts = torch.zeros(n, H, device=DEV)
+    for bad in (False, True):
+        xb = x.clone()
+        if bad:
+            xb[3, 7] = 1e6
+        xm.moe_prefill_experts(L, xb, r["src"], r["entry"], r["bounds"], r["n_groups"], r["grp_ptr"], min(n, E), n,
+                               scratch, parts)
+        torch.cuda.synchronize()
+        if bad:
+            with pytest.raises(xm.XsError, match="f16 range"):
+                xm._check(xm.lib().xs_moe_status_check(status, None))
+        xm._check(xm.lib().xs_moe_status_check(status, None))   # clear (again)

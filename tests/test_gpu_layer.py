@@ -98,19 +98,29 @@ def test_config3_prefill(xm, c2_arena, T):
 
 
 def test_prefill_outlier_activation(xm, c2_arena):
-    """The f16 prompt path saturates activations and h at +-65504 (the f16 range), never to inf or NaN: a token with a
-    1e6 activation gets a finite output row (computed from the saturated values), and every other token's row stays
-    within 2e-2 of the fp32 reference (the outlier touches only its own rows)."""
+    """The f16 prompt path saturates activations and h at +-65504 (the f16 range), never to inf or NaN, and says so: a
+    token with a 1e6 activation gets a finite output row (computed from the saturated values), the layer's status word
+    carries bit 8 (MoeLayer.check -> xs_moe_status_check raises and clears it), every other token's row stays within
+    2e-2 of the fp32 reference (the outlier touches only its own rows), and a call without the outlier leaves the word
+    clear."""
     from test_gpu_experts import torch_reference_prefill
     arena, L = c2_arena
     E, k, T, bad = 128, 8, 64, 17
     g = torch.Generator(device=DEV).manual_seed(91)
     x = torch.randn(T, L.n_embd, device=DEV, generator=g).to(torch.bfloat16).float()
+    clean = x.clone()
     x[bad, 5] = 1e6
     res = torch.randn(T, L.n_embd, device=DEV, generator=g)
     logits = zipf_logits(T, E, 91)
     out = torch.empty_like(res)
-    xm.MoeLayer(L, arena, E, k, T, prefill=True)(x, logits, res, out)
+    layer = xm.MoeLayer(L, arena, E, k, T, prefill=True)
+    layer(x, logits, res, out)
+    assert layer.status() & 8
+    with pytest.raises(xm.XsError, match="f16 range"):
+        layer.check()
+    assert layer.status() == 0
+    layer(clean, logits, res, torch.empty_like(res))
+    layer.check()
     assert bool(torch.isfinite(out).all())
     ids, w = xm.router_top10(logits, k)
     keep = torch.arange(T, device=DEV) != bad

@@ -533,7 +533,8 @@ hipError_t side_stream_fork(hipStream_t caller, SideStream** out) {
 int prefill_experts(const xs_expert_layout_t* L, const float* x, int64_t n_tok, const int32_t* src,
                     const int32_t* entry_of, const int32_t* bounds, const int32_t* n_groups,
                     const unsigned long long* grp_ptr, int64_t cap_groups, int64_t rows, void* scratch, float* parts,
-                    uint16_t* parts_h, bool mtile_ready, void* stream, const SideStream* split = nullptr) {
+                    uint16_t* parts_h, bool mtile_ready, void* stream, const SideStream* split = nullptr,
+                    int32_t* status = nullptr) {
     if (rows <= 0 || cap_groups <= 0) return ok();
     if (int r = check_layout(L, "moe_prefill_experts")) return r;
     if (cap_groups > rows) return fail(XS_EINVAL, "moe_prefill_experts: cap_groups %lld > rows %lld", (long long)cap_groups,
@@ -556,7 +557,8 @@ int prefill_experts(const xs_expert_layout_t* L, const float* x, int64_t n_tok, 
     a.h = (uint16_t*)((uint8_t*)scratch + up256((size_t)n_tok * (size_t)L->n_embd * 2));
     a.mtile = prefill_mtile(scratch, n_tok, rows, L);
     a.mtile_ready = mtile_ready;
-    a.err = (int32_t*)((uint8_t*)scratch + xs_moe_prefill_scratch_bytes(n_tok, rows, L->n_embd, L->n_ff) - 256);
+    // the f16 saturation bit goes to the caller's status word, else to the scratch's own (xs_moe_prefill_status)
+    a.err = status ? status : xs_moe_prefill_status(scratch, n_tok, rows, L->n_embd, L->n_ff);
     a.parts = parts;
     a.parts_h = parts_h;
     a.n_tok = n_tok;
@@ -796,6 +798,7 @@ DecodeWs decode_ws(const xs_expert_layout_t* L, int n_expert, int k, int n_tok, 
     return d;
 }
 struct PrefillWs {
+    int32_t* status;   // the workspace's first word (xs_moe_layer_prefill_status)
     int32_t* ids;
     float* w;
     int32_t *src, *slot, *entry, *bounds, *experts, *n_groups;
@@ -810,6 +813,7 @@ PrefillWs prefill_ws(const xs_expert_layout_t* L, int n_expert, int k, int n_tok
     const size_t n = (size_t)n_tok * k;
     size_t off = 0;
     auto take = [&](size_t b) { uint8_t* p = base ? base + off : nullptr; off += up256(b); return p; };
+    d.status = (int32_t*)take(4);
     d.ids = (int32_t*)take(n * 4);
     d.w = (float*)take(n * 4);
     d.src = (int32_t*)take(n * 4);
@@ -831,6 +835,15 @@ int32_t* xs_moe_layer_decode_status(void* workspace) {
     return workspace ? (int32_t*)workspace : nullptr;
 }
 
+int32_t* xs_moe_layer_prefill_status(void* workspace) {
+    return workspace ? (int32_t*)workspace : nullptr;
+}
+
+int32_t* xs_moe_prefill_status(void* scratch, int64_t n_tok, int64_t rows, int64_t n_embd, int64_t n_ff) {
+    if (!scratch) return nullptr;
+    return (int32_t*)((uint8_t*)scratch + xs_moe_prefill_scratch_bytes(n_tok, rows, n_embd, n_ff) - 256);
+}
+
 void xs_moe_set_wait_bound(long long ticks) { g_wait_bound.store(ticks, std::memory_order_relaxed); }
 
 void xs_moe_set_prefill_tall(int on) { g_tall.store(on == 2 ? 2 : on ? 1 : 0, std::memory_order_relaxed); }
@@ -847,11 +860,14 @@ int xs_moe_status_check(int32_t* status, void* stream) {
     e = hipMemcpyAsync(status, &zero, 4, hipMemcpyHostToDevice, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) return fail(XS_EDEVICE, "moe status check: %s", hipGetErrorString(e));
-    return fail(XS_EDEVICE, "moe layer: status 0x%x:%s%s%s", (unsigned)word,
+    return fail(XS_EDEVICE, "moe layer: status 0x%x:%s%s%s%s", (unsigned)word,
                 (word & 2) ? " a bounded wait of the persistent layer expired (its work-groups were not all resident)"
                            : "",
                 (word & 4) ? " a token's router produced fewer than k experts (NaN logits; no output written)" : "",
-                (word & ~6) ? " a blob was misaligned" : "");
+                (word & 8) ? " a prompt value passed the f16 range and was saturated at +-65504 (an activation, h or"
+                             " a part: the affected rows are not the fp32 result)"
+                           : "",
+                (word & ~14) ? " a blob was misaligned" : "");
 }
 
 size_t xs_moe_layer_decode_workspace_bytes(const xs_expert_layout_t* L, int n_expert, int k, int n_tok) {
@@ -1211,7 +1227,7 @@ int layer_prefill(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob
                            who))
             return r;
         if (int r = prefill_experts(SL, x, n_tok, sw.idx, sw.idx, sw.start, sw.n_groups, sw.grp_ptr, 1, n_tok,
-                                    sw.scratch, sw.rows, nullptr, false, ss))
+                                    sw.scratch, sw.rows, nullptr, false, ss, nullptr, w.status))
             return r;
         if (w_gate) {
             // the prompt path's gate GEMM order (f32_gemm_rows) at every token count
@@ -1246,7 +1262,7 @@ int layer_prefill(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob
                        who))
         return r;
     if (int r = prefill_experts(L, x, n_tok, w.src, w.entry, w.bounds, w.n_groups, w.grp_ptr, cap_groups, n, w.scratch,
-                                nullptr, w.parts, true, stream, split))
+                                nullptr, w.parts, true, stream, split, w.status))
         return r;
     if (side)   // the combine waits for the shared expert's rows
         if (hipError_t e = hipStreamWaitEvent(S(stream), side->join, 0)) return hip_status(e, who);

@@ -67,14 +67,21 @@ __device__ __forceinline__ uint32_t sat_f16x2(float a, float b) {   // RNE, satu
     return __builtin_bit_cast(uint32_t, (h2_t){(_Float16)a, (_Float16)b});
 }
 
+// a value past the f16 range, saturated: status bit 8 (kSatBit) of the call's status word, when it has one
+constexpr int kSatBit = 8;
+__device__ __forceinline__ bool past_f16(float v) { return __builtin_fabsf(v) > 65504.0f; }   // (NaN: false)
+
 // x [n, H] fp32 -> f16 in the step order: thread i writes chunk i (8 values)
 __global__ __launch_bounds__(256) void to_f16_kernel(const float* __restrict__ x, uint16_t* __restrict__ y,
-                                                     int64_t n_chunks) {
+                                                     int64_t n_chunks, int32_t* __restrict__ err) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n_chunks) return;
     const int c = (int)(i & 7);
     const float* s = x + (i & ~(int64_t)7) * 8 + 8 * perm8(c);
     const float4 v0 = *(const float4*)s, v1 = *(const float4*)(s + 4);
+    if (err && (past_f16(v0.x) || past_f16(v0.y) || past_f16(v0.z) || past_f16(v0.w) || past_f16(v1.x) ||
+                past_f16(v1.y) || past_f16(v1.z) || past_f16(v1.w)))
+        atomicOr(err, kSatBit);
     *(uint4*)(y + 8 * i) = make_uint4(sat_f16x2(v0.x, v0.z), sat_f16x2(v0.y, v0.w), sat_f16x2(v1.x, v1.z),
                                       sat_f16x2(v1.y, v1.w));
 }
@@ -736,6 +743,7 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
     const int cpr = 128 * esz / 16;   // 16-byte chunks a staged row
     const int sc = 32 * wave + (lane & 31);
     const int spos = DOWN ? sc : (sc & ~63) + perm64(sc & 63);
+    bool sat = false;   // a value saturated to the f16 range
 #pragma unroll
     for (int j = 0; j < (DOWN ? J : 1); ++j) {
         for (int rb = 0; rb < 32 * nrt; rb += rpp) {
@@ -748,13 +756,18 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
                     uint8_t* dst = lds + (row - rb) * stride + spos * esz;
                     if (DOWN) {
                         const float v = acc[i][j][q];
-                        if (f32out) *(float*)dst = v;
-                        else *(uint16_t*)dst = f2h(__builtin_fminf(__builtin_fmaxf(v, -65504.0f), 65504.0f));
+                        if (f32out) {
+                            *(float*)dst = v;
+                        } else {
+                            sat |= past_f16(v);
+                            *(uint16_t*)dst = f2h(__builtin_fminf(__builtin_fmaxf(v, -65504.0f), 65504.0f));
+                        }
                     } else {
                         // SwiGLU on the hardware exp2 and reciprocal (the f16 path's tolerance, not canon's bits)
                         const float gv = acc[i][0][q], uv = acc[i][J - 1][q];
                         const float e = __builtin_amdgcn_exp2f(-gv * 1.4426950408889634f);
                         float hv = gv * __builtin_amdgcn_rcpf(1.0f + e) * uv;
+                        sat |= past_f16(hv);
                         hv = __builtin_fminf(__builtin_fmaxf(hv, -65504.0f), 65504.0f);
                         *(uint16_t*)dst = f2h(hv);
                     }
@@ -779,6 +792,7 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
             lds_sync();   // the next pass writes the staging tile again
         }
     }
+    if (sat && a.err) atomicOr(a.err, kSatBit);
 }
 
 // ---------------------------------------------------------------- tall tiles
@@ -1018,6 +1032,7 @@ __global__ __launch_bounds__(512) void tall_mfma_kernel(ExpertLayout L, PrefillA
         // h column hc = (BN / 4) wn + 32 j + lane % 32 (j < JW / 2) = SwiGLU(gate acc[i][j], up acc[i][j + JW / 2]),
         // at its place in the step order of the h row
         constexpr int stride = BN + 16;   // BN / 2 f16 values a staged row
+        bool sat = false;
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -1030,10 +1045,12 @@ __global__ __launch_bounds__(512) void tall_mfma_kernel(ExpertLayout L, PrefillA
                     const float gv = acc[i][j][q], uv = acc[i][j + JW / 2][q];
                     const float e = __builtin_amdgcn_exp2f(-gv * 1.4426950408889634f);
                     float hv = gv * __builtin_amdgcn_rcpf(1.0f + e) * uv;
+                    sat |= past_f16(hv);
                     hv = __builtin_fminf(__builtin_fmaxf(hv, -65504.0f), 65504.0f);
                     *(uint16_t*)(lds + row * stride + 2 * spos) = f2h(hv);
                 }
             }
+        if (sat && a.err) atomicOr(a.err, kSatBit);
         lds_sync();
         constexpr int cpr = BN / 16;   // 16-byte chunks a row
 #pragma unroll
@@ -1046,6 +1063,7 @@ __global__ __launch_bounds__(512) void tall_mfma_kernel(ExpertLayout L, PrefillA
             constexpr int ESZ = decltype(esz_c)::value;
             constexpr int stride = BN * ESZ + 16, rpp = BN * ESZ <= 256 ? 256 : BN * ESZ <= 512 ? 128 : 64;
             constexpr int cpr = BN * ESZ / 16;   // 16-byte chunks a staged row
+            bool sat = false;
 #pragma unroll
             for (int rb = 0; rb < 256; rb += rpp) {
                 lds_sync();   // every wave is done with the buffers (or with the last pass's staging)
@@ -1059,9 +1077,13 @@ __global__ __launch_bounds__(512) void tall_mfma_kernel(ExpertLayout L, PrefillA
                             for (int q = 0; q < 16; ++q) {
                                 const int row = 64 * wm + 32 * i + 8 * (q >> 2) + 4 * hf + (q & 3) - rb;
                                 const float v = acc[i][j][q];
-                                if constexpr (ESZ == 4) *(float*)(lds + row * stride + 4 * col) = v;
-                                else *(uint16_t*)(lds + row * stride + 2 * col) =
-                                         f2h(__builtin_fminf(__builtin_fmaxf(v, -65504.0f), 65504.0f));
+                                if constexpr (ESZ == 4) {
+                                    *(float*)(lds + row * stride + 4 * col) = v;
+                                } else {
+                                    sat |= past_f16(v);
+                                    *(uint16_t*)(lds + row * stride + 2 * col) =
+                                        f2h(__builtin_fminf(__builtin_fmaxf(v, -65504.0f), 65504.0f));
+                                }
                             }
                         }
                 }
@@ -1075,6 +1097,7 @@ __global__ __launch_bounds__(512) void tall_mfma_kernel(ExpertLayout L, PrefillA
                     else *(uint4*)(a.parts_h + o) = v;
                 }
             }
+            if (sat && a.err) atomicOr(a.err, kSatBit);
         };
         if (a.parts_h) epilogue(IntC<2>{});
         else epilogue(IntC<4>{});
@@ -1133,7 +1156,7 @@ hipError_t launch_mmq_product(const ExpertLayout& L, const PrefillArgs& a, hipSt
 
 hipError_t launch_prefill_experts(const ExpertLayout& L, const PrefillArgs& a, hipStream_t s) {
     const int64_t nc = a.n_tok * L.n_embd / 8;
-    hipLaunchKernelGGL(to_f16_kernel, dim3((unsigned)((nc + 255) / 256)), dim3(256), 0, s, a.x, a.xb, nc);
+    hipLaunchKernelGGL(to_f16_kernel, dim3((unsigned)((nc + 255) / 256)), dim3(256), 0, s, a.x, a.xb, nc, a.err);
     if (!a.mtile_ready)
         hipLaunchKernelGGL(tile_map_kernel, dim3(1), dim3(1024), 0, s, a.bounds, a.n_groups, a.mtile, a.rows,
                            (int)a.cap_groups, 0);
@@ -1145,7 +1168,7 @@ hipError_t launch_prefill_experts(const ExpertLayout& L, const PrefillArgs& a, h
 hipError_t launch_prefill_experts_split(const ExpertLayout& L, const PrefillArgs& a, hipStream_t s, hipStream_t side,
                                         hipEvent_t fork, hipEvent_t join) {
     const int64_t nc = a.n_tok * L.n_embd / 8;
-    hipLaunchKernelGGL(to_f16_kernel, dim3((unsigned)((nc + 255) / 256)), dim3(256), 0, s, a.x, a.xb, nc);
+    hipLaunchKernelGGL(to_f16_kernel, dim3((unsigned)((nc + 255) / 256)), dim3(256), 0, s, a.x, a.xb, nc, a.err);
     if (!a.mtile_ready)
         hipLaunchKernelGGL(tile_map_kernel, dim3(1), dim3(1024), 0, s, a.bounds, a.n_groups, a.mtile, a.rows,
                            (int)a.cap_groups, 1);

@@ -127,6 +127,7 @@ _SIGS = {
     "xs_prefill_route": (I, [P, I64, I, I, P, P, P, P, P, P, P, LL, P, P]),
     "xs_moe_prefill_experts": (I, [LP, P, I64, P, P, P, P, P, I64, I64, P, P, P]),
     "xs_moe_prefill_scratch_bytes": (SZ, [I64, I64, I64, I64]),
+    "xs_moe_prefill_status": (P, [P, I64, I64, I64, I64]),
     "xs_native_moe_combine": (I, [P, P, P, P, I64, I64, P]),
     "xs_native_moe_combine_multi": (I, [P, P, P, P, I64, I64, I, P, P]),
     "xs_moe_combine_residual": (I, [P, P, P, P, P, P, I64, I64, I, P]),
@@ -135,6 +136,7 @@ _SIGS = {
     "xs_moe_layer_decode": (I, [LP, P, SZ, I, I, P, P, P, P, I, P, SZ, P]),
     "xs_moe_layer_decode_workspace_bytes": (SZ, [LP, I, I, I]),
     "xs_moe_layer_decode_status": (P, [P]),
+    "xs_moe_layer_prefill_status": (P, [P]),
     "xs_moe_layer_decode_noalloc": (I, [LP, P, SZ, I, I, P, P, P, P, I, P, P]),
     "xs_moe_layer_decode_noalloc_status": (P, []),
     "xs_moe_layer_prefill": (I, [LP, P, SZ, I, I, P, P, P, P, I, P, SZ, P]),
@@ -552,18 +554,18 @@ class MoeLayer:
         self.ws_ptr = (self.ws.data_ptr() + 255) & ~255
 
     def status(self):
-        """The decode workspace's status word (0: every call so far was good).  Synchronizes the device."""
-        if self.prefill:
-            return 0
+        """The workspace's status word (0: every call so far was good; the prompt layer's word is its workspace's first
+        too: bit 8, a value saturated to the f16 range).  Synchronizes the device."""
         off = self.ws_ptr - self.ws.data_ptr()
         torch.cuda.synchronize(self.ws.device)
         return int(self.ws[off:off + 4].view(torch.int32).item())
 
     def check(self):
-        """Synchronize and raise XsError when the status word is not 0 (a bounded wait of the persistent layer ran
-        out - its output is not valid - or a token's router produced fewer than k experts); the word is cleared."""
-        if not self.prefill:
-            _check(lib().xs_moe_status_check(self.ws_ptr, None))
+        """Synchronize and raise XsError when the status word is not 0 (decode: a bounded wait of the persistent layer
+        ran out - its output is not valid - or a token's router produced fewer than k experts; prompt: a value passed
+        the f16 range and was saturated); the word is cleared."""
+        fn = lib().xs_moe_layer_prefill_status if self.prefill else lib().xs_moe_layer_decode_status
+        _check(lib().xs_moe_status_check(fn(self.ws_ptr), None))
 
     def __call__(self, x, logits, residual, out, n_tok=None, arena=None, stream=None, shared_blob=None):
         """shared_blob: this call's shared-expert blob in place of the one given at construction (same layout)."""
