@@ -87,28 +87,25 @@ __global__ __launch_bounds__(256) void to_f16_kernel(const float* __restrict__ x
 }
 
 // the m-tile table (tile_list) of the groups in bounds: one work-group, the groups 1024 at a time; each thread
-// writes its group's tiles of both maps.  split: a group's whole 256-row tiles go to the tall list (tall_list) and the
-// maps cover only its rows past them.
+// writes its group's tiles of both maps
 __global__ __launch_bounds__(1024) void tile_map_kernel(const int32_t* __restrict__ bounds,
                                                         const int32_t* __restrict__ n_groups, int32_t* __restrict__ mt,
-                                                        int64_t rows, int cap_groups, int split) {
-    __shared__ int s_wave[16][5];
-    __shared__ int s_carry[5];
+                                                        int64_t rows, int cap_groups) {
+    __shared__ int s_wave[16][4];
+    __shared__ int s_carry[4];
     const int ng = min(*n_groups, cap_groups);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t cap128 = tile_cap(rows, 128, cap_groups), cap64 = tile_cap(rows, 64, cap_groups);
     int32_t* l128 = tile_list(mt, rows, cap_groups, 128);
     int32_t* l64 = tile_list(mt, rows, cap_groups, 64);
-    int32_t* lt = tall_list(mt, rows, cap_groups);
-    if (tid < 5) s_carry[tid] = 0;
+    if (tid < 4) s_carry[tid] = 0;
     __syncthreads();
     for (int g0 = 0; g0 < max(ng, 0); g0 += 1024) {
         const int g = g0 + tid;
         const int start = g < ng ? bounds[g] : 0, n = g < ng ? bounds[g + 1] - start : 0;
-        const int nt = split ? n / 256 : 0, rs = start + 256 * nt, rn = n - 256 * nt;   // tall tiles; the rest
-        int c[5] = {rn / 128, rn % 128 ? 1 : 0, rn / 64, rn % 64 ? 1 : 0, nt}, inc[5];
+        int c[4] = {n / 128, n % 128 ? 1 : 0, n / 64, n % 64 ? 1 : 0}, inc[4];
 #pragma unroll
-        for (int m = 0; m < 5; ++m) {   // inclusive wave scans of the five counts
+        for (int m = 0; m < 4; ++m) {   // inclusive wave scans of the four counts
             inc[m] = c[m];
             for (int o = 1; o < 64; o <<= 1) {
                 const int y = __shfl_up(inc[m], o, 64);
@@ -117,28 +114,23 @@ __global__ __launch_bounds__(1024) void tile_map_kernel(const int32_t* __restric
             if (lane == 63) s_wave[wave][m] = inc[m];
         }
         __syncthreads();
-        int before[5];
+        int before[4];
 #pragma unroll
-        for (int m = 0; m < 5; ++m) {
+        for (int m = 0; m < 4; ++m) {
             before[m] = s_carry[m] + inc[m] - c[m];
             for (int w = 0; w < wave; ++w) before[m] += s_wave[w][m];
         }
         if (g < ng) {
-            write_group_tiles(l128, g, rs, rn, 128, before[0], before[1], cap128);
-            write_group_tiles(l64, g, rs, rn, 64, before[2], before[3], cap64);
-            for (int t = 0; t < nt; ++t) {
-                lt[1 + 2 * (before[4] + t)] = g;
-                lt[2 + 2 * (before[4] + t)] = start + 256 * t;
-            }
+            write_group_tiles(l128, g, start, n, 128, before[0], before[1], cap128);
+            write_group_tiles(l64, g, start, n, 64, before[2], before[3], cap64);
         }
         __syncthreads();
         if (tid == 1023)
 #pragma unroll
-            for (int m = 0; m < 5; ++m) s_carry[m] = before[m] + c[m];
+            for (int m = 0; m < 4; ++m) s_carry[m] = before[m] + c[m];
         __syncthreads();
     }
     if (tid < 4) mt[tid] = s_carry[tid];
-    if (tid == 4) lt[0] = s_carry[4];
 }
 
 // Loads through a global-address-space pointer.  Blob addresses come from memory (the group table), so the compiler
@@ -1159,7 +1151,7 @@ hipError_t launch_prefill_experts(const ExpertLayout& L, const PrefillArgs& a, h
     hipLaunchKernelGGL(to_f16_kernel, dim3((unsigned)((nc + 255) / 256)), dim3(256), 0, s, a.x, a.xb, nc, a.err);
     if (!a.mtile_ready)
         hipLaunchKernelGGL(tile_map_kernel, dim3(1), dim3(1024), 0, s, a.bounds, a.n_groups, a.mtile, a.rows,
-                           (int)a.cap_groups, 0);
+                           (int)a.cap_groups);
     hipError_t e = launch_gemm<false>(L, a, s);
     if (e != hipSuccess) return e;
     return launch_gemm<true>(L, a, s);
@@ -1167,11 +1159,9 @@ hipError_t launch_prefill_experts(const ExpertLayout& L, const PrefillArgs& a, h
 
 hipError_t launch_prefill_experts_split(const ExpertLayout& L, const PrefillArgs& a, hipStream_t s, hipStream_t side,
                                         hipEvent_t fork, hipEvent_t join) {
+    if (!a.mtile_ready) return hipErrorInvalidValue;   // (the route writes the split maps and the tall list)
     const int64_t nc = a.n_tok * L.n_embd / 8;
     hipLaunchKernelGGL(to_f16_kernel, dim3((unsigned)((nc + 255) / 256)), dim3(256), 0, s, a.x, a.xb, nc, a.err);
-    if (!a.mtile_ready)
-        hipLaunchKernelGGL(tile_map_kernel, dim3(1), dim3(1024), 0, s, a.bounds, a.n_groups, a.mtile, a.rows,
-                           (int)a.cap_groups, 1);
     hipError_t e;
     const bool two = side != s;   // (side == s: the two chains one after the other)
     if (two && ((e = hipEventRecord(fork, s)) != hipSuccess || (e = hipStreamWaitEvent(side, fork, 0)) != hipSuccess))

@@ -202,10 +202,11 @@ struct PrefillArgs {
     size_t woff;
 };
 hipError_t launch_prefill_experts(const ExpertLayout& L, const PrefillArgs& a, hipStream_t s);
-// The same products split in two chains: every whole 256-row tile of a group on the tall-tile GEMMs (8 waves over 256 x
-// 256 tiles, weights dequantized once a step into LDS) on `s`, the remaining rows on the existing GEMMs on `side`
-// (which waits for `s` to have built the f16 activations and the tables: `fork` is recorded on s, `join` on side).
-// Only for the layouts tall_usable accepts.
+// The same products split in two chains: every whole 256-row tile of a group on the tall-tile GEMMs (8 waves over 256
+// rows x 256 or 128 weight rows, weights dequantized once a step into LDS) on `s`, the remaining rows on the 128-row
+// GEMMs on `side` (which waits for `s` to have built the f16 activations: `fork` is recorded on s, `join` on side;
+// side == s runs the chains one after the other).  a.mtile must hold the split form launch_prefill_route_split wrote
+// (mtile_ready); only for the layouts tall_usable accepts.
 bool tall_usable(const ExpertLayout& L);
 hipError_t launch_prefill_experts_split(const ExpertLayout& L, const PrefillArgs& a, hipStream_t s, hipStream_t side,
                                         hipEvent_t fork, hipEvent_t join);
