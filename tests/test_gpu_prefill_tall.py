@@ -1,8 +1,9 @@
 """The prompt layer's tall-tile split (xs_moe_set_prefill_tall): every whole 256-row tile of an expert's rows runs on
-the tall-tile GEMMs (8 waves over 256 x 256 tiles, the weights dequantized once a step into LDS) and the other rows
-on the 128/64-row GEMMs on a side stream.  Both kinds of tile feed each output value the same f16 fragments in the
-same K order into the same MFMA instruction, so the layer's output with the split equals the output without it bit
-for bit; it is also within the f16 path's 2e-2 of the fp32 torch reference over exactly dequantized weights.
+the tall-tile GEMMs (8 waves over 256 rows x 256 or 128 weight rows, the weights dequantized once a step into LDS) and
+the other rows on the 128-row GEMMs on a side stream.  Both kinds of tile feed each output value the same f16
+fragments in the same K order into the same MFMA instruction, so the layer's output with the split - side by side or
+its chains one after the other - equals the output without it bit for bit; it is also within the f16 path's 2e-2 of
+the fp32 torch reference over exactly dequantized weights.
 
 Cases: config 3 (Q4_K gate/up, Q6_K down, 2048 tokens, Zipf routing: 33 tall tiles beside 128 remainders); both
 pairs of the tall GEMMs' formats (Q4_K / Q6_K either way round) at group sizes around the tile edge (0, 1, 255, 256,
@@ -20,8 +21,9 @@ DEV = "cuda"
 
 
 def run_layer(xm, layer, x, logits, res, tall):
+    """tall: 0 off, 1 the split side by side (the default), 2 the split's chains one after the other."""
     out = torch.full_like(res, float("nan"))
-    xm.lib().xs_moe_set_prefill_tall(1 if tall else 0)
+    xm.lib().xs_moe_set_prefill_tall(int(tall))
     try:
         layer(x, logits, res, out)
         torch.cuda.synchronize()
@@ -68,10 +70,12 @@ def test_config3_split_equals_unsplit(xm, c3):
     x, res = inputs(T, L.n_embd, 33)
     logits = zipf_logits(T, E, 3)
     layer = xm.MoeLayer(L, arena, E, k, T, prefill=True)
-    print("[case] config3 T=2048 tall on/off", flush=True)
-    off = run_layer(xm, layer, x, logits, res, False)
-    on = run_layer(xm, layer, x, logits, res, True)
+    print("[case] config3 T=2048 tall on/off/serial", flush=True)
+    off = run_layer(xm, layer, x, logits, res, 0)
+    on = run_layer(xm, layer, x, logits, res, 1)
+    serial = run_layer(xm, layer, x, logits, res, 2)
     assert torch.equal(on.view(torch.int32), off.view(torch.int32)), float((on - off).abs().max())
+    assert torch.equal(serial.view(torch.int32), off.view(torch.int32)), float((serial - off).abs().max())
     rel = reference_rel(xm, arena, L, E, k, x, logits, res, on)
     assert rel <= 2e-2, rel
 
@@ -88,8 +92,8 @@ def test_tile_edges(xm, gu, dt):
     assert np.array_equal(np.bincount(ids.reshape(-1).cpu().numpy(), minlength=E), counts)
     layer = xm.MoeLayer(L, arena, E, k, T, prefill=True)
     print(f"[case] tile edges {gu}/{dt} T={T}", flush=True)
-    off = run_layer(xm, layer, x, logits, res, False)
-    on = run_layer(xm, layer, x, logits, res, True)
+    off = run_layer(xm, layer, x, logits, res, 0)
+    on = run_layer(xm, layer, x, logits, res, 1)
     assert torch.equal(on.view(torch.int32), off.view(torch.int32)), float((on - off).abs().max())
     rel = reference_rel(xm, arena, L, E, k, x, logits, res, on)
     assert rel <= 2e-2, rel
@@ -101,7 +105,7 @@ def test_split_under_graph_capture(xm, c3):
     x, res = inputs(T, L.n_embd, 55)
     logits = zipf_logits(T, E, 56)
     layer = xm.MoeLayer(L, arena, E, k, T, prefill=True)
-    want = run_layer(xm, layer, x, logits, res, True)
+    want = run_layer(xm, layer, x, logits, res, 1)
     out = torch.full_like(res, float("nan"))
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -118,5 +122,5 @@ def test_split_under_graph_capture(xm, c3):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(out.view(torch.int32), want.view(torch.int32)), i
-        other = run_layer(xm, layer, x, logits, res, False)   # eager work between the replays
+        other = run_layer(xm, layer, x, logits, res, 0)   # eager work between the replays
         assert torch.equal(other.view(torch.int32), want.view(torch.int32)), i
