@@ -515,6 +515,9 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
     // straight-line code that the scheduler interleaves with the next fragment's dequantization.
     auto kloop = [&](auto nrt_c) {
         constexpr int NRT = decltype(nrt_c)::value;
+        // down: a wave whose A rows hold no live row tile neither loads nor stages them (its share of the step's loads
+        // was a fifth of a small tile's TA address cycles; for gate/up the same skip measured slower)
+        const bool a_live = !DOWN || NRT == RT || RT * wave < 4 * NRT;
         // fragment kk of step ks: the B fragments fb[0 .. J) against the live row tiles of the step's A buffer
         auto mfma_step = [&](int ks, int kk, const f16x8_t (&fb)[J]) {
             const uint4* sA = (const uint4*)(lds + (ks & 1) * (kBM * 128));
@@ -534,13 +537,15 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
             // step's first LDS read, which would serialise each step with its own prefetch.
             uint4 areg[RT];
             auto load_a = [&](int ks) {
+                if (a_live)
 #pragma unroll
-                for (int i = 0; i < RT; ++i) areg[i] = a_load(i, ks);
+                    for (int i = 0; i < RT; ++i) areg[i] = a_load(i, ks);
             };
             auto store_a = [&](int buf) {
                 uint8_t* dst = lds + buf * (kBM * 128) + wave * 8 * RT * 128 + 16 * lane;
+                if (a_live)
 #pragma unroll
-                for (int i = 0; i < RT; ++i) *(uint4*)(dst + i * 1024) = a_f16(areg[i]);
+                    for (int i = 0; i < RT; ++i) *(uint4*)(dst + i * 1024) = a_f16(areg[i]);
             };
             const int nb = K / 256;
             uint4 hdr[J], q[2][J];   // header of the block; the qs run of steps (even, odd)
@@ -589,13 +594,15 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
             // first step of the half before.  With 3 blocks a row (n_ff 768) everything is straight-line code.
             uint4 areg[2][RT];   // A(ks) staging, slot ks & 1
             auto load_a = [&](int ks, int slot) {
+                if (a_live)
 #pragma unroll
-                for (int i = 0; i < RT; ++i) areg[slot][i] = a_load(i, ks);
+                    for (int i = 0; i < RT; ++i) areg[slot][i] = a_load(i, ks);
             };
             auto store_a = [&](int slot, int buf) {
                 uint8_t* dst = lds + buf * (kBM * 128) + wave * 8 * RT * 128 + 16 * lane;
+                if (a_live)
 #pragma unroll
-                for (int i = 0; i < RT; ++i) *(uint4*)(dst + i * 1024) = a_f16(areg[slot][i]);
+                    for (int i = 0; i < RT; ++i) *(uint4*)(dst + i * 1024) = a_f16(areg[slot][i]);
             };
             auto q6loop = [&](auto nbc) {
                 constexpr int NBC = decltype(nbc)::value;
