@@ -302,19 +302,24 @@ struct Q6Raw {
     uint2 sc;
     uint32_t d;
 };
-__device__ __forceinline__ void q6k_load(const uint8_t* blk, int n, int hf, Q6Raw& r) {
+__device__ __forceinline__ void q6k_load(const uint8_t* blk, int n, int hf, Q6Raw& r, bool scales = true) {
     r.l0 = ldg16(blk + 64 * n + 16 * hf);
     r.l1 = ldg16(blk + 64 * n + 32 + 16 * hf);
     r.hq = ldg16(blk + 128 + 32 * n + 16 * hf);
-    r.sc = ldg8(blk + 192 + 8 * n);
-    r.d = ldg_u16(blk + 208);
+    if (scales) {
+        r.sc = ldg8(blk + 192 + 8 * n);
+        r.d = ldg_u16(blk + 208);
+    }
 }
-__device__ __forceinline__ h2_t q6k_scale(const Q6Raw& r, int t, int kk, int hf) {
+__device__ __forceinline__ h2_t q6k_scale_of(uint2 sc, uint32_t dbits, int t, int kk, int hf) {
     const int i = 4 * t + 2 * (kk >> 1) + hf;
-    const uint32_t w = i < 4 ? r.sc.x : r.sc.y;
-    const float s = h2f((uint16_t)r.d) * (float)(int8_t)((w >> (8 * (i & 3))) & 0xFFu);
+    const uint32_t w = i < 4 ? sc.x : sc.y;
+    const float s = h2f((uint16_t)dbits) * (float)(int8_t)((w >> (8 * (i & 3))) & 0xFFu);
     const h2_t v = h2b(s);
     return t ? v * (h2_t){4.0f16, 4.0f16} : v;
+}
+__device__ __forceinline__ h2_t q6k_scale(const Q6Raw& r, int t, int kk, int hf) {
+    return q6k_scale_of(r.sc, r.d, t, kk, hf);
 }
 __device__ __forceinline__ f16x8_t q6k_frag(const Q6Raw& r, int t, int kk, h2_t sc, const QConst& qc) {
     const uint4& L = kk < 2 ? r.l0 : r.l1;
@@ -608,9 +613,20 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
                 constexpr int NBC = decltype(nbc)::value;
                 const int nb = NBC > 0 ? NBC : K / 256;
                 Q6Raw r[2][J];   // the raw words of halves (even, odd), per row
+                // with the block count known (fully unrolled), a block's 16 scales and d are loaded once (one 16-byte
+                // and one 2-byte load a lane, slot block & 1) rather than a half's 8 scales and d with every half:
+                // two fewer 32-row loads a block for the lanes' address path
+                uint4 scb[2][J];
+                uint32_t db[2][J];
                 load_a(0, 0);
 #pragma unroll
-                for (int j = 0; j < J; ++j) q6k_load(brow[j], 0, hf, r[0][j]);
+                for (int j = 0; j < J; ++j) {
+                    q6k_load(brow[j], 0, hf, r[0][j], NBC == 0);
+                    if constexpr (NBC > 0) {
+                        scb[0][j] = ldg16(brow[j] + 192);
+                        db[0][j] = ldg_u16(brow[j] + 208);
+                    }
+                }
                 load_a(1, 1);
                 store_a(0, 0);
 #pragma unroll
@@ -625,15 +641,31 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
                             if (t == 0 && 2 * b + n + 1 < 2 * nb) {   // the next half's words
                                 const int h1 = 2 * b + n + 1;
 #pragma unroll
-                                for (int j = 0; j < J; ++j)
-                                    q6k_load(brow[j] + 210 * (h1 >> 1), h1 & 1, hf, r[n ^ 1][j]);
+                                for (int j = 0; j < J; ++j) {
+                                    const uint8_t* blk = brow[j] + 210 * (h1 >> 1);
+                                    q6k_load(blk, h1 & 1, hf, r[n ^ 1][j], NBC == 0);
+                                    if constexpr (NBC > 0)
+                                        if ((h1 & 1) == 0) {   // the next block's scales
+                                            scb[(h1 >> 1) & 1][j] = ldg16(blk + 192);
+                                            db[(h1 >> 1) & 1][j] = ldg_u16(blk + 208);
+                                        }
+                                }
                             }
 #pragma unroll
                             for (int kk = 0; kk < 4; ++kk) {
                                 f16x8_t fb[J];
 #pragma unroll
-                                for (int j = 0; j < J; ++j)
-                                    fb[j] = q6k_frag(r[n][j], t, kk, q6k_scale(r[n][j], t, kk, hf), qc);
+                                for (int j = 0; j < J; ++j) {
+                                    h2_t sc;
+                                    if constexpr (NBC > 0) {
+                                        const uint4& q = scb[b & 1][j];
+                                        sc = q6k_scale_of(n ? make_uint2(q.z, q.w) : make_uint2(q.x, q.y), db[b & 1][j],
+                                                          t, kk, hf);
+                                    } else {
+                                        sc = q6k_scale(r[n][j], t, kk, hf);
+                                    }
+                                    fb[j] = q6k_frag(r[n][j], t, kk, sc, qc);
+                                }
                                 mfma_step(ks, kk, fb);
                             }
                             // A(ks + 1), loaded a step ago, into the buffer step ks - 1 read: at the step's end, so
