@@ -534,7 +534,7 @@ int prefill_experts(const xs_expert_layout_t* L, const float* x, int64_t n_tok, 
                     const int32_t* entry_of, const int32_t* bounds, const int32_t* n_groups,
                     const unsigned long long* grp_ptr, int64_t cap_groups, int64_t rows, void* scratch, float* parts,
                     uint16_t* parts_h, bool mtile_ready, void* stream, const SideStream* split = nullptr,
-                    int32_t* status = nullptr) {
+                    int32_t* status = nullptr, bool xb_ready = false) {
     if (rows <= 0 || cap_groups <= 0) return ok();
     if (int r = check_layout(L, "moe_prefill_experts")) return r;
     if (cap_groups > rows) return fail(XS_EINVAL, "moe_prefill_experts: cap_groups %lld > rows %lld", (long long)cap_groups,
@@ -557,6 +557,7 @@ int prefill_experts(const xs_expert_layout_t* L, const float* x, int64_t n_tok, 
     a.h = (uint16_t*)((uint8_t*)scratch + up256((size_t)n_tok * (size_t)L->n_embd * 2));
     a.mtile = prefill_mtile(scratch, n_tok, rows, L);
     a.mtile_ready = mtile_ready;
+    a.xb_ready = xb_ready;
     // the f16 saturation bit goes to the caller's status word, else to the scratch's own (xs_moe_prefill_status)
     a.err = status ? status : xs_moe_prefill_status(scratch, n_tok, rows, L->n_embd, L->n_ff);
     a.parts = parts;
@@ -1254,15 +1255,17 @@ int layer_prefill(const xs_expert_layout_t* L, const uint8_t* arena, size_t blob
         if (tall == 2) split = &serial;
         else if (hipError_t e = side_stream_get(&split)) return hip_status(e, who);
     }
+    // the permutation's launch also builds the GEMMs' f16 copy of x (at the scratch's start, prefill_experts' xb)
+    const xs::ToF16 conv{x, (uint16_t*)w.scratch, (int64_t)n_tok * L->n_embd / 8, w.status};
     if (int r = finish(stream,
                        xs::launch_prefill_route_split(w.ids, n, k, n_expert, w.src, w.slot, w.entry, w.bounds,
                                                       w.experts, w.n_groups, arena, (long long)blob_bytes, w.grp_ptr,
                                                       w.ghist, prefill_mtile(w.scratch, n_tok, n, L), (int)cap_groups,
-                                                      S(stream), split != nullptr),
+                                                      S(stream), split != nullptr, &conv),
                        who))
         return r;
     if (int r = prefill_experts(L, x, n_tok, w.src, w.entry, w.bounds, w.n_groups, w.grp_ptr, cap_groups, n, w.scratch,
-                                nullptr, w.parts, true, stream, split, w.status))
+                                nullptr, w.parts, true, stream, split, w.status, true))
         return r;
     if (side)   // the combine waits for the shared expert's rows
         if (hipError_t e = hipStreamWaitEvent(S(stream), side->join, 0)) return hip_status(e, who);

@@ -11,6 +11,7 @@
 //    experts inside a 64-entry step by a ballot match on the expert bits.  The rows come out in the host loop's order
 //    exactly.
 #include "xs_device.h"
+#include "xs_f16.h"
 #include "xs_kernels.h"
 #include "xs_route.h"
 
@@ -180,12 +181,18 @@ __global__ __launch_bounds__(1024) void route_fill_kernel(
     const int32_t* __restrict__ ids, int n, int k, int n_expert, int nbits, const int32_t* __restrict__ ghist, int nblk,
     int32_t* __restrict__ src, int32_t* __restrict__ slot, int32_t* __restrict__ entry, int32_t* __restrict__ bounds,
     int32_t* __restrict__ experts, int32_t* __restrict__ n_groups, const uint8_t* cache_base, long long blob,
-    unsigned long long* __restrict__ grp_ptr, int32_t* __restrict__ mtile, int cap_groups, int split) {
+    unsigned long long* __restrict__ grp_ptr, int32_t* __restrict__ mtile, int cap_groups, int split, ToF16 conv) {
     extern __shared__ int s_w[];   // [16][n_expert]: each wave's counts, then its bases
     __shared__ int s_wave[64];
     __shared__ int s_bad;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int E = n_expert, blk = blockIdx.x;
+    if (blk >= nblk) {   // the f16 copy of x, beside the permutation (it needs none of it)
+        const int64_t stride = (int64_t)(gridDim.x - nblk) * 1024;
+        for (int64_t c = (int64_t)(blk - nblk) * 1024 + tid; c < conv.n_chunks; c += stride)
+            to_f16_chunk(conv.x, conv.y, c, conv.err);
+        return;
+    }
     const int i = blk * kSeg + tid;
     const bool in = i < n;
     const int ev = in ? ids[i] : 0;
@@ -292,15 +299,20 @@ __global__ __launch_bounds__(1024) void route_fill_kernel(
 hipError_t launch_prefill_route_split(const int32_t* ids, int64_t n, int k, int n_expert, int32_t* src, int32_t* slot,
                                       int32_t* entry, int32_t* bounds, int32_t* experts, int32_t* n_groups,
                                       const uint8_t* cache_base, long long blob, unsigned long long* grp_ptr,
-                                      int32_t* ghist, int32_t* mtile, int cap_groups, hipStream_t s, bool split) {
+                                      int32_t* ghist, int32_t* mtile, int cap_groups, hipStream_t s, bool split,
+                                      const ToF16* conv) {
     int nbits = 1;
     while ((1 << nbits) < n_expert) ++nbits;
     const int nblk = (int)((n + kSeg - 1) / kSeg);
     hipLaunchKernelGGL(route_hist_kernel, dim3(nblk), dim3(256), (size_t)(n_expert + 1) * sizeof(int), s, ids, (int)n,
                        n_expert, ghist);
-    hipLaunchKernelGGL(route_fill_kernel, dim3(nblk), dim3(1024), (size_t)16 * n_expert * sizeof(int), s, ids, (int)n,
-                       k, n_expert, nbits, ghist, nblk, src, slot, entry, bounds, experts, n_groups, cache_base, blob,
-                       grp_ptr, mtile, cap_groups, split ? 1 : 0);
+    // with conv, one thread a chunk past the permutation's work-groups (up to 2048 work-groups, then a stride)
+    const ToF16 cv = conv ? *conv : ToF16{nullptr, nullptr, 0, nullptr};
+    const int64_t ncb = (cv.n_chunks + 1023) / 1024;
+    const int nconv = (int)(ncb < 2048 ? ncb : 2048);
+    hipLaunchKernelGGL(route_fill_kernel, dim3(nblk + nconv), dim3(1024), (size_t)16 * n_expert * sizeof(int), s, ids,
+                       (int)n, k, n_expert, nbits, ghist, nblk, src, slot, entry, bounds, experts, n_groups, cache_base,
+                       blob, grp_ptr, mtile, cap_groups, split ? 1 : 0, cv);
     return hipGetLastError();
 }
 

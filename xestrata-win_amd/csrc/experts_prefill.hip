@@ -32,13 +32,13 @@
 // fetched into that XCD's L2 once and reused across the n-tiles.
 #include "xs_device.h"
 #include "xs_dequant.h"
+#include "xs_f16.h"
 #include "xs_kernels.h"
 #include "xs_units.h"
 
 namespace xs {
 
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
-typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 constexpr int kBN = 256, kBK = 64;
@@ -57,33 +57,11 @@ __host__ __device__ constexpr int row_tiles(bool down, int t) {
     return t == kQ4_K || t == kQ8_0 || (down && t == kQ6_K) ? 4 : 2;
 }
 
-// slot order inside an octet and octet order inside a step (an involution)
-__host__ __device__ constexpr int perm8(int i) { return (i == 1 || i == 5) ? i + 1 : (i == 2 || i == 6) ? i - 1 : i; }
-__host__ __device__ constexpr int perm64(int p) { return 8 * perm8(p >> 3) + perm8(p & 7); }
-
-__device__ __forceinline__ uint32_t sat_f16x2(float a, float b) {   // RNE, saturated to the f16 range (NaN kept)
-    a = __builtin_fminf(__builtin_fmaxf(a, -65504.0f), 65504.0f);
-    b = __builtin_fminf(__builtin_fmaxf(b, -65504.0f), 65504.0f);
-    return __builtin_bit_cast(uint32_t, (h2_t){(_Float16)a, (_Float16)b});
-}
-
-// a value past the f16 range, saturated: status bit 8 (kSatBit) of the call's status word, when it has one
-constexpr int kSatBit = 8;
-__device__ __forceinline__ bool past_f16(float v) { return __builtin_fabsf(v) > 65504.0f; }   // (NaN: false)
-
 // x [n, H] fp32 -> f16 in the step order: thread i writes chunk i (8 values)
 __global__ __launch_bounds__(256) void to_f16_kernel(const float* __restrict__ x, uint16_t* __restrict__ y,
                                                      int64_t n_chunks, int32_t* __restrict__ err) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n_chunks) return;
-    const int c = (int)(i & 7);
-    const float* s = x + (i & ~(int64_t)7) * 8 + 8 * perm8(c);
-    const float4 v0 = *(const float4*)s, v1 = *(const float4*)(s + 4);
-    if (err && (past_f16(v0.x) || past_f16(v0.y) || past_f16(v0.z) || past_f16(v0.w) || past_f16(v1.x) ||
-                past_f16(v1.y) || past_f16(v1.z) || past_f16(v1.w)))
-        atomicOr(err, kSatBit);
-    *(uint4*)(y + 8 * i) = make_uint4(sat_f16x2(v0.x, v0.z), sat_f16x2(v0.y, v0.w), sat_f16x2(v1.x, v1.z),
-                                      sat_f16x2(v1.y, v1.w));
+    if (i < n_chunks) to_f16_chunk(x, y, i, err);
 }
 
 // the m-tile table (tile_list) of the groups in bounds: one work-group, the groups 1024 at a time; each thread
@@ -395,19 +373,20 @@ __device__ __forceinline__ void dma_rows(const uint8_t* const* src, size_t off, 
 template <bool DOWN, int T, int RT, bool MMQ = false>
 __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, PrefillArgs a,
                                                               const int32_t* __restrict__ mtile, int mt_bound,
-                                                              int n_tiles) {
+                                                              int n_tiles, int by_n) {
     constexpr int kBM = 32 * RT;
     constexpr int J = lane_rows(DOWN, T), BN = 128 * J;   // weight rows a lane; weight rows (output columns) a tile
     static_assert(DOWN || J == 2, "gate/up pairs a gate row with its up row in each lane");
     extern __shared__ __align__(16) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, hf = lane >> 5;
-    // work-group b runs on XCD x = b % 8.  With n-tiles a multiple of 8, XCD x takes n-tiles [x n8, x n8 + n8) of
-    // every m-tile, m-tile by m-tile: the weight slice of its n-tiles is fetched into its L2 once an expert and reused
-    // by the expert's m-tiles.  Otherwise XCD x takes m-tiles x, x + 8, ..., each with its n-tiles one after the
-    // other, so the m-tile's activations are fetched into its L2 once.
+    // work-group b runs on XCD x = b % 8.  With by_n (n-tiles a multiple of 8), XCD x takes n-tiles [x n8, x n8 + n8)
+    // of every m-tile, m-tile by m-tile: the weight slice of its n-tiles is fetched into its L2 once an expert and
+    // reused by the expert's m-tiles.  Otherwise XCD x takes m-tiles x, x + 8, ..., each with its n-tiles one after
+    // the other, so the m-tile's activations are fetched into its L2 once (the better order where groups hold one or
+    // two m-tiles, as the rows past the tall tiles do).
     const int c8 = (int)(blockIdx.x >> 3), xcd = (int)(blockIdx.x & 7);
     int mt, nt;
-    if (n_tiles % 8 == 0) {
+    if (by_n) {
         const int n8 = n_tiles >> 3;
         mt = c8 / n8;
         nt = xcd * n8 + c8 % n8;
@@ -1161,8 +1140,9 @@ bool tall_usable(const ExpertLayout& L) {
     return q(L.gu_type) && q(L.d_type) && L.n_ff % 256 == 0 && L.n_embd % 256 == 0;
 }
 
+// rest: the rows past the tall tiles (at most two m-tiles a group), whose tiles take the m-tile-per-XCD order
 template <bool DOWN, bool MMQ = false>
-static hipError_t launch_gemm(const ExpertLayout& L, const PrefillArgs& a, hipStream_t s) {
+static hipError_t launch_gemm(const ExpertLayout& L, const PrefillArgs& a, hipStream_t s, bool rest = false) {
     const int t = DOWN ? L.d_type : L.gu_type;
     const int n_tiles = DOWN ? (int)(L.n_embd / (128 * lane_rows(DOWN, t))) : (int)(L.n_ff / (kBN / 2));
     const bool q8_fast = (DOWN ? L.n_ff : L.n_embd) % 128 == 0;   // Q8_0's own path takes its K steps in pairs
@@ -1170,14 +1150,15 @@ static hipError_t launch_gemm(const ExpertLayout& L, const PrefillArgs& a, hipSt
     // tiles: at most ceil(rows / bm) + one partial tile a group (the standalone product counts every row of xq)
     const int64_t rows = MMQ ? a.n_tok : a.rows;
     const int mt_bound = (int)((rows + bm - 1) / bm + a.cap_groups);
-    const unsigned grid = (unsigned)(n_tiles % 8 == 0 ? mt_bound * n_tiles : 8 * ((mt_bound + 7) / 8) * n_tiles);
+    const int by_n = n_tiles % 8 == 0 && !rest;
+    const unsigned grid = (unsigned)(by_n ? mt_bound * n_tiles : 8 * ((mt_bound + 7) / 8) * n_tiles);
     const size_t lds = (size_t)entry_offset(bm) + (DOWN ? (size_t)bm * 4 : 0);
-    void (*k)(ExpertLayout, PrefillArgs, const int32_t*, int, int) =
+    void (*k)(ExpertLayout, PrefillArgs, const int32_t*, int, int, int) =
         t == kQ4_K   ? grouped_mfma_kernel<DOWN, kQ4_K, row_tiles(DOWN, kQ4_K), MMQ>
         : t == kQ6_K ? grouped_mfma_kernel<DOWN, kQ6_K, row_tiles(DOWN, kQ6_K), MMQ>
         : t == kQ8_0 && q8_fast ? grouped_mfma_kernel<DOWN, kQ8_0, row_tiles(DOWN, kQ8_0), MMQ>
                      : grouped_mfma_kernel<DOWN, 0, row_tiles(DOWN, 0), MMQ>;
-    hipLaunchKernelGGL(k, dim3(grid), dim3(256), lds, s, L, a, a.mtile, mt_bound, n_tiles);
+    hipLaunchKernelGGL(k, dim3(grid), dim3(256), lds, s, L, a, a.mtile, mt_bound, n_tiles, by_n);
     return hipGetLastError();
 }
 
@@ -1187,7 +1168,8 @@ hipError_t launch_mmq_product(const ExpertLayout& L, const PrefillArgs& a, hipSt
 
 hipError_t launch_prefill_experts(const ExpertLayout& L, const PrefillArgs& a, hipStream_t s) {
     const int64_t nc = a.n_tok * L.n_embd / 8;
-    hipLaunchKernelGGL(to_f16_kernel, dim3((unsigned)((nc + 255) / 256)), dim3(256), 0, s, a.x, a.xb, nc, a.err);
+    if (!a.xb_ready)
+        hipLaunchKernelGGL(to_f16_kernel, dim3((unsigned)((nc + 255) / 256)), dim3(256), 0, s, a.x, a.xb, nc, a.err);
     if (!a.mtile_ready)
         hipLaunchKernelGGL(tile_map_kernel, dim3(1), dim3(1024), 0, s, a.bounds, a.n_groups, a.mtile, a.rows,
                            (int)a.cap_groups);
@@ -1200,7 +1182,8 @@ hipError_t launch_prefill_experts_split(const ExpertLayout& L, const PrefillArgs
                                         hipEvent_t fork, hipEvent_t join) {
     if (!a.mtile_ready) return hipErrorInvalidValue;   // (the route writes the split maps and the tall list)
     const int64_t nc = a.n_tok * L.n_embd / 8;
-    hipLaunchKernelGGL(to_f16_kernel, dim3((unsigned)((nc + 255) / 256)), dim3(256), 0, s, a.x, a.xb, nc, a.err);
+    if (!a.xb_ready)
+        hipLaunchKernelGGL(to_f16_kernel, dim3((unsigned)((nc + 255) / 256)), dim3(256), 0, s, a.x, a.xb, nc, a.err);
     hipError_t e;
     const bool two = side != s;   // (side == s: the two chains one after the other)
     if (two && ((e = hipEventRecord(fork, s)) != hipSuccess || (e = hipStreamWaitEvent(side, fork, 0)) != hipSuccess))
@@ -1208,7 +1191,8 @@ hipError_t launch_prefill_experts_split(const ExpertLayout& L, const PrefillArgs
     // the tall tiles on s, first (a tall work-group takes a whole compute unit: issued first, they are placed before
     // the other chain's work-groups fill the units), the remainder rows on the side stream
     if ((e = launch_tall<false>(L, a, s)) != hipSuccess || (e = launch_tall<true>(L, a, s)) != hipSuccess) return e;
-    if ((e = launch_gemm<false>(L, a, side)) != hipSuccess || (e = launch_gemm<true>(L, a, side)) != hipSuccess)
+    if ((e = launch_gemm<false>(L, a, side, true)) != hipSuccess ||
+        (e = launch_gemm<true>(L, a, side, true)) != hipSuccess)
         return e;
     if (!two) return hipSuccess;
     if ((e = hipEventRecord(join, side)) != hipSuccess) return e;

@@ -62,14 +62,22 @@ hipError_t launch_prefill_route(const int32_t* ids, int64_t n, int k, int n_expe
                                 int32_t* entry, int32_t* bounds, int32_t* experts, int32_t* n_groups,
                                 const uint8_t* cache_base, long long blob, unsigned long long* grp_ptr, hipStream_t s);
 
+// the prompt GEMMs' f16 copy of x [n_tok, n_embd] (n_chunks = n_tok n_embd / 8), its saturation bit into err
+struct ToF16 {
+    const float* x;
+    uint16_t* y;
+    int64_t n_chunks;
+    int32_t* err;
+};
 // the same permutation over ceil(n / 1024) work-groups (ghist: prefill_route_split_scratch bytes), and, when mtile
 // is given, the m-tile table launch_prefill_experts would compute (PrefillArgs::mtile_ready), or with split the one
-// launch_prefill_experts_split takes (the tall list, and the maps over the rows past each group's tall tiles)
+// launch_prefill_experts_split takes (the tall list, and the maps over the rows past each group's tall tiles).  With
+// conv, work-groups past the permutation's build the f16 copy of x in the same launch (PrefillArgs::xb_ready).
 hipError_t launch_prefill_route_split(const int32_t* ids, int64_t n, int k, int n_expert, int32_t* src, int32_t* slot,
                                       int32_t* entry, int32_t* bounds, int32_t* experts, int32_t* n_groups,
                                       const uint8_t* cache_base, long long blob, unsigned long long* grp_ptr,
                                       int32_t* ghist, int32_t* mtile, int cap_groups, hipStream_t s,
-                                      bool split = false);
+                                      bool split = false, const ToF16* conv = nullptr);
 size_t prefill_route_split_scratch(int64_t n, int n_expert);
 
 // decode_layer.hip
@@ -189,6 +197,7 @@ struct PrefillArgs {
     uint16_t* parts_h;              // the same in f16 (saturated), written in place of parts when set
     int32_t* mtile;                 // scratch: the m-tile table (tile_table_words words, layout at tile_list)
     bool mtile_ready;               // mtile already holds it (launch_prefill_route_split wrote it)
+    bool xb_ready = false;          // xb already holds the f16 copy of x (launch_prefill_route_split built it)
     int32_t* err;
     int64_t n_tok, rows, cap_groups;
     int64_t ld_parts;               // values between the rows of parts / parts_h (n_embd for the layer's own)
