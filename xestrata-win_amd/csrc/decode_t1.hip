@@ -46,6 +46,7 @@ constexpr int kStoreWave = kT1Waves - 1;   // the wave that writes the hand-over
 constexpr int kDnWave0 = 4, kDnWaves = 4;   // waves 4..7: the DMA of the down rows (they quantize x before it and
                                             // decode the rows after it; they neither poll nor write h)
 constexpr int kHWords = 9;         // tagged words a 32-value q8_1 block of h: 8 x four codes, 1 scale
+constexpr int kFirstPollTicks = 140;   // wall-clock ticks (100 MHz) from a work-group's h store to its first h read
 // Every work-group polls every block of h with device-scope loads, which go past the L2 to the memory channel that
 // owns the line, and reads of one line queue there one after another: with the whole grid on each line a poll took
 // ~3 us to see a store.  So every block is written kHRep times, replica r read by the work-groups b with b % kHRep
@@ -276,7 +277,8 @@ __global__ __launch_bounds__(kT1) void moe_decode_t1_kernel(FusedArgs a) {
     int* s_ids = (int*)(lds + o.ids);
     float* s_w = (float*)(lds + o.w);
     int* s_spec = (int*)(lds + o.spec);
-    int* s_misc = (int*)(lds + o.misc);   // [0] 0 good / -1 bad routing, [1] the call's tag
+    int* s_misc = (int*)(lds + o.misc);   // [0] 0 good / -1 bad routing, [1] the call's tag, [2] down-row waves
+                                          // drained, [3] units to compute here, [4] the h store's time (| 1)
     float* s_gu = (float*)(lds + o.gu);   // gate outputs 0..31, then up outputs 0..31
     float* s_po = (float*)(lds + o.po);
     uint8_t* s_hq = lds + o.hq;
@@ -357,6 +359,9 @@ __global__ __launch_bounds__(kT1) void moe_decode_t1_kernel(FusedArgs a) {
         if (lane == 0) {
             s_misc[0] = bad ? -1 : 0;
             s_misc[1] = (int)ep;
+            s_misc[2] = 0;
+            s_misc[3] = 0;
+            s_misc[4] = 0;
         }
     } else if (spec_wave) {
         float lv[PER];
@@ -513,16 +518,23 @@ __global__ __launch_bounds__(kT1) void moe_decode_t1_kernel(FusedArgs a) {
                     a.hx + (size_t)r * t1_h_replica(k, F) + (size_t)(g_gu * nu + j_gu) * t1_h_stride(k);
                 t1_st_tag(dst + i, i < 8 ? ((const uint32_t*)s_hq)[i] : dbits, tag);
             }
+            if (lane == 0)   // when this work-group's h was stored: the pollers time their first read from it
+                __hip_atomic_store(&s_misc[4], (int)((uint32_t)wall_clock64() | 1u), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_WORKGROUP);
         }
     }
 
     // ---- 3. the down unit: rows j_dn * rd .. + rd of all k experts, combined in rank order, + residual
     if (has_dn) {
-        int* s_help = (int*)s_part;   // [0] count, then the units to compute here (s_part is free after gate/up)
-        if (tid == 0) s_help[0] = 0;
-        if (dn_wave) t1_vm_drain();   // the down rows have landed (every wave reads them after this barrier; polling
-                                      // h while they land measured slower: the polls slow the rows and the h stores)
-        t1_lds_barrier();
+        int* s_help = (int*)s_part;   // [1 ..]: the units to compute here, s_misc[3] of them (s_part is free after
+                                      // gate/up)
+        if (dn_wave) {   // the down rows have landed: counted in LDS (no barrier: the pollers need not wait for them)
+            t1_vm_drain();
+            if (lane == 0) __hip_atomic_fetch_add(&s_misc[2], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+        auto rows_in = [&]() {
+            return __hip_atomic_load(&s_misc[2], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= kDnWaves;
+        };
         uint8_t* dec = slab_gu;         // (the gate/up rows were done with at the barrier before the h hand-over)
         constexpr int dstr = t1_dec_stride(F);
         const int nblk = k * nu;
@@ -530,10 +542,14 @@ __global__ __launch_bounds__(kT1) void moe_decode_t1_kernel(FusedArgs a) {
         constexpr int kPollWaves = 3, kDecThreads = kT1 - 64 * (kPollWaves + 1);
         const bool poller = wave < kPollWaves;
         const int dtid = tid - 64 * kPollWaves;
-        // the k experts' q8_1 h: one block (9 words) a thread of the poller waves, read whole first (h is mostly
-        // stored before the down rows land, so one round trip); then the block's scale word alone (9x fewer loads in
-        // flight across the grid) until it carries the tag, and the block again.  (A word a lane, so that a wave's
-        // load reads a few lines, measured slower.)
+        // the k experts' q8_1 h: one block (9 words) a thread of the poller waves, read whole first; then the
+        // block's scale word alone (9x fewer loads in flight across the grid) until it carries the tag, and the block
+        // again.  (A word a lane, so that a wave's load reads a few lines, measured slower.)  The first read goes out
+        // kFirstPollTicks after this work-group's own h store, or when its down rows have landed if that is sooner
+        // (a work-group with no gate/up unit: when they land); a first read that misses waits for the down rows.
+        // Reads issued earlier, while h is not yet visible and the down rows are in flight, slow both: a first read
+        // at 0.6 or 1.0 us after the store took the layer from 13.7 to 15.1 or 14.6 us, at 1.4 us to 13.5 (config
+        // 1: 9.2 -> 9.0 us); polling from the end of gate/up on, 19.3 us.
         if (poller)
             for (int q = tid; q < nblk; q += 64 * kPollWaves) {
                 const int e = q / nu, j = q - e * nu;
@@ -556,8 +572,20 @@ __global__ __launch_bounds__(kT1) void moe_decode_t1_kernel(FusedArgs a) {
                 // started (other work holds the compute units it needs), so the unit goes on this work-group's list
                 // to be computed here after the polls; else the wait goes on for the rest of the bound.  So no wait
                 // depends on a work-group that is not resident.
+                // (every wait here ends: the store wave and the down-row waves are this work-group's own)
+                if (has_gu) {
+                    int st;
+                    while ((st = __hip_atomic_load(&s_misc[4], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) == 0)
+                        __builtin_amdgcn_s_sleep(1);
+                    while ((int)((uint32_t)wall_clock64() - (uint32_t)st) < kFirstPollTicks && !rows_in())
+                        __builtin_amdgcn_s_sleep(1);
+                } else {
+                    while (!rows_in()) __builtin_amdgcn_s_sleep(1);
+                }
                 poll(w);
                 bool good = a.spin_ticks > 0 && a.help_ticks >= 0 && tagged(w);
+                if (!good)
+                    while (!rows_in()) __builtin_amdgcn_s_sleep(1);
                 long long t0 = wall_clock64();
                 for (int it = 1; !good && a.spin_ticks > 0; ++it) {
                     const unsigned long long wd = t1_ld_tag(src + 8);
@@ -574,7 +602,7 @@ __global__ __launch_bounds__(kT1) void moe_decode_t1_kernel(FusedArgs a) {
                 if (!good && a.spin_ticks > 0) {
                     if (a.help_ticks < 0 || __hip_atomic_load(a.marks + 32 * (q & 31) + (q >> 5), __ATOMIC_RELAXED,
                                                               __HIP_MEMORY_SCOPE_AGENT) != tag) {
-                        s_help[1 + atomicAdd(&s_help[0], 1)] = q;
+                        s_help[1 + atomicAdd(&s_misc[3], 1)] = q;
                         continue;
                     }
                     for (int it = 1; !good; ++it) {
@@ -606,6 +634,7 @@ __global__ __launch_bounds__(kT1) void moe_decode_t1_kernel(FusedArgs a) {
                 ((float*)ad.d8)[j] = __uint_as_float((uint32_t)w[8]);
             }
         if (kDecode && !poller && wave != kStoreWave) {
+            while (!rows_in()) __builtin_amdgcn_s_sleep(1);   // (their DMA waves drained and counted themselves)
             // each row's 6-bit codes, one a byte (ql | qh << 4, Unit<Q6_K>'s words), its sub-block and block scales:
             // the products after h arrives are then plain int8 dots
             // 16 values a task (half of a 32-value group): 16 ql bytes and 16 qh bytes as aligned words, realigned
@@ -636,7 +665,7 @@ __global__ __launch_bounds__(kT1) void moe_decode_t1_kernel(FusedArgs a) {
         }
         t1_lds_barrier();
         // the units no owner ran (none when the grid was resident): computed here, one at a time
-        const int nh = s_help[0];
+        const int nh = s_misc[3];
         if (__builtin_expect(nh > 0, 0))
         for (int i = 0; i < nh; ++i) {
             const int q = s_help[1 + i];
