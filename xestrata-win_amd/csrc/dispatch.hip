@@ -183,7 +183,7 @@ __global__ __launch_bounds__(1024) void route_fill_kernel(
     int32_t* __restrict__ experts, int32_t* __restrict__ n_groups, const uint8_t* cache_base, long long blob,
     unsigned long long* __restrict__ grp_ptr, int32_t* __restrict__ mtile, int cap_groups, int split, ToF16 conv) {
     extern __shared__ int s_w[];   // [16][n_expert]: each wave's counts, then its bases
-    __shared__ int s_wave[64];
+    __shared__ int s_wave[128];    // (block_exclusive_scan_n<7>: 119)
     __shared__ int s_bad;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int E = n_expert, blk = blockIdx.x;
@@ -232,18 +232,22 @@ __global__ __launch_bounds__(1024) void route_fill_kernel(
                     if (b0 + u < blk) pre += c[u];
                 }
             }
-        int sum_all;
-        const int st = block_exclusive_scan(tot, s_wave, &sum_all) + carry;
-        if (blk == 0) {   // the groups (experts ascending), and the m-tile table of 128- and 64-row tiles
-            // (split: the group's whole 256-row tiles in the tall list, the maps over the rows past them)
+        int sum_all, st;
+        if (blk != 0) {
+            st = block_exclusive_scan(tot, s_wave, &sum_all) + carry;
+        } else {   // the groups (experts ascending), and the m-tile table of 128- and 64-row tiles
+            // (split: the group's whole 256-row tiles in the tall list, the maps over the rows past them); the seven
+            // scans in one pass of barriers
             const int ntall = split ? tot / 256 : 0, rest = tot - 256 * ntall;
-            int g_all, a0, a1, a2, a3, a4;
-            const int gi = block_exclusive_scan(tot > 0 ? 1 : 0, s_wave, &g_all) + gcarry;
-            const int b128 = block_exclusive_scan(rest / 128, s_wave, &a0) + f128;
-            const int q128 = block_exclusive_scan(rest % 128 ? 1 : 0, s_wave, &a1) + p128;
-            const int b64 = block_exclusive_scan(rest / 64, s_wave, &a2) + f64;
-            const int q64 = block_exclusive_scan(rest % 64 ? 1 : 0, s_wave, &a3) + p64;
-            const int bt = split ? block_exclusive_scan(ntall, s_wave, &a4) + ftall : 0;
+            const int sv[7] = {tot, tot > 0 ? 1 : 0, rest / 128, rest % 128 ? 1 : 0, rest / 64, rest % 64 ? 1 : 0, ntall};
+            int ex[7], tt[7];
+            block_exclusive_scan_n<7>(sv, s_wave, ex, tt);
+            st = ex[0] + carry;
+            sum_all = tt[0];
+            const int g_all = tt[1], a0 = tt[2], a1 = tt[3], a2 = tt[4], a3 = tt[5], a4 = tt[6];
+            const int gi = ex[1] + gcarry;
+            const int b128 = ex[2] + f128, q128 = ex[3] + p128, b64 = ex[4] + f64, q64 = ex[5] + p64;
+            const int bt = ex[6] + ftall;
             if (ee < E && tot > 0) {
                 experts[gi] = ee;
                 bounds[gi] = st;

@@ -231,6 +231,49 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* s_wave, int* tot
     return r;
 }
 
+// the same for N values at once (one pass of barriers for all of them): ex[i] the exclusive scan of v[i], total[i] its
+// sum; s_wave holds at least 17 N ints
+template <int N>
+__device__ __forceinline__ void block_exclusive_scan_n(const int (&v)[N], int* s_wave, int (&ex)[N], int (&total)[N]) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    int inc[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) inc[i] = v[i];
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            const int y = __shfl_up(inc[i], o, 64);
+            if (lane >= o) inc[i] += y;
+        }
+    }
+    if (lane == 63)
+#pragma unroll
+        for (int i = 0; i < N; ++i) s_wave[i * 16 + wave] = inc[i];
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            const int w = lane < nw ? s_wave[i * 16 + lane] : 0;
+            int wi = w;
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) {
+                const int y = __shfl_up(wi, o, 64);
+                if (lane >= o) wi += y;
+            }
+            if (lane == nw - 1) s_wave[16 * N + i] = wi;   // the total
+            if (lane < nw) s_wave[i * 16 + lane] = wi - w;   // exclusive over waves (after every lane read its slot)
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        ex[i] = s_wave[i * 16 + wave] + inc[i] - v[i];
+        total[i] = s_wave[16 * N + i];
+    }
+    __syncthreads();
+}
+
 // ---------------------------------------------------------------- the decode plan
 // Groups are the distinct experts in order of first occurrence and a group's entries ascend: the order the engine's
 // plan consumers expect (reference src/kernels/xe/verify_kernels.cpp:819-890, the host pool's plan
