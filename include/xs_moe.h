@@ -48,7 +48,8 @@ typedef struct xs_expert_layout {
 size_t xs_iq_row_bytes(int type, int64_t n);
 
 /* 1 when the grouped expert kernels take this gate/up and down type pair at these dimensions, else 0.
- * Replaces native_expert_supported (include/strata/kernels/iq_kernels.hpp:79). up_type -1: the gate's. */
+ * Replaces native_expert_supported (include/strata/kernels/iq_kernels.hpp:79). up_type -1: the gate's; another of the
+ * four types: a mixed layer, gate and up rows each of its own type (iq_kernels.cpp:2003-2005). */
 int xs_native_expert_supported(int gu_type, int d_type, int64_t n_embd, int64_t n_ff, int up_type);
 
 /* Replaces native_expert_layout (iq_kernels.hpp:81). */

@@ -515,20 +515,26 @@ float xso_vec_dot(int type, const uint8_t* row, const uint8_t* xq, int64_t n, in
 
 /* ------------------------------------------------------------------------------------------------ experts */
 
-/* iq_kernels.cpp:2002-2036 */
-int xso_native_layout(int gu_type, int d_type, int64_t n_embd, int64_t n_ff, xso_layout* L) {
-    const int qg = xso_block_values(gu_type), qd = xso_block_values(d_type);
-    if (!qg || !qd || n_embd <= 0 || n_ff <= 0 || n_embd % qg || n_ff % qd || n_embd % 256) return 0;
+/* iq_kernels.cpp:2002-2036 (native_expert_layout: gate rows, then up rows of up_type's row bytes, then down rows) */
+int xso_native_layout_mixed(int gu_type, int d_type, int64_t n_embd, int64_t n_ff, int up_type, xso_layout* L) {
+    const int qg = xso_block_values(gu_type), qd = xso_block_values(d_type), qu = xso_block_values(up_type);
+    if (!qg || !qd || !qu || n_embd <= 0 || n_ff <= 0 || n_embd % qg || n_embd % qu || n_ff % qd || n_embd % 256)
+        return 0;
     L->gu_type = gu_type;
     L->d_type = d_type;
+    L->up_type = up_type;
     L->n_embd = n_embd;
     L->n_ff = n_ff;
     L->gu_row = xso_row_bytes(gu_type, n_embd);
+    L->up_row = xso_row_bytes(up_type, n_embd);
     L->d_row = xso_row_bytes(d_type, n_ff);
     L->up_off = n_ff * L->gu_row;
-    L->down_off = L->up_off + n_ff * L->gu_row;
+    L->down_off = L->up_off + n_ff * L->up_row;
     L->bytes = L->down_off + n_embd * L->d_row;
     return 1;
+}
+int xso_native_layout(int gu_type, int d_type, int64_t n_embd, int64_t n_ff, xso_layout* L) {
+    return xso_native_layout_mixed(gu_type, d_type, n_embd, n_ff, gu_type, L);
 }
 
 /* iq_kernels.cpp:2042-2178 (launch_native_gu :997-1031, SwiGLU + q8_1 :2118-2133, launch_native_down :1033-1063) */
@@ -551,7 +557,7 @@ void xso_native_expert_grouped(const xso_layout* L, const uint8_t* const* blobs,
 #endif
             for (int64_t r = 0; r < F; ++r) {
                 gate[(int64_t)le * F + r] = xso_vec_dot(L->gu_type, blob + r * L->gu_row, x, H, 1);
-                up[(int64_t)le * F + r] = xso_vec_dot(L->gu_type, blob + L->up_off + r * L->gu_row, x, H, 1);
+                up[(int64_t)le * F + r] = xso_vec_dot((int)L->up_type, blob + L->up_off + r * L->up_row, x, H, 1);
             }
             float* h = (float*)malloc(sizeof(float) * (size_t)F);
             for (int64_t r = 0; r < F; ++r) h[r] = xso_canon_silu_mul(gate[(int64_t)le * F + r], up[(int64_t)le * F + r]);
@@ -820,7 +826,7 @@ void xso_expert_float(const xso_layout* L, const uint8_t* const* blobs, const fl
             float* wg = (float*)malloc(sizeof(float) * (size_t)H);
             float* wu = (float*)malloc(sizeof(float) * (size_t)H);
             xso_dequant_row(L->gu_type, blob + r * L->gu_row, H, wg);
-            xso_dequant_row(L->gu_type, blob + L->up_off + r * L->gu_row, H, wu);
+            xso_dequant_row((int)L->up_type, blob + L->up_off + r * L->up_row, H, wu);
             double g = 0.0, u = 0.0;
             for (int64_t i = 0; i < H; ++i) { g += (double)wg[i] * xr[i]; u += (double)wu[i] * xr[i]; }
             h[r] = (float)(g / (1.0 + exp(-g)) * u);

@@ -56,8 +56,12 @@ typedef struct {
     int gu_type, d_type;
     int64_t n_embd, n_ff;
     int64_t gu_row, d_row, up_off, down_off, bytes;
+    int64_t up_type, up_row;   /* the up rows' type and row bytes (the gate's, or another: a mixed layer) */
 } xso_layout;
 int xso_native_layout(int gu_type, int d_type, int64_t n_embd, int64_t n_ff, xso_layout* out);
+/* A mixed layer (iq_kernels.cpp:2003-2005, 2021-2036): gate rows of gu_type, up rows of up_type, each read as a
+ * gate/up matrix of its own type. */
+int xso_native_layout_mixed(int gu_type, int d_type, int64_t n_embd, int64_t n_ff, int up_type, xso_layout* out);
 
 /* Grouped experts (iq_kernels.cpp:2042-2178): group g reads blob blobs[g]; entries [start[g], start[g+1]) read token
  * ent_tok[e]'s q8_1 row of x_q8_1 and write row ent_dst[e] of out (n_embd floats).  gate/up/hq (optional, may be

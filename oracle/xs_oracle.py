@@ -22,7 +22,7 @@ I, I64, F = ctypes.c_int, ctypes.c_int64, ctypes.c_float
 
 class Layout(ctypes.Structure):
     _fields_ = [("gu_type", I), ("d_type", I), ("n_embd", I64), ("n_ff", I64), ("gu_row", I64), ("d_row", I64),
-                ("up_off", I64), ("down_off", I64), ("bytes", I64)]
+                ("up_off", I64), ("down_off", I64), ("bytes", I64), ("up_type", I64), ("up_row", I64)]
 
 
 _lib = None
@@ -59,6 +59,7 @@ def lib():
         L.xso_quantize_q8_1_rows.argtypes = [P, I64, I64, P]
         L.xso_quantize_q8_1_per32.argtypes = [P, I64, P]
         L.xso_native_layout.argtypes = [I, I, I64, I64, ctypes.POINTER(Layout)]
+        L.xso_native_layout_mixed.argtypes = [I, I, I64, I64, I, ctypes.POINTER(Layout)]
         L.xso_native_expert_grouped.argtypes = [ctypes.POINTER(Layout), P, P, I, P, P, P, P, P, P, P, I]
         L.xso_router_top10.argtypes = [P, I, I, I, P, P]
         L.xso_router_grouped_sigmoid.argtypes = [P, P, I, I, I, I, I, F, P, P]
@@ -240,9 +241,10 @@ def vec_dot(t, row, xq, n, s256, calls=False):
     return fn(t, _a(row), _a(xq), n, int(s256))
 
 
-def layout(gu, d, n_embd, n_ff):
+def layout(gu, d, n_embd, n_ff, up=-1):
+    """up >= 0 and not gu: a mixed layer (up rows of their own type)."""
     L = Layout()
-    if not lib().xso_native_layout(gu, d, n_embd, n_ff, ctypes.byref(L)):
+    if not lib().xso_native_layout_mixed(gu, d, n_embd, n_ff, gu if up < 0 else up, ctypes.byref(L)):
         raise ValueError("unsupported layout")
     return L
 

@@ -50,7 +50,25 @@ def test_supported(xm):
     assert not xm.native_expert_supported(12, 14, 2048 + 32, 768)       # n_embd not a whole number of 256s
     assert not xm.native_expert_supported(12, 14, 2048, 700)             # down rows not whole Q6_K blocks
     assert not xm.native_expert_supported(2, 14, 2048, 768)              # Q4_0: not one of the four formats
-    assert not xm.native_expert_supported(12, 14, 2048, 768, up=14)      # mixed gate/up types
+    # a mixed layer: gate and up each a gate/up type of its own (iq_kernels.cpp:2003-2005)
+    assert xm.native_expert_supported(12, 14, 2048, 768, up=14)
+    assert xm.native_expert_supported(14, 14, 2048, 768, up=8)
+    assert not xm.native_expert_supported(12, 14, 2048, 768, up=2)       # Q4_0 up rows: not one of the formats
+    assert not xm.native_expert_supported(8, 14, 1024 + 32, 768, up=12)  # n_embd not whole Q4_K blocks for the up rows
+
+
+def test_mixed_layout(xm, xo):
+    """The mixed layout (native_expert_layout with up_type, iq_kernels.cpp:2021-2036): gate rows of the gate's row
+    bytes, then up rows of the up type's, then down rows; the same offsets as the oracle's restatement."""
+    for gu, up, d, H, F in ((12, 14, 14, 2048, 768), (14, 8, 12, 1024, 512), (8, 23, 8, 4096, 256)):
+        L = xm.native_expert_layout(gu, d, H, F, up)
+        assert (L.gu_type, L.up_type, L.d_type) == (gu, up, d)
+        assert L.gu_row == xm.row_bytes(gu, H) and L.up_row == xm.row_bytes(up, H) and L.d_row == xm.row_bytes(d, F)
+        assert L.up_off == F * L.gu_row and L.down_off == L.up_off + F * L.up_row and L.bytes == L.down_off + H * L.d_row
+        O = xo.layout(gu, d, H, F, up)
+        assert (O.up_off, O.down_off, O.bytes, O.up_row) == (L.up_off, L.down_off, L.bytes, L.up_row)
+    same = xm.native_expert_layout(12, 14, 2048, 768)
+    assert same.up_type == 12 and same.up_row == same.gu_row
 
 
 def test_scratch_bytes(xm):

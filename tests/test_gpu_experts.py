@@ -123,7 +123,7 @@ def torch_reference_prefill(xm, arena, L, x, ids, E):
         rows = torch.nonzero(flat == e).flatten()
         blob = arena[e]
         wg = xm.iq_dequant_f32(L.gu_type, blob[:F * L.gu_row], F * H).reshape(F, H)
-        wu = xm.iq_dequant_f32(L.gu_type, blob[L.up_off:L.up_off + F * L.gu_row], F * H).reshape(F, H)
+        wu = xm.iq_dequant_f32(L.up_type, blob[L.up_off:L.up_off + F * L.up_row], F * H).reshape(F, H)
         wd = xm.iq_dequant_f32(L.d_type, blob[L.down_off:L.down_off + H * L.d_row], H * F).reshape(H, F)
         xs = x[rows // k]
         g = xs @ wg.t().contiguous()

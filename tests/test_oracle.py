@@ -633,3 +633,36 @@ def test_mmvf_block_size_known_answers(xo):
     2048 -> 256, 7168 -> 256, 2 -> 32."""
     for n_in, b in ((64, 32), (192, 96), (448, 224), (2048, 256), (7168, 256), (2, 32)):
         assert xo.lib().xso_mmvf_block(n_in) == b, n_in
+
+
+@pytest.mark.parametrize("gu,up", [(12, 14), (14, 8), (8, 23)])
+def test_mixed_layer_pinned_to_single_type(xo, gu, up):
+    """A mixed layer's rows (iq_kernels.cpp:2003-2005, 2021-2036: gate and up each a gate/up type of its own): its gate
+    rows are read as a same-type layer of the gate's type reads its gate rows, its up rows as a same-type layer of the
+    up type reads its gate rows - the oracle's mixed restatement equals its single-type one (pinned to the reference's
+    vectors above) row for row; and the down product sees that h."""
+    rng = np.random.default_rng(gu * 100 + up)
+    H, F, d = 512, 256, 14
+    M = xo.layout(gu, d, H, F, up)
+    A = xo.layout(gu, d, H, F)       # gate rows of the gate's type
+    B = xo.layout(up, d, H, F)       # the mixed layer's up rows as this layer's gate rows
+    g_rows = random_rows(xo, gu, F, H, rng)
+    u_rows = random_rows(xo, up, F, H, rng)
+    dn = random_rows(xo, d, H, F, rng)
+    mixed = np.concatenate([g_rows, u_rows, dn])
+    assert mixed.size == M.bytes
+    la = np.concatenate([g_rows, g_rows, dn])
+    lb = np.concatenate([u_rows, u_rows, dn])
+    assert la.size == A.bytes and lb.size == B.bytes
+    T = 3
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    xq = xo.quantize_q8_1_rows(x)
+    start, tok, dst = np.array([0, T], np.int32), np.arange(T, dtype=np.int32), np.arange(T, dtype=np.int32)
+    _, gm, um, hm = xo.native_expert_grouped(M, [mixed], start, dst, tok, xq, T, want_inner=True)
+    _, ga, _, _ = xo.native_expert_grouped(A, [la], start, dst, tok, xq, T, want_inner=True)
+    _, gb, _, _ = xo.native_expert_grouped(B, [lb], start, dst, tok, xq, T, want_inner=True)
+    assert np.array_equal(gm.view(np.uint32), ga.view(np.uint32))
+    assert np.array_equal(um.view(np.uint32), gb.view(np.uint32))
+    # h = SwiGLU(gate, up) to q8_1, then the down rows: as the oracle's own steps compute them
+    h = xo.canon_silu_mul(gm, um)
+    assert np.array_equal(hm, xo.quantize_q8_1_per32(h.reshape(-1)))

@@ -78,6 +78,8 @@ xs::ExpertLayout to_layout(const xs_expert_layout_t* L) {
     x.up_off = (int64_t)L->up_off;
     x.down_off = (int64_t)L->down_off;
     x.bytes = (int64_t)L->bytes;
+    x.up_type = L->up_type >= 0 ? L->up_type : L->gu_type;
+    x.up_row = L->up_row ? (int64_t)L->up_row : x.gu_row;
     return x;
 }
 
@@ -88,7 +90,7 @@ int check_layout(const xs_expert_layout_t* L, const char* what) {
                     L->d_type, (long long)L->n_embd, (long long)L->n_ff);
     xs_expert_layout_t want;
     if (xs_native_expert_layout(L->gu_type, L->d_type, L->n_embd, L->n_ff, L->up_type, &want) != XS_OK) return XS_EINVAL;
-    if (want.bytes != L->bytes || want.up_off != L->up_off || want.down_off != L->down_off)
+    if (want.bytes != L->bytes || want.up_off != L->up_off || want.down_off != L->down_off || want.up_row != L->up_row)
         return fail(XS_EINVAL, "%s: the layout's offsets are not native_expert_layout's", what);
     return ok();
 }
@@ -116,9 +118,10 @@ size_t xs_iq_row_bytes(int type, int64_t n) {
 }
 
 // the gate/up and down types of the four formats; every row a whole number of blocks; n_embd a whole number of 256s
-// (the q8_1 activation's 256-value scale; reference iq_kernels.cpp:2002-2019) and of 32s of units per lane set
+// (the q8_1 activation's 256-value scale; reference iq_kernels.cpp:2002-2019) and of 32s of units per lane set.  A
+// mixed layer (up_type >= 0 and not the gate's): gate and up each a gate/up type of its own (iq_kernels.cpp:2003-2005)
 int xs_native_expert_supported(int gu_type, int d_type, int64_t n_embd, int64_t n_ff, int up_type) {
-    if (up_type >= 0 && up_type != gu_type) return 0;   // mixed gate/up types: not built (no config uses them)
+    if (up_type >= 0 && up_type != gu_type && (!type_qk(up_type) || n_embd % type_qk(up_type))) return 0;
     if (!type_qk(gu_type) || !type_qk(d_type)) return 0;
     if (n_embd <= 0 || n_ff <= 0 || n_embd % 256 || n_ff % 32) return 0;
     if (n_embd % type_qk(gu_type) || n_ff % type_qk(d_type)) return 0;
@@ -134,11 +137,11 @@ int xs_native_expert_layout(int gu_type, int d_type, int64_t n_embd, int64_t n_f
                     gu_type, d_type, (long long)n_embd, (long long)n_ff);
     out->gu_type = gu_type;
     out->d_type = d_type;
-    out->up_type = gu_type;
+    out->up_type = up_type >= 0 ? up_type : gu_type;
     out->n_embd = n_embd;
     out->n_ff = n_ff;
     out->gu_row = xs_iq_row_bytes(gu_type, n_embd);
-    out->up_row = out->gu_row;
+    out->up_row = xs_iq_row_bytes(out->up_type, n_embd);
     out->d_row = xs_iq_row_bytes(d_type, n_ff);
     out->up_off = (size_t)n_ff * out->gu_row;
     out->down_off = out->up_off + (size_t)n_ff * out->up_row;
@@ -602,7 +605,8 @@ int xs_iq_mmq_grouped(int type, const void* w, size_t expert_bytes, int64_t w_ro
     L.gu_type = L.d_type = type;
     L.n_embd = w_rows;
     L.n_ff = w_cols;
-    L.gu_row = L.d_row = (int64_t)xs_iq_row_bytes(type, w_cols);
+    L.gu_row = L.d_row = L.up_row = (int64_t)xs_iq_row_bytes(type, w_cols);
+    L.up_type = type;
     L.up_off = L.down_off = 0;
     L.bytes = (int64_t)expert_bytes;
     xs::PrefillArgs a{};

@@ -843,7 +843,7 @@ static int device_cus() {
 
 bool fused_decode_plan(const ExpertLayout& L, int n_expert, int k, int n_tok, FusedPlan* P) {
     const int H = (int)L.n_embd, F = (int)L.n_ff, n = n_tok * k;
-    if (n > kFMaxN || n_expert > 1024 || k > 64 || n_tok > 64) return false;
+    if (n > kFMaxN || n_expert > 1024 || k > 64 || n_tok > 64 || mixed_gu(L)) return false;   // (one gate/up type)
     const bool pair = (L.gu_type == kQ4_K && L.d_type == kQ6_K) || (L.gu_type == kQ8_0 && L.d_type == kQ8_0) ||
                       (L.gu_type == kIQ4_XS && L.d_type == kIQ4_XS) || (L.gu_type == kQ4_K && L.d_type == kQ4_K);
     if (!pair || H % 256 || F % 32) return false;

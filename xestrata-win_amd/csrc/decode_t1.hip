@@ -788,7 +788,8 @@ hipError_t launch_decode_t1(const FusedArgs& a0, hipStream_t s, bool* used) {
     *used = false;
     const ExpertLayout& L = a0.L;
     const int H = (int)L.n_embd, F = (int)L.n_ff, k = a0.k;
-    if (a0.n_tok != 1 || k > kT1MaxK || a0.pre_ids || a0.sig_group > 0) return hipSuccess;   // (softmax top-k only)
+    if (a0.n_tok != 1 || k > kT1MaxK || a0.pre_ids || a0.sig_group > 0 || mixed_gu(L))
+        return hipSuccess;   // (softmax top-k only; one gate/up type)
     const T1Instance* inst = nullptr;
     for (const T1Instance& i : kT1Instances)
         if (i.gu == L.gu_type && i.d == L.d_type && i.H == H && i.F == F) inst = &i;

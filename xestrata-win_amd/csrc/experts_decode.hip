@@ -35,7 +35,7 @@ typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 // The whole grouped pass of one matrix (gate/up: DOWN false, down: DOWN true).
 template <int T, int LPR, bool DOWN, int NE>
 __global__ __launch_bounds__(kThreads) void grouped_kernel(ExpertLayout L, GroupedArgs a, int rows_total, int slab_rows,
-                                                           int64_t mat_off, int64_t rb) {
+                                                           int64_t mat_off, int64_t rb, int row0) {
     // gate/up: the staged rows carry kActPad bytes after every 256 int8 values (Unit's PAD), so that a row's lanes,
     // which read neighbouring 256-value blocks at once, hit distinct LDS banks
     constexpr int kPad = DOWN ? 0 : kActPad;
@@ -157,7 +157,7 @@ __global__ __launch_bounds__(kThreads) void grouped_kernel(ExpertLayout L, Group
 #pragma unroll
                 for (int e = 0; e < NE; ++e) acc[e] = group_sum<LPR>(acc[e]);
                 if (c == 0) {
-                    const int r = r0 + rr;
+                    const int r = row0 + r0 + rr;   // (gate/up: rows 0 .. F gate, F .. 2F up)
                     for (int e = 0; e < n; ++e) {
                         if (DOWN) a.out[(int64_t)a.ent_dst[p + e] * H + r] = acc[e];
                         else if (r < F) a.gate[(int64_t)(p + e) * F + r] = acc[e];
@@ -169,12 +169,15 @@ __global__ __launch_bounds__(kThreads) void grouped_kernel(ExpertLayout L, Group
     }
 }
 
+// part (gate/up only): 0 the gate and up rows as one matrix, 1 the gate rows alone, 2 the up rows alone (a mixed
+// layer's two launches, each of its own type)
 template <int T, bool DOWN>
-static hipError_t launch_t(const ExpertLayout& L, const GroupedArgs& a, hipStream_t s) {
+static hipError_t launch_t(const ExpertLayout& L, const GroupedArgs& a, hipStream_t s, int part = 0) {
     const int n_in = DOWN ? (int)L.n_ff : (int)L.n_embd;
-    const int rows_total = DOWN ? (int)L.n_embd : (int)(2 * L.n_ff);
-    const int64_t rb = DOWN ? L.d_row : L.gu_row;
-    const int64_t mat_off = DOWN ? L.down_off : 0;
+    const int rows_total = DOWN ? (int)L.n_embd : (int)(part ? L.n_ff : 2 * L.n_ff);
+    const int64_t rb = DOWN ? L.d_row : part == 2 ? L.up_row : L.gu_row;
+    const int64_t mat_off = DOWN ? L.down_off : part == 2 ? L.up_off : 0;
+    const int row0 = part == 2 ? (int)L.n_ff : 0;
     const int unit = Unit<T, !DOWN>::kUnit;
     const int lpr = canon_lanes(n_in / unit);
     const int per_pass = kThreads / lpr;
@@ -188,7 +191,7 @@ static hipError_t launch_t(const ExpertLayout& L, const GroupedArgs& a, hipStrea
     const size_t lds = (size_t)slab_rows * rb + (size_t)ne * (act_rowq(n_in, DOWN ? 0 : kActPad) + (n_in / 32) * 4 + (n_in / 16) * 4);
     const int64_t gy = a.grid_groups > 0 && a.grid_groups < a.cap_groups ? a.grid_groups : a.cap_groups;
     const dim3 grid((unsigned)((rows_total + slab_rows - 1) / slab_rows), (unsigned)gy);
-    void (*kern)(ExpertLayout, GroupedArgs, int, int, int64_t, int64_t) = nullptr;
+    void (*kern)(ExpertLayout, GroupedArgs, int, int, int64_t, int64_t, int) = nullptr;
     switch (lpr * 8 + ne) {
         case 8 * 8 + 1: kern = grouped_kernel<T, 8, DOWN, 1>; break;
         case 8 * 8 + 2: kern = grouped_kernel<T, 8, DOWN, 2>; break;
@@ -207,18 +210,25 @@ static hipError_t launch_t(const ExpertLayout& L, const GroupedArgs& a, hipStrea
         const hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL(kern, grid, dim3(kThreads), lds, s, L, a, rows_total, slab_rows, mat_off, rb);
+    hipLaunchKernelGGL(kern, grid, dim3(kThreads), lds, s, L, a, rows_total, slab_rows, mat_off, rb, row0);
     return hipGetLastError();
 }
 
-hipError_t launch_native_gu(const ExpertLayout& L, const GroupedArgs& a, hipStream_t s) {
-    switch (L.gu_type) {
-        case kQ4_K: return launch_t<kQ4_K, false>(L, a, s);
-        case kQ6_K: return launch_t<kQ6_K, false>(L, a, s);
-        case kQ8_0: return launch_t<kQ8_0, false>(L, a, s);
-        case kIQ4_XS: return launch_t<kIQ4_XS, false>(L, a, s);
+static hipError_t launch_gu_part(int type, const ExpertLayout& L, const GroupedArgs& a, hipStream_t s, int part) {
+    switch (type) {
+        case kQ4_K: return launch_t<kQ4_K, false>(L, a, s, part);
+        case kQ6_K: return launch_t<kQ6_K, false>(L, a, s, part);
+        case kQ8_0: return launch_t<kQ8_0, false>(L, a, s, part);
+        case kIQ4_XS: return launch_t<kIQ4_XS, false>(L, a, s, part);
         default: return hipErrorInvalidValue;
     }
+}
+
+hipError_t launch_native_gu(const ExpertLayout& L, const GroupedArgs& a, hipStream_t s) {
+    if (!mixed_gu(L)) return launch_gu_part(L.gu_type, L, a, s, 0);
+    // a mixed layer: the gate rows and the up rows as two matrices, each with its own type's unit and lanes
+    const hipError_t e = launch_gu_part(L.gu_type, L, a, s, 1);
+    return e != hipSuccess ? e : launch_gu_part(L.up_type, L, a, s, 2);
 }
 
 hipError_t launch_native_down(const ExpertLayout& L, const GroupedArgs& a, hipStream_t s) {

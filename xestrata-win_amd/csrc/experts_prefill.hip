@@ -338,6 +338,32 @@ __device__ __forceinline__ void dequant8(int type, const uint8_t* b, int g, int 
         const float d = rd_h(b);
 #pragma unroll
         for (int j = 0; j < 8; ++j) y[j] = (float)(int8_t)b[2 + o + j] * d;
+    } else if (type == kQ4_K) {   // (dequant32's arithmetic for values o .. o + 7 of group g)
+        const float d = rd_h(b), dmin = rd_h(b + 2);
+        const uint8_t* q = b + 4;
+        int sc, m;
+        if (g < 4) {
+            sc = q[g] & 63;
+            m = q[g + 4] & 63;
+        } else {
+            sc = (q[g + 4] & 0x0F) | ((q[g - 4] >> 6) << 4);
+            m = (q[g + 4] >> 4) | ((q[g] >> 6) << 4);
+        }
+        const float d1 = d * (float)sc, m1 = dmin * (float)m;
+        const uint8_t* qs = b + 16 + 32 * (g / 2) + o;
+        const int sh = 4 * (g % 2);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) y[j] = d1 * (float)((qs[j] >> sh) & 0x0F) - m1;
+    } else if (type == kQ6_K) {
+        const float d = rd_h(b + 208);
+        const int n = g / 4, s = g % 4;
+        const uint8_t* ql = b + 64 * n + 32 * (s & 1) + o;
+        const uint8_t* qh = b + 128 + 32 * n + o;
+        const float sd = d * (float)((const int8_t*)(b + 192 + 8 * n))[2 * s + o / 16];   // (o .. o + 7: one scale)
+        const int nsh = 4 * (s >> 1), hsh = 2 * s;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            y[j] = sd * (float)((int)(((ql[j] >> nsh) & 0x0F) | (((qh[j] >> hsh) & 3) << 4)) - 32);
     } else {
         const float d = rd_h(b);
         const unsigned scales_h = (unsigned)(b[2] | (b[3] << 8));
@@ -413,7 +439,6 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
     const int K = DOWN ? F : H;
     const int nk = K / kBK;
     const int n0 = nt * (DOWN ? BN : kBN / 2);
-    const int wtype = DOWN ? L.d_type : L.gu_type;
     const int64_t wrb = DOWN ? L.d_row : L.gu_row;
 
     // A by DMA: wave w fills rows [8 RT w, 8 RT (w + 1)) of the tile, 8 rows an instruction; lane l of instruction i
@@ -469,15 +494,21 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
     int cb[J];
 #pragma unroll
     for (int j = 0; j < J; ++j) cb[j] = DOWN ? 32 * J * wave + 32 * j : (j ? 128 + 32 * wave : 32 * wave);
+    // (gate/up: a gate row at wrow * gu_row, an up row at up_off + wrow * up_row - the same place as row F + wrow of
+    // one matrix when the up rows are of the gate's type; wtype[j] the row's type, which the generic path reads)
     const uint8_t* brow[J];
+    int wtype[J];
 #pragma unroll
     for (int j = 0; j < J; ++j) {
         const int col = cb[j] + (lane & 31);
-        const int wrow = DOWN ? n0 + col : (col < kBN / 2 ? n0 + col : F + n0 + (col - kBN / 2));
+        const bool up = !DOWN && col >= kBN / 2;
+        const int wrow = DOWN ? n0 + col : up ? n0 + (col - kBN / 2) : n0 + col;
         const uint8_t* wb;
         if constexpr (MMQ) wb = a.wtab ? a.wtab[g] + a.woff : a.wbase + (size_t)g * a.wstride;
         else wb = (const uint8_t*)a.wptr[g];
-        brow[j] = wb + (DOWN ? L.down_off : 0) + (int64_t)wrow * wrb;
+        brow[j] = DOWN ? wb + L.down_off + (int64_t)wrow * wrb
+                       : up ? wb + L.up_off + (int64_t)wrow * (L.up_row ? L.up_row : wrb) : wb + (int64_t)wrow * wrb;
+        wtype[j] = DOWN ? L.d_type : up && L.up_type >= 0 ? L.up_type : L.gu_type;
     }
 
     f32x16_t acc[RT][J];
@@ -719,7 +750,7 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
                 for (int kk = 0; kk < 4; ++kk) {
                     f16x8_t fb[J];
 #pragma unroll
-                    for (int j = 0; j < J; ++j) fb[j] = generic_frag(brow[j], wtype, ks * kBK, kk, hf);
+                    for (int j = 0; j < J; ++j) fb[j] = generic_frag(brow[j], wtype[j], ks * kBK, kk, hf);
                     mfma_step(ks, kk, fb);
                 }
             }
@@ -732,7 +763,7 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(ExpertLayout L, Pr
                 for (int kk = 0; kk < 4; ++kk) {
                     f16x8_t fb[J];
 #pragma unroll
-                    for (int j = 0; j < J; ++j) fb[j] = generic_frag(brow[j], wtype, ks * kBK, kk, hf);
+                    for (int j = 0; j < J; ++j) fb[j] = generic_frag(brow[j], wtype[j], ks * kBK, kk, hf);
                     mfma_step(ks, kk, fb);
                 }
             }
@@ -1137,13 +1168,14 @@ static hipError_t launch_tall(const ExpertLayout& L, const PrefillArgs& a, hipSt
 
 bool tall_usable(const ExpertLayout& L) {
     auto q = [](int t) { return t == kQ4_K || t == kQ6_K; };
-    return q(L.gu_type) && q(L.d_type) && L.n_ff % 256 == 0 && L.n_embd % 256 == 0;
+    return q(L.gu_type) && q(L.d_type) && !mixed_gu(L) && L.n_ff % 256 == 0 && L.n_embd % 256 == 0;
 }
 
 // rest: the rows past the tall tiles (at most two m-tiles a group), whose tiles take the m-tile-per-XCD order
 template <bool DOWN, bool MMQ = false>
 static hipError_t launch_gemm(const ExpertLayout& L, const PrefillArgs& a, hipStream_t s, bool rest = false) {
-    const int t = DOWN ? L.d_type : L.gu_type;
+    // (a mixed layer's gate/up: the generic path, which dequantizes each row by its own type)
+    const int t = DOWN ? L.d_type : mixed_gu(L) ? -1 : L.gu_type;
     const int n_tiles = DOWN ? (int)(L.n_embd / (128 * lane_rows(DOWN, t))) : (int)(L.n_ff / (kBN / 2));
     const bool q8_fast = (DOWN ? L.n_ff : L.n_embd) % 128 == 0;   // Q8_0's own path takes its K steps in pairs
     const int bm = 32 * row_tiles(DOWN, q8_fast ? t : (t == kQ8_0 ? 0 : t));

@@ -377,7 +377,7 @@ hipError_t launch_stream_t(const ExpertLayout& L, const GroupedArgs& a, hipStrea
 }  // namespace
 
 bool stream_usable(const ExpertLayout& L, int n_tok, int64_t cap_groups, int64_t cap_entries) {
-    if (n_tok < 2 || n_tok > 16) return false;
+    if (n_tok < 2 || n_tok > 16 || mixed_gu(L)) return false;   // (one gate/up type: the gate and up rows as one matrix)
     // the DMA reads whole 16-byte chunks: a matrix's last chunk must stay inside the blob
     if (L.bytes % 16 || L.up_off % 16 || L.down_off % 16) return false;
     const int types[2] = {L.gu_type, L.d_type};

@@ -11,7 +11,11 @@ struct ExpertLayout {   // one native expert blob: [gate rows | up rows | down r
     int gu_type, d_type;
     int64_t n_embd, n_ff;
     int64_t gu_row, d_row, up_off, down_off, bytes;
+    int up_type = -1;      // the up rows' type: gu_type's, or another gate/up type (a mixed layer; -1: gu_type)
+    int64_t up_row = 0;    // bytes of an up row (0: gu_row)
 };
+// a layer whose up rows are of another type than its gate rows (the paths that take one gate/up type refuse it)
+inline bool mixed_gu(const ExpertLayout& L) { return L.up_type >= 0 && L.up_type != L.gu_type; }
 
 // formats.hip
 hipError_t launch_quantize_rows(int type, const float* x, int64_t n, void* y, hipStream_t s);

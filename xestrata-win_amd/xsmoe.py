@@ -700,7 +700,7 @@ def fill_layer(out, L, seed, std=0.02, chunk=16):
     g.manual_seed(seed)
     for e0 in range(0, n_expert, chunk):
         c = min(chunk, n_expert - e0)
-        for off, rows, cols, t in ((0, L.n_ff, L.n_embd, L.gu_type), (L.up_off, L.n_ff, L.n_embd, L.gu_type),
+        for off, rows, cols, t in ((0, L.n_ff, L.n_embd, L.gu_type), (L.up_off, L.n_ff, L.n_embd, L.up_type),
                                    (L.down_off, L.n_embd, L.n_ff, L.d_type)):
             w = torch.randn(c * rows, cols, generator=g, device=out.device, dtype=torch.float32) * std
             nbytes = rows * row_bytes(t, cols)
@@ -710,19 +710,20 @@ def fill_layer(out, L, seed, std=0.02, chunk=16):
 
 
 def build_arena(n_expert, n_embd, n_ff, gu_type, d_type, seed=0, std=0.02, device="cuda", gen_device="cuda",
-                copies=1):
+                copies=1, up_type=-1):
     """Random fp32 N(0, std) expert weights quantized with this library's quantizer into the native in-place pack
     layout: `copies` x n_expert blobs of [gate rows | up rows | down rows] back to back in one HBM arena (uint8
     [copies * n_expert, blob]).  Weights are drawn with a torch generator seeded by `seed` on `gen_device` ("cpu"
     gives the same bits everywhere); copy c > 0 repeats copy 0's bytes at other addresses (for rotating past the
-    caches in timing loops).  Returns (arena, layout)."""
-    L = native_expert_layout(gu_type, d_type, n_embd, n_ff)
+    caches in timing loops).  up_type >= 0 (not gu_type): a mixed layer, its up rows of that type.  Returns (arena,
+    layout)."""
+    L = native_expert_layout(gu_type, d_type, n_embd, n_ff, up_type)
     blob = L.bytes
     arena = torch.empty(copies * n_expert, blob, dtype=torch.uint8, device=device)
     g = torch.Generator(device=gen_device)
     g.manual_seed(seed)
     for e in range(n_expert):
-        for off, rows, cols, t in ((0, n_ff, n_embd, gu_type), (L.up_off, n_ff, n_embd, gu_type),
+        for off, rows, cols, t in ((0, n_ff, n_embd, gu_type), (L.up_off, n_ff, n_embd, L.up_type),
                                    (L.down_off, n_embd, n_ff, d_type)):
             w = torch.randn(rows, cols, generator=g, device=gen_device, dtype=torch.float32) * std
             w = w.to(device)
