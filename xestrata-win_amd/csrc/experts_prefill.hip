@@ -1171,7 +1171,9 @@ bool tall_usable(const ExpertLayout& L) {
     return q(L.gu_type) && q(L.d_type) && !mixed_gu(L) && L.n_ff % 256 == 0 && L.n_embd % 256 == 0;
 }
 
-// rest: the rows past the tall tiles (at most two m-tiles a group), whose tiles take the m-tile-per-XCD order
+// rest: the rows past the tall tiles (at most two m-tiles a group).  Those, and groups of under 128 rows on average
+// (config 5's prompt: ~32 rows an expert, 2,394 -> 2,359 us), take the m-tile-per-XCD order: a group's weights are
+// fetched once either way, and the m-tile's activations once instead of into every XCD
 template <bool DOWN, bool MMQ = false>
 static hipError_t launch_gemm(const ExpertLayout& L, const PrefillArgs& a, hipStream_t s, bool rest = false) {
     // (a mixed layer's gate/up: the generic path, which dequantizes each row by its own type)
@@ -1182,7 +1184,7 @@ static hipError_t launch_gemm(const ExpertLayout& L, const PrefillArgs& a, hipSt
     // tiles: at most ceil(rows / bm) + one partial tile a group (the standalone product counts every row of xq)
     const int64_t rows = MMQ ? a.n_tok : a.rows;
     const int mt_bound = (int)((rows + bm - 1) / bm + a.cap_groups);
-    const int by_n = n_tiles % 8 == 0 && !rest;
+    const int by_n = n_tiles % 8 == 0 && !rest && !(rows < 128 * a.cap_groups);
     const unsigned grid = (unsigned)(by_n ? mt_bound * n_tiles : 8 * ((mt_bound + 7) / 8) * n_tiles);
     const size_t lds = (size_t)entry_offset(bm) + (DOWN ? (size_t)bm * 4 : 0);
     void (*k)(ExpertLayout, PrefillArgs, const int32_t*, int, int, int) =
