@@ -398,3 +398,34 @@ def test_decode_one_token_nan_routing(xm, c2_arena):
         layer.check()
     assert layer.status() == 0
     layer.check()
+
+
+def test_prefill_f16_copy_in_the_permutation_launch(xm):
+    """The prompt layer's f16 copy of x is built by the permutation launch's work-groups past its own, one 8-value
+    chunk a thread, at most 2,048 work-groups and a stride beyond: at 4,096 tokens of hidden 7,168 (3.7 M chunks) the
+    stride loop runs, every chunk is converted (the output within 2e-2 of the fp32 reference), and a saturating value
+    in the last chunk of the last token - the stride's last visit - still sets status bit 8."""
+    from test_gpu_experts import torch_reference_prefill
+    E, k, T, H, F = 8, 2, 4096, 7168, 256
+    arena, L = xm.build_arena(E, H, F, xm.Q8_0, xm.Q8_0, seed=21)
+    g = torch.Generator(device=DEV).manual_seed(22)
+    x = torch.randn(T, H, device=DEV, generator=g).to(torch.bfloat16).float()
+    res = torch.randn(T, H, device=DEV, generator=g)
+    logits = torch.randn(T, E, device=DEV, generator=g)
+    out = torch.empty_like(res)
+    layer = xm.MoeLayer(L, arena, E, k, T, prefill=True)
+    print(f"[case] prefill T={T} H={H} (the conversion's stride loop)", flush=True)
+    layer(x, logits, res, out)
+    torch.cuda.synchronize()
+    layer.check()
+    ids, w = xm.router_top10(logits, k)
+    moe = (torch_reference_prefill(xm, arena, L, x, ids, E).reshape(T, k, -1) * w[:, :, None]).sum(1)
+    rel = float(((out - res) - moe).abs().max() / moe.abs().max())
+    assert rel <= 2e-2, rel
+    x2 = x.clone()
+    x2[T - 1, H - 1] = 1e6
+    layer(x2, logits, res, out)
+    torch.cuda.synchronize()
+    assert layer.status() & 8
+    with pytest.raises(xm.XsError, match="f16 range"):
+        layer.check()
