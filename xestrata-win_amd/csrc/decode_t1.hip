@@ -51,9 +51,10 @@ constexpr int kFirstPollTicks = 140;   // wall-clock ticks (100 MHz) from a work
 // owns the line, and reads of one line queue there one after another: with the whole grid on each line a poll took
 // ~3 us to see a store.  So every block is written kHRep times, replica r read by the work-groups b with b % kHRep
 // == r, and the blocks of a replica lie t1_h_stride(k) words apart (other lines, mostly other channels).  The
-// hand-over region holds 256 * n_ff words: kHRep replicas of k * n_ff / 32 blocks (k <= 64; 32 replicas measured
-// no faster: past 8, the time is the loads' own latency under the polling of the whole grid).
-constexpr int kHRep = 8;
+// hand-over region holds 256 * n_ff words: kHRep replicas of k * n_ff / 32 blocks (k <= 64).  With the first reads
+// timed from the work-group's own store (below), 4 replicas measured fastest: config 2's layer 13.46 -> 13.42 us and
+// config 1's 9.11 -> 8.92 against 8, while 2 and 1 lose again (fewer stores, but more readers on each line).
+constexpr int kHRep = 4;
 __host__ __device__ constexpr int t1_h_stride(int k) { return 1024 / k < 16 ? 16 : 1024 / k; }
 __host__ __device__ constexpr int t1_h_replica(int k, int F) { return 32 * F; }   // words between replicas
 constexpr int kT1MaxK = 64;
