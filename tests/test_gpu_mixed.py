@@ -100,3 +100,35 @@ def test_prefill_layer_mixed(xm, gu, up, dt, H, F):
     moe = (parts.reshape(T, k, -1) * w[:, :, None]).sum(1)
     rel = float(((out - res) - moe).abs().max() / moe.abs().max())
     assert rel <= 2e-2, rel
+
+
+@pytest.mark.parametrize("T", [1, 3])
+def test_decode_mixed_shared_and_noalloc(xm, xo, T):
+    """A mixed routed layer with a mixed shared expert (its own one-group chain: the persistent one-expert layer takes
+    one gate/up type), against the oracle bit for bit; and the allocation-free entry point on the mixed layer equals
+    the workspace entry point bit for bit."""
+    E, k, H, F = 16, 4, 1024, 512
+    arena, L = xm.build_arena(E, H, F, 14, 12, seed=11 + T, up_type=8)
+    sarena, SL = xm.build_arena(1, H, 256, 12, 8, seed=12 + T, up_type=14)
+    g = torch.Generator(device=DEV).manual_seed(60 + T)
+    logits = torch.randn(T, E, device=DEV, generator=g)
+    x = torch.randn(T, H, device=DEV, generator=g).to(torch.bfloat16).float()
+    res = torch.randn(T, H, device=DEV, generator=g)
+    out = torch.empty_like(res)
+    print(f"[case] decode mixed + shared T={T}", flush=True)
+    layer = xm.MoeLayer(L, arena, E, k, T, shared=(SL, sarena[0], None))
+    layer(x, logits, res, out)
+    torch.cuda.synchronize()
+    assert layer.status() == 0
+    ids, _ = xo.router_top10(t2n(logits), k)
+    want = xo.moe_layer_decode_shared(xo.layout(14, 12, H, F, 8), used_blobs(arena, E, ids), k, t2n(x), t2n(logits),
+                                      t2n(res), xo.layout(12, 8, H, 256, 14), t2n(sarena[0]), None)
+    assert np.array_equal(t2n(out).view(np.uint32), want.view(np.uint32))
+    got = torch.full_like(res, float("nan"))
+    ref = torch.empty_like(res)
+    status = torch.zeros(1, dtype=torch.int32, device=DEV)
+    xm.MoeLayer(L, arena, E, k, T)(x, logits, res, ref)
+    xm.moe_layer_decode_noalloc(L, arena, E, k, x, logits, res, got, status=status)
+    torch.cuda.synchronize()
+    assert int(status.item()) == 0
+    assert torch.equal(got.view(torch.int32), ref.view(torch.int32))
