@@ -172,6 +172,66 @@ def read_traffic():
     return None
 
 
+def pmc_kernel_and_scale(rows, ctr, kernel, copy_kib, n_copies=4, min_dispatches=64):
+    """From a rocprofv3 --pmc counter CSV's rows (dicts: Dispatch_Id, Kernel_Name, Counter_Name, Counter_Value; a
+    counter may span several rows of one dispatch, which add up): (the kernel's mean `ctr` a dispatch, the scale that
+    makes the last n_copies device copies read copy_kib KiB each, the kernel's dispatch count), or None when there are
+    fewer than min_dispatches of the kernel, fewer than n_copies copies or copies whose counts differ."""
+    sums, names = {}, {}
+    for row in rows:
+        if row.get("Counter_Name") != ctr:
+            continue
+        did = int(row["Dispatch_Id"])
+        sums[did] = sums.get(did, 0.0) + float(row["Counter_Value"])
+        names[did] = row["Kernel_Name"]
+    ks = [v for i, v in sums.items() if kernel in names[i]]
+    cps = [sums[i] for i in sorted(sums) if "copyBuffer" in names[i]][-n_copies:]
+    if len(ks) < min_dispatches or len(cps) < n_copies or min(cps) <= 0 or max(cps) > 1.01 * min(cps):
+        return None   # (copies of one size read one count: anything else is not the calibration)
+    return sum(ks) / len(ks), copy_kib / (sum(cps) / len(cps)), len(ks)
+
+
+def live_traffic(timeout_s=180):
+    """HBM bytes per launch of the one-token kernel, measured in this run: two rocprofv3 --pmc passes (FETCH_SIZE, then
+    WRITE_SIZE, one counter a pass), each over a child `bench.py --pmc-run` - one cycle of the headline's rotation
+    (128 launches, every one reading its 8 experts from HBM), then 4 device copies of 256 MiB.  Each counter is scaled
+    by what it reads for those copies (a copy reads and writes its size).  Returns (bytes, detail) or (None, reason):
+    no rocprofv3, this process itself under a profiler, or a pass that failed or timed out (timeout -s KILL)."""
+    import csv
+    import glob
+    import shutil
+    import subprocess
+    import tempfile
+    rp = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
+    if not os.path.exists(rp):
+        return None, "rocprofv3 not found"
+    if any(k.startswith(("ROCPROF", "ROCP_")) for k in os.environ):
+        return None, "this run is itself under a profiler"
+    copy_kib = (256 << 20) / 1024.0
+    per = {}
+    for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
+        d = tempfile.mkdtemp(prefix="xs_pmc_")
+        try:
+            cmd = ["timeout", "-s", "KILL", str(timeout_s), rp, "--pmc", ctr, "--output-format", "csv", "-d", d,
+                   "-o", "run", "--", sys.executable, str(ROOT / "bench.py"), "--pmc-run"]
+            r = subprocess.run(cmd, capture_output=True, text=True, cwd=str(ROOT))
+            files = glob.glob(os.path.join(d, "**", "run_counter_collection.csv"), recursive=True)
+            if not files:
+                return None, f"{ctr} pass: no counter file (exit {r.returncode})"
+            with open(files[0]) as fh:
+                got = pmc_kernel_and_scale(csv.DictReader(fh), ctr, "moe_decode_t1_kernel", copy_kib)
+            if got is None:
+                return None, f"{ctr} pass: too few kernel or copy dispatches in its counters (exit {r.returncode})"
+            per[ctr] = got
+        finally:
+            shutil.rmtree(d, ignore_errors=True)
+    (f, fs, n), (w, ws, _) = per["FETCH_SIZE"], per["WRITE_SIZE"]
+    traffic = int(round((f * fs + w * ws) * 1024))
+    return traffic, (f"measured in this run: rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, over `bench.py --pmc-run` "
+                     f"({n} launches of the kernel), {f:.1f} x {fs:.3f} + {w:.1f} x {ws:.3f} KiB a launch, the "
+                     f"scales from 4 device copies of 256 MiB")
+
+
 def pmc_run(torch, xm, copies):
     """The workload of a rocprofv3 --pmc pass: the headline's rotation, one cycle of config-2 decode layers at T=1
     (8 copies x 16 disjoint expert sets = 128 launches, each reading its 8 experts from HBM) and, for calibration,
@@ -188,13 +248,14 @@ def pmc_run(torch, xm, copies):
     for i in range(copies * n_sets):
         c, s = i % copies, (i // copies) % n_sets
         layer(x, logits[s], res, out, arena=arena[c * E])
+    status = layer.status()   # (read before the calibration copies: its own small copy must not be among their last 4)
     src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda").fill_(1)
     dst = torch.empty_like(src)
     for _ in range(4):
         dst.copy_(src)
     torch.cuda.synchronize()
     log(f"pmc run: {copies * n_sets} decode layers ({k * L.bytes / 1e6:.2f} MB of expert weights each), "
-        f"4 copies of {256 << 20} bytes; status {layer.status()}")
+        f"4 copies of {256 << 20} bytes; status {status}")
 
 
 def pmc_prefill(torch, xm):
@@ -510,6 +571,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-others", action="store_true", help="skip configs 3 (verify), 4 and 5")
+    ap.add_argument("--no-live-pmc", action="store_true",
+                    help="take roofline.traffic from the committed rocprofv3 summary instead of two --pmc passes")
     ap.add_argument("--pmc-run", action="store_true", help="only the short workload of a rocprofv3 --pmc pass")
     ap.add_argument("--pmc-prefill", action="store_true", help="only 4 prefill layers, for a rocprofv3 --pmc pass")
     ap.add_argument("--pmc-verify", action="store_true",
@@ -600,10 +663,15 @@ def main():
     roof_bytes = bytes1
     roof_us = ms1 * 1e3
     roof_gbs = roof_bytes / (roof_us * 1e-6) / 1e9
-    traffic = read_traffic()
+    traffic, traffic_source = (None, "not measured (--no-live-pmc)") if args.no_live_pmc else live_traffic()
+    if traffic is None:
+        log(f"live HBM traffic: {traffic_source}; the committed summary's figure instead")
+        traffic = read_traffic()
+        traffic_source = (f"{TRAFFIC_FILE.relative_to(ROOT)}: rocprofv3 --pmc FETCH_SIZE + WRITE_SIZE of the same "
+                          "rotation (bench.py --pmc-run), scaled by a copy kernel of known size; read from the "
+                          f"committed summary, not measured in this run ({traffic_source})") if traffic else None
     log(f"fused decode kernel: {roof_us:.2f} us/launch, {roof_gbs:.0f} GB/s of {roof_bytes / 1e6:.2f} MB"
-        + (f", HBM traffic {traffic / 1e6:.2f} MB/launch (rocprofv3 --pmc, from {TRAFFIC_FILE.name})"
-           if traffic else ""))
+        + (f", HBM traffic {traffic / 1e6:.2f} MB/launch ({traffic_source.split(':')[0]})" if traffic else ""))
 
     # ---------------------------------------------------------------- this box's achieved peaks
     peaks = measured_peaks(torch, xm, arena, int(round(roof_bytes)) // 16 * 16)
@@ -693,9 +761,7 @@ def main():
                      "frac": round(roof_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "frac_measured_stream": round(roof_gbs / peaks["hbm_stream_gbs"], 4),
                      "frac_measured_one_launch": round(roof_gbs / peaks["hbm_one_launch_gbs"], 4),
-                     "traffic_source": f"{TRAFFIC_FILE.relative_to(ROOT)}: rocprofv3 --pmc FETCH_SIZE + WRITE_SIZE of "
-                                       "the same rotation (bench.py --pmc-run), scaled by a copy kernel of known size; "
-                                       "read from the committed summary, not measured in this run",
+                     "traffic_source": traffic_source,
                      "kernel": "moe_decode_t1_kernel<Q4_K, Q6_K, 2, 2048, 768, 8> (xs_moe_layer_decode at one token, "
                                "one launch a layer)",
                      "algorithmic_bytes_per_launch": round(roof_bytes), "avg_launch_us": round(roof_us, 3)},
