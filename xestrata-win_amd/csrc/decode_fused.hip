@@ -366,8 +366,30 @@ __global__ __launch_bounds__(fused_threads(NE, MODE)) void moe_decode_fused_kern
     const bool x_early = T == 1 && a.ttab == 0;
     if (x_early && wave > 0) {
         int8_t* q = (int8_t*)(lds + o.act_g);
-        for (int j8 = tid - 64; j8 < H / 8; j8 += NT - 64)
-            q8_1_256_to_act(a.x, j8, q, (float*)(q + act_q_bytes_g(H)), (int*)(q + act_q_bytes_g(H) + H / 8));
+        // every chunk of the thread loaded first, then quantized: the loads share one round trip instead of one a
+        // chunk (a chunk's quantization waits for its 32-lane block's amax, so a load-then-quantize loop exposes each
+        // load); up to kXEarly chunks a thread, past that the loop
+        constexpr int kXEarly = 8;
+        const int step = NT - 64;
+        if (H / 8 <= kXEarly * step) {
+            float v[kXEarly][8];
+#pragma unroll
+            for (int it = 0; it < kXEarly; ++it) {
+                const int j8 = tid - 64 + it * step;
+                if (j8 < H / 8)
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) v[it][i] = a.x[8 * j8 + i];
+            }
+#pragma unroll
+            for (int it = 0; it < kXEarly; ++it) {
+                const int j8 = tid - 64 + it * step;
+                if (j8 < H / 8)
+                    q8_1_256_store(v[it], j8, q, (float*)(q + act_q_bytes_g(H)), (int*)(q + act_q_bytes_g(H) + H / 8));
+            }
+        } else {
+            for (int j8 = tid - 64; j8 < H / 8; j8 += step)
+                q8_1_256_to_act(a.x, j8, q, (float*)(q + act_q_bytes_g(H)), (int*)(q + act_q_bytes_g(H) + H / 8));
+        }
     }
     // the pipelined path's token table: its first 8 chunks a thread (chunk i = 8 values of token i / (H / 8)) are
     // loaded beside the routing's logits (x does not depend on it); quantized into the table after the plan
