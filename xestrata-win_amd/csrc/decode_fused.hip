@@ -495,9 +495,19 @@ __global__ __launch_bounds__(fused_threads(NE, MODE)) void moe_decode_fused_kern
     // Round robin: when the gate/up units do not divide evenly, the work-groups that took one more of them (the first
     // n_gu % G) take the down units from the other end (work-group wg starts at G - 1 - wg), so they are the ones with
     // one down unit fewer: config 3's Zipf verify 51.2 -> 50.2 us, 8 tokens 83.0 -> 80.3, 16 tokens 133.7 -> 131.3.
-    const int d_begin = runs ? wg * dq + min(wg, dr) : (n_gu % G != 0 ? G - 1 - wg : wg);
-    const int d_end = runs ? d_begin + dq + (wg < dr ? 1 : 0) : n_dn;
-    const int d_step = runs ? 1 : G;
+    const int d_begin0 = runs ? wg * dq + min(wg, dr) : (n_gu % G != 0 ? G - 1 - wg : wg);
+    const int d_end0 = runs ? d_begin0 + dq + (wg < dr ? 1 : 0) : n_dn;
+    const int d_step0 = runs ? 1 : G;
+    // The direct form with fewer gate/up units than work-groups (config 5's routed experts at one token: 512 units,
+    // 1024 work-groups): no runs; the down units go round in the order the work-groups come free - those without a
+    // gate/up unit, then the others (a CU's later work-groups finish their units last) - while the units come in
+    // routing rank, the order in which the experts' h is complete.  In runs, work-groups still streaming gate/up rows
+    // held down units whose h was long in: config 5 T=1 107.3 -> 105.1 us.  (A constant false elsewhere: config 4's
+    // slab instance lost 3% to code that changed its register allocation though it never takes this path.)
+    const bool by_free = DIRECT && n_gu < G;
+    const int d_begin = by_free ? (wg >= n_gu ? wg - n_gu : G - n_gu + wg) : d_begin0;
+    const int d_end = by_free ? n_dn : d_end0;
+    const int d_step = by_free ? G : d_step0;
     const bool dn_early = !piped && !DIRECT && !a.slab_alias && n_gu <= G && wg < n_gu && d_begin < d_end;
     if (piped) {
         // 4..16 tokens, several units a work-group: every token's q8_1 activation once, into an LDS table, then the
