@@ -904,20 +904,30 @@ bool fused_decode_plan(const ExpertLayout& L, int n_expert, int k, int n_tok, Fu
     if (rd > 64) rd = 64;
     while (rd > 8 && H % rd) rd -= 8;
     if (H % rd) return false;
-    // one token with at least as many gate/up units as two work-groups a CU (large experts; a shared expert of
-    // hidden 7168 as a one-expert layer is one exactly: 111.3 -> 108.5 us at config 5): the direct form - a unit's rows
+    // one token with at least as many gate/up units as two work-groups a CU (large experts: config 5's routed layer):
+    // the direct form - a unit's rows
     // fill the work-group's lanes (each row's canonical lanes, 256 in all), every lane reads its blocks from HBM
     // itself, and without slabs the LDS holds up to four work-groups a CU, whose loads hide each other's latency
     // (only with at least 4 gate/up units a lane: fewer, and each lane's few dependent loads leave it idle - measured
     // slower at hidden 4096, 2 a lane)
     P->direct = 0;
     const int ug = H / (L.gu_type == kQ8_0 ? 32 : 256);
-    if (n_tok == 1 && (int64_t)k * (F / rh) >= 2 * device_cus() && ug / canon_lanes(ug) >= 4) {
+    if (n_tok == 1 && n_expert == 1 && (int64_t)k * (F / rh) >= 2 * device_cus() && ug / canon_lanes(ug) >= 4) {
+        // a one-expert layer (a shared expert as its own layer) that large stays in slabs: its rows, 8 canonical lanes
+        // each, fill only two waves a CU in the direct form, each lane reading scattered 34- or 144-byte blocks, while
+        // a slab's DMA streams whole rows; ~72 KB down slabs (config 5's Q8_0 shared expert: 32 rows, one down unit a
+        // work-group).  Config 5 T=1: direct 105.3 us; slabs with 16-row down slabs 101.3, 32 rows 99.1; 2 or 8 gate
+        // rows a gate/up unit instead of 4: 111 and 117 us (bit for bit throughout)
+        int rd1 = (int)((73728 / L.d_row) & ~7ll);
+        while (rd1 > 8 && H % rd1) rd1 -= 8;
+        if (rd1 >= 8 && H % rd1 == 0 && rd1 <= 64 &&
+            fused_lds<1>(n_expert, H, F, rh, 2 * rh * (int)L.gu_row, rd1 * (int)L.d_row, 0, 0).total <= 160 * 1024)
+            rd = rd1;
+    } else if (n_tok == 1 && (int64_t)k * (F / rh) >= 2 * device_cus() && ug / canon_lanes(ug) >= 4) {
         const int lg = canon_lanes(ug), ld = canon_lanes(F / 32);
-        // a gate/up unit fills the work-group's lanes; where that leaves fewer units than CUs (a one-expert layer: a
-        // shared expert of hidden 7168, 128 units), half as many rows a unit, so that twice the CUs stream the rows
-        // with half of each work-group's lanes (config 5 T=1: 105.6 -> 104.3 us; halving the down units as well,
-        // 118 us)
+        // a gate/up unit fills the work-group's lanes; where that leaves fewer units than CUs, half as many rows a
+        // unit, so that twice the CUs stream the rows with half of each work-group's lanes (measured on config 5's
+        // shared expert when it took this form: 105.6 -> 104.3 us; halving the down units as well, 118 us)
         const int rh2 = (int64_t)k * (F / (128 / lg)) < device_cus() ? 64 / lg : 128 / lg;
         const int rd2 = 256 / ld;
         if (F % rh2 == 0 && H % rd2 == 0 && rd2 <= 64) {
