@@ -884,6 +884,11 @@ bool fused_decode_plan(const ExpertLayout& L, int n_expert, int k, int n_tok, Fu
     if (rh < 8) rh = 8;
     while (rh > 8 && F % rh) rh -= 8;
     if (F % rh) return false;
+    // 4-8 tokens: 8-row h-slabs and (below) a token table for the call's tokens, so that two 512-thread work-groups
+    // fit a CU (~62 KB of LDS at 4 tokens, ~78 KB at 8; 16-row slabs and a 16-token table took ~135 KB, one a CU):
+    // config 2 T=4 54.6 -> 46.3 us, config 3's Zipf verify 49.4 -> 43.1, T=8 79.3 -> 75.5 (bit for bit).  At 16
+    // tokens the table alone is 47 KB: 4-row h-slabs and 16-row down slabs fit two a CU but took 207 against 130 us.
+    if (n_tok >= 4 && n_tok <= 8 && rh > 8 && F % 8 == 0) rh = 8;
     // one token: its k groups' gate/up units as close to one a resident work-group (two a CU) as the slab allows -
     // smaller slabs spread the weight stream over more CUs, and each work-group then also fetches its down rows
     // while its gate/up products run
@@ -955,9 +960,10 @@ bool fused_decode_plan(const ExpertLayout& L, int n_expert, int k, int n_tok, Fu
     // and 196.2 -> 177.3 us); without the table, two work-groups a CU measured no faster than one
     P->alias = n_tok >= 2;
     if (P->ne == 4 && n_tok <= 16 && lds_of(16) <= 160 * 1024) {
-        const FusedLds o4 = fused_lds<4>(n_expert, H, F, rh, P->slab_gu, P->slab_dn, 16, P->alias);
+        const int tt = (n_tok + 3) & ~3;   // the table: the call's tokens (rounded up to 4), not 16
+        const FusedLds o4 = fused_lds<4>(n_expert, H, F, rh, P->slab_gu, P->slab_dn, tt, P->alias);
         // the pipelined path plans in the LDS past its slab offset: E words for each 32 entries
-        if ((int64_t)n_expert * ((kFMaxN + 31) / 32) * 4 <= o4.total - o4.slab_gu) P->ttab = 16;
+        if ((int64_t)n_expert * ((kFMaxN + 31) / 32) * 4 <= o4.total - o4.slab_gu) P->ttab = tt;
     }
     P->lds = lds_of(P->ttab);
     return P->lds <= 160 * 1024;
