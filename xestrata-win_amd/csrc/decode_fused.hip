@@ -885,7 +885,7 @@ bool fused_decode_plan(const ExpertLayout& L, int n_expert, int k, int n_tok, Fu
     while (rh > 8 && F % rh) rh -= 8;
     if (F % rh) return false;
     // 4-8 tokens: 8-row h-slabs and (below) a token table for the call's tokens, so that two 512-thread work-groups
-    // fit a CU (~62 KB of LDS at 4 tokens, ~78 KB at 8; 16-row slabs and a 16-token table took ~135 KB, one a CU):
+    // fit a CU (~65 KB of LDS at 4 tokens, ~78 KB at 8; 16-row slabs and a 16-token table took ~135 KB, one a CU):
     // config 2 T=4 54.6 -> 46.3 us, config 3's Zipf verify 49.4 -> 43.1, T=8 79.3 -> 75.5 (bit for bit).  At 16
     // tokens the table alone is 47 KB: 4-row h-slabs and 16-row down slabs fit two a CU but took 207 against 130 us.
     if (n_tok >= 4 && n_tok <= 8 && rh > 8 && F % 8 == 0) rh = 8;
@@ -900,11 +900,12 @@ bool fused_decode_plan(const ExpertLayout& L, int n_expert, int k, int n_tok, Fu
                 break;
             }
     }
-    // down-slab rows: about 20 KB of down rows; 40 KB for one token (config 4's IQ4_XS rows: 32 rows, two down units
-    // a work-group of the grid: 46.6 -> 40.3 us a layer; 64 rows, one a work-group: 55.3 us) and from 8 tokens on
-    // (config 2 at 16 tokens: 198.2 -> 195.3 us); at 4 tokens, 40 KB slabs left Zipf-routed windows with too few down
-    // units: config 3's verify 59.7 -> 63.0 us
-    int rd = (int)(((n_tok == 1 || n_tok >= 8 ? 40960 : 20480) / L.d_row) & ~7ll);
+    // down-slab rows: about 20 KB of down rows at 2-3 tokens; 40 KB for one token (config 4's IQ4_XS rows: 32 rows,
+    // two down units a work-group of the grid: 46.6 -> 40.3 us a layer; 64 rows, one a work-group: 55.3 us) and from 4
+    // tokens on (config 2 at 16 tokens: 198.2 -> 195.3 us; at 4 tokens, with two work-groups a CU: 46.2 -> 43.7 us,
+    // config 3's Zipf verify 43.0 -> 40.6 - with one a CU the same slabs had cost the verify 59.7 -> 63.0; 16 rows at
+    // 4 tokens 54.3 us, 32 rows at 8 tokens 75.5 -> 82.3)
+    int rd = (int)(((n_tok == 1 || n_tok >= 4 ? 40960 : 20480) / L.d_row) & ~7ll);
     if (rd < 8) rd = 8;
     if (rd > 64) rd = 64;
     while (rd > 8 && H % rd) rd -= 8;
