@@ -307,6 +307,37 @@ def pmc_verify(torch, xm):
     log(f"pmc verify run: {copies} config-3 verify layers (T=4, Zipf); status {layer.status()}")
 
 
+def pmc_c5dec(torch, xm):
+    """The workload of a rocprofv3 pass on config 5's one-token decode: the bench's own rotation (32 routed sets, 8
+    copies of the shared expert; the group-limited sigmoid router inside the routed launch), one call a step, then 2
+    calibration copies of 256 MiB."""
+    E, H, F, k = 256, 7168, 2048, 8
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    arena, L = xm.build_arena(E, H, F, xm.Q4_K, xm.Q4_K, seed=5)
+    sarena, SL = xm.build_arena(1, H, 2048, xm.Q8_0, xm.Q8_0, seed=55, copies=8)
+    bias = torch.randn(E, device="cuda", generator=gen) * 0.1
+    router = xm.grouped_sigmoid_router(bias, 8, 4, 2.5)
+    n_sets = E // k
+    lg = torch.randn(n_sets, 1, E, device="cuda", generator=gen) - 4.0
+    for st in range(n_sets):
+        idx = [gi * 32 + 2 * (st // 2) + j for gi in ((0, 1, 2, 3) if st % 2 == 0 else (4, 5, 6, 7)) for j in (0, 1)]
+        lg[st, :, idx] += 12.0
+    x = torch.randn(1, H, device="cuda", generator=gen).to(torch.bfloat16).float()
+    res = torch.randn(1, H, device="cuda", generator=gen)
+    o = torch.empty(1, H, device="cuda")
+    layer = xm.MoeLayer(L, arena, E, k, 1, shared=(SL, sarena[0], None), router=router)
+    for st in range(n_sets):
+        layer(x, lg[st], res, o, shared_blob=sarena[st % 8])
+    status = layer.status()
+    src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(2):   # calibration of FETCH_SIZE / WRITE_SIZE: copies of a known size
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"pmc config-5 decode run: {n_sets} one-token layers (8 routed Q4_K experts + the Q8_0 shared expert each); "
+        f"status {status}")
+
+
 def pmc_tput(torch, xm):
     """The workload of a rocprofv3 --pmc pass on the throughput decode: one rotation of config-2 layers at T=16 (8 HBM
     copies, disjoint expert sets) and of config-4 layers at T=8 (2 HBM copies of the IQ4_XS layer, disjoint sets)."""
@@ -580,6 +611,7 @@ def main():
     ap.add_argument("--prefill-split", type=int, default=1, choices=(0, 1, 2),
                     help="the prompt layer's tall-tile split (xs_moe_set_prefill_tall): 1 on (the default), 0 off, 2 "
                          "its two chains one after the other (each kernel then times alone)")
+    ap.add_argument("--pmc-c5dec", action="store_true", help="only config 5's one-token rotation, for a rocprofv3 pass")
     ap.add_argument("--pmc-tput", action="store_true",
                     help="only config-2 T=16 and config-4 T=8 decode rotations, for a rocprofv3 --pmc pass")
     args = ap.parse_args()
@@ -604,6 +636,9 @@ def main():
         return
     if args.pmc_tput:
         pmc_tput(torch, xm)
+        return
+    if args.pmc_c5dec:
+        pmc_c5dec(torch, xm)
         return
     if args.pmc_verify:
         pmc_verify(torch, xm)
