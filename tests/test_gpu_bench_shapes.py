@@ -119,10 +119,12 @@ def c2_arena(xm):
     return xm.build_arena(128, 2048, 768, 12, 14, seed=2)
 
 
-@pytest.mark.parametrize("T,k", [(2, 8), (3, 8), (24, 8), (32, 8), (64, 4)])
+@pytest.mark.parametrize("T,k", [(2, 8), (3, 8), (5, 8), (8, 8), (12, 8), (24, 8), (32, 8), (64, 4)])
 def test_config2_decode_token_classes(xm, xo, c2_arena, T, k):
-    """The fused layer's other token classes at config 2: 2-3 tokens (NE = 2) and 17-64 tokens (NE = 4 without the
-    LDS token table: T = 24, 32 at top-8, T = 64 at top-4, 256 entries, the persistent layer's largest call)."""
+    """The fused layer's other token classes at config 2: 2-3 tokens (NE = 2); 5, 8 and 12 tokens (the pipelined
+    instance with its token table sized to the call, 8 and 12 tokens, and at 5-8 tokens 8-row h-slabs, two work-groups
+    a CU); 17-64 tokens (NE = 4 without the LDS token table: T = 24, 32 at top-8, T = 64 at top-4, 256 entries, the
+    persistent layer's largest call)."""
     arena, L = c2_arena
     g = torch.Generator(device=DEV).manual_seed(500 + T)
     logits = torch.randn(T, 128, device=DEV, generator=g)
