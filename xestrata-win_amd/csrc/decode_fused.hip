@@ -911,9 +911,9 @@ bool fused_decode_plan(const ExpertLayout& L, int n_expert, int k, int n_tok, Fu
     while (rd > 8 && H % rd) rd -= 8;
     if (H % rd) return false;
     // one token with at least as many gate/up units as two work-groups a CU (large experts: config 5's routed layer):
-    // the direct form - a unit's rows
-    // fill the work-group's lanes (each row's canonical lanes, 256 in all), every lane reads its blocks from HBM
-    // itself, and without slabs the LDS holds up to four work-groups a CU, whose loads hide each other's latency
+    // the direct form - a unit's rows fill the work-group's lanes (each row's canonical lanes, 256 in all), every lane
+    // reads its blocks from HBM itself, and without slabs the LDS holds up to four work-groups a CU, whose loads hide
+    // each other's latency
     // (only with at least 4 gate/up units a lane: fewer, and each lane's few dependent loads leave it idle - measured
     // slower at hidden 4096, 2 a lane)
     P->direct = 0;
