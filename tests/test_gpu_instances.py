@@ -4,6 +4,7 @@
   cpu_baseline line at T=1 runs it;
 * the one-token kernel's router widths at config 2's expert shape (Q4_K / Q6_K, hidden 2048, F 768, top-8): PER = 1
   (64 experts), PER = 2 (128, config 2 itself, tested in test_gpu_layer.py) and PER = 4 (256);
+* the one-token kernel's instance for config 2's shape quantized all Q4_K;
 * config 3's spec-verify batch exactly as bench.py builds it (4 tokens, Zipf(1.2) popularity from numpy's
   default_rng(3), Gumbel-top-k logits, the layer sized for 4 tokens), every copy of its rotation."""
 import numpy as np
@@ -55,3 +56,15 @@ def test_config3_verify_as_benched(xm, xo):
         print(f"[case] config3 verify copy={c}", flush=True)
         rel, moe_rel = decode_case(xm, xo, arena, L, E, k, T, zv[c].contiguous(), 40 + c)
         assert rel <= 1e-3 and moe_rel <= 1e-3, (c, rel, moe_rel)
+
+
+def test_one_token_all_q4k_instance(xm, xo):
+    """The one-token kernel's instance for config 2's shape quantized all Q4_K (hidden 2048, F 768, 128 experts,
+    top-8): gate/up as config 2's, the down rows Q4_K (Unit<Q4_K>'s 32-value units on the raw rows, no decode)."""
+    arena, L = xm.build_arena(128, 2048, 768, xm.Q4_K, xm.Q4_K, seed=31)
+    for seed in range(2):
+        g = torch.Generator(device=DEV).manual_seed(700 + seed)
+        logits = torch.randn(1, 128, device=DEV, generator=g)
+        print(f"[case] t1 all-Q4_K seed={seed}", flush=True)
+        rel, moe_rel = decode_case(xm, xo, arena, L, 128, 8, 1, logits, 710 + seed)
+        assert rel <= 1e-3 and moe_rel <= 1e-3, (rel, moe_rel)

@@ -25,8 +25,8 @@
 // One hand-over is left (h), written and read with device-scope relaxed atomics in 64-bit words whose upper half is
 // the call's tag (decode_fused.hip's scheme: no cache maintenance, no word ever reset).  Every wait is bounded and
 // points backwards (down units on gate/up units, which wait on nothing), and every work-group of the grid is resident.
-// Instances exist for config 2's (Q4_K / Q6_K, hidden 2048, F 768) and config 1's (Q8_0, 1024, 512) layers; other
-// layouts run decode_fused.hip's kernel.
+// Instances exist for config 2's (Q4_K / Q6_K, hidden 2048, F 768), the same shape all Q4_K, and config 1's (Q8_0,
+// 1024, 512) layers; other layouts run decode_fused.hip's kernel.
 #include "xs_device.h"
 #include "xs_kernels.h"
 #include "xs_route.h"
@@ -743,14 +743,15 @@ const void* t1_pick(int n_expert) {
                              : nullptr;
 }
 
-// the instances: config 2's layer (Q4_K gate/up, Q6_K down, hidden 2048, F 768) and config 1's (Q8_0, 1024, 512),
-// with as many down rows a unit as a 256-CU grid of one work-group a CU needs
+// the instances: config 2's layer (Q4_K gate/up, Q6_K down, hidden 2048, F 768), the same shape with Q4_K down rows,
+// and config 1's (Q8_0, 1024, 512), with as many down rows a unit as a 256-CU grid of one work-group a CU needs
 struct T1Instance {
     int gu, d, H, F, rd;
     const void* (*pick)(int);
 };
 const T1Instance kT1Instances[] = {
     {kQ4_K, kQ6_K, 2048, 768, 8, t1_pick<kQ4_K, kQ6_K, 2048, 768, 8>},
+    {kQ4_K, kQ4_K, 2048, 768, 8, t1_pick<kQ4_K, kQ4_K, 2048, 768, 8>},   // the same shape quantized all Q4_K
     {kQ8_0, kQ8_0, 1024, 512, 4, t1_pick<kQ8_0, kQ8_0, 1024, 512, 4>},
 };
 
