@@ -5,9 +5,9 @@
 // waits on as few memory round trips as possible.  One work-group of 1024 threads a CU:
 //
 //   1. Wave 0 of every work-group routes the token exactly (softmax over all experts in double, top-k, renormalised:
-//      router.cpp:59-145's arithmetic, xs_route.h).  Meanwhile waves 1-3 take the top-k of the raw logits - the same
+//      router.cpp:59-145's arithmetic, xs_route.h).  Meanwhile waves 1-6 take the top-k of the raw logits - the same
 //      experts in the same order unless two probabilities round to one float - and at once issue the LDS DMA of the
-//      work-group's gate/up rows for those experts; waves 4-7 quantize x to q8_1 (one scale a 256).  When the exact
+//      work-group's gate/up rows for those experts; waves 8-11 quantize x to q8_1 (one scale a 256).  When the exact
 //      routing disagrees with the speculation, the DMA is drained and issued again.  The down rows are fetched once
 //      the gate/up rows are in (or right after routing by a work-group with no gate/up unit), so that the gate/up
 //      rows, which every output waits on, have the memory system to themselves.
@@ -15,7 +15,7 @@
 //      is computed as it lands.  For Q4_K the integer sums of a block are split over four lanes (exact), then the
 //      block scales are applied in the canonical order and the canonical butterfly taken.  h = SwiGLU(gate, up) is
 //      quantized per 32 (the canonical q8_1 of the SwiGLU pass, iq_kernels.cpp:2118-2133) and handed over as 9
-//      tagged words (8 of four int8 codes, one of the scale), written to 8 replicas.
+//      tagged words (8 of four int8 codes, one of the scale), written to 4 replicas.
 //   3. A down unit is RD rows of the output for ALL k experts.  Its rows arrived with the first DMA; while h is on its
 //      way the Q6_K rows are decoded in LDS to one 6-bit code a byte.  The work-group polls the k experts' q8_1 h,
 //      computes the k x RD row dots, and combines them itself in rank order - fl(p0 w0) + fl(p1 w1) + ... then the
@@ -41,10 +41,16 @@ namespace {
 
 constexpr int kT1 = 1024;          // threads a work-group: 16 waves, 4 a SIMD
 constexpr int kT1Waves = kT1 / 64;
-constexpr int kSpecWaves = 3;      // waves 1..3: speculative routing and the weight DMA
+// waves 1..6: speculative routing and the weight DMA.  The issuing waves stall while the memory queues are full, so
+// more of them put the rows in flight sooner: config 2's layer 13.40 us with 3, 13.45 with 4, 12.96 with 5, 12.91 with
+// 6, 12.96 with 7, 13.13 with 8, 13.07 with 10 (config 1's: 8.98, 8.40, 8.30, 8.04, 8.07 us with 3 to 7)
+constexpr int kSpecWaves = 6;
+constexpr int kXWave0 = 8;         // waves 8..11: x to q8_1 (H / 8 chunks of 8 values, a thread each a round)
+static_assert(kXWave0 > kSpecWaves && kXWave0 + 4 <= 15, "x's waves are neither routing, DMA nor store waves");
 constexpr int kStoreWave = kT1Waves - 1;   // the wave that writes the hand-over words (and loads nothing after x)
-constexpr int kDnWave0 = 4, kDnWaves = 4;   // waves 4..7: the DMA of the down rows (they quantize x before it and
-                                            // decode the rows after it; they neither poll nor write h)
+constexpr int kDnWave0 = 4, kDnWaves = 4;   // waves 4..7: the DMA of the down rows (4..6 issue it after their
+                                            // speculative gate/up DMA has drained) and the decode of the rows after it;
+                                            // they neither poll nor write h
 constexpr int kHWords = 9;         // tagged words a 32-value q8_1 block of h: 8 x four codes, 1 scale
 constexpr int kFirstPollTicks = 140;   // wall-clock ticks (100 MHz) from a work-group's h store to its first h read
 // Every work-group polls every block of h with device-scope loads, which go past the L2 to the memory channel that
@@ -344,7 +350,7 @@ __global__ __launch_bounds__(kT1) void moe_decode_t1_kernel(FusedArgs a) {
         if (a.shared && a.shared_gate) c_gate = a.shared_gate[0];
     }
 
-    // ---- 1. routing (wave 0 exact; waves 1..3 speculate and fetch; waves 4..7 quantize x)
+    // ---- 1. routing (wave 0 exact; waves 1..6 speculate and fetch; waves 8..11 quantize x)
     if (wave == 0) {
         float lv[PER];
         load_logits_wave<PER>(a.logits, E, lv);
@@ -371,8 +377,8 @@ __global__ __launch_bounds__(kT1) void moe_decode_t1_kernel(FusedArgs a) {
         const bool ok = __ballot(lane < k && (sp < 0 || sp >= E)) == 0;
         if (wave == 1 && lane < k) s_spec[lane] = ok ? sp : -1;
         if (ok) issue([&](int i) { return __builtin_amdgcn_readlane(sp, i); });   // lane i holds the i-th
-    } else if (wave < 8) {
-        for (int j8 = tid - 256; j8 < H / 8; j8 += 256) {
+    } else if (wave >= kXWave0 && wave < kXWave0 + 4) {
+        for (int j8 = tid - 64 * kXWave0; j8 < H / 8; j8 += 256) {
             // q8_1 of values 8 j8 .. + 7, one scale a 256 (32 neighbouring lanes): quantize_q8_1_rows's values
             float v[8], am = 0.0f;
 #pragma unroll
