@@ -36,8 +36,8 @@ constexpr int kFT = 256;          // threads a work-group
 constexpr int kFTPiped = 512;
 __host__ __device__ constexpr int fused_threads(int ne, int mode) { return ne == 4 && mode == 1 ? kFTPiped : kFT; }
 constexpr int kFMaxN = 256;       // routed entries (tokens x k) a call
-constexpr int kLoadWaves = 3;     // waves 0..2 issue every global load; wave 3 every tagged store
-constexpr int kLT = 64 * kLoadWaves;
+constexpr int kLoadWaves = 3;     // waves 0..2 issue every global load; wave 3 every tagged store (the 256-thread
+                                  // instances; the pipelined one: FusedArgs::load_waves, wave 7 the stores)
 
 struct FusedLds {                 // byte offsets in the dynamic LDS
     int ids, w, excl, wave, first, gexp, start, dst, tok, misc, gu, po, slab_gu, slab_dn, act_g, act_d, total;
@@ -167,11 +167,12 @@ __device__ __forceinline__ void dma_wave_to_lds(uint8_t* dst, int n16, Src src) 
 }
 
 // n16 16-byte chunks to LDS dst[0 .. n16) by DMA (global_load_lds_dwordx4: a wave's instruction fills 64 consecutive
-// chunks at a wave-uniform LDS address), chunk i from src(i); issued by the load waves, complete at their vm_drain()
+// chunks at a wave-uniform LDS address), chunk i from src(i); issued by the lt / 64 load waves, complete at their
+// vm_drain()
 template <typename Src>
-__device__ __forceinline__ void dma_to_lds(uint8_t* dst, int n16, Src src) {
+__device__ __forceinline__ void dma_to_lds(uint8_t* dst, int n16, Src src, int lt) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    for (int base = 64 * wave; base < n16; base += kLT) {
+    for (int base = 64 * wave; base < n16; base += lt) {
         const int i = base + lane;
         if (i < n16)
             __builtin_amdgcn_global_load_lds(src(i), (__attribute__((address_space(3))) void*)(dst + 16 * base), 16, 0,
@@ -476,10 +477,16 @@ __global__ __launch_bounds__(fused_threads(NE, MODE)) void moe_decode_fused_kern
     // ---- 2. gate/up units
     const int n16a = rh * (int)L.gu_row / 16, n16d = rd * (int)L.d_row / 16;
     float* s_po = (float*)(lds + o.po);
-    const bool loader = wave < kLoadWaves;
-    // the one wave that writes tagged words (the others past the load waves only compute); with 512 threads, wave 4,
-    // which has no rows of a gate/up slab (32 rows x 8 lanes fill waves 0..3), so its SwiGLU and stores overlap them
-    const bool storer = wave == (NT > 256 ? 4 : kLoadWaves);
+    // the waves that issue every global load.  The issuing waves stall while the memory queues are full, so the
+    // pipelined instance issues from more of them: from 6 where one work-group fills a CU (config 2 at 16 tokens:
+    // 130.4 us with 3, 127.5 with 4, 124.8 with 5, 123.0 with 6), from 4 where two do (8 tokens: 75.5 with 3, 74.4 with
+    // 4, 74.9 with 5, 76.2 with 6; 4 tokens: 43.6, 43.3, 43.2, 44.1) - same box, alternating builds, bit for bit
+    const int LW = NT > 256 ? a.load_waves : kLoadWaves, LT = 64 * LW;
+    const bool loader = wave < LW;
+    // the one wave that writes tagged words (the others past the load waves only compute); with 512 threads, wave 7,
+    // which has no rows of a gate/up slab (32 rows x 8 lanes fill waves 0..3) and issues no loads, so its SwiGLU and
+    // stores overlap them
+    const bool storer = wave == (NT > 256 ? 7 : kLoadWaves);
     // with at most one gate/up unit a work-group, the store wave fetches the work-group's first down rows once the
     // gate/up slab is in: they then land while the gate/up products run and h travels
     const bool piped = NE == 4 && MODE == 1;   // the pipelined gate/up path below (4..16 tokens, the table in use)
@@ -515,7 +522,7 @@ __global__ __launch_bounds__(fused_threads(NE, MODE)) void moe_decode_fused_kern
         // but those DMAs meanwhile, so waiting for unit i is vmcnt <= (unit i + 1's DMA instructions of the wave).
         int8_t* ttab = (int8_t*)(lds + o.act_g);
         uint8_t* slab2[2] = {slab_gu, slab_gu + up16(a.slab_gu_bytes)};
-        const int per_wave = loader && 2 * n16a > 64 * wave ? (2 * n16a - 64 * wave + kLT - 1) / kLT : 0;
+        const int per_wave = loader && 2 * n16a > 64 * wave ? (2 * n16a - 64 * wave + LT - 1) / LT : 0;
         auto dma_unit = [&](int u, uint8_t* dst) {
             const int g = u / nu, j = u - g * nu;
             const uint8_t* blob = a.arena + (size_t)s_gexp[g] * (size_t)a.blob;
@@ -523,7 +530,7 @@ __global__ __launch_bounds__(fused_threads(NE, MODE)) void moe_decode_fused_kern
             const uint8_t* srcu = blob + L.up_off + (size_t)j * rh * L.gu_row;
             dma_to_lds(dst, 2 * n16a, [&](int i) {
                 return (const void*)(i < n16a ? srcg + 16 * (size_t)i : srcu + 16 * (size_t)(i - n16a));
-            });
+            }, LT);
         };
         // the first unit's DMA goes out before the table, so that its rows land while the table is built
         if (loader && wg < n_gu) dma_unit(wg, slab2[0]);
@@ -646,7 +653,7 @@ __global__ __launch_bounds__(fused_threads(NE, MODE)) void moe_decode_fused_kern
         if (loader && !DIRECT)
             dma_to_lds(slab_gu, 2 * n16a, [&](int i) {
                 return (const void*)(i < n16a ? srcg + 16 * (size_t)i : srcu + 16 * (size_t)(i - n16a));
-            });
+            }, LT);
         const int e0 = s_start[g], e1 = s_start[g + 1];
         for (int p = e0; p < e1; p += NE) {
             const int m = min(NE, e1 - p);
@@ -655,7 +662,7 @@ __global__ __launch_bounds__(fused_threads(NE, MODE)) void moe_decode_fused_kern
                 for (int e = 0; e < (x_early ? 0 : m); ++e) {    // the entries' tokens to q8_1, one scale a 256
                     const float* xr = a.x + (int64_t)s_tok[p + e] * H;
                     int8_t* q = (int8_t*)(lds + o.act_g) + e * act_stride_g(H);
-                    for (int j8 = tid; j8 < H / 8; j8 += kLT)
+                    for (int j8 = tid; j8 < H / 8; j8 += LT)
                         q8_1_256_to_act(xr, j8, q, (float*)(q + act_q_bytes_g(H)), (int*)(q + act_q_bytes_g(H) + H / 8));
                 }
                 vm_drain();   // the slab and the activations have landed
@@ -709,7 +716,7 @@ __global__ __launch_bounds__(fused_threads(NE, MODE)) void moe_decode_fused_kern
         lds_barrier();   // the previous unit's readers of the slab are done
         const bool fetched = dn_early && u2 == d_begin;
         if (loader && !fetched && !DIRECT)
-            dma_to_lds(slab_dn, n16d, [&](int i) { return (const void*)(srcd + 16 * (size_t)i); });
+            dma_to_lds(slab_dn, n16d, [&](int i) { return (const void*)(srcd + 16 * (size_t)i); }, LT);
         const int e0 = s_start[g], e1 = s_start[g + 1];
         for (int p = e0; p < e1; p += NE) {
             const int m = min(NE, e1 - p);
@@ -722,7 +729,7 @@ __global__ __launch_bounds__(fused_threads(NE, MODE)) void moe_decode_fused_kern
                 vm_drain();   // the slab has landed
             } else if (loader) {
                 const int c8n = F / 8;
-                for (int i0 = 0; i0 < m * c8n; i0 += kLT) {
+                for (int i0 = 0; i0 < m * c8n; i0 += LT) {
                     const int i = i0 + tid;
                     const bool in = i < m * c8n;
                     const int e = in ? i / c8n : 0, c8 = in ? i - e * c8n : 0;
@@ -1065,8 +1072,11 @@ hipError_t launch_decode_fused(const FusedArgs& a, const FusedPlan& P, hipStream
     if (e != hipSuccess) return e;
     const int cap = a.n_tok * a.k < a.n_expert ? a.n_tok * a.k : a.n_expert;
     const int need = cap * (P.nu > P.nj ? P.nu : P.nj);
+    FusedArgs a2 = a;
+    if (threads > kFT) a2.load_waves = grid > device_cus() ? 4 : 6;   // the pipelined instance: 4 load waves at two
+                                                                       // work-groups a CU, 6 at one
     if (grid > need) grid = need;
-    void* args[] = {(void*)&a};
+    void* args[] = {(void*)&a2};
     return hipLaunchKernel(kern, dim3(grid), dim3(threads), args, P.lds, s);
 }
 

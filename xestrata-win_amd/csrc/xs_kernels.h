@@ -136,6 +136,9 @@ struct FusedArgs {
     const float* sig_bias = nullptr;
     int sig_group = 0, sig_topk_group = 0;
     float sig_scale = 1.0f;
+    // the waves that issue the pipelined (512-thread) instance's loads: 6 where one work-group fills a CU, 4 where two
+    // do (launch_decode_fused sets it; the other instances use 3)
+    int load_waves = 4;
 };
 bool fused_decode_plan(const ExpertLayout& L, int n_expert, int k, int n_tok, FusedPlan* P);
 hipError_t launch_decode_fused(const FusedArgs& a, const FusedPlan& P, hipStream_t s);
