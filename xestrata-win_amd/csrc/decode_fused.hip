@@ -36,8 +36,10 @@ constexpr int kFT = 256;          // threads a work-group
 constexpr int kFTPiped = 512;
 __host__ __device__ constexpr int fused_threads(int ne, int mode) { return ne == 4 && mode == 1 ? kFTPiped : kFT; }
 constexpr int kFMaxN = 256;       // routed entries (tokens x k) a call
-constexpr int kLoadWaves = 3;     // waves 0..2 issue every global load; wave 3 every tagged store (the 256-thread
-                                  // instances; the pipelined one: FusedArgs::load_waves, wave 7 the stores)
+constexpr int kLoadWaves = 4;     // the 256-thread instances: all four waves issue the global loads, wave 3 also every
+                                  // tagged store (config 5 T=1 99.2-100.3 -> 98.2-98.3 us against three load waves,
+                                  // config 4's stack unchanged); the pipelined instance: FusedArgs::load_waves, wave 7
+                                  // the stores
 
 struct FusedLds {                 // byte offsets in the dynamic LDS
     int ids, w, excl, wave, first, gexp, start, dst, tok, misc, gu, po, slab_gu, slab_dn, act_g, act_d, total;
@@ -483,10 +485,10 @@ __global__ __launch_bounds__(fused_threads(NE, MODE)) void moe_decode_fused_kern
     // 4, 74.9 with 5, 76.2 with 6; 4 tokens: 43.6, 43.3, 43.2, 44.1) - same box, alternating builds, bit for bit
     const int LW = NT > 256 ? a.load_waves : kLoadWaves, LT = 64 * LW;
     const bool loader = wave < LW;
-    // the one wave that writes tagged words (the others past the load waves only compute); with 512 threads, wave 7,
+    // the one wave that writes tagged words (with 256 threads also a load wave); with 512 threads, wave 7,
     // which has no rows of a gate/up slab (32 rows x 8 lanes fill waves 0..3) and issues no loads, so its SwiGLU and
     // stores overlap them
-    const bool storer = wave == (NT > 256 ? 7 : kLoadWaves);
+    const bool storer = wave == (NT > 256 ? 7 : kLoadWaves - 1);
     // with at most one gate/up unit a work-group, the store wave fetches the work-group's first down rows once the
     // gate/up slab is in: they then land while the gate/up products run and h travels
     const bool piped = NE == 4 && MODE == 1;   // the pipelined gate/up path below (4..16 tokens, the table in use)
